@@ -1,0 +1,239 @@
+// Bidirectional-softmax C ABI: argument checks, workspace layout, launches.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdlib>
+#include <string>
+
+#include "bidi_kernels.cuh"
+#include "host.hpp"
+
+namespace dot_amd {
+namespace {
+
+int strip_rows_bidi(int B, int L1) {
+    static const int forced = [] {
+        const char* s = std::getenv("DOT_AMD_ROWS");
+        return s ? std::atoi(s) : 0;
+    }();
+    if (forced >= 1) return forced;
+    int r = 64;
+    while (r > 4 && int64_t(B) * ((L1 + r - 1) / r) < 1024) r /= 2;
+    return r;
+}
+
+size_t lds_bytes(int N) { return (size_t(2) * N + 8) * sizeof(float); }
+
+struct FwdLayout {
+    float *part_m, *part_s, *row_stats, *col_stats;
+    int rows, nstrips;
+    size_t bytes;
+};
+
+FwdLayout fwd_layout(void* ws, int B, int L1, int L2, bool own_stats) {
+    Carver c(ws);
+    FwdLayout L{};
+    L.rows = strip_rows_bidi(B, L1);
+    L.nstrips = (L1 + L.rows - 1) / L.rows;
+    L.part_m = c.take<float>(size_t(B) * L.nstrips * L2);
+    L.part_s = c.take<float>(size_t(B) * L.nstrips * L2);
+    if (own_stats) {
+        L.row_stats = c.take<float>(size_t(B) * 2 * L1);
+        L.col_stats = c.take<float>(size_t(B) * 2 * L2);
+    }
+    L.bytes = c.used();
+    return L;
+}
+
+struct BwdLayout {
+    float *dot_r, *dot_c, *partial, *tau_partial;
+    int rows, nstrips;
+    size_t bytes;
+};
+
+BwdLayout bwd_layout(void* ws, int B, int L1, int L2) {
+    Carver c(ws);
+    BwdLayout L{};
+    L.rows = strip_rows_bidi(B, L1);
+    L.nstrips = (L1 + L.rows - 1) / L.rows;
+    L.dot_r = c.take<float>(size_t(B) * L1);
+    L.dot_c = c.take<float>(size_t(B) * L2);
+    L.partial = c.take<float>(size_t(B) * L.nstrips * L2);
+    L.tau_partial = c.take<float>(size_t(B) * L.nstrips);
+    L.bytes = c.used();
+    return L;
+}
+
+__global__ void column_fold(const float* partial, int nstrips, int N, float* out) {
+    const int b = blockIdx.y;
+    const int j = blockIdx.x * kBlock + threadIdx.x;
+    if (j >= N) return;
+    const size_t base = size_t(b) * nstrips * N + j;
+    float s = 0.0f;
+    for (int k = 0; k < nstrips; ++k) s += partial[base + size_t(k) * N];
+    out[size_t(b) * N + j] = s;
+}
+
+__global__ void batch_sum(const float* partial, int nblk, float scale, float* out) {
+    const int b = blockIdx.x;
+    float s = 0.0f;
+    for (int k = threadIdx.x; k < nblk; k += kWave) s += partial[size_t(b) * nblk + k];
+    s = wave_sum(s);
+    if (threadIdx.x == 0) out[b] = s * scale;
+}
+
+__global__ void fill_value(float* p, size_t n, float value) {
+    for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+         i += size_t(gridDim.x) * blockDim.x)
+        p[i] = value;
+}
+
+int check_common(int B, int L1, int L2, float tau, const void* lengths) {
+    if (B < 0 || L1 < 0 || L2 < 0) return fail(DOT_ERR_INVALID_ARG, "B, L1 and L2 must be >= 0");
+    if (B > 65535) return fail(DOT_ERR_UNSUPPORTED, "batch size above 65535 is not supported");
+    if (L2 > kMaxRowLen)
+        return fail(DOT_ERR_UNSUPPORTED,
+                    "rows longer than 4096 columns are not supported by this build (L2=" +
+                        std::to_string(L2) + ")");
+    if (!(std::isfinite(tau) && tau > 0.0f)) return fail(DOT_ERR_INVALID_ARG, "tau must be > 0");
+    if (B > 0 && !lengths) return fail(DOT_ERR_INVALID_ARG, "lengths is NULL");
+    return DOT_OK;
+}
+
+}  // namespace
+}  // namespace dot_amd
+
+using namespace dot_amd;
+
+extern "C" size_t dot_bidisoftmax_forward_workspace_bytes(int B, int L1, int L2) {
+    if (B < 0 || L1 < 0 || L2 < 0) return 0;
+    return fwd_layout(nullptr, B, L1, L2, true).bytes;
+}
+
+extern "C" int dot_bidisoftmax_forward(const dot_bidisoftmax_fwd_args* a, dot_stream_t stream_) {
+    hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+    if (!a) return fail(DOT_ERR_INVALID_ARG, "args is NULL");
+    if (int rc = check_common(a->B, a->L1, a->L2, a->tau, a->lengths)) return rc;
+    const int B = a->B, L1 = a->L1, L2 = a->L2;
+    if (size_t(B) * L1 * L2 == 0) return ok();
+    if (!a->sim || !a->out) return fail(DOT_ERR_INVALID_ARG, "sim and out must be non-NULL");
+    const bool own_stats = !a->row_stats || !a->col_stats;
+    const FwdLayout L = fwd_layout(a->workspace, B, L1, L2, own_stats);
+    if (!a->workspace || a->workspace_bytes < L.bytes)
+        return fail(DOT_ERR_WORKSPACE, "workspace smaller than dot_bidisoftmax_forward_workspace_bytes()");
+    bidi::FwdArgs x{};
+    x.sim = a->sim;
+    x.lengths = a->lengths;
+    x.inv_T = 1.0f / a->tau;  // kernels.cu:426
+    x.L1 = L1;
+    x.L2 = L2;
+    x.rows = L.rows;
+    x.nstrips = L.nstrips;
+    x.row_stats = own_stats ? L.row_stats : a->row_stats;
+    x.col_stats = own_stats ? L.col_stats : a->col_stats;
+    x.part_m = L.part_m;
+    x.part_s = L.part_s;
+    x.out = a->out;
+    x.row_sm = a->row_sm;
+    x.col_sm = a->col_sm;
+    const bool vec4 = (L2 % 4 == 0) && aligned16(a->sim) && aligned16(a->out) &&
+                      (!a->row_sm || aligned16(a->row_sm)) && (!a->col_sm || aligned16(a->col_sm));
+    const dim3 strips(L.nstrips, B);
+    bool launched = dispatch_row(L2, vec4, [&](auto vc, auto cc) {
+        constexpr int V = decltype(vc)::value;
+        constexpr int C = decltype(cc)::value;
+        {
+            ProfScope prof("bidi_fwd_stats", stream);
+            hipLaunchKernelGGL((bidi::fwd_stats<V, C>), strips, dim3(kBlock), lds_bytes(L2), stream, x);
+        }
+        {
+            ProfScope prof("bidi_fwd_col_combine", stream);
+            hipLaunchKernelGGL(bidi::fwd_col_combine, dim3((L2 + kBlock - 1) / kBlock, B),
+                               dim3(kBlock), 0, stream, x);
+        }
+        {
+            ProfScope prof("bidi_fwd_write", stream);
+            hipLaunchKernelGGL((bidi::fwd_write<V, C>), strips, dim3(kBlock), 0, stream, x);
+        }
+    });
+    if (!launched) return fail(DOT_ERR_UNSUPPORTED, "row length outside the supported range");
+    return check_launch("dot_bidisoftmax_forward");
+}
+
+extern "C" size_t dot_bidisoftmax_backward_workspace_bytes(int B, int L1, int L2) {
+    if (B < 0 || L1 < 0 || L2 < 0) return 0;
+    return bwd_layout(nullptr, B, L1, L2).bytes;
+}
+
+extern "C" int dot_bidisoftmax_backward(const dot_bidisoftmax_bwd_args* a, dot_stream_t stream_) {
+    hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+    if (!a) return fail(DOT_ERR_INVALID_ARG, "args is NULL");
+    if (int rc = check_common(a->B, a->L1, a->L2, a->tau, a->lengths)) return rc;
+    const int B = a->B, L1 = a->L1, L2 = a->L2;
+    if (size_t(B) * L1 * L2 == 0) {
+        if (B > 0 && a->grad_tau)
+            hipLaunchKernelGGL(fill_value, dim3(1), dim3(kBlock), 0, stream, a->grad_tau, size_t(B), 0.0f);
+        return check_launch("dot_bidisoftmax_backward");
+    }
+    if (!a->sim || !a->grad_out || !a->grad_sim || !a->grad_tau)
+        return fail(DOT_ERR_INVALID_ARG, "sim, grad_out, grad_sim and grad_tau must be non-NULL");
+    const bool buffers = a->out && a->row_sm && a->col_sm;
+    if (!buffers && !(a->row_stats && a->col_stats))
+        return fail(DOT_ERR_INVALID_ARG,
+                    "pass either (out, row_sm, col_sm) or (row_stats, col_stats)");
+    const BwdLayout L = bwd_layout(a->workspace, B, L1, L2);
+    if (!a->workspace || a->workspace_bytes < L.bytes)
+        return fail(DOT_ERR_WORKSPACE, "workspace smaller than dot_bidisoftmax_backward_workspace_bytes()");
+    bidi::BwdArgs x{};
+    x.sim = a->sim;
+    x.lengths = a->lengths;
+    x.inv_T = 1.0f / a->tau;
+    x.L1 = L1;
+    x.L2 = L2;
+    x.rows = L.rows;
+    x.nstrips = L.nstrips;
+    x.grad_out = a->grad_out;
+    x.out = a->out;
+    x.row_sm = a->row_sm;
+    x.col_sm = a->col_sm;
+    x.row_stats = a->row_stats;
+    x.col_stats = a->col_stats;
+    x.dot_r = L.dot_r;
+    x.dot_c = L.dot_c;
+    x.partial = L.partial;
+    x.grad_sim = a->grad_sim;
+    x.tau_partial = L.tau_partial;
+    bool vec4 = (L2 % 4 == 0) && aligned16(a->sim) && aligned16(a->grad_out) && aligned16(a->grad_sim);
+    if (buffers) vec4 = vec4 && aligned16(a->out) && aligned16(a->row_sm) && aligned16(a->col_sm);
+    const dim3 strips(L.nstrips, B);
+    bool launched = dispatch_row(L2, vec4, [&](auto vc, auto cc) {
+        constexpr int V = decltype(vc)::value;
+        constexpr int C = decltype(cc)::value;
+        auto run = [&](auto recompute) {
+            constexpr bool RC = decltype(recompute)::value;
+            {
+                ProfScope prof("bidi_bwd_dots", stream);
+                hipLaunchKernelGGL((bidi::bwd_dots<V, C, RC>), strips, dim3(kBlock), lds_bytes(L2),
+                                   stream, x);
+            }
+            {
+                ProfScope prof("bidi_bwd_fold", stream);
+                hipLaunchKernelGGL(column_fold, dim3((L2 + kBlock - 1) / kBlock, B), dim3(kBlock), 0,
+                                   stream, L.partial, L.nstrips, L2, L.dot_c);
+            }
+            {
+                ProfScope prof("bidi_bwd_write", stream);
+                hipLaunchKernelGGL((bidi::bwd_write<V, C, RC>), strips, dim3(kBlock), 0, stream, x);
+            }
+        };
+        if (buffers) run(std::false_type{});
+        else run(std::true_type{});
+        {
+            ProfScope prof("bidi_batch_sum", stream);
+            hipLaunchKernelGGL(batch_sum, dim3(B), dim3(kWave), 0, stream, L.tau_partial, L.nstrips,
+                               -x.inv_T, a->grad_tau);
+        }
+    });
+    if (!launched) return fail(DOT_ERR_UNSUPPORTED, "row length outside the supported range");
+    return check_launch("dot_bidisoftmax_backward");
+}

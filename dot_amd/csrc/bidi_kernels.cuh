@@ -1,0 +1,341 @@
+// Bidirectional softmax device kernels.
+//
+// out = sqrt(1e-9 + r * c) with r the row softmax and c the column softmax of
+// sim / tau inside the valid region [0, L1_b) x [0, L2_b), 0 outside
+// (src/bidirectional_softmax/kernels.cu:90-242).  The forward is two sweeps:
+// a statistics sweep (row max/sum per wave; per-column online max/sum over the
+// strip, merged across strips) and a write sweep.  The backward is two sweeps
+// too: row and column dot products of q = d * r * c, then the gradient.
+// Statistics are stored as planes: row_stats [B, 2, L1] (max plane, then sum
+// plane) and col_stats [B, 2, L2].
+#pragma once
+
+#include <cfloat>
+#include <cstdint>
+
+#include "row.cuh"
+
+namespace dot_amd {
+namespace bidi {
+
+constexpr float kEps = 1.0e-9f;  // kernels.cu:29
+
+__device__ __forceinline__ void valid_extent(const int32_t* lengths, int b, int L1, int L2, int& l1,
+                                             int& l2) {
+    l1 = min(max(lengths[2 * b], 0), L1);
+    l2 = min(max(lengths[2 * b + 1], 0), L2);
+}
+
+// Online log-sum-exp state (m, s) meaning sum = s * exp(m); one exponential per update.
+__device__ __forceinline__ void lse_push(float& m, float& s, float y) {
+    const float d = y - m;
+    const float e = fast_exp(-fabsf(d));
+    const bool gt = d > 0.0f;
+    s = gt ? fmaf(s, e, 1.0f) : s + e;
+    m = gt ? y : m;
+}
+
+__device__ __forceinline__ void lse_merge(float& m, float& s, float m2, float s2) {
+    const float M = fmaxf(m, m2);
+    s = s * fast_exp(m - M) + s2 * fast_exp(m2 - M);
+    m = M;
+}
+
+// Fold the (m, s) column states of the 4 waves into wave 0 in the fixed order
+// (w0 + w2) + (w1 + w3).  `lds` holds 2*N floats; every thread must call it.
+template <int VEC, int CH>
+__device__ __forceinline__ void block_column_combine_lse(float (&m)[VEC * CH], float (&s)[VEC * CH],
+                                                         float* lds, int N) {
+    using R = Row<VEC, CH>;
+    const int lane = threadIdx.x % kWave;
+    const int wave = threadIdx.x / kWave;
+    // (source wave, destination wave) per round
+    constexpr int kRounds[3][2] = {{3, 1}, {2, 0}, {1, 0}};
+#pragma unroll
+    for (int r = 0; r < 3; ++r) {
+        __syncthreads();
+        if (wave == kRounds[r][0]) {
+            R::store(lds, lane, N, m);
+            R::store(lds + N, lane, N, s);
+        }
+        __syncthreads();
+        if (wave == kRounds[r][1]) {
+            float m2[R::PL], s2[R::PL];
+            R::load(lds, lane, N, m2, -FLT_MAX);
+            R::load(lds + N, lane, N, s2, 0.0f);
+#pragma unroll
+            for (int e = 0; e < R::PL; ++e) lse_merge(m[e], s[e], m2[e], s2[e]);
+        }
+    }
+}
+
+struct FwdArgs {
+    const float* sim;
+    const int32_t* lengths;
+    float inv_T;
+    int L1, L2, rows, nstrips;
+    float* row_stats;    // [B,2,L1]
+    float* col_stats;    // [B,2,L2]
+    float* part_m;       // [B,nstrips,L2]
+    float* part_s;       // [B,nstrips,L2]
+    float* out;          // [B,L1,L2]
+    float* row_sm;       // or null
+    float* col_sm;       // or null
+};
+
+// Row statistics (kernels.cu:90-139: max of sim*inv_T, sum of safe_exp(y - max))
+// and per-strip column statistics (kernels.cu:153-202) in one read of sim.
+template <int VEC, int CH>
+__global__ __launch_bounds__(kBlock) void fwd_stats(FwdArgs a) {
+    using R = Row<VEC, CH>;
+    extern __shared__ float lds[];
+    const int lane = threadIdx.x % kWave;
+    const int wave = threadIdx.x / kWave;
+    const int st = blockIdx.x;
+    const int b = blockIdx.y;
+    int l1, l2;
+    valid_extent(a.lengths, b, a.L1, a.L2, l1, l2);
+    const int r0 = st * a.rows;
+    const int r1 = min(r0 + a.rows, l1);
+    float cm[R::PL], cs[R::PL];
+#pragma unroll
+    for (int e = 0; e < R::PL; ++e) {
+        cm[e] = -FLT_MAX;
+        cs[e] = 0.0f;
+    }
+    float* rmax = a.row_stats + size_t(b) * 2 * a.L1;
+    float* rsum = rmax + a.L1;
+    for (int i = r0 + wave; i < r1; i += kWavesPerBlock) {
+        float y[R::PL];
+        R::load(a.sim + (size_t(b) * a.L1 + i) * a.L2, lane, a.L2, y, 0.0f);
+        float ml = -FLT_MAX;
+#pragma unroll
+        for (int e = 0; e < R::PL; ++e) {
+            y[e] = R::valid(lane, e, l2) ? y[e] * a.inv_T : -INFINITY;
+            ml = fmaxf(ml, y[e]);
+            lse_push(cm[e], cs[e], y[e]);
+        }
+        const float rm = wave_max(ml);
+        float sl = 0.0f;
+#pragma unroll
+        for (int e = 0; e < R::PL; ++e) sl += fast_exp(y[e] - rm);
+        const float rs = wave_sum(sl);
+        if (lane == 0) {
+            rmax[i] = rm;
+            rsum[i] = rs;
+        }
+    }
+    block_column_combine_lse<VEC, CH>(cm, cs, lds, a.L2);
+    if (wave == 0) {
+        const size_t off = (size_t(b) * a.nstrips + st) * a.L2;
+        R::store(a.part_m + off, lane, a.L2, cm);
+        R::store(a.part_s + off, lane, a.L2, cs);
+    }
+}
+
+__global__ __launch_bounds__(kBlock) void fwd_col_combine(FwdArgs a) {
+    const int b = blockIdx.y;
+    const int j = blockIdx.x * kBlock + threadIdx.x;
+    if (j >= a.L2) return;
+    const size_t base = size_t(b) * a.nstrips * a.L2 + j;
+    float m = -FLT_MAX, s = 0.0f;
+    for (int k = 0; k < a.nstrips; ++k)
+        lse_merge(m, s, a.part_m[base + size_t(k) * a.L2], a.part_s[base + size_t(k) * a.L2]);
+    float* cmax = a.col_stats + size_t(b) * 2 * a.L2;
+    cmax[j] = m;
+    cmax[a.L2 + j] = s;
+}
+
+// r = exp(y - rmax) / rsum, c = exp(y - cmax) / csum, out = sqrt(1e-9 + r c);
+// zeros outside the valid region (kernels.cu:143-149, :206-212, :216-242).
+template <int VEC, int CH>
+__global__ __launch_bounds__(kBlock) void fwd_write(FwdArgs a) {
+    using R = Row<VEC, CH>;
+    const int lane = threadIdx.x % kWave;
+    const int wave = threadIdx.x / kWave;
+    const int b = blockIdx.y;
+    int l1, l2;
+    valid_extent(a.lengths, b, a.L1, a.L2, l1, l2);
+    const int r0 = blockIdx.x * a.rows;
+    const int r1 = min(r0 + a.rows, a.L1);
+    const float* cstat = a.col_stats + size_t(b) * 2 * a.L2;
+    float cm[R::PL], ics[R::PL];
+    R::load(cstat, lane, a.L2, cm, 0.0f);
+    R::load(cstat + a.L2, lane, a.L2, ics, 0.0f);
+#pragma unroll
+    for (int e = 0; e < R::PL; ++e) ics[e] = ics[e] > 0.0f ? 1.0f / ics[e] : 0.0f;
+    const float* rstat = a.row_stats + size_t(b) * 2 * a.L1;
+    for (int i = r0 + wave; i < r1; i += kWavesPerBlock) {
+        const size_t off = (size_t(b) * a.L1 + i) * a.L2;
+        float o[R::PL], rr[R::PL], cc[R::PL];
+        if (i < l1) {
+            float y[R::PL];
+            R::load(a.sim + off, lane, a.L2, y, 0.0f);
+            const float rm = rstat[i];
+            const float rsv = rstat[a.L1 + i];
+            const float irs = rsv > 0.0f ? 1.0f / rsv : 0.0f;
+#pragma unroll
+            for (int e = 0; e < R::PL; ++e) {
+                const bool ok = R::valid(lane, e, l2);
+                const float yy = y[e] * a.inv_T;
+                rr[e] = ok ? fast_exp(yy - rm) * irs : 0.0f;
+                cc[e] = ok ? fast_exp(yy - cm[e]) * ics[e] : 0.0f;
+                o[e] = ok ? sqrtf(kEps + rr[e] * cc[e]) : 0.0f;
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < R::PL; ++e) o[e] = rr[e] = cc[e] = 0.0f;
+        }
+        R::store(a.out + off, lane, a.L2, o);
+        if (a.row_sm) R::store(a.row_sm + off, lane, a.L2, rr);
+        if (a.col_sm) R::store(a.col_sm + off, lane, a.L2, cc);
+    }
+}
+
+struct BwdArgs {
+    const float* sim;
+    const int32_t* lengths;
+    float inv_T;
+    int L1, L2, rows, nstrips;
+    const float* grad_out;
+    const float* out;      // buffer mode
+    const float* row_sm;
+    const float* col_sm;
+    const float* row_stats;  // recompute mode
+    const float* col_stats;
+    float* dot_r;          // [B,L1]
+    float* dot_c;          // [B,L2]
+    float* partial;        // [B,nstrips,L2]
+    float* grad_sim;
+    float* tau_partial;    // [B,gridDim.x]
+};
+
+// Per-row view of r, c and out for one row, from buffers or recomputed.
+template <int VEC, int CH, bool RECOMPUTE>
+struct BwdRow {
+    using R = Row<VEC, CH>;
+    float cm[R::PL], ics[R::PL];
+
+    __device__ void init(const BwdArgs& a, int b, int lane) {
+        if constexpr (RECOMPUTE) {
+            const float* cstat = a.col_stats + size_t(b) * 2 * a.L2;
+            R::load(cstat, lane, a.L2, cm, 0.0f);
+            R::load(cstat + a.L2, lane, a.L2, ics, 0.0f);
+#pragma unroll
+            for (int e = 0; e < R::PL; ++e) ics[e] = ics[e] > 0.0f ? 1.0f / ics[e] : 0.0f;
+        }
+    }
+
+    // Fills r, c, o for row i (valid region only; other lanes get 0).
+    __device__ void get(const BwdArgs& a, int b, int i, size_t off, int lane, int l2,
+                        float (&r)[R::PL], float (&c)[R::PL], float (&o)[R::PL],
+                        float (&y)[R::PL]) const {
+        R::load(a.sim + off, lane, a.L2, y, 0.0f);
+        if constexpr (RECOMPUTE) {
+            const float* rstat = a.row_stats + size_t(b) * 2 * a.L1;
+            const float rm = rstat[i];
+            const float rsv = rstat[a.L1 + i];
+            const float irs = rsv > 0.0f ? 1.0f / rsv : 0.0f;
+#pragma unroll
+            for (int e = 0; e < R::PL; ++e) {
+                const bool ok = R::valid(lane, e, l2);
+                const float yy = y[e] * a.inv_T;
+                r[e] = ok ? fast_exp(yy - rm) * irs : 0.0f;
+                c[e] = ok ? fast_exp(yy - cm[e]) * ics[e] : 0.0f;
+                o[e] = ok ? sqrtf(kEps + r[e] * c[e]) : 0.0f;
+            }
+        } else {
+            R::load(a.row_sm + off, lane, a.L2, r, 0.0f);
+            R::load(a.col_sm + off, lane, a.L2, c, 0.0f);
+            R::load(a.out + off, lane, a.L2, o, 0.0f);
+        }
+    }
+};
+
+// d = g * 0.5 / out (kernels.cu:249-274), d_r = d c, d_c = d r (:363-376);
+// row dots sum_j d_r r and column partials of d_c c (:277-311, :320-354).
+template <int VEC, int CH, bool RECOMPUTE>
+__global__ __launch_bounds__(kBlock) void bwd_dots(BwdArgs a) {
+    using R = Row<VEC, CH>;
+    extern __shared__ float lds[];
+    const int lane = threadIdx.x % kWave;
+    const int wave = threadIdx.x / kWave;
+    const int st = blockIdx.x;
+    const int b = blockIdx.y;
+    int l1, l2;
+    valid_extent(a.lengths, b, a.L1, a.L2, l1, l2);
+    const int r0 = st * a.rows;
+    const int r1 = min(r0 + a.rows, l1);
+    BwdRow<VEC, CH, RECOMPUTE> src;
+    src.init(a, b, lane);
+    float acc[R::PL];
+#pragma unroll
+    for (int e = 0; e < R::PL; ++e) acc[e] = 0.0f;
+    for (int i = r0 + wave; i < r1; i += kWavesPerBlock) {
+        const size_t off = (size_t(b) * a.L1 + i) * a.L2;
+        float r[R::PL], c[R::PL], o[R::PL], y[R::PL], g[R::PL];
+        src.get(a, b, i, off, lane, l2, r, c, o, y);
+        R::load(a.grad_out + off, lane, a.L2, g, 0.0f);
+        float dl = 0.0f;
+#pragma unroll
+        for (int e = 0; e < R::PL; ++e) {
+            const bool ok = R::valid(lane, e, l2) && o[e] > kEps;
+            const float d = ok ? (g[e] * 0.5f) / o[e] : 0.0f;
+            dl += (d * c[e]) * r[e];
+            acc[e] += (d * r[e]) * c[e];
+        }
+        const float dr = wave_sum(dl);
+        if (lane == 0) a.dot_r[size_t(b) * a.L1 + i] = dr;
+    }
+    block_column_combine<VEC, CH>(acc, lds, a.L2);
+    if (wave == 0) R::store(a.partial + (size_t(b) * a.nstrips + st) * a.L2, lane, a.L2, acc);
+}
+
+// grad = ((d_r - dot_r) r) / tau + ((d_c - dot_c) c) / tau in the valid region,
+// 0 elsewhere; per-block sums of grad * sim for grad_tau (kernels.cu:379-411).
+template <int VEC, int CH, bool RECOMPUTE>
+__global__ __launch_bounds__(kBlock) void bwd_write(BwdArgs a) {
+    using R = Row<VEC, CH>;
+    __shared__ float scratch[kWavesPerBlock];
+    const int lane = threadIdx.x % kWave;
+    const int wave = threadIdx.x / kWave;
+    const int b = blockIdx.y;
+    int l1, l2;
+    valid_extent(a.lengths, b, a.L1, a.L2, l1, l2);
+    const int r0 = blockIdx.x * a.rows;
+    const int r1 = min(r0 + a.rows, a.L1);
+    BwdRow<VEC, CH, RECOMPUTE> src;
+    src.init(a, b, lane);
+    float dc[R::PL];
+    R::load(a.dot_c + size_t(b) * a.L2, lane, a.L2, dc, 0.0f);
+    float tacc = 0.0f;
+    for (int i = r0 + wave; i < r1; i += kWavesPerBlock) {
+        const size_t off = (size_t(b) * a.L1 + i) * a.L2;
+        float gs[R::PL];
+        if (i < l1) {
+            float r[R::PL], c[R::PL], o[R::PL], y[R::PL], g[R::PL];
+            src.get(a, b, i, off, lane, l2, r, c, o, y);
+            R::load(a.grad_out + off, lane, a.L2, g, 0.0f);
+            const float dr = a.dot_r[size_t(b) * a.L1 + i];
+#pragma unroll
+            for (int e = 0; e < R::PL; ++e) {
+                const bool valid = R::valid(lane, e, l2);
+                const bool ok = valid && o[e] > kEps;
+                const float d = ok ? (g[e] * 0.5f) / o[e] : 0.0f;
+                const float row_term = ((d * c[e] - dr) * r[e]) * a.inv_T;
+                const float col_term = ((d * r[e] - dc[e]) * c[e]) * a.inv_T;
+                gs[e] = valid ? row_term + col_term : 0.0f;
+                if (valid) tacc = fmaf(gs[e], y[e], tacc);
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < R::PL; ++e) gs[e] = 0.0f;
+        }
+        R::store(a.grad_sim + off, lane, a.L2, gs);
+    }
+    const float t = block_reduce<kWavesPerBlock>(wave_sum(tacc), scratch, OpSum{});
+    if (threadIdx.x == 0) a.tau_partial[size_t(b) * gridDim.x + blockIdx.x] = t;
+}
+
+}  // namespace bidi
+}  // namespace dot_amd

@@ -1,0 +1,75 @@
+// Host-side helpers for the C ABI: thread-local error text, launch checking,
+// workspace carving and the optional per-kernel event profiler.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <string>
+
+#include "../../include/dot_amd.h"
+
+namespace dot_amd {
+
+// Records `msg` as this thread's last error and returns `code`.
+int fail(int code, const std::string& msg);
+// Clears this thread's last error and returns DOT_OK.
+int ok();
+
+// Checks hipGetLastError() after a launch; returns DOT_OK or DOT_ERR_HIP.
+int check_launch(const char* what);
+
+// Bump allocator over a caller-provided workspace; every carve is 256-byte aligned.
+class Carver {
+  public:
+    explicit Carver(void* base) : base_(static_cast<char*>(base)), off_(0) {}
+    template <class T>
+    T* take(size_t count) {
+        off_ = (off_ + 255) & ~size_t(255);
+        T* p = base_ ? reinterpret_cast<T*>(base_ + off_) : nullptr;
+        off_ += count * sizeof(T);
+        return p;
+    }
+    size_t used() const { return (off_ + 255) & ~size_t(255); }
+
+  private:
+    char* base_;
+    size_t off_;
+};
+
+// Event profiler.  When enabled, `ProfScope` brackets a launch with two events
+// on the launch stream; dot_profile_collect() folds finished pairs into
+// per-kernel totals.
+bool profiling_enabled();
+void profile_push(const char* name, hipEvent_t start, hipEvent_t stop);
+hipEvent_t profile_event();
+
+class ProfScope {
+  public:
+    ProfScope(const char* name, hipStream_t stream) : name_(name), stream_(stream) {
+        if (profiling_enabled()) {
+            start_ = profile_event();
+            stop_ = profile_event();
+            (void)hipEventRecord(start_, stream_);
+        }
+    }
+    ~ProfScope() {
+        if (start_) {
+            (void)hipEventRecord(stop_, stream_);
+            profile_push(name_, start_, stop_);
+        }
+    }
+    ProfScope(const ProfScope&) = delete;
+    ProfScope& operator=(const ProfScope&) = delete;
+
+  private:
+    const char* name_;
+    hipStream_t stream_;
+    hipEvent_t start_ = nullptr;
+    hipEvent_t stop_ = nullptr;
+};
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace dot_amd

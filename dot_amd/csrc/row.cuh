@@ -1,0 +1,128 @@
+// Row-in-registers layout shared by every sweep kernel.
+//
+// A wave owns whole rows.  Lane `l` holds, for chunk k = 0..CH-1, the VEC
+// consecutive columns starting at k*64*VEC + l*VEC, so each chunk is one
+// coalesced 64*VEC*4-byte access per wave (a 1 KiB float4 access when VEC=4).
+// A row of up to 64*VEC*CH columns lives in VEC*CH registers per lane, which is
+// what lets a sweep reduce a row across the wave and keep per-column partial
+// sums in the same registers for all the rows the wave visits.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <cfloat>
+#include <type_traits>
+
+#include "wave.cuh"
+
+namespace dot_amd {
+
+constexpr int kBlock = 256;                 // threads per workgroup (4 waves)
+constexpr int kWavesPerBlock = kBlock / kWave;
+constexpr int kMaxRowLen = 4096;            // longest row held in registers
+
+template <int VEC, int CH>
+struct Row {
+    static constexpr int PL = VEC * CH;  // floats per lane
+
+    __device__ static __forceinline__ int col(int lane, int k) { return k * (kWave * VEC) + lane * VEC; }
+
+    // Load a row; lanes past N receive `fill`.  VEC=4 requires N % 4 == 0 and a
+    // 16-byte aligned row start.
+    __device__ static __forceinline__ void load(const float* __restrict__ row, int lane, int N,
+                                                float (&x)[PL], float fill) {
+#pragma unroll
+        for (int k = 0; k < CH; ++k) {
+            const int c = col(lane, k);
+            if constexpr (VEC == 4) {
+                if (c < N) {
+                    const float4 t = *reinterpret_cast<const float4*>(row + c);
+                    x[4 * k + 0] = t.x;
+                    x[4 * k + 1] = t.y;
+                    x[4 * k + 2] = t.z;
+                    x[4 * k + 3] = t.w;
+                } else {
+                    x[4 * k + 0] = x[4 * k + 1] = x[4 * k + 2] = x[4 * k + 3] = fill;
+                }
+            } else {
+                x[k] = (c < N) ? row[c] : fill;
+            }
+        }
+    }
+
+    __device__ static __forceinline__ void store(float* __restrict__ row, int lane, int N,
+                                                 const float (&x)[PL]) {
+#pragma unroll
+        for (int k = 0; k < CH; ++k) {
+            const int c = col(lane, k);
+            if (c < N) {
+                if constexpr (VEC == 4) {
+                    *reinterpret_cast<float4*>(row + c) =
+                        make_float4(x[4 * k + 0], x[4 * k + 1], x[4 * k + 2], x[4 * k + 3]);
+                } else {
+                    row[c] = x[k];
+                }
+            }
+        }
+    }
+
+    // true when element e of this lane is a real column (< N)
+    __device__ static __forceinline__ bool valid(int lane, int e, int N) {
+        return col(lane, e / VEC) + (e % VEC) < N;
+    }
+};
+
+// Sum the per-lane column accumulators of the 4 waves of a workgroup in a fixed
+// order, ((w0 + w2) + (w1 + w3)), and leave the result in wave 0's `acc`.
+// `lds` must hold 2*N floats.  Contains barriers: every thread must call it.
+template <int VEC, int CH>
+__device__ __forceinline__ void block_column_combine(float (&acc)[VEC * CH], float* lds, int N) {
+    using R = Row<VEC, CH>;
+    const int lane = threadIdx.x % kWave;
+    const int wave = threadIdx.x / kWave;
+    __syncthreads();
+    if (wave >= 2) R::store(lds + (wave - 2) * N, lane, N, acc);
+    __syncthreads();
+    if (wave < 2) {
+        float o[R::PL];
+        R::load(lds + wave * N, lane, N, o, 0.0f);
+#pragma unroll
+        for (int e = 0; e < R::PL; ++e) acc[e] += o[e];
+    }
+    __syncthreads();
+    if (wave == 1) R::store(lds, lane, N, acc);
+    __syncthreads();
+    if (wave == 0) {
+        float o[R::PL];
+        R::load(lds, lane, N, o, 0.0f);
+#pragma unroll
+        for (int e = 0; e < R::PL; ++e) acc[e] += o[e];
+    }
+}
+
+// Pick (VEC, CH) for a row length and call f(integral_constant<VEC>, integral_constant<CH>).
+// Returns false when N is outside the register-resident range.
+template <class F>
+bool dispatch_row(int N, bool vec4, F&& f) {
+    using std::integral_constant;
+    if (N <= 0 || N > kMaxRowLen) return false;
+    if (vec4) {
+        const int chunks = (N + 255) / 256;
+        if (chunks <= 1) f(integral_constant<int, 4>{}, integral_constant<int, 1>{});
+        else if (chunks <= 2) f(integral_constant<int, 4>{}, integral_constant<int, 2>{});
+        else if (chunks <= 4) f(integral_constant<int, 4>{}, integral_constant<int, 4>{});
+        else if (chunks <= 8) f(integral_constant<int, 4>{}, integral_constant<int, 8>{});
+        else f(integral_constant<int, 4>{}, integral_constant<int, 16>{});
+    } else {
+        const int chunks = (N + 63) / 64;
+        if (chunks <= 1) f(integral_constant<int, 1>{}, integral_constant<int, 1>{});
+        else if (chunks <= 2) f(integral_constant<int, 1>{}, integral_constant<int, 2>{});
+        else if (chunks <= 4) f(integral_constant<int, 1>{}, integral_constant<int, 4>{});
+        else if (chunks <= 8) f(integral_constant<int, 1>{}, integral_constant<int, 8>{});
+        else if (chunks <= 16) f(integral_constant<int, 1>{}, integral_constant<int, 16>{});
+        else if (chunks <= 32) f(integral_constant<int, 1>{}, integral_constant<int, 32>{});
+        else f(integral_constant<int, 1>{}, integral_constant<int, 64>{});
+    }
+    return true;
+}
+
+}  // namespace dot_amd

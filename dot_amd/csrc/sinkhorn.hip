@@ -1,0 +1,457 @@
+// Sinkhorn C ABI: argument checks, workspace layout and the launch sequences.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdlib>
+#include <string>
+
+#include "host.hpp"
+#include "sinkhorn_kernels.cuh"
+
+namespace dot_amd {
+namespace {
+
+using sk::kColSumFloor;
+
+// Rows per workgroup strip: the largest power of two in [4, 64] that still
+// yields >= 1024 workgroups (4 per CU on 256 CUs), so every sweep fills the
+// chip.  DOT_AMD_ROWS overrides it (tuning only).
+int strip_rows(int B, int M) {
+    static const int forced = [] {
+        const char* s = std::getenv("DOT_AMD_ROWS");
+        return s ? std::atoi(s) : 0;
+    }();
+    if (forced >= 1) return forced;
+    int r = 64;
+    while (r > 4 && int64_t(B) * ((M + r - 1) / r) < 1024) r /= 2;
+    return r;
+}
+
+size_t lds_bytes(int N) { return (size_t(2) * N + 8) * sizeof(float); }
+
+dim3 column_grid(int N, int B) { return dim3((N + kBlock - 1) / kBlock, B); }
+
+struct FwdLayout {
+    uint32_t* delta;
+    float* ubuf;
+    float* vbuf;
+    size_t zero_words;
+    float* partial;
+    float* cost_partial;
+    int rows, nstrips;
+    size_t bytes;
+};
+
+FwdLayout fwd_layout(void* ws, int B, int M, int N, int max_iter) {
+    Carver c(ws);
+    FwdLayout L{};
+    L.delta = c.take<uint32_t>(size_t(max_iter) + 1);
+    L.ubuf = c.take<float>(size_t(2) * B * M);
+    L.vbuf = c.take<float>(size_t(2) * B * N);
+    L.zero_words = c.used() / sizeof(uint32_t);
+    L.rows = strip_rows(B, M);
+    L.nstrips = (M + L.rows - 1) / L.rows;
+    L.partial = c.take<float>(size_t(B) * L.nstrips * N);
+    L.cost_partial = c.take<float>(size_t(B) * L.nstrips);
+    L.bytes = c.used();
+    return L;
+}
+
+struct ImpLayout {
+    float *r, *rs, *lam, *c, *cs, *mu, *partA, *partB, *tau_partial;
+    int rows, nstrips;
+    size_t bytes;
+};
+
+ImpLayout imp_layout(void* ws, int B, int M, int N) {
+    Carver c(ws);
+    ImpLayout L{};
+    L.rows = strip_rows(B, M);
+    L.nstrips = (M + L.rows - 1) / L.rows;
+    L.r = c.take<float>(size_t(B) * M);
+    L.rs = c.take<float>(size_t(B) * M);
+    L.lam = c.take<float>(size_t(B) * M);
+    L.c = c.take<float>(size_t(B) * N);
+    L.cs = c.take<float>(size_t(B) * N);
+    L.mu = c.take<float>(size_t(B) * N);
+    L.partA = c.take<float>(size_t(B) * L.nstrips * N);
+    L.partB = c.take<float>(size_t(B) * L.nstrips * N);
+    L.tau_partial = c.take<float>(size_t(B) * L.nstrips);
+    L.bytes = c.used();
+    return L;
+}
+
+struct UnrLayout {
+    float *gamma, *partial, *colsum, *tau_partial;
+    int rows, nstrips;
+    size_t bytes;
+};
+
+UnrLayout unr_layout(void* ws, int B, int M, int N) {
+    Carver c(ws);
+    UnrLayout L{};
+    L.rows = strip_rows(B, M);
+    L.nstrips = (M + L.rows - 1) / L.rows;
+    L.gamma = c.take<float>(size_t(B) * M * N);
+    L.partial = c.take<float>(size_t(B) * L.nstrips * N);
+    L.colsum = c.take<float>(size_t(B) * N);
+    L.tau_partial = c.take<float>(size_t(B) * L.nstrips);
+    L.bytes = c.used();
+    return L;
+}
+
+__global__ void set_counts(int32_t* iters_used, int32_t* converged, int used, int conv) {
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        *iters_used = used;
+        *converged = conv;
+    }
+}
+
+__global__ void fill_value(float* p, size_t n, float value) {
+    for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+         i += size_t(gridDim.x) * blockDim.x)
+        p[i] = value;
+}
+
+void launch_fill_zero(void* p, size_t words, hipStream_t stream) {
+    if (words == 0) return;
+    const unsigned blocks = unsigned(std::min<size_t>((words + kBlock - 1) / kBlock, 2048));
+    ProfScope prof("dot_fill_zero", stream);
+    hipLaunchKernelGGL(sk::fill_zero, dim3(blocks), dim3(kBlock), 0, stream,
+                       static_cast<uint32_t*>(p), words);
+}
+
+int check_shape(int B, int M, int N) {
+    if (B < 0 || M < 0 || N < 0) return fail(DOT_ERR_INVALID_ARG, "B, M and N must be >= 0");
+    if (B > 65535) return fail(DOT_ERR_UNSUPPORTED, "batch size above 65535 is not supported");
+    if (N > kMaxRowLen)
+        return fail(DOT_ERR_UNSUPPORTED,
+                    "rows longer than 4096 columns are not supported by this build (N=" +
+                        std::to_string(N) + ")");
+    return DOT_OK;
+}
+
+bool valid_tau(float tau) { return std::isfinite(tau) && tau > 0.0f; }
+
+}  // namespace
+}  // namespace dot_amd
+
+using namespace dot_amd;
+
+extern "C" size_t dot_sinkhorn_forward_workspace_bytes(int B, int M, int N, int max_iter, int flags) {
+    (void)flags;
+    if (B < 0 || M < 0 || N < 0 || max_iter < 0) return 0;
+    return fwd_layout(nullptr, B, M, N, max_iter).bytes;
+}
+
+extern "C" int dot_sinkhorn_forward(const dot_sinkhorn_fwd_args* a, dot_stream_t stream_) {
+    hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+    if (!a) return fail(DOT_ERR_INVALID_ARG, "args is NULL");
+    if (int rc = check_shape(a->B, a->M, a->N)) return rc;
+    if (!valid_tau(a->tau)) return fail(DOT_ERR_INVALID_ARG, "tau must be > 0");
+    if (a->max_iter < 0) return fail(DOT_ERR_INVALID_ARG, "max_iter must be >= 0");
+    if (a->scores_kind != DOT_SCORES_LOG_ALPHA && a->scores_kind != DOT_SCORES_COST)
+        return fail(DOT_ERR_INVALID_ARG, "scores_kind must be DOT_SCORES_LOG_ALPHA or DOT_SCORES_COST");
+    if (!a->iters_used || !a->converged)
+        return fail(DOT_ERR_INVALID_ARG, "iters_used and converged must be device pointers");
+    const bool keep = (a->flags & DOT_SK_KEEP_HISTORY) != 0;
+    const bool ret_log = (a->flags & DOT_SK_RETURN_LOG) != 0;
+    if (a->flags & ~(DOT_SK_KEEP_HISTORY | DOT_SK_RETURN_LOG))
+        return fail(DOT_ERR_INVALID_ARG, "unknown flag bits");
+    if (ret_log && a->cost) return fail(DOT_ERR_INVALID_ARG, "cost is undefined with DOT_SK_RETURN_LOG");
+    if (keep && a->max_iter > 0 && (!a->u_hist || !a->v_hist))
+        return fail(DOT_ERR_INVALID_ARG, "DOT_SK_KEEP_HISTORY needs u_hist and v_hist");
+    const int B = a->B, M = a->M, N = a->N, T = a->max_iter;
+    const size_t elems = size_t(B) * M * N;
+
+    if (elems == 0) {
+        // Degenerate shapes: the reference's loop still runs one delta check of an
+        // empty vector (delta = 0), so a positive tol reports convergence at t = 1.
+        const bool stop = a->tol > 0.0f && T > 0;
+        hipLaunchKernelGGL(set_counts, dim3(1), dim3(1), 0, stream, a->iters_used, a->converged,
+                           stop ? 1 : T, stop ? 1 : 0);
+        if (a->cost && B > 0) hipLaunchKernelGGL(fill_value, dim3(1), dim3(kBlock), 0, stream, a->cost, size_t(B), 0.0f);
+        return check_launch("dot_sinkhorn_forward");
+    }
+    if (!a->scores) return fail(DOT_ERR_INVALID_ARG, "scores is NULL");
+
+    const FwdLayout L = fwd_layout(a->workspace, B, M, N, T);
+    if (!a->workspace || a->workspace_bytes < L.bytes)
+        return fail(DOT_ERR_WORKSPACE, "workspace smaller than dot_sinkhorn_forward_workspace_bytes()");
+
+    const float tau = a->tau;
+    const float inv_tau = 1.0f / tau;                       // torch_cuda.cpp / kernels.cu:1350
+    const float kscale = float(a->scores_kind) * inv_tau;
+    const float log_a_default = -std::log(static_cast<float>(M));  // torch_cuda.cpp:42
+    const float log_b_default = -std::log(static_cast<float>(N));
+    const bool vec4 = (N % 4 == 0) && aligned16(a->scores) && (!a->plan || aligned16(a->plan));
+    const size_t lds = lds_bytes(N);
+
+    launch_fill_zero(a->workspace, L.zero_words, stream);
+
+    bool launched = dispatch_row(N, vec4, [&](auto vc, auto cc) {
+        constexpr int V = decltype(vc)::value;
+        constexpr int C = decltype(cc)::value;
+        for (int t = 1; t <= T; ++t) {
+            const int cur = t & 1, prev = (t - 1) & 1;
+            sk::FwdSweepArgs s{};
+            s.X = a->scores;
+            s.kscale = kscale;
+            s.log_a = a->log_a;
+            s.log_a_default = log_a_default;
+            s.v_old = L.vbuf + size_t(prev) * B * N;
+            s.u_old = L.ubuf + size_t(prev) * B * M;
+            s.u_new = L.ubuf + size_t(cur) * B * M;
+            s.u_hist = keep ? a->u_hist + size_t(t - 1) * B * M : nullptr;
+            s.partial = L.partial;
+            s.delta_bits = L.delta;
+            s.M = M;
+            s.N = N;
+            s.rows = L.rows;
+            s.nstrips = L.nstrips;
+            s.t = t;
+            s.tol = a->tol;
+            {
+                ProfScope prof("sk_fwd_sweep", stream);
+                hipLaunchKernelGGL((sk::fwd_sweep<V, C>), dim3(L.nstrips, B), dim3(kBlock), lds,
+                                   stream, s);
+            }
+            sk::FwdCombineArgs cb{};
+            cb.partial = L.partial;
+            cb.nstrips = L.nstrips;
+            cb.X = a->scores;
+            cb.kscale = kscale;
+            cb.u_new = s.u_new;
+            cb.log_b = a->log_b;
+            cb.log_b_default = log_b_default;
+            cb.v_old = s.v_old;
+            cb.v_new = L.vbuf + size_t(cur) * B * N;
+            cb.v_hist = keep ? a->v_hist + size_t(t - 1) * B * N : nullptr;
+            cb.delta_bits = L.delta;
+            cb.tol = a->tol;
+            cb.t = t;
+            cb.M = M;
+            cb.N = N;
+            {
+                ProfScope prof("sk_fwd_combine", stream);
+                hipLaunchKernelGGL(sk::fwd_combine, column_grid(N, B), dim3(kBlock), 0, stream, cb);
+            }
+        }
+        {
+            ProfScope prof("sk_fwd_finalize", stream);
+            hipLaunchKernelGGL(sk::fwd_finalize, dim3(1), dim3(kWave), 0, stream, L.delta, T,
+                               a->tol, a->iters_used, a->converged);
+        }
+        if (a->plan || a->cost || a->u_out || a->v_out) {
+            sk::MaterializeArgs m{};
+            m.X = a->scores;
+            m.kscale = kscale;
+            m.scores_kind = a->scores_kind;
+            m.ubuf = L.ubuf;
+            m.vbuf = L.vbuf;
+            m.iters_used = a->iters_used;
+            m.plan = a->plan;
+            m.return_log = ret_log ? 1 : 0;
+            m.cost_partial = a->cost ? L.cost_partial : nullptr;
+            m.u_out = a->u_out;
+            m.v_out = a->v_out;
+            m.B = B;
+            m.M = M;
+            m.N = N;
+            m.rows = L.rows;
+            {
+                ProfScope prof("sk_materialize", stream);
+                hipLaunchKernelGGL((sk::materialize<V, C>), dim3(L.nstrips, B), dim3(kBlock), 0,
+                                   stream, m);
+            }
+            if (a->cost) {
+                ProfScope prof("sk_batch_sum", stream);
+                hipLaunchKernelGGL(sk::batch_sum, dim3(B), dim3(kWave), 0, stream, L.cost_partial,
+                                   L.nstrips, 1.0f, a->cost);
+            }
+        }
+    });
+    if (!launched) return fail(DOT_ERR_UNSUPPORTED, "row length outside the supported range");
+    return check_launch("dot_sinkhorn_forward");
+}
+
+// ---------------------------------------------------------------------------
+// Backward
+// ---------------------------------------------------------------------------
+namespace {
+
+int check_bwd(const dot_sinkhorn_bwd_args* a) {
+    if (!a) return fail(DOT_ERR_INVALID_ARG, "args is NULL");
+    if (int rc = check_shape(a->B, a->M, a->N)) return rc;
+    if (!valid_tau(a->tau)) return fail(DOT_ERR_INVALID_ARG, "tau must be > 0");
+    if (a->iters < 0) return fail(DOT_ERR_INVALID_ARG, "iters must be >= 0");
+    if (a->scores_kind != DOT_SCORES_LOG_ALPHA && a->scores_kind != DOT_SCORES_COST)
+        return fail(DOT_ERR_INVALID_ARG, "scores_kind must be DOT_SCORES_LOG_ALPHA or DOT_SCORES_COST");
+    const size_t elems = size_t(a->B) * a->M * a->N;
+    if (elems > 0 && (!a->scores || !a->plan || !a->grad_scores))
+        return fail(DOT_ERR_INVALID_ARG, "scores, plan and grad_scores must be non-NULL");
+    if (a->B > 0 && !a->grad_tau) return fail(DOT_ERR_INVALID_ARG, "grad_tau must be non-NULL");
+    return DOT_OK;
+}
+
+bool bwd_vec4(const dot_sinkhorn_bwd_args* a) {
+    return (a->N % 4 == 0) && aligned16(a->scores) && aligned16(a->plan) &&
+           aligned16(a->grad_scores) && (!a->grad_plan || aligned16(a->grad_plan));
+}
+
+sk::GradSource grad_source(const dot_sinkhorn_bwd_args* a) {
+    sk::GradSource g{};
+    g.X = a->scores;
+    g.scores_kind = a->scores_kind;
+    g.gP = a->grad_plan;
+    g.gC = a->grad_cost;
+    return g;
+}
+
+// Zero gradients for empty matrices with a non-empty batch.
+int bwd_degenerate(const dot_sinkhorn_bwd_args* a, hipStream_t stream, const char* what) {
+    if (a->B > 0)
+        hipLaunchKernelGGL(fill_value, dim3(1), dim3(kBlock), 0, stream, a->grad_tau, size_t(a->B), 0.0f);
+    return check_launch(what);
+}
+
+}  // namespace
+
+extern "C" size_t dot_sinkhorn_backward_implicit_workspace_bytes(int B, int M, int N) {
+    if (B < 0 || M < 0 || N < 0) return 0;
+    return imp_layout(nullptr, B, M, N).bytes;
+}
+
+extern "C" int dot_sinkhorn_backward_implicit(const dot_sinkhorn_bwd_args* a, dot_stream_t stream_) {
+    hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+    if (int rc = check_bwd(a)) return rc;
+    const int B = a->B, M = a->M, N = a->N;
+    if (size_t(B) * M * N == 0) return bwd_degenerate(a, stream, "dot_sinkhorn_backward_implicit");
+    const ImpLayout L = imp_layout(a->workspace, B, M, N);
+    if (!a->workspace || a->workspace_bytes < L.bytes)
+        return fail(DOT_ERR_WORKSPACE,
+                    "workspace smaller than dot_sinkhorn_backward_implicit_workspace_bytes()");
+    const float inv_tau = 1.0f / a->tau;
+    sk::ImpArgs x{};
+    x.g = grad_source(a);
+    x.P = a->plan;
+    x.r = L.r;
+    x.rs = L.rs;
+    x.lam = L.lam;
+    x.c = L.c;
+    x.cs = L.cs;
+    x.mu = L.mu;
+    x.partA = L.partA;
+    x.partB = L.partB;
+    x.nstrips = L.nstrips;
+    x.grad = a->grad_scores;
+    x.tau_partial = L.tau_partial;
+    x.inv_tau = inv_tau;
+    x.M = M;
+    x.N = N;
+    x.rows = L.rows;
+    const size_t lds = lds_bytes(N);
+    const dim3 strips(L.nstrips, B);
+    bool launched = dispatch_row(N, bwd_vec4(a), [&](auto vc, auto cc) {
+        constexpr int V = decltype(vc)::value;
+        constexpr int C = decltype(cc)::value;
+        {
+            ProfScope prof("sk_imp_prep", stream);
+            hipLaunchKernelGGL((sk::imp_prep<V, C>), strips, dim3(kBlock), lds, stream, x);
+        }
+        {
+            ProfScope prof("sk_imp_prep_combine", stream);
+            hipLaunchKernelGGL(sk::imp_prep_combine, column_grid(N, B), dim3(kBlock), 0, stream, x);
+        }
+        for (int it = 0; it < a->iters; ++it) {
+            {
+                ProfScope prof("sk_imp_sweep", stream);
+                hipLaunchKernelGGL((sk::imp_lambda_sweep<V, C>), strips, dim3(kBlock), lds, stream, x);
+            }
+            {
+                ProfScope prof("sk_imp_combine", stream);
+                hipLaunchKernelGGL(sk::imp_mu_combine, column_grid(N, B), dim3(kBlock), 0, stream, x);
+            }
+        }
+        {
+            ProfScope prof("sk_imp_final", stream);
+            hipLaunchKernelGGL((sk::imp_final<V, C>), strips, dim3(kBlock), 0, stream, x);
+        }
+        {
+            ProfScope prof("sk_batch_sum", stream);
+            hipLaunchKernelGGL(sk::batch_sum, dim3(B), dim3(kWave), 0, stream, L.tau_partial,
+                               L.nstrips, -inv_tau, a->grad_tau);
+        }
+    });
+    if (!launched) return fail(DOT_ERR_UNSUPPORTED, "row length outside the supported range");
+    return check_launch("dot_sinkhorn_backward_implicit");
+}
+
+extern "C" size_t dot_sinkhorn_backward_unrolled_workspace_bytes(int B, int M, int N) {
+    if (B < 0 || M < 0 || N < 0) return 0;
+    return unr_layout(nullptr, B, M, N).bytes;
+}
+
+extern "C" int dot_sinkhorn_backward_unrolled(const dot_sinkhorn_bwd_args* a, dot_stream_t stream_) {
+    hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+    if (int rc = check_bwd(a)) return rc;
+    const int B = a->B, M = a->M, N = a->N, T = a->iters;
+    if (size_t(B) * M * N == 0) return bwd_degenerate(a, stream, "dot_sinkhorn_backward_unrolled");
+    if (T > 0 && (!a->u_hist || !a->v_hist))
+        return fail(DOT_ERR_INVALID_ARG, "u_hist and v_hist are required when iters > 0");
+    const UnrLayout L = unr_layout(a->workspace, B, M, N);
+    if (!a->workspace || a->workspace_bytes < L.bytes)
+        return fail(DOT_ERR_WORKSPACE,
+                    "workspace smaller than dot_sinkhorn_backward_unrolled_workspace_bytes()");
+    const float tau = a->tau;
+    const float inv_tau = 1.0f / tau;
+    const float neg_inv_tau2 = -1.0f / (tau * tau);  // kernels.cu:1642
+    sk::UnrArgs x{};
+    x.g = grad_source(a);
+    x.kscale = float(a->scores_kind) * inv_tau;
+    x.P = a->plan;
+    x.gamma = L.gamma;
+    x.partial = L.partial;
+    x.nstrips = L.nstrips;
+    x.colsum = L.colsum;
+    x.grad = a->grad_scores;
+    x.tau_partial = L.tau_partial;
+    x.inv_tau = inv_tau;
+    x.M = M;
+    x.N = N;
+    x.rows = L.rows;
+    const size_t lds = lds_bytes(N);
+    const dim3 strips(L.nstrips, B);
+    bool launched = dispatch_row(N, bwd_vec4(a), [&](auto vc, auto cc) {
+        constexpr int V = decltype(vc)::value;
+        constexpr int C = decltype(cc)::value;
+        x.final_step = T == 0;
+        {
+            ProfScope prof("sk_unr_init", stream);
+            hipLaunchKernelGGL((sk::unr_init<V, C>), strips, dim3(kBlock), lds, stream, x);
+        }
+        for (int t = T - 1; t >= 0; --t) {
+            {
+                ProfScope prof("sk_unr_fold", stream);
+                hipLaunchKernelGGL(sk::column_fold, column_grid(N, B), dim3(kBlock), 0, stream,
+                                   L.partial, L.nstrips, N, L.colsum);
+            }
+            x.u_t = a->u_hist + size_t(t) * B * M;
+            x.v_t = a->v_hist + size_t(t) * B * N;
+            x.v_tm1 = t > 0 ? a->v_hist + size_t(t - 1) * B * N : nullptr;
+            x.final_step = t == 0;
+            {
+                ProfScope prof("sk_unr_step", stream);
+                hipLaunchKernelGGL((sk::unr_step<V, C>), strips, dim3(kBlock), lds, stream, x);
+            }
+        }
+        {
+            ProfScope prof("sk_batch_sum", stream);
+            hipLaunchKernelGGL(sk::batch_sum, dim3(B), dim3(kWave), 0, stream, L.tau_partial,
+                               L.nstrips, neg_inv_tau2, a->grad_tau);
+        }
+    });
+    if (!launched) return fail(DOT_ERR_UNSUPPORTED, "row length outside the supported range");
+    return check_launch("dot_sinkhorn_backward_unrolled");
+}

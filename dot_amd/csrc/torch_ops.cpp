@@ -1,0 +1,511 @@
+// PyTorch binding of the dot_amd C ABI.
+//
+// * TORCH_LIBRARY(dot): the reference's eight schemas, verbatim
+//   (src/sinkhorn/registry.cpp:31-56, src/bidirectional_softmax/registry.cpp:31-34),
+//   so dot/_ops.py-style code binds the same torch.ops.dot.* handles.
+// * TORCH_LIBRARY_IMPL(dot, CUDA): HIP tensors (PyTorch-ROCm dispatches them
+//   under the CUDA key) go to the C ABI on the current HIP stream.
+// * TORCH_LIBRARY(dot_amd): fused operators used by the Python autograd
+//   functions (cost-fused forward, fused backward, statistics-based
+//   bidirectional softmax).  HIP only.
+//
+// CPU tensors are served by cpu_ops.cpp.  No GPU tensor is ever computed on
+// the CPU: a missing or failing HIP path raises.
+#include <ATen/ATen.h>
+#include <c10/core/DeviceGuard.h>
+#include <c10/hip/HIPStream.h>
+#include <torch/library.h>
+
+#include <cmath>
+#include <string>
+#include <vector>
+
+#include "../../include/dot_amd.h"
+
+namespace {
+
+using at::Tensor;
+using c10::optional;
+
+void check_rc(int rc, const char* what) {
+    TORCH_CHECK(rc == DOT_OK, what, " failed (code ", rc, "): ", dot_last_error());
+}
+
+dot_stream_t current_stream(const Tensor& t) {
+    return reinterpret_cast<dot_stream_t>(c10::hip::getCurrentHIPStream(t.device().index()).stream());
+}
+
+void check_hip_input(const Tensor& t, const char* name) {
+    TORCH_CHECK(t.device().is_cuda(), name, " must be a CUDA tensor");
+}
+
+Tensor f32c(const Tensor& t) { return t.to(at::kFloat).contiguous(); }
+
+Tensor workspace(size_t bytes, const Tensor& like) {
+    return at::empty({static_cast<int64_t>(std::max<size_t>(bytes, 1))},
+                     like.options().dtype(at::kByte));
+}
+
+const float* ptr_or_null(const optional<Tensor>& t) {
+    return t.has_value() ? t->data_ptr<float>() : nullptr;
+}
+
+// Shape checks of torch_cuda.cpp:286-302.
+void check_marginals(const optional<Tensor>& log_a, const optional<Tensor>& log_b, int64_t B,
+                     int64_t n, int64_t m) {
+    if (log_a.has_value()) {
+        check_hip_input(*log_a, "*log_a");
+        TORCH_CHECK(log_a->dim() == 2 && log_a->size(0) == B && log_a->size(1) == n,
+                    "log_a must have shape [B, n]");
+    }
+    if (log_b.has_value()) {
+        check_hip_input(*log_b, "*log_b");
+        TORCH_CHECK(log_b->dim() == 2 && log_b->size(0) == B && log_b->size(1) == m,
+                    "log_b must have shape [B, m]");
+    }
+}
+
+struct ForwardOut {
+    Tensor plan, cost, counts, u_hist, v_hist;
+};
+
+// One call of dot_sinkhorn_forward; counts = int32 [2] on the device: (iters_used, converged).
+ForwardOut run_forward(const Tensor& scores_f, int kind, double tau, int64_t n_iters, double tol,
+                       const optional<Tensor>& log_a_f, const optional<Tensor>& log_b_f,
+                       bool return_log, bool want_plan, bool want_cost, bool keep_history) {
+    const int64_t B = scores_f.size(0), M = scores_f.size(1), N = scores_f.size(2);
+    TORCH_CHECK(n_iters <= INT32_MAX, "n_iters too large");
+    auto opts = scores_f.options().dtype(at::kFloat);
+    ForwardOut o;
+    if (want_plan) o.plan = at::empty({B, M, N}, opts);
+    if (want_cost) o.cost = at::empty({B}, opts);
+    o.counts = at::empty({2}, scores_f.options().dtype(at::kInt));
+    const int flags = (return_log ? DOT_SK_RETURN_LOG : 0) | (keep_history ? DOT_SK_KEEP_HISTORY : 0);
+    if (keep_history) {
+        o.u_hist = at::empty({n_iters, B, M}, opts);
+        o.v_hist = at::empty({n_iters, B, N}, opts);
+    }
+    const size_t ws_bytes = dot_sinkhorn_forward_workspace_bytes(int(B), int(M), int(N), int(n_iters), flags);
+    Tensor ws = workspace(ws_bytes, scores_f);
+    dot_sinkhorn_fwd_args a{};
+    a.scores = scores_f.data_ptr<float>();
+    a.log_a = ptr_or_null(log_a_f);
+    a.log_b = ptr_or_null(log_b_f);
+    a.B = int(B);
+    a.M = int(M);
+    a.N = int(N);
+    a.scores_kind = kind;
+    a.tau = static_cast<float>(tau);
+    a.max_iter = int(n_iters);
+    a.tol = static_cast<float>(tol);
+    a.flags = flags;
+    a.plan = want_plan ? o.plan.data_ptr<float>() : nullptr;
+    a.cost = want_cost ? o.cost.data_ptr<float>() : nullptr;
+    a.u_hist = keep_history ? o.u_hist.data_ptr<float>() : nullptr;
+    a.v_hist = keep_history ? o.v_hist.data_ptr<float>() : nullptr;
+    a.iters_used = o.counts.data_ptr<int32_t>();
+    a.converged = o.counts.data_ptr<int32_t>() + 1;
+    a.workspace = ws.data_ptr();
+    a.workspace_bytes = ws_bytes;
+    check_rc(dot_sinkhorn_forward(&a, current_stream(scores_f)), "dot_sinkhorn_forward");
+    return o;
+}
+
+optional<Tensor> f32c_opt(const optional<Tensor>& t) {
+    if (!t.has_value()) return c10::nullopt;
+    return f32c(*t);
+}
+
+void check_common(const Tensor& log_alpha, double tau, int64_t n_iters) {
+    check_hip_input(log_alpha, "log_alpha");
+    TORCH_CHECK(log_alpha.dim() == 3, "log_alpha must be 3D [B, n, m]");
+    TORCH_CHECK(tau > 0.0, "tau must be > 0");
+    TORCH_CHECK(n_iters >= 0, "n_iters must be >= 0");
+}
+
+// ---------------------------------------------------------------------------
+// torch.ops.dot.* on HIP tensors
+// ---------------------------------------------------------------------------
+
+// sinkhorn / sinkhorn_log (torch_cuda.cpp:599-715).  The reference runs the
+// primal full-matrix iteration here; the dual iteration with tol = 0 computes
+// the same plan (test_sinkhorn.py:792-803 holds them to 1e-5).
+Tensor sinkhorn_hip(const Tensor& log_alpha, double tau, int64_t n_iters,
+                    const optional<Tensor>& log_a, const optional<Tensor>& log_b, bool return_log) {
+    check_common(log_alpha, tau, n_iters);
+    check_marginals(log_a, log_b, log_alpha.size(0), log_alpha.size(1), log_alpha.size(2));
+    c10::OptionalDeviceGuard guard(log_alpha.device());
+    return run_forward(f32c(log_alpha), DOT_SCORES_LOG_ALPHA, tau, n_iters, 0.0, f32c_opt(log_a),
+                       f32c_opt(log_b), return_log, true, false, false)
+        .plan;
+}
+
+Tensor sinkhorn_op(Tensor log_alpha, double tau, int64_t n_iters, optional<Tensor> log_a,
+                   optional<Tensor> log_b) {
+    return sinkhorn_hip(log_alpha, tau, n_iters, log_a, log_b, false);
+}
+
+Tensor sinkhorn_log_op(Tensor log_alpha, double tau, int64_t n_iters, optional<Tensor> log_a,
+                       optional<Tensor> log_b) {
+    return sinkhorn_hip(log_alpha, tau, n_iters, log_a, log_b, true);
+}
+
+std::vector<Tensor> counts_to_cpu(const Tensor& counts) {
+    Tensor c = counts.to(at::kCPU);
+    const int32_t* p = c.data_ptr<int32_t>();
+    auto opt = at::TensorOptions().dtype(at::kLong).device(at::kCPU);
+    return {at::scalar_tensor(int64_t(p[0]), opt), at::scalar_tensor(int64_t(p[1]), opt)};
+}
+
+// sinkhorn_dual_forward (torch_cuda.cpp:266-321): returns [P or log P,
+// used (CPU int64 0-d), converged (CPU int64 0-d)].
+std::vector<Tensor> sinkhorn_dual_forward_op(Tensor log_alpha, double tau, int64_t n_iters, double tol,
+                                             optional<Tensor> log_a, optional<Tensor> log_b,
+                                             bool return_log, int64_t method, double omega,
+                                             int64_t anderson_k, double mixing_beta, double lr,
+                                             double beta1, double beta2, double eps_adam,
+                                             bool bias_correction, double reg_start, int64_t schedule) {
+    (void)omega;
+    (void)mixing_beta;
+    (void)lr;
+    (void)beta1;
+    (void)beta2;
+    (void)eps_adam;
+    (void)bias_correction;
+    (void)reg_start;
+    check_common(log_alpha, tau, n_iters);
+    TORCH_CHECK(anderson_k >= 1, "anderson_k must be >= 1");
+    TORCH_CHECK(method == 0,
+                "sinkhorn_dual_forward: method ", method,
+                " (momentum/anderson/adam) is not implemented by dot_amd; only method=0 (vanilla)");
+    TORCH_CHECK(schedule == 0,
+                "sinkhorn_dual_forward: regularisation schedules are not implemented by dot_amd");
+    check_marginals(log_a, log_b, log_alpha.size(0), log_alpha.size(1), log_alpha.size(2));
+    c10::OptionalDeviceGuard guard(log_alpha.device());
+    ForwardOut o = run_forward(f32c(log_alpha), DOT_SCORES_LOG_ALPHA, tau, n_iters, tol,
+                               f32c_opt(log_a), f32c_opt(log_b), return_log, true, false, false);
+    std::vector<Tensor> c = counts_to_cpu(o.counts);
+    return {o.plan, c[0], c[1]};
+}
+
+// sinkhorn_spectral_preflight (torch_cuda.cpp:559-593; kernel kernels.cu:141-241):
+// the same power iteration on P = softmax_row(log_alpha / tau) with the
+// reference's deterministic sin() start vector, written with ATen batched
+// products.  Not a hand-written kernel: this op is off the hot path.
+Tensor sinkhorn_spectral_preflight_op(Tensor log_alpha, double tau, int64_t n_power) {
+    check_hip_input(log_alpha, "log_alpha");
+    TORCH_CHECK(log_alpha.dim() == 3, "log_alpha must be 3D [B, n, m]");
+    TORCH_CHECK(tau > 0.0, "tau must be > 0");
+    TORCH_CHECK(n_power >= 1, "n_power must be >= 1");
+    c10::OptionalDeviceGuard guard(log_alpha.device());
+    const int64_t B = log_alpha.size(0), m = log_alpha.size(2);
+    Tensor K = f32c(log_alpha) * (1.0f / static_cast<float>(tau));
+    Tensor P = at::exp(K - at::logsumexp(K, {2}, true));
+    auto opts = K.options();
+    Tensor j = at::arange(1, m + 1, opts).unsqueeze(0);
+    Tensor bb = at::arange(1, B + 1, opts).unsqueeze(1);
+    Tensor v = at::sin(j * 12.9898f + bb * 78.233f);
+    auto center = [](const Tensor& x) { return x - x.mean({-1}, true); };
+    auto normalize = [](const Tensor& x) {
+        return x / at::sqrt(at::clamp_min((x * x).sum({-1}, true), 1.0e-12f));
+    };
+    v = normalize(center(v));
+    for (int64_t it = 0; it < n_power; ++it) {
+        Tensor u = center(at::bmm(P, v.unsqueeze(-1)).squeeze(-1));
+        v = normalize(center(at::bmm(P.transpose(1, 2).contiguous(), u.unsqueeze(-1)).squeeze(-1)));
+    }
+    Tensor u = center(at::bmm(P, v.unsqueeze(-1)).squeeze(-1));
+    Tensor est = at::sqrt(at::clamp_min((u * u).sum({-1}), 1.0e-12f));
+    return at::clamp(est, 0.0f, 0.999999f);
+}
+
+std::vector<Tensor> run_backward(bool implicit, const Tensor& scores_f, int kind, const Tensor& plan,
+                                 const optional<Tensor>& grad_plan, const optional<Tensor>& grad_cost,
+                                 double tau, int64_t iters, const Tensor& u_hist, const Tensor& v_hist) {
+    const int64_t B = scores_f.size(0), M = scores_f.size(1), N = scores_f.size(2);
+    auto opts = scores_f.options().dtype(at::kFloat);
+    Tensor grad = at::empty({B, M, N}, opts);
+    Tensor grad_tau = at::empty({B}, opts);
+    const size_t ws_bytes = implicit ? dot_sinkhorn_backward_implicit_workspace_bytes(int(B), int(M), int(N))
+                                     : dot_sinkhorn_backward_unrolled_workspace_bytes(int(B), int(M), int(N));
+    Tensor ws = workspace(ws_bytes, scores_f);
+    dot_sinkhorn_bwd_args a{};
+    a.scores = scores_f.data_ptr<float>();
+    a.scores_kind = kind;
+    a.plan = plan.data_ptr<float>();
+    a.grad_plan = ptr_or_null(grad_plan);
+    a.grad_cost = ptr_or_null(grad_cost);
+    a.B = int(B);
+    a.M = int(M);
+    a.N = int(N);
+    a.tau = static_cast<float>(tau);
+    TORCH_CHECK(iters <= INT32_MAX, "iteration count too large");
+    a.iters = int(iters);
+    a.u_hist = u_hist.defined() ? u_hist.data_ptr<float>() : nullptr;
+    a.v_hist = v_hist.defined() ? v_hist.data_ptr<float>() : nullptr;
+    a.grad_scores = grad.data_ptr<float>();
+    a.grad_tau = grad_tau.data_ptr<float>();
+    a.workspace = ws.data_ptr();
+    a.workspace_bytes = ws_bytes;
+    const dot_stream_t s = current_stream(scores_f);
+    if (implicit) check_rc(dot_sinkhorn_backward_implicit(&a, s), "dot_sinkhorn_backward_implicit");
+    else check_rc(dot_sinkhorn_backward_unrolled(&a, s), "dot_sinkhorn_backward_unrolled");
+    return {grad, grad_tau};
+}
+
+void check_grad_shape(const Tensor& log_alpha, const Tensor& grad_P) {
+    check_hip_input(grad_P, "grad_P");
+    TORCH_CHECK(grad_P.sizes() == log_alpha.sizes(), "grad_P must match log_alpha shape");
+}
+
+// sinkhorn_with_grads_unrolled (torch_cuda.cpp:717-801): forward with the u/v
+// history, then the reverse pass -> [P, grad_log_alpha, grad_tau].
+std::vector<Tensor> sinkhorn_with_grads_unrolled_op(Tensor log_alpha, Tensor grad_P, double tau,
+                                                    int64_t n_iters, optional<Tensor> log_a,
+                                                    optional<Tensor> log_b) {
+    check_common(log_alpha, tau, n_iters);
+    check_grad_shape(log_alpha, grad_P);
+    check_marginals(log_a, log_b, log_alpha.size(0), log_alpha.size(1), log_alpha.size(2));
+    c10::OptionalDeviceGuard guard(log_alpha.device());
+    Tensor la = f32c(log_alpha);
+    ForwardOut o = run_forward(la, DOT_SCORES_LOG_ALPHA, tau, n_iters, 0.0, f32c_opt(log_a),
+                               f32c_opt(log_b), false, true, false, true);
+    std::vector<Tensor> g = run_backward(false, la, DOT_SCORES_LOG_ALPHA, o.plan, f32c(grad_P),
+                                         c10::nullopt, tau, n_iters, o.u_hist, o.v_hist);
+    return {o.plan, g[0], g[1]};
+}
+
+// sinkhorn_with_grads_implicit (torch_cuda.cpp:803-871): forward with tol = 0,
+// then exactly backward_iters adjoint sweeps -> [P, grad_log_alpha, grad_tau].
+std::vector<Tensor> sinkhorn_with_grads_implicit_op(Tensor log_alpha, Tensor grad_P, double tau,
+                                                    int64_t n_iters, int64_t backward_iters,
+                                                    optional<Tensor> log_a, optional<Tensor> log_b) {
+    check_common(log_alpha, tau, n_iters);
+    check_grad_shape(log_alpha, grad_P);
+    TORCH_CHECK(backward_iters >= 0, "backward_iters must be >= 0");
+    check_marginals(log_a, log_b, log_alpha.size(0), log_alpha.size(1), log_alpha.size(2));
+    c10::OptionalDeviceGuard guard(log_alpha.device());
+    Tensor la = f32c(log_alpha);
+    ForwardOut o = run_forward(la, DOT_SCORES_LOG_ALPHA, tau, n_iters, 0.0, f32c_opt(log_a),
+                               f32c_opt(log_b), false, true, false, false);
+    std::vector<Tensor> g = run_backward(true, la, DOT_SCORES_LOG_ALPHA, o.plan, f32c(grad_P),
+                                         c10::nullopt, tau, backward_iters, Tensor(), Tensor());
+    return {o.plan, g[0], g[1]};
+}
+
+void check_lengths(const Tensor& lengths, int64_t B) {
+    check_hip_input(lengths, "lengths");
+    TORCH_CHECK(lengths.dim() == 2 && lengths.size(1) == 2, "lengths must be [B, 2]");
+    TORCH_CHECK(lengths.dtype() == at::kInt, "lengths must be int32");
+    TORCH_CHECK(lengths.size(0) == B, "lengths must have one row per batch element");
+}
+
+// bidirectional_softmax (bidirectional_softmax/torch_cuda.cpp:42-76) -> [P, row_sm, col_sm].
+std::vector<Tensor> bidirectional_softmax_op(Tensor sim, double tau, Tensor lengths) {
+    check_hip_input(sim, "sim_matrix");
+    TORCH_CHECK(sim.dim() == 3, "sim_matrix must be 3D [B, L1, L2]");
+    check_lengths(lengths, sim.size(0));
+    TORCH_CHECK(tau > 0.0, "tau must be > 0");
+    c10::OptionalDeviceGuard guard(sim.device());
+    Tensor s = f32c(sim);
+    Tensor ln = lengths.contiguous();
+    const int64_t B = s.size(0), L1 = s.size(1), L2 = s.size(2);
+    auto opts = s.options();
+    Tensor out = at::empty({B, L1, L2}, opts);
+    Tensor r = at::empty({B, L1, L2}, opts);
+    Tensor c = at::empty({B, L1, L2}, opts);
+    const size_t ws_bytes = dot_bidisoftmax_forward_workspace_bytes(int(B), int(L1), int(L2));
+    Tensor ws = workspace(ws_bytes, s);
+    dot_bidisoftmax_fwd_args a{};
+    a.sim = s.data_ptr<float>();
+    a.lengths = ln.data_ptr<int32_t>();
+    a.B = int(B);
+    a.L1 = int(L1);
+    a.L2 = int(L2);
+    a.tau = static_cast<float>(tau);
+    a.out = out.data_ptr<float>();
+    a.row_sm = r.data_ptr<float>();
+    a.col_sm = c.data_ptr<float>();
+    a.workspace = ws.data_ptr();
+    a.workspace_bytes = ws_bytes;
+    check_rc(dot_bidisoftmax_forward(&a, current_stream(s)), "dot_bidisoftmax_forward");
+    return {out, r, c};
+}
+
+std::vector<Tensor> bidi_backward_common(const Tensor& sim, const Tensor& grad_output, double tau,
+                                         const Tensor& lengths, const Tensor& out, const Tensor& r,
+                                         const Tensor& c, const Tensor& row_stats,
+                                         const Tensor& col_stats) {
+    const int64_t B = sim.size(0), L1 = sim.size(1), L2 = sim.size(2);
+    auto opts = sim.options();
+    Tensor grad = at::empty({B, L1, L2}, opts);
+    Tensor grad_tau = at::empty({B}, opts);
+    const size_t ws_bytes = dot_bidisoftmax_backward_workspace_bytes(int(B), int(L1), int(L2));
+    Tensor ws = workspace(ws_bytes, sim);
+    dot_bidisoftmax_bwd_args a{};
+    a.sim = sim.data_ptr<float>();
+    a.lengths = lengths.data_ptr<int32_t>();
+    a.B = int(B);
+    a.L1 = int(L1);
+    a.L2 = int(L2);
+    a.tau = static_cast<float>(tau);
+    a.grad_out = grad_output.data_ptr<float>();
+    a.out = out.defined() ? out.data_ptr<float>() : nullptr;
+    a.row_sm = r.defined() ? r.data_ptr<float>() : nullptr;
+    a.col_sm = c.defined() ? c.data_ptr<float>() : nullptr;
+    a.row_stats = row_stats.defined() ? row_stats.data_ptr<float>() : nullptr;
+    a.col_stats = col_stats.defined() ? col_stats.data_ptr<float>() : nullptr;
+    a.grad_sim = grad.data_ptr<float>();
+    a.grad_tau = grad_tau.data_ptr<float>();
+    a.workspace = ws.data_ptr();
+    a.workspace_bytes = ws_bytes;
+    check_rc(dot_bidisoftmax_backward(&a, current_stream(sim)), "dot_bidisoftmax_backward");
+    return {grad, grad_tau};
+}
+
+// bidirectional_softmax_backward (bidirectional_softmax/torch_cuda.cpp:78-139) -> [grad_sim, grad_tau].
+std::vector<Tensor> bidirectional_softmax_backward_op(Tensor sim, Tensor output, Tensor grad_output,
+                                                      Tensor row_softmax, Tensor col_softmax,
+                                                      double tau, Tensor lengths) {
+    for (auto* t : {&sim, &output, &grad_output, &row_softmax, &col_softmax})
+        check_hip_input(*t, "bidirectional_softmax_backward inputs");
+    TORCH_CHECK(sim.dim() == 3, "sim_matrix must be 3D [B, L1, L2]");
+    TORCH_CHECK(output.sizes() == sim.sizes(), "output must match sim_matrix shape");
+    TORCH_CHECK(grad_output.sizes() == sim.sizes(), "grad_output must match sim_matrix shape");
+    TORCH_CHECK(row_softmax.sizes() == sim.sizes(), "row_softmax must match sim_matrix shape");
+    TORCH_CHECK(col_softmax.sizes() == sim.sizes(), "col_softmax must match sim_matrix shape");
+    check_lengths(lengths, sim.size(0));
+    TORCH_CHECK(tau > 0.0, "tau must be > 0");
+    c10::OptionalDeviceGuard guard(sim.device());
+    return bidi_backward_common(f32c(sim), f32c(grad_output), tau, lengths.contiguous(), f32c(output),
+                                f32c(row_softmax), f32c(col_softmax), Tensor(), Tensor());
+}
+
+// ---------------------------------------------------------------------------
+// torch.ops.dot_amd.* fused operators (HIP only)
+// ---------------------------------------------------------------------------
+
+// -> [P, cost (B,) or undefined, counts int32[2] on device, u_hist, v_hist]
+std::vector<Tensor> fused_forward_op(Tensor scores, int64_t scores_kind, double tau, int64_t n_iters,
+                                     double tol, optional<Tensor> log_a, optional<Tensor> log_b,
+                                     bool want_cost, bool keep_history) {
+    check_common(scores, tau, n_iters);
+    TORCH_CHECK(scores_kind == DOT_SCORES_LOG_ALPHA || scores_kind == DOT_SCORES_COST,
+                "scores_kind must be 1 (log_alpha) or -1 (cost)");
+    check_marginals(log_a, log_b, scores.size(0), scores.size(1), scores.size(2));
+    c10::OptionalDeviceGuard guard(scores.device());
+    ForwardOut o = run_forward(f32c(scores), int(scores_kind), tau, n_iters, tol, f32c_opt(log_a),
+                               f32c_opt(log_b), false, true, want_cost, keep_history);
+    auto or_empty = [&](const Tensor& t) { return t.defined() ? t : at::empty({0}, scores.options().dtype(at::kFloat)); };
+    return {o.plan, or_empty(o.cost), o.counts, or_empty(o.u_hist), or_empty(o.v_hist)};
+}
+
+// -> [grad_scores, grad_tau (B,)]; mode 0 implicit (iters = adjoint sweeps), 1 unrolled (iters = T).
+std::vector<Tensor> fused_backward_op(Tensor scores, int64_t scores_kind, Tensor plan,
+                                      optional<Tensor> grad_plan, optional<Tensor> grad_cost,
+                                      double tau, int64_t mode, int64_t iters,
+                                      optional<Tensor> u_hist, optional<Tensor> v_hist) {
+    check_hip_input(scores, "scores");
+    check_hip_input(plan, "plan");
+    TORCH_CHECK(scores.dim() == 3 && plan.sizes() == scores.sizes(), "plan must match scores");
+    TORCH_CHECK(tau > 0.0, "tau must be > 0");
+    TORCH_CHECK(iters >= 0, "iters must be >= 0");
+    if (grad_plan.has_value()) TORCH_CHECK(grad_plan->sizes() == scores.sizes(), "grad_plan shape");
+    if (grad_cost.has_value())
+        TORCH_CHECK(grad_cost->dim() == 1 && grad_cost->size(0) == scores.size(0), "grad_cost shape");
+    c10::OptionalDeviceGuard guard(scores.device());
+    Tensor uh = u_hist.has_value() ? f32c(*u_hist) : Tensor();
+    Tensor vh = v_hist.has_value() ? f32c(*v_hist) : Tensor();
+    if (mode == 1 && iters > 0)
+        TORCH_CHECK(uh.defined() && vh.defined() && uh.size(0) >= iters && vh.size(0) >= iters,
+                    "unrolled backward needs the u/v history of every iteration");
+    return run_backward(mode == 0, f32c(scores), int(scores_kind), f32c(plan), f32c_opt(grad_plan),
+                        f32c_opt(grad_cost), tau, iters, uh, vh);
+}
+
+// -> [out, row_stats (B,2,L1), col_stats (B,2,L2)]
+std::vector<Tensor> bidi_forward_op(Tensor sim, double tau, Tensor lengths) {
+    check_hip_input(sim, "sim_matrix");
+    TORCH_CHECK(sim.dim() == 3, "sim_matrix must be 3D [B, L1, L2]");
+    check_lengths(lengths, sim.size(0));
+    TORCH_CHECK(tau > 0.0, "tau must be > 0");
+    c10::OptionalDeviceGuard guard(sim.device());
+    Tensor s = f32c(sim);
+    Tensor ln = lengths.contiguous();
+    const int64_t B = s.size(0), L1 = s.size(1), L2 = s.size(2);
+    auto opts = s.options();
+    Tensor out = at::empty({B, L1, L2}, opts);
+    Tensor rs = at::empty({B, 2, L1}, opts);
+    Tensor cs = at::empty({B, 2, L2}, opts);
+    const size_t ws_bytes = dot_bidisoftmax_forward_workspace_bytes(int(B), int(L1), int(L2));
+    Tensor ws = workspace(ws_bytes, s);
+    dot_bidisoftmax_fwd_args a{};
+    a.sim = s.data_ptr<float>();
+    a.lengths = ln.data_ptr<int32_t>();
+    a.B = int(B);
+    a.L1 = int(L1);
+    a.L2 = int(L2);
+    a.tau = static_cast<float>(tau);
+    a.out = out.data_ptr<float>();
+    a.row_stats = rs.data_ptr<float>();
+    a.col_stats = cs.data_ptr<float>();
+    a.workspace = ws.data_ptr();
+    a.workspace_bytes = ws_bytes;
+    check_rc(dot_bidisoftmax_forward(&a, current_stream(s)), "dot_bidisoftmax_forward");
+    return {out, rs, cs};
+}
+
+std::vector<Tensor> bidi_backward_op(Tensor sim, Tensor grad_output, Tensor row_stats,
+                                     Tensor col_stats, double tau, Tensor lengths) {
+    for (auto* t : {&sim, &grad_output, &row_stats, &col_stats}) check_hip_input(*t, "inputs");
+    TORCH_CHECK(sim.dim() == 3 && grad_output.sizes() == sim.sizes(), "grad_output must match sim");
+    check_lengths(lengths, sim.size(0));
+    TORCH_CHECK(tau > 0.0, "tau must be > 0");
+    c10::OptionalDeviceGuard guard(sim.device());
+    return bidi_backward_common(f32c(sim), f32c(grad_output), tau, lengths.contiguous(), Tensor(),
+                                Tensor(), Tensor(), f32c(row_stats), f32c(col_stats));
+}
+
+}  // namespace
+
+TORCH_LIBRARY(dot, m) {
+    m.def("sinkhorn(Tensor log_alpha, float tau, int n_iters, Tensor? log_a=None, Tensor? log_b=None) -> Tensor");
+    m.def("sinkhorn_log(Tensor log_alpha, float tau, int n_iters, Tensor? log_a=None, Tensor? log_b=None) -> Tensor");
+    m.def(
+        "sinkhorn_dual_forward("
+        "Tensor log_alpha, float tau, int n_iters, float tol=0.0, Tensor? log_a=None, Tensor? log_b=None, "
+        "bool return_log=False, int method=0, float omega=1.5, int anderson_k=5, float mixing_beta=1.0, "
+        "float lr=1.0, float beta1=0.9, float beta2=0.999, float eps_adam=1e-8, bool bias_correction=True, "
+        "float reg_start=-1.0, int schedule=0"
+        ") -> Tensor[]");
+    m.def("sinkhorn_spectral_preflight(Tensor log_alpha, float tau, int n_power=8) -> Tensor");
+    m.def("sinkhorn_with_grads_unrolled(Tensor log_alpha, Tensor grad_P, float tau, int n_iters, Tensor? log_a=None, Tensor? log_b=None) -> Tensor[]");
+    m.def("sinkhorn_with_grads_implicit(Tensor log_alpha, Tensor grad_P, float tau, int n_iters, int backward_iters, Tensor? log_a=None, Tensor? log_b=None) -> Tensor[]");
+    m.def("bidirectional_softmax(Tensor sim, float tau, Tensor lengths) -> Tensor[]");
+    m.def("bidirectional_softmax_backward(Tensor sim, Tensor output, Tensor grad_output, Tensor row_softmax, Tensor col_softmax, float tau, Tensor lengths) -> Tensor[]");
+}
+
+TORCH_LIBRARY_IMPL(dot, CUDA, m) {
+    m.impl("sinkhorn", sinkhorn_op);
+    m.impl("sinkhorn_log", sinkhorn_log_op);
+    m.impl("sinkhorn_dual_forward", sinkhorn_dual_forward_op);
+    m.impl("sinkhorn_spectral_preflight", sinkhorn_spectral_preflight_op);
+    m.impl("sinkhorn_with_grads_unrolled", sinkhorn_with_grads_unrolled_op);
+    m.impl("sinkhorn_with_grads_implicit", sinkhorn_with_grads_implicit_op);
+    m.impl("bidirectional_softmax", bidirectional_softmax_op);
+    m.impl("bidirectional_softmax_backward", bidirectional_softmax_backward_op);
+}
+
+TORCH_LIBRARY(dot_amd, m) {
+    m.def("sinkhorn_forward(Tensor scores, int scores_kind, float tau, int n_iters, float tol, Tensor? log_a, Tensor? log_b, bool want_cost, bool keep_history) -> Tensor[]");
+    m.def("sinkhorn_backward(Tensor scores, int scores_kind, Tensor plan, Tensor? grad_plan, Tensor? grad_cost, float tau, int mode, int iters, Tensor? u_hist, Tensor? v_hist) -> Tensor[]");
+    m.def("bidirectional_softmax_forward(Tensor sim, float tau, Tensor lengths) -> Tensor[]");
+    m.def("bidirectional_softmax_backward(Tensor sim, Tensor grad_output, Tensor row_stats, Tensor col_stats, float tau, Tensor lengths) -> Tensor[]");
+}
+
+TORCH_LIBRARY_IMPL(dot_amd, CUDA, m) {
+    m.impl("sinkhorn_forward", fused_forward_op);
+    m.impl("sinkhorn_backward", fused_backward_op);
+    m.impl("bidirectional_softmax_forward", bidi_forward_op);
+    m.impl("bidirectional_softmax_backward", bidi_backward_op);
+}

@@ -1,0 +1,87 @@
+// wave64 reduction primitives for gfx950 (CDNA4).
+//
+// Replaces the reference's warp-32 shuffle reductions (src/sinkhorn/kernels.cu:27-69,
+// src/bidirectional_softmax/kernels.cu:41-83).  A wave is 64 lanes; a reduction
+// is four DPP steps inside each 16-lane row, one ds_swizzle step across the two
+// rows of each 32-lane half, and a scalar combine of the two halves through
+// v_readlane.  The combine order is fixed, so results are bitwise reproducible.
+// Every lane of the wave must be active when these are called.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <cstdint>
+
+namespace dot_amd {
+
+constexpr int kWave = 64;
+
+// DPP control words (GFX9 encoding).
+constexpr int kDppQuadXor1 = 0xB1;       // quad_perm [1,0,3,2]
+constexpr int kDppQuadXor2 = 0x4E;       // quad_perm [2,3,0,1]
+constexpr int kDppRowHalfMirror = 0x141; // lane i <- 7-i inside each 8-lane half-row
+constexpr int kDppRowMirror = 0x140;     // lane i <- 15-i inside each 16-lane row
+// ds_swizzle bit-mask mode: and=0x1F, or=0, xor=0x10 -> lane ^ 16 inside 32 lanes.
+constexpr int kSwizzleXor16 = (0x10 << 10) | 0x1F;
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_move(float x) {
+    return __builtin_bit_cast(
+        float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
+}
+
+__device__ __forceinline__ float swizzle_xor16(float x) {
+    return __builtin_bit_cast(float,
+                              __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, x), kSwizzleXor16));
+}
+
+__device__ __forceinline__ float read_lane(float x, int lane) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), lane));
+}
+
+struct OpSum {
+    __device__ __forceinline__ float operator()(float a, float b) const { return a + b; }
+};
+struct OpMax {
+    __device__ __forceinline__ float operator()(float a, float b) const { return fmaxf(a, b); }
+};
+
+// All-reduce over the 64 lanes; the result is wave-uniform.
+template <class Op>
+__device__ __forceinline__ float wave_reduce(float x, Op op) {
+    x = op(x, dpp_move<kDppQuadXor1>(x));
+    x = op(x, dpp_move<kDppQuadXor2>(x));
+    x = op(x, dpp_move<kDppRowHalfMirror>(x));
+    x = op(x, dpp_move<kDppRowMirror>(x));
+    x = op(x, swizzle_xor16(x));
+    return op(read_lane(x, 0), read_lane(x, 32));
+}
+
+__device__ __forceinline__ float wave_sum(float x) { return wave_reduce(x, OpSum{}); }
+__device__ __forceinline__ float wave_max(float x) { return wave_reduce(x, OpMax{}); }
+
+// Workgroup all-reduce of one value per wave through LDS, combined in wave order.
+// `scratch` needs kMaxWaves floats; contains a barrier on entry and exit.
+template <int NWAVES, class Op>
+__device__ __forceinline__ float block_reduce(float wave_value, float* scratch, Op op) {
+    const int wave = threadIdx.x / kWave;
+    __syncthreads();
+    if ((threadIdx.x % kWave) == 0) scratch[wave] = wave_value;
+    __syncthreads();
+    float r = scratch[0];
+#pragma unroll
+    for (int w = 1; w < NWAVES; ++w) r = op(r, scratch[w]);
+    return r;
+}
+
+// Exponentials.  The reference's safe_exp (src/sinkhorn/kernels.cu:21-25):
+// 0 below -88, exp(88) above 88.  fast_exp2 is the hardware v_exp_f32 (2^x).
+constexpr float kLog2E = 1.4426950408889634f;
+
+__device__ __forceinline__ float fast_exp(float x) { return __builtin_amdgcn_exp2f(x * kLog2E); }
+
+__device__ __forceinline__ float safe_exp(float x) {
+    if (x < -88.0f) return 0.0f;
+    return expf(fminf(x, 88.0f));
+}
+
+}  // namespace dot_amd

@@ -1,0 +1,483 @@
+"""Sinkhorn optimal transport and soft permutations — the reference's Python API.
+
+Mirrors dot/sinkhorn.py of the reference: ``sinkhorn`` (:1284-1714),
+``sinkhorn_from_scores`` (:1717-1860), ``spectral_preflight`` (:860-905),
+``SinkhornResult`` (:22-34), ``Sinkhorn`` (:1863-1906) and
+``SinkhornFromScores`` (:1909-1954), with the same argument names, defaults,
+validation errors and result fields.  ``max_iter`` is accepted as an alias of
+``n_iters`` (the reference README's spelling, README.md:43).
+
+On HIP tensors the forward and backward run as fused dot_amd operators:
+
+* the forward iterates on the device, decides the stopping test on the
+  device, and writes the plan and the transport cost ``sum(P * C)`` in one
+  pass (one host sync at the end, for ``n_iters_used``);
+* the backward takes the plan saved by the forward (the reference recomputes
+  the whole forward, torch_cuda.cpp:842-853, which yields the same plan) and
+  runs the implicit adjoint (exactly ``backward_iters`` sweeps) or the
+  unrolled reverse pass over the ``n_iters_used`` recorded potentials, with the
+  cost's direct gradient ``grad_cost * P`` folded in.
+
+On CPU tensors the reference's CPU path is followed through the
+``torch.ops.dot`` CPU operators.  The alternative solvers (momentum, Anderson,
+Adam, Newton, Muon) and regularisation schedules are not implemented; asking
+for one raises ``NotImplementedError`` unless the reference itself would fall
+back to the vanilla solver (sinkhorn.py:1378-1390).
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from typing import Literal, Optional
+
+import torch
+import torch.nn as nn
+
+from . import _ops
+
+SCORES_LOG_ALPHA = 1
+SCORES_COST = -1
+_MODE_IMPLICIT = 0
+_MODE_UNROLLED = 1
+
+DEFAULT_SPECTRAL_PREFLIGHT_ALPHA = 1.0
+SPECTRAL_PREFLIGHT_MIN_ITERS = 3
+SPECTRAL_PREFLIGHT_MAX_ITERS = 1000
+
+
+@dataclass
+class SinkhornResult:
+    """Result from Sinkhorn computation.
+
+    Attributes:
+        transport_plan: Transport plan P of shape (B, n, m)
+        cost: Transport cost sum(P * C) of shape (B,)
+        converged: Whether the stopping test fired (True when tol == 0)
+        n_iters_used: Forward iterations executed
+    """
+
+    transport_plan: torch.Tensor
+    cost: Optional[torch.Tensor] = None
+    converged: bool = True
+    n_iters_used: Optional[int] = None
+
+
+def _tau_value(tau) -> float:
+    return float(tau.detach().item()) if torch.is_tensor(tau) else float(tau)
+
+
+def _check_tau_tensor(tau):
+    if torch.is_tensor(tau) and tau.numel() != 1:
+        raise ValueError("reg/tau tensor must be scalar")
+
+
+# ---------------------------------------------------------------------------
+# HIP: fused autograd function
+# ---------------------------------------------------------------------------
+class _SinkhornFusedFunction(torch.autograd.Function):
+    """Fused forward (plan + cost + device-side stop) and fused backward on HIP tensors.
+
+    Outputs ``(P, cost, counts)``; ``counts`` is int32 ``[iters_used, converged]``
+    on the device.  ``scores_kind`` says whether ``scores`` is a cost matrix C
+    (log_alpha = -C) or log_alpha itself.
+    """
+
+    @staticmethod
+    def forward(ctx, scores, tau, scores_kind, n_iters, backward_iters, log_a, log_b, tol, mode,
+                want_cost):
+        _check_tau_tensor(tau)
+        tau_value = _tau_value(tau)
+        needs_grad = ctx.needs_input_grad[0] or (torch.is_tensor(tau) and ctx.needs_input_grad[1])
+        keep_history = bool(needs_grad and mode == _MODE_UNROLLED)
+        P, cost, counts, u_hist, v_hist = _ops.fused.sinkhorn_forward(
+            scores, scores_kind, tau_value, n_iters, tol, log_a, log_b, want_cost, keep_history
+        )
+        ctx.mark_non_differentiable(counts)
+        if not want_cost:
+            ctx.mark_non_differentiable(cost)
+        ctx.save_for_backward(scores, P, counts, u_hist, v_hist)
+        ctx.tau = tau_value
+        ctx.tau_is_tensor = torch.is_tensor(tau)
+        ctx.scores_kind = scores_kind
+        ctx.backward_iters = backward_iters
+        ctx.mode = mode
+        ctx.scores_dtype = scores.dtype
+        return P, cost, counts
+
+    @staticmethod
+    def backward(ctx, grad_P, grad_cost, _grad_counts):
+        scores, P, counts, u_hist, v_hist = ctx.saved_tensors
+        if grad_cost is not None and grad_cost.numel() == 0:
+            grad_cost = None
+        if ctx.mode == _MODE_UNROLLED:
+            iters = int(counts[0].item())
+            uh, vh = u_hist, v_hist
+        else:
+            iters = ctx.backward_iters
+            uh = vh = None
+        grad_scores, grad_tau = _ops.fused.sinkhorn_backward(
+            scores,
+            ctx.scores_kind,
+            P,
+            grad_P.contiguous() if grad_P is not None else None,
+            grad_cost.contiguous() if grad_cost is not None else None,
+            ctx.tau,
+            ctx.mode,
+            iters,
+            uh,
+            vh,
+        )
+        tau_grad = None
+        if ctx.tau_is_tensor and ctx.needs_input_grad[1]:
+            tau_grad = grad_tau.sum()
+        return grad_scores.to(ctx.scores_dtype), tau_grad, None, None, None, None, None, None, None, None
+
+
+def _run_fused(scores, reg, scores_kind, n_iters, backward_iters, log_a, log_b, tol, mode, want_cost):
+    tau_arg = reg
+    if torch.is_tensor(reg):
+        tau_arg = reg.reshape(()).to(device=scores.device)
+    P, cost, counts = _SinkhornFusedFunction.apply(
+        scores, tau_arg, scores_kind, int(n_iters), int(backward_iters), log_a, log_b, float(tol),
+        mode, want_cost
+    )
+    used, conv = (int(x) for x in counts.tolist())
+    return P, cost, used, bool(conv)
+
+
+# ---------------------------------------------------------------------------
+# CPU: the reference's autograd functions over the CPU operators
+# ---------------------------------------------------------------------------
+class _SinkhornUnrolledFunction(torch.autograd.Function):
+    """CPU autograd with the unrolled backward (reference sinkhorn.py:46-96)."""
+
+    @staticmethod
+    def forward(ctx, log_alpha, tau, n_iters, log_a, log_b):
+        _check_tau_tensor(tau)
+        tau_value = _tau_value(tau)
+        P = _ops.sinkhorn(log_alpha, tau_value, n_iters, log_a, log_b)
+        ctx.save_for_backward(log_alpha,
+                              log_a if log_a is not None else torch.Tensor(),
+                              log_b if log_b is not None else torch.Tensor())
+        ctx.tau, ctx.n_iters = tau_value, n_iters
+        ctx.tau_is_tensor = torch.is_tensor(tau)
+        ctx.has_log_a, ctx.has_log_b = log_a is not None, log_b is not None
+        return P
+
+    @staticmethod
+    def backward(ctx, grad_P):
+        log_alpha, log_a, log_b = ctx.saved_tensors
+        _, grad_log_alpha, grad_tau = _ops.sinkhorn_with_grads_unrolled(
+            log_alpha, grad_P.contiguous(), ctx.tau, ctx.n_iters,
+            log_a if ctx.has_log_a else None, log_b if ctx.has_log_b else None)
+        tau_grad = grad_tau.sum() if ctx.tau_is_tensor else None
+        return grad_log_alpha, tau_grad, None, None, None
+
+
+class _SinkhornImplicitFunction(torch.autograd.Function):
+    """CPU autograd with the implicit backward (reference sinkhorn.py:99-152)."""
+
+    @staticmethod
+    def forward(ctx, log_alpha, tau, n_iters, backward_iters, log_a, log_b):
+        _check_tau_tensor(tau)
+        tau_value = _tau_value(tau)
+        P = _ops.sinkhorn(log_alpha, tau_value, n_iters, log_a, log_b)
+        ctx.save_for_backward(log_alpha,
+                              log_a if log_a is not None else torch.Tensor(),
+                              log_b if log_b is not None else torch.Tensor())
+        ctx.tau, ctx.n_iters, ctx.backward_iters = tau_value, n_iters, backward_iters
+        ctx.tau_is_tensor = torch.is_tensor(tau)
+        ctx.has_log_a, ctx.has_log_b = log_a is not None, log_b is not None
+        return P
+
+    @staticmethod
+    def backward(ctx, grad_P):
+        log_alpha, log_a, log_b = ctx.saved_tensors
+        _, grad_log_alpha, grad_tau = _ops.sinkhorn_with_grads_implicit(
+            log_alpha, grad_P.contiguous(), ctx.tau, ctx.n_iters, ctx.backward_iters,
+            log_a if ctx.has_log_a else None, log_b if ctx.has_log_b else None)
+        tau_grad = grad_tau.sum() if ctx.tau_is_tensor else None
+        return grad_log_alpha, tau_grad, None, None, None, None
+
+
+# ---------------------------------------------------------------------------
+# Argument handling
+# ---------------------------------------------------------------------------
+def _prepare_marginal(marginal, batch, size, name, device, dtype):
+    """Validation of the reference's _prepare_marginal (sinkhorn.py:1259-1281)."""
+    if marginal is None:
+        return None
+    if marginal.dim() == 1:
+        marginal = marginal.unsqueeze(0).expand(batch, -1)
+    if marginal.shape != (batch, size):
+        raise ValueError(f"{name} must have shape ({batch}, {size}) or ({size},)")
+    if torch.any(marginal <= 0):
+        raise ValueError(f"{name} must be strictly positive")
+    marginal = marginal.to(device=device, dtype=dtype)
+    sums = marginal.sum(dim=-1)
+    if not torch.allclose(sums, torch.ones_like(sums), atol=1e-4, rtol=1e-4):
+        raise ValueError(f"{name} must sum to 1 along the last dimension")
+    return marginal
+
+
+def _resolve_iters(n_iters, max_iter):
+    if max_iter is not None:
+        if n_iters is not None and n_iters != 20 and n_iters != max_iter:
+            raise ValueError("pass n_iters or its alias max_iter, not both")
+        return max_iter
+    return 20 if n_iters is None else n_iters
+
+
+def _effective_method(method, schedule, reg_start, omega, tau_value, lr, beta1, beta2, eps_adam,
+                      bias_correction, backward_mode, on_gpu, dual, size):
+    """The reference's method/schedule resolution (sinkhorn.py:1362-1390)."""
+    if method == "auto":
+        method = "newton" if size[0] <= 100 and size[1] <= 100 else "vanilla"
+    effective = method
+    eff_schedule = schedule
+    if dual and on_gpu and backward_mode == "implicit":
+        if effective == "momentum" and omega is None:
+            effective = "vanilla"
+        elif effective == "anderson" and eff_schedule is None:
+            if tau_value >= 0.05:
+                effective = "vanilla"
+            elif tau_value <= 0.01:
+                eff_schedule = "exponential"
+        elif effective == "adam" and eff_schedule is None:
+            is_default_adam = (lr == 1.0 and beta1 == 0.9 and beta2 == 0.999 and eps_adam == 1e-8
+                               and bias_correction)
+            if tau_value >= 0.05 or is_default_adam:
+                effective = "vanilla"
+    return method, effective, eff_schedule
+
+
+_METHODS = ("vanilla", "momentum", "anderson", "adam", "newton", "muon", "auto")
+
+
+def sinkhorn(
+    cost_matrix: torch.Tensor,
+    reg: float | torch.Tensor = 1.0,
+    n_iters: int | Literal["auto"] = 20,
+    backward_mode: Literal["unrolled", "implicit"] = "implicit",
+    backward_iters: Optional[int] = None,
+    a: Optional[torch.Tensor] = None,
+    b: Optional[torch.Tensor] = None,
+    method: Literal["vanilla", "momentum", "anderson", "adam", "newton", "muon", "auto"] = "vanilla",
+    omega: Optional[float] = None,
+    anderson_k: int = 5,
+    mixing_beta: float = 1.0,
+    lr: float = 1.0,
+    beta1: float = 0.9,
+    beta2: float = 0.999,
+    eps_adam: float = 1e-8,
+    bias_correction: bool = True,
+    reg_start: Optional[float] = None,
+    schedule: Optional[Literal["linear", "exponential", "cosine"]] = None,
+    tol: float = 1e-6,
+    dual: bool = True,
+    max_iter: Optional[int] = None,
+) -> SinkhornResult:
+    """Entropy-regularised optimal transport with the Sinkhorn algorithm.
+
+    Args:
+        cost_matrix: Cost matrix of shape (B, n, m) or (n, m)
+        reg: Regularization strength / temperature (float or scalar tensor)
+        n_iters: Maximum Sinkhorn iterations, or 'auto' for the spectral preflight
+        backward_mode: 'implicit' (adjoint, default) or 'unrolled'
+        backward_iters: Adjoint sweeps of the implicit backward (default: n_iters)
+        a, b: Optional source/target marginals, shape (B, n)/(n,) and (B, m)/(m,)
+        method: Solver; only 'vanilla' (and the cases the reference maps to it)
+            is implemented
+        tol: Stop after the first iteration with max|u_t - u_{t-1}| < tol over
+            the whole batch (HIP tensors); 0 forces all iterations
+        dual: Prefer the dual-state device path (HIP tensors)
+        max_iter: Alias of n_iters
+
+    Returns:
+        SinkhornResult(transport_plan, cost, converged, n_iters_used)
+    """
+    n_iters = _resolve_iters(n_iters, max_iter)
+    if method not in _METHODS:
+        raise ValueError(f"Unsupported method: {method}")
+    if backward_mode not in ("implicit", "unrolled"):
+        raise ValueError("backward_mode must be 'unrolled' or 'implicit'")
+
+    unbatched = cost_matrix.dim() == 2
+    if unbatched:
+        cost_matrix = cost_matrix.unsqueeze(0)
+    if cost_matrix.dim() != 3:
+        raise ValueError("cost_matrix must have shape (B, n, m) or (n, m)")
+
+    a = _prepare_marginal(a, cost_matrix.size(0), cost_matrix.size(-2), "a", cost_matrix.device,
+                          cost_matrix.dtype)
+    b = _prepare_marginal(b, cost_matrix.size(0), cost_matrix.size(-1), "b", cost_matrix.device,
+                          cost_matrix.dtype)
+    log_a = torch.log(a) if a is not None else None
+    log_b = torch.log(b) if b is not None else None
+
+    tau_value = _tau_value(reg)
+    if isinstance(n_iters, str):
+        if n_iters != "auto":
+            raise ValueError("n_iters must be an int or 'auto'")
+        predicted = spectral_preflight(-cost_matrix.detach(), tau_value, tol=tol)
+        n_iters = int(predicted.max().item()) if torch.is_tensor(predicted) else int(predicted)
+    if backward_iters is None:
+        backward_iters = n_iters
+
+    on_gpu = cost_matrix.is_cuda
+    method, effective, eff_schedule = _effective_method(
+        method, schedule, reg_start, omega, tau_value, lr, beta1, beta2, eps_adam, bias_correction,
+        backward_mode, on_gpu, dual, (cost_matrix.size(-2), cost_matrix.size(-1)))
+    if effective != "vanilla":
+        raise NotImplementedError(
+            f"method={effective!r} is not implemented by dot_amd; use method='vanilla'")
+    if eff_schedule is not None:
+        raise NotImplementedError("regularisation schedules are not implemented by dot_amd")
+
+    mode = _MODE_UNROLLED if backward_mode == "unrolled" else _MODE_IMPLICIT
+    if on_gpu:
+        # dual=False is the reference's full-matrix path: it ignores tol and
+        # always runs n_iters (sinkhorn.py:1693 with torch_cuda.cpp:599-656).
+        run_tol = tol if dual else 0.0
+        P, cost, used, conv = _run_fused(cost_matrix, reg, SCORES_COST, n_iters, backward_iters,
+                                         log_a, log_b, run_tol, mode, True)
+        if dual:
+            converged = conv if tol > 0 else True
+        else:
+            converged = True if tol == 0 else used < n_iters
+        cost = cost.to(torch.result_type(P, cost_matrix))
+    else:
+        log_alpha = -cost_matrix
+        if mode == _MODE_UNROLLED:
+            P = _SinkhornUnrolledFunction.apply(log_alpha, reg, n_iters, log_a, log_b)
+        else:
+            P = _SinkhornImplicitFunction.apply(log_alpha, reg, n_iters, backward_iters, log_a, log_b)
+        used = n_iters
+        converged = True if tol == 0 else used < n_iters
+        cost = (P * cost_matrix).sum(dim=(-2, -1))
+
+    if unbatched:
+        P = P.squeeze(0)
+        cost = cost.squeeze(0)
+    return SinkhornResult(transport_plan=P, cost=cost, converged=converged, n_iters_used=used)
+
+
+def sinkhorn_from_scores(
+    log_alpha: torch.Tensor,
+    tau: float | torch.Tensor = 1.0,
+    n_iters: int | Literal["auto"] = 20,
+    backward_mode: Literal["unrolled", "implicit"] = "implicit",
+    backward_iters: Optional[int] = None,
+    return_log: bool = False,
+    a: Optional[torch.Tensor] = None,
+    b: Optional[torch.Tensor] = None,
+    tol: float = 1e-6,
+    dual: bool = True,
+    max_iter: Optional[int] = None,
+) -> torch.Tensor:
+    """Normalised transport plan (or its log) directly from log-space scores.
+
+    Same contract as the reference's sinkhorn_from_scores (sinkhorn.py:1717-1860).
+    """
+    n_iters = _resolve_iters(n_iters, max_iter)
+    unbatched = log_alpha.dim() == 2
+    if unbatched:
+        log_alpha = log_alpha.unsqueeze(0)
+    a = _prepare_marginal(a, log_alpha.size(0), log_alpha.size(-2), "a", log_alpha.device,
+                          log_alpha.dtype)
+    b = _prepare_marginal(b, log_alpha.size(0), log_alpha.size(-1), "b", log_alpha.device,
+                          log_alpha.dtype)
+    log_a = torch.log(a) if a is not None else None
+    log_b = torch.log(b) if b is not None else None
+    tau_value = _tau_value(tau)
+    if isinstance(n_iters, str):
+        if n_iters != "auto":
+            raise ValueError("n_iters must be an int or 'auto'")
+        predicted = spectral_preflight(log_alpha.detach(), tau_value, tol=tol)
+        n_iters = int(predicted.max().item()) if torch.is_tensor(predicted) else int(predicted)
+    if backward_iters is None:
+        backward_iters = n_iters
+
+    if log_alpha.is_cuda and dual and backward_mode in ("implicit", "unrolled"):
+        if return_log:
+            result, _, _ = _ops.sinkhorn_dual_forward(log_alpha, tau_value, n_iters, tol, log_a, log_b,
+                                                      True)
+        else:
+            mode = _MODE_UNROLLED if backward_mode == "unrolled" else _MODE_IMPLICIT
+            result, _, _, _ = _run_fused(log_alpha, tau, SCORES_LOG_ALPHA, n_iters, backward_iters,
+                                         log_a, log_b, tol, mode, False)
+    elif return_log:
+        result = _ops.sinkhorn_log(log_alpha, tau_value, n_iters, log_a, log_b)
+    elif backward_mode == "unrolled":
+        result = _SinkhornUnrolledFunction.apply(log_alpha, tau, n_iters, log_a, log_b)
+    else:
+        result = _SinkhornImplicitFunction.apply(log_alpha, tau, n_iters, backward_iters, log_a, log_b)
+    if unbatched:
+        result = result.squeeze(0)
+    return result
+
+
+def spectral_preflight(
+    log_alpha: torch.Tensor,
+    tau: float | torch.Tensor,
+    tol: float = 1e-6,
+    n_power: int = 5,
+    alpha: Optional[float] = None,
+) -> int | torch.Tensor:
+    """Predicted iteration counts from a spectral contraction estimate (reference
+    sinkhorn.py:860-905): ceil(alpha * log(1/tol) / -log(tau_hat)), clamped to [3, 1000]."""
+    if tol <= 0:
+        raise ValueError("spectral_preflight requires tol > 0")
+    tau_value = _tau_value(tau)
+    if tau_value <= 0:
+        raise ValueError("tau/reg must be positive")
+    alpha_value = DEFAULT_SPECTRAL_PREFLIGHT_ALPHA if alpha is None else float(alpha)
+    unbatched = log_alpha.dim() == 2
+    if unbatched:
+        log_alpha = log_alpha.unsqueeze(0)
+    tau_est = _ops.sinkhorn_spectral_preflight(log_alpha, tau_value, n_power)
+    tau_hat = tau_est.clamp(min=1e-6, max=0.999999)
+    pred = torch.ceil(alpha_value * math.log(1.0 / tol) / (-torch.log(tau_hat))).to(torch.int64)
+    pred = pred.clamp(min=SPECTRAL_PREFLIGHT_MIN_ITERS, max=SPECTRAL_PREFLIGHT_MAX_ITERS)
+    if unbatched:
+        return int(pred.item())
+    return pred
+
+
+class Sinkhorn(nn.Module):
+    """Module wrapper of :func:`sinkhorn` (reference sinkhorn.py:1863-1906).
+
+    Accepts ``max_iter`` as an alias of ``n_iters``.
+    """
+
+    def __init__(self, reg: float = 1.0, n_iters: Optional[int] = None,
+                 backward_mode: Literal["unrolled", "implicit"] = "implicit",
+                 backward_iters: Optional[int] = None, max_iter: Optional[int] = None):
+        super().__init__()
+        self.reg = reg
+        self.n_iters = _resolve_iters(n_iters, max_iter)
+        self.backward_mode = backward_mode
+        self.backward_iters = backward_iters
+
+    def forward(self, cost_matrix: torch.Tensor) -> SinkhornResult:
+        return sinkhorn(cost_matrix, reg=self.reg, n_iters=self.n_iters,
+                        backward_mode=self.backward_mode, backward_iters=self.backward_iters)
+
+
+class SinkhornFromScores(nn.Module):
+    """Module wrapper of :func:`sinkhorn_from_scores` (reference sinkhorn.py:1909-1954)."""
+
+    def __init__(self, tau: float = 1.0, n_iters: Optional[int] = None,
+                 backward_mode: Literal["unrolled", "implicit"] = "implicit",
+                 backward_iters: Optional[int] = None, max_iter: Optional[int] = None):
+        super().__init__()
+        self.tau = tau
+        self.n_iters = _resolve_iters(n_iters, max_iter)
+        self.backward_mode = backward_mode
+        self.backward_iters = backward_iters
+
+    def forward(self, log_alpha: torch.Tensor) -> torch.Tensor:
+        return sinkhorn_from_scores(log_alpha, tau=self.tau, n_iters=self.n_iters,
+                                    backward_mode=self.backward_mode,
+                                    backward_iters=self.backward_iters)

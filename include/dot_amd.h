@@ -1,0 +1,204 @@
+/*
+ * dot_amd — C ABI of the MI355X (gfx950) Sinkhorn and bidirectional-softmax engine.
+ *
+ * Plain pointers and sizes only.  Every pointer argument is device memory
+ * owned by the caller (fp32 unless stated); the library allocates nothing on
+ * its hot path: scratch comes from the caller's `workspace`, sized by the
+ * matching *_workspace_bytes() query.  All work is enqueued on `stream`
+ * (a hipStream_t); no call synchronises the device.  Functions return
+ * DOT_OK (0) or a DOT_ERR_* code; dot_last_error() gives the message for the
+ * calling thread.
+ *
+ * Layouts: matrices are row-major [B, M, N] (B batch elements, M rows, N
+ * columns); row vectors are [B, M]; column vectors are [B, N].
+ *
+ * The reference implements this path as PyTorch custom ops whose CUDA
+ * implementations call raw-pointer launchers.  Each entry point below replaces
+ * the launchers named in its comment (paths relative to the reference root).
+ */
+#ifndef DOT_AMD_H
+#define DOT_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* dot_stream_t; /* same type as hipStream_t */
+
+enum {
+    DOT_OK = 0,
+    DOT_ERR_INVALID_ARG = 1,  /* bad shape, pointer, size or parameter */
+    DOT_ERR_WORKSPACE = 2,    /* workspace missing or smaller than the query */
+    DOT_ERR_UNSUPPORTED = 3,  /* a shape this build does not handle (see message) */
+    DOT_ERR_HIP = 4           /* a HIP launch or runtime call failed */
+};
+
+/* Flags of dot_sinkhorn_fwd_args.flags */
+#define DOT_SK_RETURN_LOG 0x1    /* write log P instead of P (the reference's return_log) */
+#define DOT_SK_KEEP_HISTORY 0x2  /* write u_t, v_t of every iteration for the unrolled backward */
+
+/* Meaning of `scores` in the Sinkhorn calls. */
+#define DOT_SCORES_LOG_ALPHA 1   /* scores are log_alpha; the log kernel is K = log_alpha / tau */
+#define DOT_SCORES_COST (-1)     /* scores are a cost C; log_alpha = -C (dot/sinkhorn.py:1346) */
+
+/* ---------------------------------------------------------------------- */
+/* Sinkhorn forward                                                        */
+/* ---------------------------------------------------------------------- */
+typedef struct {
+    const float* scores;   /* [B,M,N] log_alpha or cost, per scores_kind */
+    const float* log_a;    /* [B,M] log row marginal, or NULL for -log(M) */
+    const float* log_b;    /* [B,N] log column marginal, or NULL for -log(N) */
+    int B, M, N;
+    int scores_kind;       /* DOT_SCORES_LOG_ALPHA or DOT_SCORES_COST */
+    float tau;             /* > 0 */
+    int max_iter;          /* >= 0 */
+    float tol;             /* > 0: stop after the first iteration with max|u_t - u_{t-1}| < tol
+                              over the whole batch; <= 0: run max_iter iterations */
+    int flags;             /* DOT_SK_* */
+    float* plan;           /* [B,M,N] out: P (or log P); may be NULL */
+    float* cost;           /* [B] out: sum(P * C) with C = -log_alpha; may be NULL */
+    float* u_out;          /* [B,M] out: final row potential; may be NULL */
+    float* v_out;          /* [B,N] out: final column potential; may be NULL */
+    float* u_hist;         /* [max_iter,B,M] out when DOT_SK_KEEP_HISTORY */
+    float* v_hist;         /* [max_iter,B,N] out when DOT_SK_KEEP_HISTORY */
+    int32_t* iters_used;   /* device int32 out: iterations executed */
+    int32_t* converged;    /* device int32 out: 1 if the tol test fired */
+    void* workspace;
+    size_t workspace_bytes;
+} dot_sinkhorn_fwd_args;
+
+/* Dual log-domain Sinkhorn: u_i = log a_i - LSE_j(K_ij + v_j), then
+ * v_j = log b_j - LSE_i(K_ij + u_i), from u = v = 0, with the stopping test
+ * evaluated on the device; P = safe_exp(K + u_i + v_j).
+ * Replaces sinkhorn_dual_init_cuda / sinkhorn_dual_row_update_cuda /
+ * sinkhorn_dual_col_update_cuda / sinkhorn_max_abs_diff_cuda /
+ * sinkhorn_dual_materialize_cuda (src/sinkhorn/kernels.cuh:84-162) as driven by
+ * sinkhorn_dual_vanilla_cuda (src/sinkhorn/torch_cuda.cpp:147-264), the
+ * primal sinkhorn_forward_cuda (kernels.cuh:61) behind the sinkhorn /
+ * sinkhorn_log ops (torch_cuda.cpp:599-715), and
+ * sinkhorn_dual_forward_with_intermediates_cuda (kernels.cuh:164) when
+ * DOT_SK_KEEP_HISTORY is set.  Ops: src/sinkhorn/registry.cpp:31-45. */
+size_t dot_sinkhorn_forward_workspace_bytes(int B, int M, int N, int max_iter, int flags);
+int dot_sinkhorn_forward(const dot_sinkhorn_fwd_args* args, dot_stream_t stream);
+
+/* ---------------------------------------------------------------------- */
+/* Sinkhorn backward                                                       */
+/* ---------------------------------------------------------------------- */
+/* Upstream gradient G of the plan: G = grad_plan + grad_cost[b] * C, either
+ * term optional.  Output when scores_kind == DOT_SCORES_LOG_ALPHA:
+ * grad_scores = dL/dlog_alpha.  When scores_kind == DOT_SCORES_COST:
+ * grad_scores = dL/dC = grad_cost[b] * P - dL/dlog_alpha (the direct term of
+ * cost = sum(P * C) plus the path through the plan). */
+typedef struct {
+    const float* scores;      /* [B,M,N] */
+    int scores_kind;
+    const float* plan;        /* [B,M,N] P of the forward */
+    const float* grad_plan;   /* [B,M,N] or NULL */
+    const float* grad_cost;   /* [B] or NULL */
+    int B, M, N;
+    float tau;
+    int iters;                /* implicit: adjoint sweeps; unrolled: T (history length used) */
+    const float* u_hist;      /* unrolled only: [T,B,M] */
+    const float* v_hist;      /* unrolled only: [T,B,N] */
+    float* grad_scores;       /* [B,M,N] out */
+    float* grad_tau;          /* [B] out (per batch element) */
+    void* workspace;
+    size_t workspace_bytes;
+} dot_sinkhorn_bwd_args;
+
+/* Implicit-function adjoint: exactly `iters` Gauss-Seidel sweeps
+ * lambda_i = (sum_k P G - sum_k P mu_k) / max(sum_k P, 1e-12),
+ * mu_k = (sum_i P G - sum_i P lambda_i) / max(sum_i P, 1e-12),
+ * grad = P (G - lambda_i - mu_k) / tau, grad_tau = -sum(grad * log_alpha) / tau.
+ * Replaces sinkhorn_backward_implicit_cuda (src/sinkhorn/kernels.cuh:325;
+ * kernels.cu:1682-1726) behind sinkhorn_with_grads_implicit
+ * (torch_cuda.cpp:803-871; registry.cpp:56). */
+size_t dot_sinkhorn_backward_implicit_workspace_bytes(int B, int M, int N);
+int dot_sinkhorn_backward_implicit(const dot_sinkhorn_bwd_args* args, dot_stream_t stream);
+
+/* Reverse pass through the T recorded iterations with the reference's formula
+ * (Gamma_Y = Gamma - exp(K+u_t+v_t) colsum(Gamma); Gamma = Gamma_Y -
+ * exp(K+u_t+v_{t-1}) rowsum(Gamma_Y)); grad = Gamma / tau,
+ * grad_tau = -sum(Gamma * log_alpha) / tau^2.
+ * Replaces sinkhorn_backward_unrolled_dual_cuda (src/sinkhorn/kernels.cuh:292;
+ * kernels.cu:1622-1680) behind sinkhorn_with_grads_unrolled
+ * (torch_cuda.cpp:717-801; registry.cpp:52). */
+size_t dot_sinkhorn_backward_unrolled_workspace_bytes(int B, int M, int N);
+int dot_sinkhorn_backward_unrolled(const dot_sinkhorn_bwd_args* args, dot_stream_t stream);
+
+/* ---------------------------------------------------------------------- */
+/* Bidirectional softmax                                                   */
+/* ---------------------------------------------------------------------- */
+typedef struct {
+    const float* sim;         /* [B,L1,L2] */
+    const int32_t* lengths;   /* [B,2] valid (rows, cols) per batch element, device int32 */
+    int B, L1, L2;
+    float tau;
+    float* out;               /* [B,L1,L2] sqrt(1e-9 + r*c) in the valid region, else 0 */
+    float* row_sm;            /* [B,L1,L2] row softmax r, or NULL */
+    float* col_sm;            /* [B,L1,L2] column softmax c, or NULL */
+    float* row_stats;         /* [B,L1,2] (max, sum) of each row, or NULL */
+    float* col_stats;         /* [B,L2,2] (max, sum) of each column, or NULL */
+    void* workspace;
+    size_t workspace_bytes;
+} dot_bidisoftmax_fwd_args;
+
+/* Replaces bidirectional_softmax_forward_cuda
+ * (src/bidirectional_softmax/kernels.cuh:27; kernels.cu:417-448) behind the
+ * bidirectional_softmax op (bidirectional_softmax/torch_cuda.cpp:42-76;
+ * registry.cpp:31).  Runs on `stream` with no device synchronisation. */
+size_t dot_bidisoftmax_forward_workspace_bytes(int B, int L1, int L2);
+int dot_bidisoftmax_forward(const dot_bidisoftmax_fwd_args* args, dot_stream_t stream);
+
+typedef struct {
+    const float* sim;         /* [B,L1,L2] */
+    const int32_t* lengths;   /* [B,2] */
+    int B, L1, L2;
+    float tau;
+    const float* grad_out;    /* [B,L1,L2] */
+    /* Either the forward's buffers (out, row_sm, col_sm all non-NULL) ... */
+    const float* out;
+    const float* row_sm;
+    const float* col_sm;
+    /* ... or its statistics, from which r, c and out are recomputed from sim. */
+    const float* row_stats;   /* [B,L1,2] */
+    const float* col_stats;   /* [B,L2,2] */
+    float* grad_sim;          /* [B,L1,L2] out (0 outside the valid region) */
+    float* grad_tau;          /* [B] out: -sum(grad_sim * sim) / tau over the valid region */
+    void* workspace;
+    size_t workspace_bytes;
+} dot_bidisoftmax_bwd_args;
+
+/* Replaces bidirectional_softmax_backward_cuda
+ * (src/bidirectional_softmax/kernels.cuh:56; kernels.cu:450-501) behind the
+ * bidirectional_softmax_backward op (bidirectional_softmax/torch_cuda.cpp:78-139;
+ * registry.cpp:34). */
+size_t dot_bidisoftmax_backward_workspace_bytes(int B, int L1, int L2);
+int dot_bidisoftmax_backward(const dot_bidisoftmax_bwd_args* args, dot_stream_t stream);
+
+/* ---------------------------------------------------------------------- */
+/* Diagnostics (no counterpart in the reference)                           */
+/* ---------------------------------------------------------------------- */
+/* Message of the calling thread's most recent failure ("" after success). */
+const char* dot_last_error(void);
+/* Library version string. */
+const char* dot_version(void);
+
+/* Kernel-duration profiler: when enabled, every launch is bracketed by two
+ * HIP events on its stream.  dot_profile_collect() waits for the recorded
+ * events and folds them into per-kernel totals; dot_profile_query() reads a
+ * total by kernel name.  For measurement only: it adds event records between
+ * launches. */
+void dot_profile_enable(int on);
+int dot_profile_collect(void);
+int dot_profile_query(const char* kernel, int64_t* launches, double* total_ms);
+void dot_profile_reset(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DOT_AMD_H */

@@ -1,0 +1,225 @@
+"""TEST INFRASTRUCTURE ONLY — numpy restatement of the reference's Sinkhorn hot path.
+
+This is the checker the HIP kernels are compared against.  Only ``tests/``,
+``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` leg may import
+it, and never as a product code path: the ``dot_amd`` package does not import
+anything under ``oracle/``.
+
+Every function follows the reference's GPU semantics unless it says otherwise,
+and computes in float64 by default (``dtype=np.float32`` gives an fp32 run of
+the same algorithm, used to measure the rounding spread of fp32 itself).
+
+Pinning (which independent checks fix each function) is stated per function
+and exercised by ``tests/test_oracle.py``:
+
+* ``dual_forward`` — golden vectors of the reference's compiled
+  ``sinkhorn_forward_cpu`` at matched iteration counts; closed forms (rank-one
+  kernels converge in one iteration to ``a b^T``); exact column marginals
+  after every iteration; row/column shift invariance.  The batch-global
+  ``max|u_t - u_{t-1}| < tol`` stopping rule (GPU only, torch_cuda.cpp:199-238)
+  is restated from the source; it is checked against the reference tests'
+  behavioural property (early stop before ``n_iters`` with the plan within
+  2e-3 of the fixed-count plan, test_sinkhorn.py:827-839) and by a mutation
+  check (a u-and-v criterion or a per-batch criterion gives a different count
+  on a designed input).  The exact crossing iteration is therefore only
+  partially pinned.
+* ``implicit_backward`` — golden vectors of the reference's compiled
+  ``sinkhorn_backward_implicit_cpu`` with ``tol=0`` (which runs exactly the
+  GPU's fixed sweep count); at convergence, a dense float64 solve of the
+  adjoint system / float64 autograd through a converged Sinkhorn; finite
+  differences of ``cost`` in ``reg``.
+* ``unrolled_backward`` — golden vectors of the reference's compiled
+  ``sinkhorn_backward_unrolled_cpu`` (autograd cannot pin it: the reference's
+  formula is not the exact Jacobian; see ``unrolled_backward``).
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Optional
+
+import numpy as np
+
+SAFE_EXP_LO = -88.0
+SAFE_EXP_HI = 88.0
+SUM_FLOOR = 1.0e-12
+
+
+def safe_exp(x: np.ndarray) -> np.ndarray:
+    """``safe_exp`` of src/sinkhorn/kernels.cu:21-25 (and kernels_cpu.cpp:18-22):
+    0 below -88, exp(88) above 88."""
+    with np.errstate(over="ignore", under="ignore"):
+        y = np.exp(np.minimum(x, SAFE_EXP_HI))
+    return np.where(x < SAFE_EXP_LO, np.zeros_like(y), y)
+
+
+def default_log_marginal(batch: int, size: int, dtype) -> np.ndarray:
+    """``-log(size)`` per entry (torch_cuda.cpp:33-43; computed in fp32 there)."""
+    return np.full((batch, size), -np.log(np.float32(size)), dtype=np.float32).astype(dtype)
+
+
+def _lse(x: np.ndarray, axis: int) -> np.ndarray:
+    """Max-shifted log-sum-exp with the reference's guards
+    (kernels.cu:523-538 rows, :649-664 columns): ``max + log(max(sum safe_exp(x - max), 1e-12))``."""
+    mx = x.max(axis=axis, keepdims=True)
+    s = safe_exp(x - mx).sum(axis=axis, keepdims=True)
+    return np.squeeze(mx + np.log(np.maximum(s, SUM_FLOOR)), axis=axis)
+
+
+@dataclass
+class ForwardResult:
+    P: np.ndarray                      # [B, n, m] plan (or log plan when return_log)
+    n_iters_used: int
+    converged: bool
+    u: np.ndarray                      # [B, n] final row potential
+    v: np.ndarray                      # [B, m] final column potential
+    K: np.ndarray                      # [B, n, m] log kernel = log_alpha / tau
+    u_hist: Optional[np.ndarray] = None  # [T, B, n] when history was requested
+    v_hist: Optional[np.ndarray] = None  # [T, B, m]
+    deltas: Optional[np.ndarray] = None  # [T] batch-global max|u_t - u_{t-1}|
+
+
+def dual_forward(log_alpha, tau: float, n_iters: int, tol: float = 0.0,
+                 log_a=None, log_b=None, return_log: bool = False,
+                 keep_history: bool = False, dtype=np.float64) -> ForwardResult:
+    """Dual log-domain Sinkhorn, the reference's default GPU forward.
+
+    Follows ``sinkhorn_dual_vanilla_cuda`` (src/sinkhorn/torch_cuda.cpp:147-264):
+    K = log_alpha * (1/tau) (kernels.cu:1104-1137); u = v = 0; each iteration
+    updates all rows (u_i = log a_i - LSE_j(K_ij + v_j), kernels.cu:503-545),
+    then all columns from the new u (v_j = log b_j - LSE_i(K_ij + u_i),
+    kernels.cu:629-671); when tol > 0 it stops after the first iteration whose
+    batch-global ``max|u - u_prev|`` (u only, kernels.cu:825-842) is below tol.
+    The plan is ``safe_exp(K + u_i + v_j)`` (kernels.cu:755-775).
+    """
+    la = np.asarray(log_alpha, dtype=np.float32)
+    B, n, m = la.shape
+    inv_tau = np.float32(1.0) / np.float32(tau)
+    K = (la * inv_tau).astype(dtype)
+    lga = default_log_marginal(B, n, dtype) if log_a is None else np.asarray(log_a, np.float32).astype(dtype)
+    lgb = default_log_marginal(B, m, dtype) if log_b is None else np.asarray(log_b, np.float32).astype(dtype)
+    u = np.zeros((B, n), dtype)
+    v = np.zeros((B, m), dtype)
+    u_hist, v_hist, deltas = [], [], []
+    used, converged = 0, False
+    for it in range(n_iters):
+        u_prev = u
+        u = lga - _lse(K + v[:, None, :], axis=2)
+        v = lgb - _lse(K + u[:, :, None], axis=1)
+        used = it + 1
+        if keep_history:
+            u_hist.append(u.copy())
+            v_hist.append(v.copy())
+        d = float(np.abs(u - u_prev).max()) if u.size else 0.0
+        deltas.append(d)
+        if tol > 0.0 and d < tol:
+            converged = True
+            break
+    logP = K + u[:, :, None] + v[:, None, :]
+    P = logP if return_log else safe_exp(logP)
+    return ForwardResult(
+        P=P, n_iters_used=used, converged=converged, u=u, v=v, K=K,
+        u_hist=np.stack(u_hist) if keep_history and u_hist else None,
+        v_hist=np.stack(v_hist) if keep_history and v_hist else None,
+        deltas=np.asarray(deltas),
+    )
+
+
+def transport_cost(P, cost) -> np.ndarray:
+    """``(P * C).sum((-2, -1))`` of dot/sinkhorn.py:1703."""
+    return (np.asarray(P) * np.asarray(cost)).sum(axis=(-2, -1))
+
+
+def implicit_backward(log_alpha, P, grad_P, tau: float, iters: int,
+                      tol: Optional[float] = None, dtype=np.float64):
+    """Implicit-function adjoint (Gauss-Seidel on lambda then mu, from zero).
+
+    GPU semantics (``tol=None``): exactly ``iters`` sweeps, no early exit
+    (src/sinkhorn/kernels.cu:1682-1726 with the lambda/mu kernels :965-1047).
+    CPU semantics (``tol`` given): per batch element, stop after the first
+    sweep whose max change over lambda and mu is below tol
+    (kernels_cpu.cpp:276-312; the CPU op passes 1e-6, torch_cpu.cpp:324).
+
+    lambda_i = (sum_k P_ik G_ik - sum_k P_ik mu_k) / max(sum_k P_ik, 1e-12)
+    mu_k     = (sum_i P_ik G_ik - sum_i P_ik lambda_i) / max(sum_i P_ik, 1e-12)
+    grad     = P (G - lambda_i - mu_k) / tau        (kernels.cu:1049-1071)
+    grad_tau = -sum(grad * log_alpha) / tau          (kernels.cu:1073-1098)
+
+    Returns ``(grad_log_alpha [B,n,m], grad_tau [B], sweeps_run [B])``.
+    """
+    la = np.asarray(log_alpha, np.float32).astype(dtype)
+    P = np.asarray(P).astype(dtype)
+    G = np.asarray(grad_P).astype(dtype)
+    B, n, m = P.shape
+    r = (P * G).sum(axis=2)
+    rs = np.maximum(P.sum(axis=2), SUM_FLOOR)
+    c = (P * G).sum(axis=1)
+    cs = np.maximum(P.sum(axis=1), SUM_FLOOR)
+    lam = np.zeros((B, n), dtype)
+    mu = np.zeros((B, m), dtype)
+    sweeps = np.zeros(B, dtype=np.int64)
+    active = np.ones(B, dtype=bool)
+    for _ in range(iters):
+        if not active.any():
+            break
+        lam_new = (r - np.einsum("bik,bk->bi", P, mu)) / rs
+        mu_new = (c - np.einsum("bik,bi->bk", P, lam_new)) / cs
+        change = np.maximum(np.abs(lam_new - lam).max(axis=1, initial=0.0),
+                            np.abs(mu_new - mu).max(axis=1, initial=0.0))
+        lam = np.where(active[:, None], lam_new, lam)
+        mu = np.where(active[:, None], mu_new, mu)
+        sweeps += active
+        if tol is not None:
+            active &= ~(change < tol)
+    grad = P * (G - lam[:, :, None] - mu[:, None, :]) / dtype(tau)
+    grad_tau = -(grad * la).sum(axis=(1, 2)) / dtype(tau)
+    return grad, grad_tau, sweeps
+
+
+def unrolled_backward(log_alpha, P, grad_P, K, u_hist, v_hist, tau: float, dtype=np.float64):
+    """Reverse pass through T iterations, as the reference computes it.
+
+    Follows ``sinkhorn_backward_unrolled_dual_cuda`` (src/sinkhorn/kernels.cu:1622-1680)
+    and its CPU twin ``sinkhorn_backward_unrolled_cpu`` (kernels_cpu.cpp:169-245):
+    Gamma = grad_P * P; for t = T-1 .. 0, with X = K + u_t + v_t and
+    Y = K + u_t + v_{t-1} (v_{-1} = 0):
+        Gamma_Y = Gamma   - safe_exp(X) * colsum(Gamma)      (kernels.cu:856-889)
+        Gamma   = Gamma_Y - safe_exp(Y) * rowsum(Gamma_Y)    (kernels.cu:891-924)
+    grad = Gamma / tau; grad_tau = -sum(Gamma * log_alpha) / tau^2.
+
+    This is NOT the exact Jacobian of the forward: the true softmax factors
+    would be exp(X - log b) and exp(Y - log a).  The reference's formula is
+    reproduced literally because parity is with the reference.
+    """
+    la = np.asarray(log_alpha, np.float32).astype(dtype)
+    K = np.asarray(K).astype(dtype)
+    G = (np.asarray(grad_P).astype(dtype) * np.asarray(P).astype(dtype))
+    T = 0 if u_hist is None else len(u_hist)
+    for t in range(T - 1, -1, -1):
+        u_t = u_hist[t].astype(dtype)
+        v_t = v_hist[t].astype(dtype)
+        v_p = v_hist[t - 1].astype(dtype) if t > 0 else np.zeros_like(v_t)
+        q = safe_exp(K + u_t[:, :, None] + v_t[:, None, :])
+        G = G - q * G.sum(axis=1, keepdims=True)
+        p = safe_exp(K + u_t[:, :, None] + v_p[:, None, :])
+        G = G - p * G.sum(axis=2, keepdims=True)
+    grad = G / dtype(tau)
+    grad_tau = -(G * la).sum(axis=(1, 2)) / (dtype(tau) * dtype(tau))
+    return grad, grad_tau
+
+
+def with_grads_implicit(log_alpha, grad_P, tau, n_iters, backward_iters,
+                        log_a=None, log_b=None, dtype=np.float64):
+    """The GPU op ``sinkhorn_with_grads_implicit`` (torch_cuda.cpp:803-871):
+    forward with tol=0 for ``n_iters``, then exactly ``backward_iters`` adjoint sweeps."""
+    fwd = dual_forward(log_alpha, tau, n_iters, 0.0, log_a, log_b, dtype=dtype)
+    grad, grad_tau, _ = implicit_backward(log_alpha, fwd.P, grad_P, tau, backward_iters, None, dtype)
+    return fwd.P, grad, grad_tau
+
+
+def with_grads_unrolled(log_alpha, grad_P, tau, n_iters, log_a=None, log_b=None, dtype=np.float64):
+    """The GPU op ``sinkhorn_with_grads_unrolled`` (torch_cuda.cpp:717-801)."""
+    fwd = dual_forward(log_alpha, tau, n_iters, 0.0, log_a, log_b, keep_history=True, dtype=dtype)
+    grad, grad_tau = unrolled_backward(log_alpha, fwd.P, grad_P, fwd.K, fwd.u_hist, fwd.v_hist,
+                                       tau, dtype)
+    return fwd.P, grad, grad_tau
