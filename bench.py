@@ -1,0 +1,385 @@
+#!/usr/bin/env python3
+"""Benchmark of the dot_amd hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c3|c1|c4|c5]
+
+One "step" is one pass of the hot path over one batch of synthetic input, as
+the reference's users run it: ``result = dot.sinkhorn(C, reg, n_iters)``
+followed by ``result.cost.sum().backward()``.  The default workload is config
+C3 of BASELINE.json (B=64, M=N=512 fp32, squared Euclidean costs between
+seeded 64-d Gaussian clouds normalised to max 1, uniform marginals, reg=0.1,
+n_iters=200, tol=1e-6): the configuration the Sinkhorn headline metric is
+quoted on.  Inputs are generated on the CPU from fixed seeds and are resident
+in HBM before the timed region starts.
+
+Printed: one JSON line.  ``value`` is Sinkhorn element-iterations per second,
+E * (T_f + T_b) per step with E = B*M*N, T_f = forward iterations executed
+and T_b = adjoint sweeps executed.  The same line carries
+
+* ``roofline`` — the dominant kernel's algorithmic bytes per launch (one fp32
+  read of the [B,M,N] matrix per sweep) over its average duration, measured
+  with HIP events on the launch stream during the timed steps;
+* ``cpu_baseline`` — the reference's own CPU kernels (oracle/_ref, compiled
+  from the reference sources) timed on a bounded sample of the same input on
+  one host core, or the numpy oracle when oracle/_ref is absent;
+* ``bidirectional_softmax`` — config C2 (B=32, 1024x1024, fwd+bwd) in GB/s of
+  algorithmic traffic (20 bytes per element), with its own roofline.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import sys
+import time
+
+HBM_PEAK_GBPS = 8000.0  # MI355X HBM3E, 8 TB/s
+ROOT = os.path.dirname(os.path.abspath(__file__))
+
+WORKLOADS = {
+    "c1": dict(B=8, M=64, N=64, reg=1.0, n_iters=100, tol=1e-6, seed=0),
+    "c3": dict(B=64, M=512, N=512, reg=0.1, n_iters=200, tol=1e-6, seed=3),
+    "c4": dict(B=16, M=1024, N=2048, reg=0.05, n_iters=500, tol=1e-6, seed=4),
+    "c5": dict(B=4, M=4096, N=4096, reg=0.02, n_iters=1000, tol=1e-6, seed=5),
+}
+
+
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def make_inputs(name: str, torch, device):
+    """Seeded inputs of BASELINE.md section 3; returns (C, a, b) with a, b None for uniform."""
+    cfg = WORKLOADS[name]
+    g = torch.Generator().manual_seed(cfg["seed"])
+    B, M, N = cfg["B"], cfg["M"], cfg["N"]
+    a = b = None
+    if name == "c1":
+        C = torch.rand(B, M, N, generator=g)
+    elif name == "c3":
+        x = torch.randn(B, M, 64, generator=g)
+        y = torch.randn(B, N, 64, generator=g)
+        C = torch.cdist(x.to(device), y.to(device)).square()
+        C = C / C.amax(dim=(-2, -1), keepdim=True)
+    elif name == "c4":
+        C = torch.rand(B, M, N, generator=g)
+        ea = -torch.log(torch.rand(B, M, generator=g))
+        eb = -torch.log(torch.rand(B, N, generator=g))
+        a = ea / ea.sum(-1, keepdim=True)
+        b = eb / eb.sum(-1, keepdim=True)
+    elif name == "c5":
+        x = torch.randn(B, M, 128, generator=g)
+        y = torch.randn(B, N, 128, generator=g)
+        C = torch.cdist(x.to(device), y.to(device))
+        C = C / C.amax(dim=(-2, -1), keepdim=True)
+    else:
+        raise ValueError(name)
+    C = C.to(device=device, dtype=torch.float32).contiguous()
+    if a is not None:
+        a, b = a.to(device), b.to(device)
+    return C, a, b
+
+
+def kernel_stats(profiler, names):
+    out = {}
+    for n in names:
+        launches, ms = profiler.query(n)
+        if launches:
+            out[n] = {"launches": launches, "total_ms": ms, "avg_us": 1000.0 * ms / launches}
+    return out
+
+
+# ---------------------------------------------------------------------------
+# CPU baselines (bounded samples)
+# ---------------------------------------------------------------------------
+def sinkhorn_cpu_baseline(C_cpu, reg, a, b, target_s):
+    """Reference CPU path, as torch_cpu.cpp runs it: forward T, then backward =
+    recomputed forward T + adjoint T (here with tol 0 so the adjoint runs all T
+    sweeps).  Timed on a growing number of batch elements until ~target_s."""
+    import numpy as np
+
+    sys.path.insert(0, ROOT)
+    from oracle import ref
+
+    kind = "reference" if ref.available() else "port"
+    T = 20
+    la = (-C_cpu).numpy()
+    lga = None if a is None else np.log(a.cpu().numpy())
+    lgb = None if b is None else np.log(b.cpu().numpy())
+    Bt, M, N = la.shape
+
+    def run(nb):
+        sl = slice(0, nb)
+        x = la[sl]
+        A = None if lga is None else lga[sl]
+        Bm = None if lgb is None else lgb[sl]
+        t0 = time.perf_counter()
+        if kind == "reference":
+            P = ref.sinkhorn_forward(x, reg, T, A, Bm)
+            P2 = ref.sinkhorn_forward(x, reg, T, A, Bm)
+            ref.sinkhorn_backward_implicit(x, P2, -x, reg, T, 0.0)
+        else:
+            from oracle import sinkhorn as osk
+
+            f = osk.dual_forward(x, reg, T, 0.0, A, Bm, dtype=np.float32)
+            f2 = osk.dual_forward(x, reg, T, 0.0, A, Bm, dtype=np.float32)
+            osk.implicit_backward(x, f2.P, -x, reg, T, None, dtype=np.float32)
+        return time.perf_counter() - t0
+
+    t1 = run(1)
+    nb = max(1, min(Bt, int(target_s / max(t1, 1e-6))))
+    t = run(nb) if nb > 1 else t1
+    elem_iters = nb * M * N * (T + T)  # the metric counts forward + adjoint, not the recompute
+    return {
+        "value": elem_iters / t,
+        "unit": "elem-iters/s",
+        "cores": 1,
+        "kind": kind,
+        "sample": f"{nb} of {Bt} batch elements of this workload ({M}x{N}), {T} forward + "
+                  f"{T} recomputed forward + {T} adjoint iterations, single-threaded "
+                  f"({t:.1f} s on {_cpu_model()}, host has {os.cpu_count()} logical CPUs)",
+    }
+
+
+def bidi_cpu_baseline(sim_cpu, G_cpu, lengths_np, tau, target_s):
+    import numpy as np
+
+    sys.path.insert(0, ROOT)
+    from oracle import ref
+
+    kind = "reference" if ref.available() else "port"
+    s = sim_cpu.numpy()
+    g = G_cpu.numpy()
+    B, L1, L2 = s.shape
+
+    def run(nb):
+        t0 = time.perf_counter()
+        if kind == "reference":
+            out, r, c = ref.bidirectional_softmax(s[:nb], tau, lengths_np[:nb])
+            ref.bidirectional_softmax_backward(s[:nb], out, g[:nb], r, c, tau, lengths_np[:nb])
+        else:
+            from oracle import bidirectional_softmax as obs
+
+            out, r, c = obs.forward(s[:nb], tau, lengths_np[:nb], dtype=np.float32)
+            obs.backward(s[:nb], out, g[:nb], r, c, tau, lengths_np[:nb], dtype=np.float32)
+        return time.perf_counter() - t0
+
+    t1 = run(1)
+    nb = max(1, min(B, int(target_s / max(t1, 1e-6))))
+    t = run(nb) if nb > 1 else t1
+    return {
+        "value": 20.0 * nb * L1 * L2 / t / 1e9,
+        "unit": "GB/s",
+        "cores": 1,
+        "kind": kind,
+        "sample": f"{nb} of {B} batch elements ({L1}x{L2}) forward + backward, single-threaded "
+                  f"({t:.1f} s on {_cpu_model()})",
+    }
+
+
+# ---------------------------------------------------------------------------
+def bench_sinkhorn(args, torch, dot_amd, profiler):
+    cfg = WORKLOADS[args.workload]
+    dev = torch.device("cuda", 0)
+    C, a, b = make_inputs(args.workload, torch, dev)
+    B, M, N = C.shape
+    E = B * M * N
+    reg, n_iters, tol = cfg["reg"], cfg["n_iters"], cfg["tol"]
+
+    def step():
+        leaf = C.detach().requires_grad_(True)
+        res = dot_amd.sinkhorn(leaf, reg=reg, n_iters=n_iters, tol=tol, a=a, b=b)
+        res.cost.sum().backward()
+        return res.n_iters_used
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    sweeps = ["sk_fwd_sweep", "sk_imp_sweep"]
+    profiler.reset()
+    profiler.enable(True, kernels=sweeps)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    used = []
+    for _ in range(args.steps):
+        used.append(step())
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    profiler.enable(False)
+    profiler.collect()
+    stats = kernel_stats(profiler, sweeps)
+
+    T_f = sum(used) / len(used)
+    T_b = n_iters  # backward_iters defaults to n_iters; the adjoint runs exactly that many sweeps
+    sec_per_step = (t1 - t0) / args.steps
+    value = E * (T_f + T_b) / sec_per_step
+
+    dominant = max(stats, key=lambda k: stats[k]["total_ms"]) if stats else None
+    roofline = None
+    if dominant:
+        bytes_per_launch = 4.0 * E
+        achieved = bytes_per_launch / (stats[dominant]["avg_us"] * 1e-6) / 1e9
+        roofline = {"bound": "hbm", "kernel": dominant, "achieved": round(achieved, 1),
+                    "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
+                    "traffic": _pmc_traffic(dominant, args.workload),
+                    "bytes_per_launch": bytes_per_launch}
+    algo_bytes = 4.0 * E * (T_f + T_b) + 20.0 * E
+    return {
+        "value": value,
+        "ms_per_step": 1000.0 * sec_per_step,
+        "E": E,
+        "T_f": T_f,
+        "T_b": T_b,
+        "config": {"workload": f"{args.workload}: sinkhorn fwd+bwd B={B} M={M} N={N} reg={reg} "
+                               f"n_iters={n_iters} tol={tol}",
+                   "B": B, "M": M, "N": N, "reg": reg, "n_iters": n_iters, "tol": tol,
+                   "n_iters_used": used[-1], "backward_iters": T_b},
+        "algorithmic_GBps": algo_bytes / sec_per_step / 1e9,
+        "kernels": stats,
+        "roofline": roofline,
+        "C_cpu": C.cpu(), "a": a, "b": b, "reg": reg,
+    }
+
+
+def bench_bidi(args, torch, dot_amd, profiler):
+    dev = torch.device("cuda", 0)
+    B, L1, L2 = 32, 1024, 1024
+    sim = torch.randn(B, L1, L2, generator=torch.Generator().manual_seed(1))
+    G = torch.randn(B, L1, L2, generator=torch.Generator().manual_seed(2))
+    sim_d, G_d = sim.to(dev), G.to(dev)
+    lengths = torch.tensor([[L1, L2]] * B, dtype=torch.int32, device=dev)
+
+    def step():
+        leaf = sim_d.detach().requires_grad_(True)
+        P = dot_amd.bidirectional_softmax(leaf, 1.0, lengths)
+        P.backward(G_d)
+
+    for _ in range(args.warmup):
+        step()
+    names = ["bidi_fwd_stats", "bidi_fwd_write", "bidi_bwd_dots", "bidi_bwd_write"]
+    profiler.reset()
+    profiler.enable(True, kernels=names)
+    torch.cuda.synchronize()
+    steps = max(args.steps, 10)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    profiler.enable(False)
+    profiler.collect()
+    stats = kernel_stats(profiler, names)
+    E = B * L1 * L2
+    sec = (t1 - t0) / steps
+    # algorithmic bytes per launch of each kernel (reads + writes of [B,L1,L2] fp32 arrays)
+    kernel_bytes = {"bidi_fwd_stats": 4.0 * E, "bidi_fwd_write": 8.0 * E,
+                    "bidi_bwd_dots": 8.0 * E, "bidi_bwd_write": 12.0 * E}
+    dominant = max(stats, key=lambda k: stats[k]["total_ms"]) if stats else None
+    roofline = None
+    if dominant:
+        achieved = kernel_bytes[dominant] / (stats[dominant]["avg_us"] * 1e-6) / 1e9
+        roofline = {"bound": "hbm", "kernel": dominant, "achieved": round(achieved, 1),
+                    "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
+                    "traffic": _pmc_traffic(dominant, "c2"), "bytes_per_launch": kernel_bytes[dominant]}
+    return {
+        "metric": "bidirectional softmax fwd+bwd algorithmic GB/s (20 B/elem)",
+        "value": 20.0 * E / sec / 1e9,
+        "unit": "GB/s",
+        "ms_per_step": 1000.0 * sec,
+        "frac_of_hbm_peak": 20.0 * E / sec / 1e9 / HBM_PEAK_GBPS,
+        "config": {"workload": "c2: bidirectional_softmax fwd+bwd B=32 L1=L2=1024 tau=1.0"},
+        "kernels": stats,
+        "roofline": roofline,
+        "_cpu": (sim, G, lengths.cpu().numpy()),
+    }
+
+
+def _pmc_traffic(kernel, workload):
+    """HBM bytes per dispatch from committed rocprofv3 --pmc summaries, if present."""
+    path = os.path.join(ROOT, "profiles", "pmc_traffic.json")
+    try:
+        with open(path) as f:
+            table = json.load(f)
+        return table.get(workload, {}).get(kernel)
+    except (OSError, ValueError):
+        return None
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--workload", default="c3", choices=sorted(WORKLOADS))
+    ap.add_argument("--no-bidi", action="store_true", help="skip the bidirectional-softmax leg")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0,
+                    help="approximate CPU time of each CPU-baseline sample")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported by this build "
+              "(the batch shards across GPUs with no communication; see DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a HIP device", file=sys.stderr)
+        sys.exit(1)
+    sys.path.insert(0, ROOT)
+    import dot_amd
+    from dot_amd import profiler
+
+    sk = bench_sinkhorn(args, torch, dot_amd, profiler)
+    bidi = None if args.no_bidi else bench_bidi(args, torch, dot_amd, profiler)
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = sinkhorn_cpu_baseline(sk["C_cpu"], sk["reg"], sk["a"], sk["b"], args.cpu_seconds)
+        if bidi is not None:
+            sim, G, ln = bidi["_cpu"]
+            bidi["cpu_baseline"] = bidi_cpu_baseline(sim, G, ln, 1.0, args.cpu_seconds)
+            bidi["speedup_vs_cpu"] = bidi["value"] / bidi["cpu_baseline"]["value"]
+
+    line = {
+        "metric": "Sinkhorn fwd+bwd elem-iters/s and % HBM peak; bidir-softmax GB/s, 1 GPU",
+        "value": sk["value"],
+        "unit": "elem-iters/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": sk["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic (seeded inputs per BASELINE.md section 3)",
+        "config": sk["config"],
+        "n_iters_used": sk["T_f"],
+        "backward_iters": sk["T_b"],
+        "algorithmic_GBps": sk["algorithmic_GBps"],
+        "frac_of_hbm_peak": sk["algorithmic_GBps"] / HBM_PEAK_GBPS,
+        "roofline": sk["roofline"],
+        "kernels": sk["kernels"],
+        "cpu_baseline": cpu,
+        "speedup_vs_cpu": (sk["value"] / cpu["value"]) if cpu else None,
+    }
+    if bidi is not None:
+        bidi.pop("_cpu", None)
+        line["bidirectional_softmax"] = bidi
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -27,6 +27,7 @@ struct Total {
 struct Profiler {
     std::mutex mu;
     bool enabled = false;
+    std::string select;  // ",name1,name2," or empty for every kernel
     std::vector<Pending> pending;
     std::vector<hipEvent_t> pool;
     std::map<std::string, Total> totals;
@@ -56,10 +57,12 @@ int check_launch(const char* what) {
     return ok();
 }
 
-bool profiling_enabled() {
+bool profiling_enabled(const char* name) {
     Profiler& p = profiler();
     std::lock_guard<std::mutex> lock(p.mu);
-    return p.enabled;
+    if (!p.enabled) return false;
+    if (p.select.empty()) return true;
+    return p.select.find("," + std::string(name) + ",") != std::string::npos;
 }
 
 hipEvent_t profile_event() {
@@ -95,6 +98,12 @@ extern "C" void dot_profile_enable(int on) {
     Profiler& p = profiler();
     std::lock_guard<std::mutex> lock(p.mu);
     p.enabled = on != 0;
+}
+
+extern "C" void dot_profile_select(const char* names) {
+    Profiler& p = profiler();
+    std::lock_guard<std::mutex> lock(p.mu);
+    p.select = (names && *names) ? "," + std::string(names) + "," : std::string();
 }
 
 extern "C" int dot_profile_collect(void) {

@@ -41,14 +41,14 @@ class Carver {
 // Event profiler.  When enabled, `ProfScope` brackets a launch with two events
 // on the launch stream; dot_profile_collect() folds finished pairs into
 // per-kernel totals.
-bool profiling_enabled();
+bool profiling_enabled(const char* name);
 void profile_push(const char* name, hipEvent_t start, hipEvent_t stop);
 hipEvent_t profile_event();
 
 class ProfScope {
   public:
     ProfScope(const char* name, hipStream_t stream) : name_(name), stream_(stream) {
-        if (profiling_enabled()) {
+        if (profiling_enabled(name)) {
             start_ = profile_event();
             stop_ = profile_event();
             (void)hipEventRecord(start_, stream_);

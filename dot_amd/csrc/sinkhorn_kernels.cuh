@@ -336,6 +336,7 @@ __global__ __launch_bounds__(kBlock) void imp_prep(ImpArgs a) {
         if (lane == 0) {
             a.r[bM + i] = rr;
             a.rs[bM + i] = rrs;
+            a.lam[bM + i] = 0.0f;  // lambda = mu = 0 before the first sweep (kernels.cu:1712-1713)
         }
     }
     block_column_combine<VEC, CH>(accA, lds, a.N);

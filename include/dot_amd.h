@@ -140,8 +140,8 @@ typedef struct {
     float* out;               /* [B,L1,L2] sqrt(1e-9 + r*c) in the valid region, else 0 */
     float* row_sm;            /* [B,L1,L2] row softmax r, or NULL */
     float* col_sm;            /* [B,L1,L2] column softmax c, or NULL */
-    float* row_stats;         /* [B,L1,2] (max, sum) of each row, or NULL */
-    float* col_stats;         /* [B,L2,2] (max, sum) of each column, or NULL */
+    float* row_stats;         /* [B,2,L1] row max plane then row sum plane, or NULL */
+    float* col_stats;         /* [B,2,L2] column max plane then column sum plane, or NULL */
     void* workspace;
     size_t workspace_bytes;
 } dot_bidisoftmax_fwd_args;
@@ -164,8 +164,8 @@ typedef struct {
     const float* row_sm;
     const float* col_sm;
     /* ... or its statistics, from which r, c and out are recomputed from sim. */
-    const float* row_stats;   /* [B,L1,2] */
-    const float* col_stats;   /* [B,L2,2] */
+    const float* row_stats;   /* [B,2,L1] as written by the forward */
+    const float* col_stats;   /* [B,2,L2] */
     float* grad_sim;          /* [B,L1,L2] out (0 outside the valid region) */
     float* grad_tau;          /* [B] out: -sum(grad_sim * sim) / tau over the valid region */
     void* workspace;
@@ -193,6 +193,9 @@ const char* dot_version(void);
  * total by kernel name.  For measurement only: it adds event records between
  * launches. */
 void dot_profile_enable(int on);
+/* Restrict the profiler to a comma-separated list of kernel names (NULL or
+ * "" selects every kernel). */
+void dot_profile_select(const char* names);
 int dot_profile_collect(void);
 int dot_profile_query(const char* kernel, int64_t* launches, double* total_ms);
 void dot_profile_reset(void);

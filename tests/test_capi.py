@@ -1,0 +1,102 @@
+"""CPU: the C ABI library loads, exports every declared symbol, and rejects bad
+arguments on the host before touching a device.  No compute call is made."""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from conftest import ROOT
+
+HEADER = os.path.join(ROOT, "include", "dot_amd.h")
+LIB = os.path.join(ROOT, "dot_amd", "libdot_amd.so")
+
+DOT_OK, DOT_ERR_INVALID_ARG, DOT_ERR_WORKSPACE, DOT_ERR_UNSUPPORTED = 0, 1, 2, 3
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    names = re.findall(r"^\s*(?:const\s+)?[A-Za-z_][A-Za-z0-9_]*\s*\*?\s*(dot_[a-z0-9_]+)\s*\(", text, re.M)
+    return sorted(set(names))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    assert os.path.exists(LIB), "libdot_amd.so is not built (python -m dot_amd._build)"
+    return ctypes.CDLL(LIB)
+
+
+class FwdArgs(ctypes.Structure):
+    _fields_ = [("scores", ctypes.c_void_p), ("log_a", ctypes.c_void_p), ("log_b", ctypes.c_void_p),
+                ("B", ctypes.c_int), ("M", ctypes.c_int), ("N", ctypes.c_int),
+                ("scores_kind", ctypes.c_int), ("tau", ctypes.c_float), ("max_iter", ctypes.c_int),
+                ("tol", ctypes.c_float), ("flags", ctypes.c_int),
+                ("plan", ctypes.c_void_p), ("cost", ctypes.c_void_p), ("u_out", ctypes.c_void_p),
+                ("v_out", ctypes.c_void_p), ("u_hist", ctypes.c_void_p), ("v_hist", ctypes.c_void_p),
+                ("iters_used", ctypes.c_void_p), ("converged", ctypes.c_void_p),
+                ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t)]
+
+
+def test_header_declares_the_expected_entry_points():
+    names = declared_functions()
+    for required in ("dot_sinkhorn_forward", "dot_sinkhorn_backward_implicit",
+                     "dot_sinkhorn_backward_unrolled", "dot_bidisoftmax_forward",
+                     "dot_bidisoftmax_backward", "dot_last_error"):
+        assert required in names
+
+
+def test_every_declared_symbol_is_exported(lib):
+    missing = [n for n in declared_functions() if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_workspace_queries_are_pure_host(lib):
+    for fn, args in (("dot_sinkhorn_forward_workspace_bytes", (64, 512, 512, 200, 0)),
+                     ("dot_sinkhorn_backward_implicit_workspace_bytes", (64, 512, 512)),
+                     ("dot_sinkhorn_backward_unrolled_workspace_bytes", (64, 512, 512)),
+                     ("dot_bidisoftmax_forward_workspace_bytes", (32, 1024, 1024)),
+                     ("dot_bidisoftmax_backward_workspace_bytes", (32, 1024, 1024))):
+        f = getattr(lib, fn)
+        f.restype = ctypes.c_size_t
+        assert f(*args) > 0
+        assert f(*((-1,) + args[1:])) == 0
+    f = lib.dot_sinkhorn_backward_unrolled_workspace_bytes
+    f.restype = ctypes.c_size_t
+    assert f(4, 64, 64) >= 4 * 64 * 64 * 4  # holds the Gamma matrix
+
+
+def _last_error(lib):
+    lib.dot_last_error.restype = ctypes.c_char_p
+    return lib.dot_last_error().decode()
+
+
+def test_forward_rejects_bad_arguments_on_the_host(lib):
+    lib.dot_sinkhorn_forward.argtypes = [ctypes.POINTER(FwdArgs), ctypes.c_void_p]
+    assert lib.dot_sinkhorn_forward(None, None) == DOT_ERR_INVALID_ARG
+    assert "NULL" in _last_error(lib)
+    a = FwdArgs(B=2, M=8, N=8, scores_kind=1, tau=0.0, max_iter=10)
+    assert lib.dot_sinkhorn_forward(ctypes.byref(a), None) == DOT_ERR_INVALID_ARG
+    assert "tau" in _last_error(lib)
+    a.tau = 1.0
+    a.scores_kind = 7
+    assert lib.dot_sinkhorn_forward(ctypes.byref(a), None) == DOT_ERR_INVALID_ARG
+    a.scores_kind = 1
+    a.N = 8192
+    assert lib.dot_sinkhorn_forward(ctypes.byref(a), None) == DOT_ERR_UNSUPPORTED
+    assert "4096" in _last_error(lib)
+    a.N = 8
+    a.max_iter = -1
+    assert lib.dot_sinkhorn_forward(ctypes.byref(a), None) == DOT_ERR_INVALID_ARG
+    a.max_iter = 10
+    dummy = ctypes.c_int(0)
+    a.iters_used = a.converged = ctypes.addressof(dummy)
+    a.scores = ctypes.addressof(dummy)
+    a.workspace, a.workspace_bytes = ctypes.addressof(dummy), 4
+    assert lib.dot_sinkhorn_forward(ctypes.byref(a), None) == DOT_ERR_WORKSPACE
+
+
+def test_version_string(lib):
+    lib.dot_version.restype = ctypes.c_char_p
+    assert lib.dot_version().decode().startswith("dot_amd")

@@ -1,0 +1,500 @@
+"""GPU parity of the Sinkhorn path: HIP kernels against the oracle and the golden fixtures.
+
+Tolerances (norm-wise relative, max|a - e| / max|e|): plan and cost 1e-5,
+gradients 1e-4.  grad_tau, a sum with heavy
+cancellation, is judged against the magnitude of its terms (conftest.sum_err).
+Comparisons of early-stopped runs use the oracle at the HIP run's own
+n_iters_used with tol = 0: fp32 and float64 can cross the tolerance one
+iteration apart.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import dot_amd
+from dot_amd import _ops
+from conftest import load_golden, rel_err, sum_err
+from oracle import sinkhorn as osk
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda", 0)
+FWD_TOL, GRAD_TOL = 1e-5, 1e-4
+
+
+def _t(x):
+    return torch.as_tensor(np.ascontiguousarray(x)).to(DEV)
+
+
+def _dirichlet(rng, B, n):
+    e = -np.log(rng.random((B, n)))
+    return (e / e.sum(1, keepdims=True)).astype(np.float32)
+
+
+def test_native_library_is_loaded():
+    maps = open("/proc/self/maps").read()
+    assert "libdot_amd.so" in maps and "_C.so" in maps
+    assert _ops._extension_loaded
+
+
+# ---------------------------------------------------------------------------
+# Golden fixtures of the reference through the drop-in torch.ops.dot operators
+# ---------------------------------------------------------------------------
+def test_ops_forward_golden_6x9():
+    g = load_golden("sk_fwd_6x9")
+    la, lga, lgb = _t(g["log_alpha"]), _t(g["log_a"]), _t(g["log_b"])
+    tau, T = float(g["tau"]), int(g["n_iters"])
+    P, used, conv = _ops.sinkhorn_dual_forward(la, tau, T, 0.0, lga, lgb)
+    assert used.device.type == "cpu" and int(used) == T and int(conv) == 0
+    assert rel_err(P, g["P"]) < FWD_TOL
+    logP, _, _ = _ops.sinkhorn_dual_forward(la, tau, T, 0.0, lga, lgb, True)
+    assert (logP.cpu().numpy() - g["logP"]).__abs__().max() < 1e-4
+    assert rel_err(_ops.sinkhorn(la, tau, T, lga, lgb), g["P"]) < FWD_TOL
+    assert (_ops.sinkhorn_log(la, tau, T, lga, lgb).cpu().numpy() - g["logP"]).__abs__().max() < 1e-4
+
+
+def test_ops_c1_golden_forward_and_implicit():
+    g = load_golden("sk_c1")
+    C = g["cost"]
+    P, grad, gtau = _ops.sinkhorn_with_grads_implicit(_t(-C), _t(C), float(g["tau"]),
+                                                      int(g["n_iters"]), int(g["backward_iters"]))
+    assert rel_err(P, g["P"]) < FWD_TOL
+    assert rel_err(grad, g["grad_fixed"]) < GRAD_TOL
+    assert sum_err(gtau, g["grad_tau_fixed"], grad.cpu().numpy() * -C / float(g["tau"])) < GRAD_TOL
+
+
+def test_ops_small_reg_golden():
+    g = load_golden("sk_fwd_smallreg")
+    P = _ops.sinkhorn(_t(-g["cost"]), float(g["tau"]), int(g["n_iters"]))
+    assert rel_err(P, g["P"]) < FWD_TOL
+
+
+def test_ops_grads_golden_rectangular_nonuniform():
+    g = load_golden("sk_grads_8x16")
+    la, G, lga, lgb = _t(g["log_alpha"]), _t(g["grad_P"]), _t(g["log_a"]), _t(g["log_b"])
+    tau, T, BT = float(g["tau"]), int(g["n_iters"]), int(g["backward_iters"])
+    terms = lambda gr: gr.cpu().numpy() * g["log_alpha"] / tau  # noqa: E731
+    P, gi, gti = _ops.sinkhorn_with_grads_implicit(la, G, tau, T, BT, lga, lgb)
+    assert rel_err(P, g["P"]) < FWD_TOL
+    assert rel_err(gi, g["grad_implicit"]) < GRAD_TOL
+    assert sum_err(gti, g["grad_tau_implicit"], terms(gi)) < GRAD_TOL
+    Pu, gu, gtu = _ops.sinkhorn_with_grads_unrolled(la, G, tau, T, lga, lgb)
+    assert rel_err(Pu, g["P_unrolled"]) < FWD_TOL
+    assert rel_err(gu, g["grad_unrolled"]) < GRAD_TOL
+    assert sum_err(gtu, g["grad_tau_unrolled"], terms(gu)) < GRAD_TOL
+
+
+def test_ops_unrolled_golden_48x64():
+    g = load_golden("sk_unrolled_48x64")
+    C = g["cost"]
+    P, gu, gtu = _ops.sinkhorn_with_grads_unrolled(_t(-C), _t(C), float(g["tau"]), int(g["n_iters"]))
+    assert rel_err(P, g["P"]) < FWD_TOL
+    assert rel_err(gu, g["grad_unrolled"]) < GRAD_TOL
+    assert sum_err(gtu, g["grad_tau_unrolled"], gu.cpu().numpy() * -C / float(g["tau"])) < GRAD_TOL
+
+
+# ---------------------------------------------------------------------------
+# Oracle parity across shapes and kernel variants
+# ---------------------------------------------------------------------------
+SHAPES = [
+    # (B, M, N, tau, T, nonuniform)   N % 4 != 0 takes the scalar-load kernels
+    (1, 1, 1, 1.0, 5, False),
+    (3, 5, 7, 0.5, 30, True),
+    (2, 64, 64, 1.0, 50, False),
+    (2, 37, 250, 0.1, 40, True),
+    (4, 200, 96, 0.2, 60, True),
+    (1, 300, 1024, 0.05, 80, False),
+    (2, 64, 2048, 0.1, 30, True),
+    (1, 96, 4096, 0.1, 20, False),
+    (1, 257, 4095, 0.3, 15, True),
+    (5, 1000, 3, 1.0, 25, True),
+]
+
+
+@pytest.mark.parametrize("B,M,N,tau,T,nonuni", SHAPES)
+def test_forward_and_implicit_match_oracle(B, M, N, tau, T, nonuni):
+    rng = np.random.default_rng(B * 1000 + M + N)
+    C = rng.random((B, M, N)).astype(np.float32)
+    G = rng.standard_normal((B, M, N)).astype(np.float32)
+    lga = lgb = None
+    if nonuni:
+        lga, lgb = np.log(_dirichlet(rng, B, M)), np.log(_dirichlet(rng, B, N))
+    P, gi, gti = _ops.sinkhorn_with_grads_implicit(
+        _t(-C), _t(G), tau, T, T, None if lga is None else _t(lga), None if lgb is None else _t(lgb))
+    Po, go, gto = osk.with_grads_implicit(-C, G, tau, T, T, lga, lgb)
+    assert rel_err(P, Po) < FWD_TOL
+    assert rel_err(gi, go) < GRAD_TOL
+    assert sum_err(gti, gto, go * -C / tau) < GRAD_TOL
+
+
+@pytest.mark.parametrize("B,M,N,tau,T,nonuni", SHAPES[:8])
+def test_unrolled_matches_oracle(B, M, N, tau, T, nonuni):
+    rng = np.random.default_rng(B * 7 + M + N)
+    C = rng.random((B, M, N)).astype(np.float32)
+    G = rng.standard_normal((B, M, N)).astype(np.float32)
+    lga = lgb = None
+    if nonuni:
+        lga, lgb = np.log(_dirichlet(rng, B, M)), np.log(_dirichlet(rng, B, N))
+    T = min(T, 20)
+    P, gu, gtu = _ops.sinkhorn_with_grads_unrolled(
+        _t(-C), _t(G), tau, T, None if lga is None else _t(lga), None if lgb is None else _t(lgb))
+    Po, go, gto = osk.with_grads_unrolled(-C, G, tau, T, lga, lgb)
+    assert rel_err(P, Po) < FWD_TOL
+    assert rel_err(gu, go) < GRAD_TOL
+    assert sum_err(gtu, gto, go * -C / tau) < GRAD_TOL
+
+
+@pytest.mark.parametrize("seed,shape,tau", [(0, (1, 256, 256), 0.1), (1, (4, 96, 128), 0.05),
+                                            (2, (3, 40, 60), 0.5), (3, (2, 512, 300), 0.02)])
+def test_early_stop_matches_oracle(seed, shape, tau):
+    C = torch.rand(*shape, generator=torch.Generator().manual_seed(seed)).numpy()
+    P, used, conv = _ops.sinkhorn_dual_forward(_t(-C), tau, 300, 1e-6)
+    used, conv = int(used), int(conv)
+    o = osk.dual_forward(-C, tau, 300, tol=1e-6)
+    assert abs(used - o.n_iters_used) <= 1, (used, o.n_iters_used)
+    if used < 300:
+        assert conv == 1
+    matched = osk.dual_forward(-C, tau, used)
+    assert rel_err(P, matched.P) < FWD_TOL
+
+
+def test_zero_iterations_and_degenerate_shapes():
+    C = np.random.default_rng(0).random((2, 5, 6)).astype(np.float32)
+    P, used, conv = _ops.sinkhorn_dual_forward(_t(-C), 0.5, 0, 1e-6)
+    assert int(used) == 0 and int(conv) == 0
+    assert rel_err(P, osk.dual_forward(-C, 0.5, 0).P) < FWD_TOL
+    P, used, conv = _ops.sinkhorn_dual_forward(torch.zeros(0, 4, 4, device=DEV), 1.0, 10, 1e-6)
+    assert P.shape == (0, 4, 4)
+    _, g, gt = _ops.sinkhorn_with_grads_implicit(_t(-C), _t(C), 0.5, 0, 0)
+    o = osk.dual_forward(-C, 0.5, 0)
+    go, _, _ = osk.implicit_backward(-C, o.P, C, 0.5, 0)
+    assert rel_err(g, go) < GRAD_TOL
+
+
+def test_op_argument_errors():
+    x = torch.rand(2, 4, 4, device=DEV)
+    with pytest.raises(RuntimeError, match="tau must be > 0"):
+        _ops.sinkhorn(x, 0.0, 5)
+    with pytest.raises(RuntimeError, match="3D"):
+        _ops.sinkhorn(x[0], 1.0, 5)
+    with pytest.raises(RuntimeError, match="log_a must have shape"):
+        _ops.sinkhorn(x, 1.0, 5, torch.zeros(2, 5, device=DEV))
+    with pytest.raises(RuntimeError, match="grad_P must match"):
+        _ops.sinkhorn_with_grads_implicit(x, torch.zeros(2, 4, 5, device=DEV), 1.0, 5, 5)
+    with pytest.raises(RuntimeError, match="not implemented"):
+        _ops.sinkhorn_dual_forward(x, 1.0, 5, 0.0, None, None, False, 2)
+    with pytest.raises(RuntimeError, match="4096"):
+        _ops.sinkhorn(torch.rand(1, 2, 4097, device=DEV), 1.0, 1)
+
+
+# ---------------------------------------------------------------------------
+# Public API (fused autograd path)
+# ---------------------------------------------------------------------------
+def _oracle_cost_grads(C, tau, T, BT, a=None, b=None, W=None, mode="implicit"):
+    """dL/dC for L = cost.sum() (+ sum(P * W)) as the reference composes it."""
+    lga = None if a is None else np.log(a)
+    lgb = None if b is None else np.log(b)
+    G = C.copy() if W is None else C + W
+    if mode == "implicit":
+        f = osk.dual_forward(-C, tau, T, 0.0, lga, lgb)
+        gla, gt, _ = osk.implicit_backward(-C, f.P, G, tau, BT)
+    else:
+        f = osk.dual_forward(-C, tau, T, 0.0, lga, lgb, keep_history=True)
+        gla, gt = osk.unrolled_backward(-C, f.P, G, f.K, f.u_hist, f.v_hist, tau)
+    return f.P, (f.P * C).sum((1, 2)), f.P - gla, gt, gla
+
+
+@pytest.mark.parametrize("mode", ["implicit", "unrolled"])
+def test_api_plan_cost_and_cost_gradient(mode):
+    rng = np.random.default_rng(11)
+    C = rng.random((3, 48, 80)).astype(np.float32)
+    a, b = _dirichlet(rng, 3, 48), _dirichlet(rng, 3, 80)
+    leaf = _t(C).requires_grad_(True)
+    res = dot_amd.sinkhorn(leaf, reg=0.3, n_iters=40, backward_mode=mode, a=_t(a), b=_t(b), tol=0)
+    res.cost.sum().backward()
+    P, cost, dC, _, _ = _oracle_cost_grads(C, 0.3, 40, 40, a, b, mode=mode)
+    assert res.n_iters_used == 40 and res.converged is True
+    assert rel_err(res.transport_plan, P) < FWD_TOL
+    assert rel_err(res.cost, cost) < FWD_TOL
+    assert rel_err(leaf.grad, dC) < GRAD_TOL
+
+
+def test_api_gradient_through_plan_and_cost():
+    rng = np.random.default_rng(12)
+    C = rng.random((2, 30, 20)).astype(np.float32)
+    W = rng.standard_normal((2, 30, 20)).astype(np.float32)
+    leaf = _t(C).requires_grad_(True)
+    res = dot_amd.sinkhorn(leaf, reg=0.5, n_iters=60, tol=0)
+    (res.cost.sum() + (res.transport_plan * _t(W)).sum()).backward()
+    _, _, dC, _, _ = _oracle_cost_grads(C, 0.5, 60, 60, W=W)
+    assert rel_err(leaf.grad, dC) < GRAD_TOL
+
+
+def test_api_reg_tensor_gradient():
+    rng = np.random.default_rng(13)
+    C = rng.random((2, 16, 24)).astype(np.float32)
+    reg = torch.tensor(0.4, device=DEV, requires_grad=True)
+    leaf = _t(C).requires_grad_(True)
+    res = dot_amd.sinkhorn(leaf, reg=reg, n_iters=50, tol=0)
+    res.cost.sum().backward()
+    _, _, _, gt, gla = _oracle_cost_grads(C, 0.4, 50, 50)
+    assert reg.grad is not None
+    assert sum_err(reg.grad.reshape(1), np.array([gt.sum()]), (gla * -C / 0.4).reshape(1, -1)) < GRAD_TOL
+
+
+def test_api_early_stop_and_result_fields():
+    C = torch.rand(2, 128, 128, generator=torch.Generator().manual_seed(5))
+    leaf = C.to(DEV).requires_grad_(True)
+    res = dot_amd.sinkhorn(leaf, reg=0.1, n_iters=200)  # default tol 1e-6
+    assert isinstance(res, dot_amd.SinkhornResult)
+    assert isinstance(res.n_iters_used, int) and res.n_iters_used < 200 and res.converged is True
+    res.cost.sum().backward()
+    P, _, dC, _, _ = _oracle_cost_grads(C.numpy(), 0.1, res.n_iters_used, 200)
+    assert rel_err(res.transport_plan, P) < FWD_TOL
+    assert rel_err(leaf.grad, dC) < GRAD_TOL
+
+
+def test_api_unbatched_alias_and_modules():
+    C = torch.rand(24, 40, generator=torch.Generator().manual_seed(6))
+    r1 = dot_amd.sinkhorn(C.to(DEV), reg=0.5, max_iter=30, tol=0)
+    r2 = dot_amd.Sinkhorn(reg=0.5, max_iter=30)(C.to(DEV))
+    P = osk.dual_forward(-C.numpy()[None], 0.5, 30).P[0]
+    assert r1.transport_plan.shape == (24, 40) and r1.cost.shape == ()
+    assert rel_err(r1.transport_plan, P) < FWD_TOL
+    assert r2.transport_plan.shape == (24, 40)
+    la = torch.randn(2, 8, 8, generator=torch.Generator().manual_seed(7))
+    Q = dot_amd.SinkhornFromScores(tau=0.7, n_iters=25)(la.to(DEV))
+    assert Q.shape == (2, 8, 8)
+    Q0 = dot_amd.sinkhorn_from_scores(la.to(DEV), tau=0.7, n_iters=25, tol=0)
+    assert rel_err(Q0, osk.dual_forward(la.numpy(), 0.7, 25).P) < FWD_TOL
+    logQ = dot_amd.sinkhorn_from_scores(la.to(DEV), tau=0.7, n_iters=25, tol=0, return_log=True)
+    assert (logQ.cpu().numpy() - osk.dual_forward(la.numpy(), 0.7, 25, return_log=True).P).__abs__().max() < 1e-4
+
+
+def test_from_scores_gradient():
+    rng = np.random.default_rng(14)
+    la = rng.standard_normal((2, 10, 12)).astype(np.float32)
+    W = rng.standard_normal((2, 10, 12)).astype(np.float32)
+    x = _t(la).requires_grad_(True)
+    P = dot_amd.sinkhorn_from_scores(x, tau=0.8, n_iters=40, tol=0)
+    (P * _t(W)).sum().backward()
+    f = osk.dual_forward(la, 0.8, 40)
+    g, _, _ = osk.implicit_backward(la, f.P, W, 0.8, 40)
+    assert rel_err(x.grad, g) < GRAD_TOL
+
+
+def test_dual_false_is_the_fixed_count_path():
+    C = torch.rand(1, 96, 128, generator=torch.Generator().manual_seed(0)).to(DEV)
+    dual = dot_amd.sinkhorn(C, reg=0.1, n_iters=50, tol=0, dual=True)
+    full = dot_amd.sinkhorn(C, reg=0.1, n_iters=50, tol=0, dual=False)
+    assert dual.n_iters_used == 50 and full.n_iters_used == 50
+    assert torch.allclose(dual.transport_plan, full.transport_plan, atol=1e-5)
+    # dual=False ignores tol (the reference's full-matrix op) and reports converged=False
+    f2 = dot_amd.sinkhorn(C, reg=0.1, n_iters=50, dual=False)
+    assert f2.n_iters_used == 50 and f2.converged is False
+
+
+def test_api_errors():
+    C = torch.rand(2, 6, 6, device=DEV)
+    with pytest.raises(ValueError, match="strictly positive"):
+        dot_amd.sinkhorn(C, a=torch.zeros(6, device=DEV))
+    with pytest.raises(ValueError, match="sum to 1"):
+        dot_amd.sinkhorn(C, a=torch.full((6,), 0.5, device=DEV))
+    with pytest.raises(ValueError, match="n_iters must be an int"):
+        dot_amd.sinkhorn(C, n_iters="many")
+    with pytest.raises(NotImplementedError):
+        dot_amd.sinkhorn(C, reg=0.02, method="adam", lr=0.5)
+    with pytest.raises(ValueError):
+        dot_amd.sinkhorn(C, backward_mode="sideways")
+
+
+# ---------------------------------------------------------------------------
+# The reference's own GPU tests (tests/test_sinkhorn.py), re-expressed
+# ---------------------------------------------------------------------------
+def _uniform(B, n):
+    return torch.full((B, n), 1.0 / n, device=DEV)
+
+
+def _assert_marginals(plan, a, b, atol=1e-3):
+    assert torch.allclose(plan.sum(-1), a, atol=atol)
+    assert torch.allclose(plan.sum(-2), b, atol=atol)
+
+
+def _reference_from_scores(log_alpha, tau, n_iters):
+    x = log_alpha / tau
+    B, n, m = x.shape
+    log_a = torch.full((B, n, 1), -np.log(n), device=x.device, dtype=x.dtype)
+    log_b = torch.full((B, 1, m), -np.log(m), device=x.device, dtype=x.dtype)
+    for _ in range(n_iters):
+        x = x - torch.logsumexp(x, dim=-1, keepdim=True) + log_a
+        x = x - torch.logsumexp(x, dim=-2, keepdim=True) + log_b
+    return x.exp()
+
+
+@pytest.mark.parametrize("n,m", [(10, 10), (8, 16)])
+def test_reference_uniform_marginals(n, m):  # test_sinkhorn.py:144-183
+    cost = torch.rand(2, n, m, device=DEV)
+    res = dot_amd.sinkhorn(cost, reg=1.0)
+    _assert_marginals(res.transport_plan, _uniform(2, n), _uniform(2, m))
+
+
+def test_reference_nonuniform_marginals():  # :212-223
+    cost = torch.rand(1, 8, 16, device=DEV)
+    a = torch.tensor([[0.20, 0.10, 0.15, 0.15, 0.10, 0.10, 0.10, 0.10]], device=DEV)
+    res = dot_amd.sinkhorn(cost, reg=1.0, n_iters=100, a=a, b=_uniform(1, 16))
+    _assert_marginals(res.transport_plan, a, _uniform(1, 16))
+
+
+def test_reference_backward_and_modes():  # :254-313
+    cost = torch.rand(2, 8, 16, device=DEV)
+    a = torch.softmax(torch.randn(2, 8, device=DEV), -1)
+    b = torch.softmax(torch.randn(2, 16, device=DEV), -1)
+    cu = cost.clone().requires_grad_(True)
+    ru = dot_amd.sinkhorn(cu, reg=1.0, backward_mode="unrolled", a=a, b=b)
+    ru.cost.sum().backward()
+    ci = cost.clone().requires_grad_(True)
+    ri = dot_amd.sinkhorn(ci, reg=1.0, backward_mode="implicit", a=a, b=b)
+    ri.cost.sum().backward()
+    assert cu.grad is not None and ci.grad is not None and cu.grad.shape == cost.shape
+    assert torch.allclose(ru.transport_plan, ri.transport_plan, atol=1e-4)
+
+
+def test_reference_differentiable_reg_finite_difference():  # :399-416
+    cost = torch.eye(5, device=DEV).unsqueeze(0)
+    eps = torch.tensor(0.2, requires_grad=True, device=DEV)
+    res = dot_amd.sinkhorn(cost, reg=eps, n_iters=80)
+    res.cost.sum().backward()
+    analytic = eps.grad.item()
+    d = 1e-3
+    plus = dot_amd.sinkhorn(cost, reg=float(eps.detach() + d), n_iters=80).cost.sum().item()
+    minus = dot_amd.sinkhorn(cost, reg=float(eps.detach() - d), n_iters=80).cost.sum().item()
+    assert analytic > 0
+    assert abs(analytic - (plus - minus) / (2 * d)) < 5e-2
+
+
+def test_reference_large_rectangular_matches_torch():  # :763-773
+    torch.manual_seed(0)
+    cost = torch.rand(1, 320, 640, device=DEV)
+    res = dot_amd.sinkhorn(cost, reg=0.1, n_iters=50)
+    ref = _reference_from_scores(-cost.double(), 0.1, 50)
+    assert torch.allclose(res.transport_plan.double(), ref, atol=2e-3)
+
+
+def test_reference_very_large_square_marginals():  # :776-788
+    torch.manual_seed(0)
+    n = 1300
+    cost = torch.rand(1, n, n, device=DEV)
+    res = dot_amd.sinkhorn(cost, reg=0.1, n_iters=50)
+    assert torch.isfinite(res.transport_plan).all()
+    _assert_marginals(res.transport_plan, _uniform(1, n), _uniform(1, n), atol=2e-3)
+
+
+def test_reference_unrolled_dual_matches_full():  # :806-823
+    torch.manual_seed(0)
+    dc = torch.rand(1, 48, 64, device=DEV, requires_grad=True)
+    fc = dc.detach().clone().requires_grad_(True)
+    d = dot_amd.sinkhorn(dc, reg=0.1, n_iters=30, tol=0, dual=True, backward_mode="unrolled")
+    f = dot_amd.sinkhorn(fc, reg=0.1, n_iters=30, tol=0, dual=False, backward_mode="unrolled")
+    d.cost.sum().backward()
+    f.cost.sum().backward()
+    assert d.n_iters_used == 30 and f.n_iters_used == 30
+    assert torch.allclose(d.transport_plan, f.transport_plan, atol=1e-5)
+    assert torch.allclose(dc.grad, fc.grad, atol=1e-4)
+
+
+def test_reference_convergence_reduces_iterations():  # :826-839
+    torch.manual_seed(0)
+    cost = torch.rand(1, 256, 256, device=DEV)
+    early = dot_amd.sinkhorn(cost, reg=0.1, n_iters=50)
+    fixed = dot_amd.sinkhorn(cost, reg=0.1, n_iters=50, tol=0)
+    assert early.n_iters_used is not None and early.n_iters_used < 50
+    assert fixed.n_iters_used == 50
+    assert torch.allclose(early.transport_plan, fixed.transport_plan, atol=2e-3)
+
+
+# ---------------------------------------------------------------------------
+# BASELINE.json configurations at full size
+# ---------------------------------------------------------------------------
+def _c3_cost():
+    g = torch.Generator().manual_seed(3)
+    x, y = torch.randn(64, 512, 64, generator=g), torch.randn(64, 512, 64, generator=g)
+    C = torch.cdist(x.to(DEV), y.to(DEV)).square()
+    return (C / C.amax(dim=(-2, -1), keepdim=True)).contiguous()
+
+
+def test_config_c1_full_against_golden():
+    g = load_golden("sk_c1")
+    leaf = _t(g["cost"]).requires_grad_(True)
+    res = dot_amd.sinkhorn(leaf, reg=1.0, n_iters=100, tol=0)
+    res.cost.sum().backward()
+    assert rel_err(res.transport_plan, g["P"]) < FWD_TOL
+    assert rel_err(leaf.grad, g["P"] - g["grad_fixed"]) < GRAD_TOL
+
+
+def test_config_c3_full_size():
+    C = _c3_cost()
+    leaf = C.clone().requires_grad_(True)
+    res = dot_amd.sinkhorn(leaf, reg=0.1, n_iters=200)
+    res.cost.sum().backward()
+    T = res.n_iters_used
+    P = res.transport_plan.detach()
+    # size-independent properties on the whole batch
+    assert torch.allclose(P.sum(-2), torch.full_like(P.sum(-2), 1 / 512), rtol=1e-4, atol=0)
+    assert torch.allclose(res.cost.detach(), (P * C).sum((-2, -1)), rtol=1e-5)
+    # dL/dlog_alpha = P - dC; after the final mu update its column sums vanish exactly
+    # (in exact arithmetic): sum_i P (G - lambda - mu) = c - P^T lambda - mu * colsum(P) = 0
+    grad_la = P - leaf.grad
+    scale = grad_la.abs().sum(-2).amax()
+    assert (grad_la.sum(-2).abs().amax() / scale) < 1e-3
+    # parity with the oracle on two batch elements at the run's own iteration count
+    Cn = C.cpu().numpy()
+    for b in (0, 63):
+        Pb, costb, dCb, _, _ = _oracle_cost_grads(Cn[b:b + 1], 0.1, T, 200)
+        assert rel_err(P[b:b + 1], Pb) < FWD_TOL
+        assert rel_err(res.cost[b:b + 1], costb) < FWD_TOL
+        assert rel_err(leaf.grad[b:b + 1], dCb) < GRAD_TOL
+    # bitwise reproducible
+    leaf2 = C.clone().requires_grad_(True)
+    res2 = dot_amd.sinkhorn(leaf2, reg=0.1, n_iters=200)
+    res2.cost.sum().backward()
+    assert torch.equal(res2.transport_plan, res.transport_plan) and torch.equal(leaf2.grad, leaf.grad)
+
+
+def test_config_c4_full_size():
+    g = torch.Generator().manual_seed(4)
+    C = torch.rand(16, 1024, 2048, generator=g)
+    ea, eb = -torch.log(torch.rand(16, 1024, generator=g)), -torch.log(torch.rand(16, 2048, generator=g))
+    a, b = ea / ea.sum(-1, keepdim=True), eb / eb.sum(-1, keepdim=True)
+    leaf = C.to(DEV).requires_grad_(True)
+    res = dot_amd.sinkhorn(leaf, reg=0.05, n_iters=500, a=a.to(DEV), b=b.to(DEV))
+    res.cost.sum().backward()
+    P = res.transport_plan.detach()
+    assert torch.isfinite(P).all() and torch.isfinite(leaf.grad).all()
+    assert torch.allclose(P.sum(-2), b.to(DEV), rtol=1e-4, atol=1e-9)
+    if res.converged:
+        assert torch.allclose(P.sum(-1), a.to(DEV), rtol=1e-3, atol=1e-8)
+    # parity at the real shape with a short fixed count (float64 oracle on one element)
+    Cn = C[:1].numpy()
+    r20 = dot_amd.sinkhorn(C[:1].to(DEV).requires_grad_(True), reg=0.05, n_iters=20, tol=0,
+                           a=a[:1].to(DEV), b=b[:1].to(DEV))
+    Po, costo, _, _, _ = _oracle_cost_grads(Cn, 0.05, 20, 1, a[:1].numpy(), b[:1].numpy())
+    assert rel_err(r20.transport_plan, Po) < FWD_TOL
+    assert rel_err(r20.cost, costo) < FWD_TOL
+
+
+def test_config_c5_full_size():
+    g = torch.Generator().manual_seed(5)
+    x, y = torch.randn(4, 4096, 128, generator=g), torch.randn(4, 4096, 128, generator=g)
+    C = torch.cdist(x.to(DEV), y.to(DEV))
+    C = (C / C.amax(dim=(-2, -1), keepdim=True)).contiguous()
+    leaf = C.clone().requires_grad_(True)
+    res = dot_amd.sinkhorn(leaf, reg=0.02, n_iters=1000)
+    res.cost.sum().backward()
+    P = res.transport_plan.detach()
+    assert torch.isfinite(P).all() and torch.isfinite(leaf.grad).all()
+    assert torch.allclose(P.sum(-2), torch.full_like(P.sum(-2), 1 / 4096), rtol=1e-4, atol=0)
+    assert torch.allclose(P.sum((-2, -1)), torch.ones(4, device=DEV), rtol=1e-4)
+    # parity at the real shape, 5 iterations, one element, float64 oracle
+    r5 = dot_amd.sinkhorn(C[:1], reg=0.02, n_iters=5, tol=0)
+    Po = osk.dual_forward(-C[:1].cpu().numpy(), 0.02, 5).P
+    assert rel_err(r5.transport_plan, Po) < FWD_TOL
