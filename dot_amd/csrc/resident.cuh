@@ -1,0 +1,652 @@
+// Register-resident persistent kernels.
+//
+// When one batch element's [M, N] matrix fits the vector registers of W
+// workgroups (8 waves each, one workgroup per CU), the iterations run inside
+// one cooperative launch: every workgroup loads its strip of rows into VGPRs
+// once and then only exchanges one row of per-column partial sums per
+// iteration with the other W-1 workgroups of its batch element.
+//
+// Exchange protocol.  Cross-workgroup agent-scope release/acquire fences
+// write back and invalidate the per-XCD L2 and serialise across workgroups,
+// which costs more than a kernel launch on MI355X.  Instead every exchanged
+// value travels with its iteration number: a 64-bit word (float bits low,
+// iteration tag high) written and read with relaxed agent-scope atomics,
+// which are single-copy atomic and coherent per location.  A reader polls
+// until the tag it expects appears, so no separate flag or fence is needed.
+// Slots alternate by iteration parity, which keeps a fast workgroup from
+// overwriting a slot before the slow ones have read it (it cannot finish
+// iteration t+1 before everyone has published iteration t+1, which each
+// workgroup does only after reading iteration t).  Polls are bounded; a
+// timeout sets `status` and the outputs are written as NaN.
+#pragma once
+
+#include <cfloat>
+#include <cstdint>
+
+#include "row.cuh"
+#include "sinkhorn_kernels.cuh"
+
+namespace dot_amd {
+namespace res {
+
+// 8 waves per workgroup (2 per SIMD) leave each wave 256 registers, of which
+// up to 128 per lane hold the resident strip; a 16-wave workgroup would hold
+// the same strip in 64 registers per lane but leave only 64 for everything else.
+constexpr int kThreads = 512;
+constexpr int kWaves = kThreads / kWave;  // 8
+constexpr int kMaxRegFloats = 128;        // per-lane VGPR budget for the resident strip
+constexpr int kMaxGroup = 8;              // workgroups per batch element (staging rows in LDS)
+
+__device__ __forceinline__ unsigned long long tag_pack(float v, unsigned t) {
+    return (static_cast<unsigned long long>(t) << 32) | __float_as_uint(v);
+}
+
+__device__ __forceinline__ void publish(unsigned long long* p, float v, unsigned t) {
+    __hip_atomic_store(p, tag_pack(v, t), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Waits for slot `p` to carry tag `t` and returns its value.  Gives up after
+// `spin_limit` polls, or as soon as any workgroup has reported a timeout in
+// `status` (checked every 256 polls); `dead` then short-circuits every later
+// call of this lane, so a failure costs one bounded wait, not one per value.
+__device__ __forceinline__ float collect(unsigned long long* p, unsigned t, int spin_limit,
+                                         int* status, bool& dead) {
+    if (dead) return __builtin_nanf("");
+    for (int spins = 0;; ++spins) {
+        const unsigned long long x = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (static_cast<unsigned>(x >> 32) == t) return __uint_as_float(static_cast<unsigned>(x));
+        if ((spins & 255) == 255 &&
+            __hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) {
+            dead = true;
+            return __builtin_nanf("");
+        }
+        if (spins >= spin_limit) {
+            atomicOr(status, 1);
+            dead = true;
+            return __builtin_nanf("");
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+}
+
+// Collects one published row (this lane's PL columns) with every load of a poll
+// round in flight at once; returns false after a timeout (values are then NaN).
+template <int VEC, int CH>
+__device__ __forceinline__ void collect_row(unsigned long long* row, unsigned t, int N, int spin_limit,
+                                            int* status, bool& dead, float (&out)[VEC * CH]) {
+    using R = Row<VEC, CH>;
+    const int lane = threadIdx.x % kWave;
+    if (dead) {
+#pragma unroll
+        for (int e = 0; e < R::PL; ++e) out[e] = __builtin_nanf("");
+        return;
+    }
+    for (int spins = 0;; ++spins) {
+        bool ready = true;
+#pragma unroll
+        for (int k = 0; k < CH; ++k) {
+#pragma unroll
+            for (int v = 0; v < VEC; ++v) {
+                const int col = R::col(lane, k) + v;
+                unsigned long long x = tag_pack(0.0f, t);
+                if (col < N) x = __hip_atomic_load(row + col, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                ready = ready && static_cast<unsigned>(x >> 32) == t;
+                out[k * VEC + v] = __uint_as_float(static_cast<unsigned>(x));
+            }
+        }
+        if (ready) return;
+        if (((spins & 255) == 255 &&
+             __hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) ||
+            spins >= spin_limit) {
+            if (spins >= spin_limit) atomicOr(status, 1);
+            dead = true;
+#pragma unroll
+            for (int e = 0; e < R::PL; ++e) out[e] = __builtin_nanf("");
+            return;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+}
+
+// Fold the waves' per-lane column values into wave 0 in a fixed order
+// (halving tree 4, 2, 1).  `lds` holds kWaves/2 * N floats.  Every thread must call it.
+template <int VEC, int CH, class Op = OpSum>
+__device__ __forceinline__ void tree_combine(float (&acc)[VEC * CH], float* lds, int N, Op op = Op{}) {
+    using R = Row<VEC, CH>;
+    const int lane = threadIdx.x % kWave;
+    const int wave = threadIdx.x / kWave;
+#pragma unroll
+    for (int half = kWaves / 2; half >= 1; half /= 2) {
+        __syncthreads();
+        if (wave >= half && wave < 2 * half) R::store(lds + (wave - half) * N, lane, N, acc);
+        __syncthreads();
+        if (wave < half) {
+            float o[R::PL];
+            R::load(lds + wave * N, lane, N, o, 0.0f);
+#pragma unroll
+            for (int e = 0; e < R::PL; ++e) acc[e] = op(acc[e], o[e]);
+        }
+    }
+}
+
+struct ImpResArgs {
+    const float* X;        // scores (for the gradient's log_alpha and the cost-path G)
+    int scores_kind;
+    const float* gP;       // [B,M,N] or null
+    const float* gC;       // [B] or null
+    const float* P;        // [B,M,N]
+    const float* r;        // [B,M] sum_k P G
+    const float* rs;       // [B,M] sum_k P
+    const float* c;        // [B,N] sum_i P G
+    const float* cs;       // [B,N] sum_i P
+    unsigned long long* xchg;  // [2,B,W,N] tagged partials
+    float* grad;           // [B,M,N]
+    float* tau_partial;    // [B*W]
+    int* status;
+    float inv_tau;
+    int M, N, W, R, iters, spin_limit;
+};
+
+// The implicit adjoint (kernels.cu:965-1098) with P held in registers.
+// Per iteration: lambda_i = (r_i - sum_k P mu_k) / max(rs_i, 1e-12) for the
+// workgroup's rows, the workgroup's column sums of P lambda, one tagged
+// exchange with the batch element's other workgroups, then
+// mu_k = (c_k - sum_i P lambda) / max(cs_k, 1e-12).  The final phase streams
+// G and writes grad = P (G - lambda - mu) / tau (cost path: grad_cost P - that).
+template <int VEC, int CH, int RPW>
+__global__ __launch_bounds__(kThreads) void implicit_adjoint(ImpResArgs a) {
+    using R = Row<VEC, CH>;
+    constexpr int PL = R::PL;
+    constexpr int ROWS = kWaves * RPW;  // rows per workgroup
+    // LDS: tree 8N | mu N | c N | cs N | r ROWS | 1/rs ROWS | lambda ROWS | scratch 16
+    extern __shared__ float lds[];
+    float* lds_mu = lds + 8 * a.N;
+    float* lds_c = lds_mu + a.N;
+    float* lds_cs = lds_c + a.N;
+    float* lds_r = lds_cs + a.N;
+    float* lds_rs = lds_r + ROWS;
+    float* lds_lam = lds_rs + ROWS;
+    float* scratch = lds_lam + ROWS;
+    const int lane = threadIdx.x % kWave;
+    const int wave = threadIdx.x / kWave;
+    const int b = blockIdx.x / a.W;
+    const int w = blockIdx.x % a.W;
+    const int row0 = w * a.R;
+    const int rend = min(row0 + a.R, a.M);
+    const size_t bM = size_t(b) * a.M;
+    const size_t bN = size_t(b) * a.N;
+
+    // local row index l = wave + kWaves * k  <->  global row row0 + l
+    float p[RPW][PL];
+#pragma unroll
+    for (int k = 0; k < RPW; ++k) {
+        const int i = row0 + wave + kWaves * k;
+        if (i < rend) {
+            R::load(a.P + (bM + i) * a.N, lane, a.N, p[k], 0.0f);
+        } else {
+#pragma unroll
+            for (int e = 0; e < PL; ++e) p[k][e] = 0.0f;
+        }
+    }
+    for (int l = threadIdx.x; l < ROWS; l += kThreads) {
+        const int i = row0 + l;
+        const bool ok = i < rend;
+        lds_r[l] = ok ? a.r[bM + i] : 0.0f;
+        lds_rs[l] = ok ? fmaxf(a.rs[bM + i], 1.0e-12f) : 1.0f;
+        lds_lam[l] = 0.0f;
+    }
+    for (int j = threadIdx.x; j < a.N; j += kThreads) {
+        lds_c[j] = a.c[bN + j];
+        lds_cs[j] = fmaxf(a.cs[bN + j], 1.0e-12f);
+    }
+    __syncthreads();
+    float mu[PL];
+#pragma unroll
+    for (int e = 0; e < PL; ++e) mu[e] = 0.0f;
+    bool dead = false;
+
+    for (int t = 1; t <= a.iters; ++t) {
+        float acc[PL];
+#pragma unroll
+        for (int e = 0; e < PL; ++e) acc[e] = 0.0f;
+#pragma unroll
+        for (int k = 0; k < RPW; ++k) {
+            const int l = wave + kWaves * k;
+            float d0 = 0.0f, d1 = 0.0f;
+#pragma unroll
+            for (int e = 0; e < PL; e += 2) {
+                d0 = fmaf(p[k][e], mu[e], d0);
+                if (e + 1 < PL) d1 = fmaf(p[k][e + 1], mu[e + 1], d1);
+            }
+            const float dot = wave_sum(d0 + d1);
+            const float lam = (lds_r[l] - dot) / lds_rs[l];
+#pragma unroll
+            for (int e = 0; e < PL; ++e) acc[e] = fmaf(p[k][e], lam, acc[e]);
+            if (lane == 0) lds_lam[l] = lam;
+        }
+        tree_combine<VEC, CH>(acc, lds, a.N);
+        // Exchange: wave 0 publishes this workgroup's column sums; waves 0..W-1 each
+        // collect one workgroup's row into LDS (all loads of a wave in flight at once).
+        unsigned long long* slot = a.xchg + size_t(t & 1) * gridDim.x * a.N;
+        if (wave == 0) {
+            unsigned long long* mine = slot + size_t(blockIdx.x) * a.N;
+#pragma unroll
+            for (int k = 0; k < CH; ++k) {
+#pragma unroll
+                for (int v = 0; v < VEC; ++v) {
+                    const int col = R::col(lane, k) + v;
+                    if (col < a.N) publish(mine + col, acc[k * VEC + v], unsigned(t));
+                }
+            }
+        }
+        __syncthreads();  // the tree area is reused for the collected rows
+        unsigned long long* batch = slot + size_t(b) * a.W * a.N;
+        for (int w2 = wave; w2 < a.W; w2 += kWaves) {
+            float got[PL];
+            collect_row<VEC, CH>(batch + size_t(w2) * a.N, unsigned(t), a.N, a.spin_limit, a.status,
+                                 dead, got);
+            R::store(lds + w2 * a.N, lane, a.N, got);  // W <= kMaxGroup rows fit the tree area
+        }
+        __syncthreads();
+        for (int j = threadIdx.x; j < a.N; j += kThreads) {
+            float s = 0.0f;
+            for (int w2 = 0; w2 < a.W; ++w2) s += lds[w2 * a.N + j];
+            lds_mu[j] = (lds_c[j] - s) / lds_cs[j];
+        }
+        __syncthreads();
+        R::load(lds_mu, lane, a.N, mu, 0.0f);
+    }
+
+    // Final phase: stream G and write the gradient of this workgroup's rows.
+    const bool cost_kind = a.scores_kind < 0;
+    const float gc = (cost_kind && a.gC) ? a.gC[b] : 0.0f;
+    const bool failed = __hip_atomic_load(a.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
+    float tacc = 0.0f;
+#pragma unroll
+    for (int k = 0; k < RPW; ++k) {
+        const int l = wave + kWaves * k;
+        const int i = row0 + l;
+        if (i >= rend) continue;
+        const float lam = lds_lam[l];
+        const size_t off = (bM + i) * a.N;
+        float x[PL], G[PL];
+        R::load(a.X + off, lane, a.N, x, 0.0f);
+        if (a.gP) R::load(a.gP + off, lane, a.N, G, 0.0f);
+        else {
+#pragma unroll
+            for (int e = 0; e < PL; ++e) G[e] = 0.0f;
+        }
+        float o[PL];
+#pragma unroll
+        for (int e = 0; e < PL; ++e) {
+            if (a.gC) G[e] += gc * (cost_kind ? x[e] : -x[e]);
+            const float gl = (p[k][e] * ((G[e] - lam) - mu[e])) * a.inv_tau;
+            const float la = cost_kind ? -x[e] : x[e];
+            if (R::valid(lane, e, a.N)) tacc = fmaf(gl, la, tacc);
+            o[e] = failed ? __builtin_nanf("") : (cost_kind ? gc * p[k][e] - gl : gl);
+        }
+        R::store(a.grad + off, lane, a.N, o);
+    }
+    const float tsum = block_reduce<kWaves>(wave_sum(tacc), scratch, OpSum{});
+    if (threadIdx.x == 0) a.tau_partial[blockIdx.x] = failed ? __builtin_nanf("") : tsum;
+}
+
+}  // namespace res
+}  // namespace dot_amd
+
+
+namespace dot_amd {
+namespace res {
+
+constexpr int kDeltaSlots = 4;  // lagged stop test: workgroups drift at most 2 iterations apart
+constexpr int kFwdScratch = 32;
+
+struct OpMaxNan {  // max that keeps a NaN (a timed-out poll) instead of dropping it
+    __device__ __forceinline__ float operator()(float a, float b) const {
+        return (a != a || b != b) ? __builtin_nanf("") : fmaxf(a, b);
+    }
+};
+
+struct FwdResArgs {
+    const float* X;       // scores [B,M,N]
+    float kscale;         // K = X * kscale
+    int scores_kind;      // +1 log_alpha, -1 cost
+    const float* log_a;   // [B,M] or null
+    const float* log_b;   // [B,N] or null
+    float log_a_default, log_b_default;
+    float tol;
+    int max_iter;
+    int return_log;
+    float* plan;          // [B,M,N] or null
+    float* cost_partial;  // [B*W] or null
+    float* u_out;         // [B,M] or null
+    float* v_out;         // [B,N] or null
+    float* u_hist;        // [T,B,M] or null
+    float* v_hist;        // [T,B,N] or null
+    int32_t* iters_used;
+    int32_t* converged;
+    unsigned long long* xchg;   // [2, G, N] tagged column partials
+    unsigned long long* fxchg;  // [2, 2, G, N] tagged exact-fallback column max / sum
+    unsigned long long* dxchg;  // [kDeltaSlots, G] tagged per-workgroup deltas
+    int* status;                // non-zero after a poll timeout
+    int B, M, N, W, R, spin_limit;
+};
+
+// Waits for G tagged per-workgroup deltas of iteration t and returns their
+// maximum (order-free, so every workgroup gets the same value).  Every thread
+// must call it; wave 0 polls.
+__device__ __forceinline__ float global_delta(const FwdResArgs& a, int t, float* scratch, bool& dead) {
+    const int lane = threadIdx.x % kWave;
+    const int G = gridDim.x;
+    __syncthreads();
+    if (threadIdx.x < kWave) {
+        unsigned long long* ds = a.dxchg + size_t(t % kDeltaSlots) * G;
+        float m = 0.0f;
+        for (int g = lane; g < G; g += kWave) {
+            const float d = collect(ds + g, unsigned(t), a.spin_limit, a.status, dead);
+            m = (d != d) ? d : fmaxf(m, d);  // NaN (timeout) propagates
+        }
+        m = wave_reduce(m, OpMaxNan{});
+        if (lane == 0) scratch[0] = m;
+    }
+    __syncthreads();
+    return scratch[0];
+}
+
+// Dual log-domain Sinkhorn forward (torch_cuda.cpp:147-264) with the scores
+// of this workgroup's rows held in registers for all iterations.
+// Iteration t: the row update of sk::fwd_sweep from v_{t-1}, whose shared
+// exponentials also give this workgroup's column sums of exp(K + u_t + v_{t-1});
+// one tagged exchange of those sums inside the batch element; then every
+// workgroup of the element forms v_t = log b + v_{t-1} - log colsum in the same
+// fixed order.  Columns whose sum is below the floor take the exact max-shifted
+// LSE (kernels.cu:629-671) through two more exchanges (column max, then sum);
+// the decision is the same in every workgroup of the element because they all
+// hold the same sums.  The batch-global stop test (torch_cuda.cpp:225-237) of
+// iteration t-1 is evaluated during iteration t from every workgroup's
+// published delta, so no grid-wide wait sits on the critical path; when it
+// fires, iteration t is discarded and (u_{t-1}, v_{t-1}) are the result.
+template <int VEC, int CH, int RPW>
+__global__ __launch_bounds__(kThreads) void forward(FwdResArgs a) {
+    using R = Row<VEC, CH>;
+    constexpr int PL = R::PL;
+    constexpr int ROWS = kWaves * RPW;
+    // LDS: tree 8N | v 2N | log b N | column max N | u 2*ROWS | log a ROWS | scratch 32
+    extern __shared__ float lds[];
+    float* lds_v = lds + 8 * a.N;
+    float* lds_lb = lds_v + 2 * a.N;
+    float* lds_mx = lds_lb + a.N;
+    float* lds_u = lds_mx + a.N;
+    float* lds_la = lds_u + 2 * ROWS;
+    float* scratch = lds_la + ROWS;
+    const int lane = threadIdx.x % kWave;
+    const int wave = threadIdx.x / kWave;
+    const int G = gridDim.x;
+    const int b = blockIdx.x / a.W;
+    const int w = blockIdx.x % a.W;
+    const int row0 = w * a.R;
+    const int rend = min(row0 + a.R, a.M);
+    const size_t bM = size_t(b) * a.M;
+    const size_t bN = size_t(b) * a.N;
+    const bool check = a.tol > 0.0f;
+    // Padding (columns >= N, rows >= rend) holds the value whose K is -inf.
+    const float pad = a.kscale > 0.0f ? -INFINITY : INFINITY;
+
+    float x[RPW][PL];
+#pragma unroll
+    for (int k = 0; k < RPW; ++k) {
+        const int i = row0 + wave + kWaves * k;
+        if (i < rend) {
+            R::load(a.X + (bM + i) * a.N, lane, a.N, x[k], 0.0f);
+#pragma unroll
+            for (int e = 0; e < PL; ++e)
+                if (!R::valid(lane, e, a.N)) x[k][e] = pad;
+        } else {
+#pragma unroll
+            for (int e = 0; e < PL; ++e) x[k][e] = pad;
+        }
+    }
+    for (int l = threadIdx.x; l < ROWS; l += kThreads) {
+        const int i = row0 + l;
+        lds_la[l] = (i < rend && a.log_a) ? a.log_a[bM + i] : a.log_a_default;
+        lds_u[l] = 0.0f;
+        lds_u[ROWS + l] = 0.0f;
+    }
+    for (int j = threadIdx.x; j < a.N; j += kThreads) {
+        lds_lb[j] = a.log_b ? a.log_b[bN + j] : a.log_b_default;
+        lds_v[j] = 0.0f;
+        lds_v[a.N + j] = 0.0f;
+    }
+    __syncthreads();
+    float v[PL];
+#pragma unroll
+    for (int e = 0; e < PL; ++e) v[e] = 0.0f;
+    bool dead = false;
+    int used = a.max_iter;
+    int conv = 0;
+
+    for (int t = 1; t <= a.max_iter; ++t) {
+        const int cur = t & 1, prev = cur ^ 1;
+        // Row update (kernels.cu:503-545) and the shared-exponential column sums.
+        float acc[PL];
+#pragma unroll
+        for (int e = 0; e < PL; ++e) acc[e] = 0.0f;
+        float uk[RPW];  // this wave's new u values; stored after the loop, which keeps it branch-free
+#pragma unroll
+        for (int k = 0; k < RPW; ++k) {
+            const int l = wave + kWaves * k;
+            float y[PL];
+            float ml = -FLT_MAX;
+#pragma unroll
+            for (int e = 0; e < PL; ++e) {
+                y[e] = fmaf(x[k][e], a.kscale, v[e]);
+                ml = fmaxf(ml, y[e]);
+            }
+            const float m = wave_max(ml);
+            float sl = 0.0f;
+#pragma unroll
+            for (int e = 0; e < PL; ++e) {
+                y[e] = fast_exp(y[e] - m);
+                sl += y[e];
+            }
+            const float ssum = wave_sum(sl);
+            const float lga = lds_la[l];
+            const float ls = logf(fmaxf(ssum, sk::kSumFloor));
+            const float u = lga - (m + ls);
+            const float wgt = fast_exp(lga - ls);
+#pragma unroll
+            for (int e = 0; e < PL; ++e) acc[e] = fmaf(y[e], wgt, acc[e]);
+            // Materialise acc here: left alone, the compiler postpones every row's
+            // update to the end of the loop and keeps all rows' exponentials live.
+#pragma unroll
+            for (int e = 0; e < PL; ++e) asm volatile("" : "+v"(acc[e]));
+            uk[k] = u;
+        }
+        float dmax = 0.0f;
+#pragma unroll
+        for (int k = 0; k < RPW; ++k) {
+            const int l = wave + kWaves * k;
+            const int i = row0 + l;
+            if (i < rend) {
+                dmax = fmaxf(dmax, fabsf(uk[k] - lds_u[prev * ROWS + l]));
+                if (lane == 0) {
+                    lds_u[cur * ROWS + l] = uk[k];
+                    if (a.u_hist) a.u_hist[(size_t(t - 1) * a.B + b) * a.M + i] = uk[k];
+                }
+            }
+        }
+        tree_combine<VEC, CH>(acc, lds, a.N);
+        const float wg_delta = check ? block_reduce<kWaves>(dmax, scratch + 1, OpMax{}) : 0.0f;
+        unsigned long long* slot = a.xchg + size_t(cur) * G * a.N;
+        if (wave == 0) {
+            unsigned long long* mine = slot + size_t(blockIdx.x) * a.N;
+#pragma unroll
+            for (int k = 0; k < CH; ++k) {
+#pragma unroll
+                for (int q = 0; q < VEC; ++q) {
+                    const int col = R::col(lane, k) + q;
+                    if (col < a.N) publish(mine + col, acc[k * VEC + q], unsigned(t));
+                }
+            }
+            if (check && lane == 0)
+                publish(a.dxchg + size_t(t % kDeltaSlots) * G + blockIdx.x, wg_delta, unsigned(t));
+        }
+        __syncthreads();  // the tree area now receives the collected rows
+        unsigned long long* batch = slot + size_t(b) * a.W * a.N;
+        for (int w2 = wave; w2 < a.W; w2 += kWaves) {
+            float got[PL];
+            collect_row<VEC, CH>(batch + size_t(w2) * a.N, unsigned(t), a.N, a.spin_limit, a.status,
+                                 dead, got);
+            R::store(lds + w2 * a.N, lane, a.N, got);
+        }
+        __syncthreads();
+        int low = 0;
+        for (int j = threadIdx.x; j < a.N; j += kThreads) {
+            float cs = 0.0f;
+            for (int w2 = 0; w2 < a.W; ++w2) cs += lds[w2 * a.N + j];
+            if (cs >= sk::kColSumFloor && cs <= FLT_MAX) {
+                lds_v[cur * a.N + j] = lds_lb[j] + lds_v[prev * a.N + j] - logf(cs);
+            } else {
+                lds_v[cur * a.N + j] = __builtin_nanf("");  // marks the column for the exact LSE
+                low = 1;
+            }
+        }
+        if (__syncthreads_or(low)) {
+            // Exact column LSE of K + u_t over the element's rows: max, then sum.
+            float cm[PL];
+#pragma unroll
+            for (int e = 0; e < PL; ++e) cm[e] = -FLT_MAX;
+#pragma unroll
+            for (int k = 0; k < RPW; ++k) {
+                const int l = wave + kWaves * k;
+                if (row0 + l >= rend) continue;
+                const float u = lds_u[cur * ROWS + l];
+#pragma unroll
+                for (int e = 0; e < PL; ++e)
+                    if (R::valid(lane, e, a.N)) cm[e] = fmaxf(cm[e], fmaf(x[k][e], a.kscale, u));
+            }
+            tree_combine<VEC, CH>(cm, lds, a.N, OpMax{});
+            unsigned long long* fslot = a.fxchg + size_t(cur) * 2 * G * a.N;
+            if (wave == 0) {
+                unsigned long long* mine = fslot + size_t(blockIdx.x) * a.N;
+#pragma unroll
+                for (int k = 0; k < CH; ++k)
+#pragma unroll
+                    for (int q = 0; q < VEC; ++q) {
+                        const int col = R::col(lane, k) + q;
+                        if (col < a.N) publish(mine + col, cm[k * VEC + q], unsigned(t));
+                    }
+            }
+            __syncthreads();
+            for (int w2 = wave; w2 < a.W; w2 += kWaves) {
+                float got[PL];
+                collect_row<VEC, CH>(fslot + (size_t(b) * a.W + w2) * a.N, unsigned(t), a.N,
+                                     a.spin_limit, a.status, dead, got);
+                R::store(lds + w2 * a.N, lane, a.N, got);
+            }
+            __syncthreads();
+            for (int j = threadIdx.x; j < a.N; j += kThreads) {
+                float mx = -FLT_MAX;
+                for (int w2 = 0; w2 < a.W; ++w2) mx = fmaxf(mx, lds[w2 * a.N + j]);
+                lds_mx[j] = mx;
+            }
+            __syncthreads();
+            float mxl[PL], sm[PL];
+            R::load(lds_mx, lane, a.N, mxl, 0.0f);
+#pragma unroll
+            for (int e = 0; e < PL; ++e) sm[e] = 0.0f;
+#pragma unroll
+            for (int k = 0; k < RPW; ++k) {
+                const int l = wave + kWaves * k;
+                if (row0 + l >= rend) continue;
+                const float u = lds_u[cur * ROWS + l];
+#pragma unroll
+                for (int e = 0; e < PL; ++e)
+                    if (R::valid(lane, e, a.N)) sm[e] += safe_exp(fmaf(x[k][e], a.kscale, u) - mxl[e]);
+            }
+            tree_combine<VEC, CH>(sm, lds, a.N);
+            unsigned long long* sslot = fslot + size_t(G) * a.N;
+            if (wave == 0) {
+                unsigned long long* mine = sslot + size_t(blockIdx.x) * a.N;
+#pragma unroll
+                for (int k = 0; k < CH; ++k)
+#pragma unroll
+                    for (int q = 0; q < VEC; ++q) {
+                        const int col = R::col(lane, k) + q;
+                        if (col < a.N) publish(mine + col, sm[k * VEC + q], unsigned(t));
+                    }
+            }
+            __syncthreads();
+            for (int w2 = wave; w2 < a.W; w2 += kWaves) {
+                float got[PL];
+                collect_row<VEC, CH>(sslot + (size_t(b) * a.W + w2) * a.N, unsigned(t), a.N,
+                                     a.spin_limit, a.status, dead, got);
+                R::store(lds + w2 * a.N, lane, a.N, got);
+            }
+            __syncthreads();
+            for (int j = threadIdx.x; j < a.N; j += kThreads) {
+                const float vj = lds_v[cur * a.N + j];
+                if (vj != vj) {
+                    float s = 0.0f;
+                    for (int w2 = 0; w2 < a.W; ++w2) s += lds[w2 * a.N + j];
+                    lds_v[cur * a.N + j] = lds_lb[j] - (lds_mx[j] + logf(fmaxf(s, sk::kSumFloor)));
+                }
+            }
+        }
+        __syncthreads();
+        if (a.v_hist && w == 0)
+            for (int j = threadIdx.x; j < a.N; j += kThreads)
+                a.v_hist[(size_t(t - 1) * a.B + b) * a.N + j] = lds_v[cur * a.N + j];
+        // Lagged stop test on iteration t-1.
+        if (check && t >= 2) {
+            const float g = global_delta(a, t - 1, scratch, dead);
+            if (g < a.tol) {
+                used = t - 1;
+                conv = 1;
+                break;
+            }
+        }
+        R::load(lds_v + cur * a.N, lane, a.N, v, 0.0f);
+    }
+    if (check && conv == 0 && a.max_iter >= 1) {
+        if (global_delta(a, a.max_iter, scratch, dead) < a.tol) conv = 1;  // the last iteration
+    }
+
+    // P = safe_exp(K + u + v) (kernels.cu:755-775) and this workgroup's share of sum(P C).
+    const int par = used & 1;
+    __syncthreads();
+    const bool failed = __hip_atomic_load(a.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
+    float vf[PL];
+    R::load(lds_v + par * a.N, lane, a.N, vf, 0.0f);
+    if (a.v_out && w == 0 && wave == 0) R::store(a.v_out + bN, lane, a.N, vf);
+    const float csign = a.scores_kind < 0 ? 1.0f : -1.0f;  // C = -log_alpha
+    float cacc = 0.0f;
+#pragma unroll
+    for (int k = 0; k < RPW; ++k) {
+        const int l = wave + kWaves * k;
+        const int i = row0 + l;
+        if (i >= rend) continue;
+        const float ui = lds_u[par * ROWS + l];
+        if (a.u_out && lane == 0) a.u_out[bM + i] = ui;
+        float pv[PL];
+#pragma unroll
+        for (int e = 0; e < PL; ++e) {
+            const float lp = (x[k][e] * a.kscale + ui) + vf[e];
+            pv[e] = a.return_log ? lp : safe_exp(lp);
+            if (a.cost_partial && R::valid(lane, e, a.N)) cacc = fmaf(pv[e], csign * x[k][e], cacc);
+            if (failed) pv[e] = __builtin_nanf("");
+        }
+        if (a.plan) R::store(a.plan + (bM + i) * a.N, lane, a.N, pv);
+    }
+    if (a.cost_partial) {
+        const float cs = block_reduce<kWaves>(wave_sum(cacc), scratch + 1, OpSum{});
+        if (threadIdx.x == 0) a.cost_partial[blockIdx.x] = failed ? __builtin_nanf("") : cs;
+    }
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        *a.iters_used = failed ? -1 : used;  // -1: an exchange timed out, the outputs are NaN
+        *a.converged = conv;
+    }
+}
+
+}  // namespace res
+}  // namespace dot_amd

@@ -7,6 +7,7 @@
 #include <string>
 
 #include "host.hpp"
+#include "resident.cuh"
 #include "sinkhorn_kernels.cuh"
 
 namespace dot_amd {
@@ -32,6 +33,14 @@ size_t lds_bytes(int N) { return (size_t(2) * N + 8) * sizeof(float); }
 
 dim3 column_grid(int N, int B) { return dim3((N + kBlock - 1) / kBlock, B); }
 
+// Upper bound on the workgroups of a resident launch: at most kMaxGroup per
+// batch element, at least 16 rows each, and at most 1024 in all.
+size_t resident_groups_max(int B, int M, int N) {
+    if (N > 1024 || N < 1) return 0;
+    const size_t per_b = size_t(std::min((M + res::kWaves - 1) / res::kWaves, res::kMaxGroup));
+    return std::min<size_t>(size_t(B) * per_b, 1024);
+}
+
 struct FwdLayout {
     uint32_t* delta;
     float* ubuf;
@@ -39,6 +48,13 @@ struct FwdLayout {
     size_t zero_words;
     float* partial;
     float* cost_partial;
+    // resident path: tagged exchange slots, cleared before each resident launch
+    unsigned long long* xchg;   // [2, G, N]
+    unsigned long long* fxchg;  // [2, 2, G, N]
+    unsigned long long* dxchg;  // [kDeltaSlots, G]
+    int* status;
+    size_t groups;
+    size_t res_words;           // 32-bit words from xchg through status
     int rows, nstrips;
     size_t bytes;
 };
@@ -53,13 +69,26 @@ FwdLayout fwd_layout(void* ws, int B, int M, int N, int max_iter) {
     L.rows = strip_rows(B, M);
     L.nstrips = (M + L.rows - 1) / L.rows;
     L.partial = c.take<float>(size_t(B) * L.nstrips * N);
-    L.cost_partial = c.take<float>(size_t(B) * L.nstrips);
+    L.cost_partial = c.take<float>(size_t(B) * std::max(L.nstrips, res::kMaxGroup));
+    L.groups = resident_groups_max(B, M, N);
+    const size_t gn = L.groups * size_t(N);
+    const size_t words = 6 * gn + res::kDeltaSlots * L.groups + 1;
+    L.xchg = c.take<unsigned long long>(words);
+    if (L.xchg) {
+        L.fxchg = L.xchg + 2 * gn;
+        L.dxchg = L.fxchg + 4 * gn;
+        L.status = reinterpret_cast<int*>(L.dxchg + res::kDeltaSlots * L.groups);
+    }
+    L.res_words = 2 * words;
     L.bytes = c.used();
     return L;
 }
 
 struct ImpLayout {
     float *r, *rs, *lam, *c, *cs, *mu, *partA, *partB, *tau_partial;
+    unsigned long long* xchg;  // resident path: [2, B*W, N] tagged partials, then status
+    int* status;
+    size_t xchg_words;         // 32-bit words to clear (slots and status)
     int rows, nstrips;
     size_t bytes;
 };
@@ -77,7 +106,12 @@ ImpLayout imp_layout(void* ws, int B, int M, int N) {
     L.mu = c.take<float>(size_t(B) * N);
     L.partA = c.take<float>(size_t(B) * L.nstrips * N);
     L.partB = c.take<float>(size_t(B) * L.nstrips * N);
-    L.tau_partial = c.take<float>(size_t(B) * L.nstrips);
+    L.tau_partial = c.take<float>(size_t(B) * std::max(L.nstrips, 64));
+    // The resident path runs at most one workgroup per CU and only for N <= 1024.
+    const size_t groups = resident_groups_max(B, M, N);
+    L.xchg = c.take<unsigned long long>(2 * groups * size_t(N) + 1);
+    L.status = reinterpret_cast<int*>(L.xchg ? L.xchg + 2 * groups * size_t(N) : nullptr);
+    L.xchg_words = (2 * groups * size_t(N) + 1) * 2;
     L.bytes = c.used();
     return L;
 }
@@ -134,6 +168,165 @@ int check_shape(int B, int M, int N) {
 
 bool valid_tau(float tau) { return std::isfinite(tau) && tau > 0.0f; }
 
+int device_cus() {
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    return cus;
+}
+
+int pow2_ceil(int x) {
+    int p = 1;
+    while (p < x) p *= 2;
+    return p;
+}
+
+// Register-resident configuration: a batch element's rows split over W
+// workgroups of 8 waves, each wave holding RPW rows of PL floats per lane in
+// VGPRs (PL * RPW <= strip_budget), one workgroup per CU.
+struct ResidentCfg {
+    bool ok = false;
+    int vec = 1, ch = 1, rpw = 1, W = 1, R = 1;
+};
+
+// Resident strip budget (floats per lane) for a kernel and row width PL: the
+// forward needs more working registers per row than the adjoint, so with
+// 16-float rows it keeps 64 floats of strip instead of 128.
+template <bool Forward>
+constexpr int strip_budget(int pl) {
+    return (Forward && pl >= 16) ? res::kMaxRegFloats / 2 : res::kMaxRegFloats;
+}
+
+template <bool Forward>
+ResidentCfg resident_config(int B, int M, int N, bool vec4) {
+    ResidentCfg c;
+    const char* env = std::getenv("DOT_AMD_RESIDENT");
+    if (env && env[0] == '0') return c;
+    if (N < 1 || N > 1024 || M < 1 || B < 1) return c;
+    if (N <= 64) {
+        c.vec = 1;
+        c.ch = 1;
+    } else if (vec4) {
+        c.vec = 4;
+        c.ch = pow2_ceil((N + 255) / 256);
+    } else {
+        c.vec = 1;
+        c.ch = pow2_ceil((N + 63) / 64);
+    }
+    const int pl = c.vec * c.ch;
+    int rpw_max = 16;
+    while (rpw_max > 1 && pl * rpw_max > strip_budget<Forward>(pl)) rpw_max /= 2;
+    const int per_wg = res::kWaves * rpw_max;
+    c.W = (M + per_wg - 1) / per_wg;
+    if (c.W > res::kMaxGroup) return c;
+    const int cus = device_cus();
+    if (cus <= 0 || int64_t(B) * c.W > std::min(cus, 1024)) return c;
+    c.R = (M + c.W - 1) / c.W;
+    c.rpw = pow2_ceil((c.R + res::kWaves - 1) / res::kWaves);
+    c.ok = c.rpw <= rpw_max;
+    return c;
+}
+
+template <bool Forward, class F>
+bool dispatch_resident(const ResidentCfg& c, F&& f) {
+    constexpr bool Fwd = Forward;
+    using std::integral_constant;
+    auto rows = [&](auto vc, auto cc) {
+        constexpr int PL = decltype(vc)::value * decltype(cc)::value;
+        switch (c.rpw) {
+            case 1: f(vc, cc, integral_constant<int, 1>{}); return true;
+            case 2: if constexpr (PL * 2 <= strip_budget<Fwd>(PL)) { f(vc, cc, integral_constant<int, 2>{}); return true; } break;
+            case 4: if constexpr (PL * 4 <= strip_budget<Fwd>(PL)) { f(vc, cc, integral_constant<int, 4>{}); return true; } break;
+            case 8: if constexpr (PL * 8 <= strip_budget<Fwd>(PL)) { f(vc, cc, integral_constant<int, 8>{}); return true; } break;
+            case 16: if constexpr (PL * 16 <= strip_budget<Fwd>(PL)) { f(vc, cc, integral_constant<int, 16>{}); return true; } break;
+        }
+        return false;
+    };
+    if (c.vec == 4) {
+        switch (c.ch) {
+            case 1: return rows(integral_constant<int, 4>{}, integral_constant<int, 1>{});
+            case 2: return rows(integral_constant<int, 4>{}, integral_constant<int, 2>{});
+            case 4: return rows(integral_constant<int, 4>{}, integral_constant<int, 4>{});
+        }
+        return false;
+    }
+    switch (c.ch) {
+        case 1: return rows(integral_constant<int, 1>{}, integral_constant<int, 1>{});
+        case 2: return rows(integral_constant<int, 1>{}, integral_constant<int, 2>{});
+        case 4: return rows(integral_constant<int, 1>{}, integral_constant<int, 4>{});
+        case 8: return rows(integral_constant<int, 1>{}, integral_constant<int, 8>{});
+        case 16: return rows(integral_constant<int, 1>{}, integral_constant<int, 16>{});
+    }
+    return false;
+}
+
+constexpr int kSpinLimit = 1 << 20;  // ~1-2 s of polling before a resident kernel gives up
+
+// Cooperative launch of the register-resident forward; false when this shape or
+// device cannot host it (the caller then runs the streaming sweeps).
+bool launch_resident_forward(const dot_sinkhorn_fwd_args* a, const FwdLayout& L, const ResidentCfg& rc,
+                             float kscale, float log_a_default, float log_b_default, bool keep,
+                             bool ret_log, hipStream_t stream) {
+    const int groups = a->B * rc.W;
+    if (!L.xchg || size_t(groups) > L.groups) return false;
+    res::FwdResArgs r{};
+    r.X = a->scores;
+    r.kscale = kscale;
+    r.scores_kind = a->scores_kind;
+    r.log_a = a->log_a;
+    r.log_b = a->log_b;
+    r.log_a_default = log_a_default;
+    r.log_b_default = log_b_default;
+    r.tol = a->tol;
+    r.max_iter = a->max_iter;
+    r.return_log = ret_log ? 1 : 0;
+    r.plan = a->plan;
+    r.cost_partial = a->cost ? L.cost_partial : nullptr;
+    r.u_out = a->u_out;
+    r.v_out = a->v_out;
+    r.u_hist = keep ? a->u_hist : nullptr;
+    r.v_hist = keep ? a->v_hist : nullptr;
+    r.iters_used = a->iters_used;
+    r.converged = a->converged;
+    // The exchange regions are laid out for L.groups workgroups; index them by the real grid.
+    r.xchg = L.xchg;
+    r.fxchg = L.xchg + 2 * size_t(groups) * a->N;
+    r.dxchg = r.fxchg + 4 * size_t(groups) * a->N;
+    r.status = L.status;
+    r.B = a->B;
+    r.M = a->M;
+    r.N = a->N;
+    r.W = rc.W;
+    r.R = rc.R;
+    r.spin_limit = kSpinLimit;
+    bool ok = false;
+    dispatch_resident<true>(rc, [&](auto vc, auto cc, auto rr) {
+        constexpr int V = decltype(vc)::value;
+        constexpr int C = decltype(cc)::value;
+        constexpr int RPW = decltype(rr)::value;
+        const size_t lds =
+            (size_t(12) * a->N + 3 * res::kWaves * RPW + res::kFwdScratch) * sizeof(float);
+        auto kernel = res::forward<V, C, RPW>;
+        int per_cu = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, res::kThreads, lds) != hipSuccess ||
+            per_cu < 1 || int64_t(per_cu) * device_cus() < groups)
+            return;
+        launch_fill_zero(L.xchg, L.res_words, stream);
+        void* params[] = {&r};
+        ProfScope prof("sk_fwd_resident", stream);
+        ok = hipLaunchCooperativeKernel(reinterpret_cast<const void*>(kernel), dim3(groups),
+                                        dim3(res::kThreads), params, static_cast<unsigned>(lds),
+                                        stream) == hipSuccess;
+    });
+    if (!ok) return false;
+    if (a->cost) {
+        ProfScope prof("sk_batch_sum", stream);
+        hipLaunchKernelGGL(sk::batch_sum, dim3(a->B), dim3(kWave), 0, stream, L.cost_partial, rc.W,
+                           1.0f, a->cost);
+    }
+    return true;
+}
+
 }  // namespace
 }  // namespace dot_amd
 
@@ -187,6 +380,12 @@ extern "C" int dot_sinkhorn_forward(const dot_sinkhorn_fwd_args* a, dot_stream_t
     const float log_b_default = -std::log(static_cast<float>(N));
     const bool vec4 = (N % 4 == 0) && aligned16(a->scores) && (!a->plan || aligned16(a->plan));
     const size_t lds = lds_bytes(N);
+
+    const ResidentCfg rc = resident_config<true>(B, M, N, vec4);
+    if (rc.ok && launch_resident_forward(a, L, rc, kscale, log_a_default, log_b_default, keep, ret_log,
+                                         stream))
+        return check_launch("dot_sinkhorn_forward");
+    (void)hipGetLastError();  // a refused cooperative launch falls back to the sweeps
 
     launch_fill_zero(a->workspace, L.zero_words, stream);
 
@@ -318,6 +517,62 @@ int bwd_degenerate(const dot_sinkhorn_bwd_args* a, hipStream_t stream, const cha
 
 }  // namespace
 
+namespace {
+
+// Cooperative launch of the register-resident adjoint; false when this shape or
+// device cannot host it (the caller then runs the streaming sweeps).
+bool launch_resident_adjoint(const dot_sinkhorn_bwd_args* a, const sk::ImpArgs& x,
+                             const ImpLayout& L, const ResidentCfg& rc, hipStream_t stream) {
+    res::ImpResArgs r{};
+    r.X = a->scores;
+    r.scores_kind = a->scores_kind;
+    r.gP = a->grad_plan;
+    r.gC = a->grad_cost;
+    r.P = a->plan;
+    r.r = x.r;
+    r.rs = x.rs;
+    r.c = x.c;
+    r.cs = x.cs;
+    r.xchg = L.xchg;
+    r.grad = a->grad_scores;
+    r.tau_partial = L.tau_partial;
+    r.status = L.status;
+    r.inv_tau = x.inv_tau;
+    r.M = a->M;
+    r.N = a->N;
+    r.W = rc.W;
+    r.R = rc.R;
+    r.iters = a->iters;
+    r.spin_limit = kSpinLimit;
+    const int groups = a->B * rc.W;
+    if (size_t(groups) * size_t(a->N) * 2 + 1 > L.xchg_words / 2) return false;
+    bool ok = false;
+    dispatch_resident<false>(rc, [&](auto vc, auto cc, auto rr) {
+        constexpr int V = decltype(vc)::value;
+        constexpr int C = decltype(cc)::value;
+        constexpr int RPW = decltype(rr)::value;
+        const size_t lds = (size_t(11) * a->N + 3 * res::kWaves * RPW + 16) * sizeof(float);
+        auto kernel = res::implicit_adjoint<V, C, RPW>;
+        int per_cu = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, res::kThreads, lds) != hipSuccess ||
+            per_cu < 1 || int64_t(per_cu) * device_cus() < groups)
+            return;
+        launch_fill_zero(L.xchg, L.xchg_words, stream);
+        void* params[] = {&r};
+        ProfScope prof("sk_imp_resident", stream);
+        ok = hipLaunchCooperativeKernel(reinterpret_cast<const void*>(kernel), dim3(groups),
+                                        dim3(res::kThreads), params, static_cast<unsigned>(lds),
+                                        stream) == hipSuccess;
+    });
+    if (!ok) return false;
+    ProfScope prof("sk_batch_sum", stream);
+    hipLaunchKernelGGL(sk::batch_sum, dim3(a->B), dim3(kWave), 0, stream, L.tau_partial, rc.W,
+                       -x.inv_tau, a->grad_tau);
+    return true;
+}
+
+}  // namespace
+
 extern "C" size_t dot_sinkhorn_backward_implicit_workspace_bytes(int B, int M, int N) {
     if (B < 0 || M < 0 || N < 0) return 0;
     return imp_layout(nullptr, B, M, N).bytes;
@@ -353,6 +608,7 @@ extern "C" int dot_sinkhorn_backward_implicit(const dot_sinkhorn_bwd_args* a, do
     x.rows = L.rows;
     const size_t lds = lds_bytes(N);
     const dim3 strips(L.nstrips, B);
+    const ResidentCfg rc = resident_config<false>(B, M, N, bwd_vec4(a));
     bool launched = dispatch_row(N, bwd_vec4(a), [&](auto vc, auto cc) {
         constexpr int V = decltype(vc)::value;
         constexpr int C = decltype(cc)::value;
@@ -364,6 +620,8 @@ extern "C" int dot_sinkhorn_backward_implicit(const dot_sinkhorn_bwd_args* a, do
             ProfScope prof("sk_imp_prep_combine", stream);
             hipLaunchKernelGGL(sk::imp_prep_combine, column_grid(N, B), dim3(kBlock), 0, stream, x);
         }
+        if (rc.ok && launch_resident_adjoint(a, x, L, rc, stream)) return;
+        (void)hipGetLastError();  // a refused cooperative launch falls back to the sweeps
         for (int it = 0; it < a->iters; ++it) {
             {
                 ProfScope prof("sk_imp_sweep", stream);

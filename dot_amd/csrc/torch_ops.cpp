@@ -153,6 +153,7 @@ Tensor sinkhorn_log_op(Tensor log_alpha, double tau, int64_t n_iters, optional<T
 std::vector<Tensor> counts_to_cpu(const Tensor& counts) {
     Tensor c = counts.to(at::kCPU);
     const int32_t* p = c.data_ptr<int32_t>();
+    TORCH_CHECK(p[0] >= 0, "dot_sinkhorn_forward: a cross-workgroup exchange timed out (outputs are NaN)");
     auto opt = at::TensorOptions().dtype(at::kLong).device(at::kCPU);
     return {at::scalar_tensor(int64_t(p[0]), opt), at::scalar_tensor(int64_t(p[1]), opt)};
 }

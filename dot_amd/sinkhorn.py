@@ -143,6 +143,8 @@ def _run_fused(scores, reg, scores_kind, n_iters, backward_iters, log_a, log_b, 
         mode, want_cost
     )
     used, conv = (int(x) for x in counts.tolist())
+    if used < 0:
+        raise RuntimeError("dot_sinkhorn_forward: a cross-workgroup exchange timed out (outputs are NaN)")
     return P, cost, used, bool(conv)
 
 

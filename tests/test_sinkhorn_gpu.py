@@ -498,3 +498,108 @@ def test_config_c5_full_size():
     r5 = dot_amd.sinkhorn(C[:1], reg=0.02, n_iters=5, tol=0)
     Po = osk.dual_forward(-C[:1].cpu().numpy(), 0.02, 5).P
     assert rel_err(r5.transport_plan, Po) < FWD_TOL
+
+
+@pytest.mark.parametrize("B,M,N,tau,T", [(8, 64, 64, 1.0, 100), (4, 512, 512, 0.1, 150),
+                                         (3, 130, 70, 0.5, 40), (2, 1000, 1024, 0.2, 30),
+                                         (1, 2048, 256, 0.3, 20)])
+def test_resident_and_streaming_adjoints_agree_with_oracle(B, M, N, tau, T, monkeypatch):
+    """The register-resident adjoint (one cooperative launch) and the streaming
+    sweeps (one launch pair per sweep) against the oracle on the same inputs."""
+    rng = np.random.default_rng(M + N)
+    C = rng.random((B, M, N)).astype(np.float32)
+    G = rng.standard_normal((B, M, N)).astype(np.float32)
+    Po, go, gto = osk.with_grads_implicit(-C, G, tau, T, T)
+    out = {}
+    for mode in ("1", "0"):
+        monkeypatch.setenv("DOT_AMD_RESIDENT", mode)
+        P, g, gt = _ops.sinkhorn_with_grads_implicit(_t(-C), _t(G), tau, T, T)
+        assert rel_err(P, Po) < FWD_TOL
+        assert rel_err(g, go) < GRAD_TOL, mode
+        assert sum_err(gt, gto, go * -C / tau) < GRAD_TOL
+        out[mode] = g
+    assert rel_err(out["1"], out["0"].cpu().numpy()) < 1e-5
+
+
+def _both_paths(monkeypatch, fn):
+    """fn() with the register-resident kernels allowed ("1") and disabled ("0")."""
+    out = {}
+    for mode in ("1", "0"):
+        monkeypatch.setenv("DOT_AMD_RESIDENT", mode)
+        out[mode] = fn()
+    monkeypatch.delenv("DOT_AMD_RESIDENT")
+    return out
+
+
+@pytest.mark.parametrize("B,M,N,tau,T,tol,nonuni", [
+    (8, 64, 64, 1.0, 50, 0.0, False),
+    (16, 512, 512, 0.1, 200, 1e-4, False),
+    (4, 96, 128, 0.05, 300, 1e-6, True),
+    (3, 130, 70, 0.5, 40, 0.0, True),
+    (2, 1000, 1024, 0.2, 20, 0.0, False),
+    (5, 300, 257, 0.3, 60, 1e-5, True),
+    (1, 7, 3, 0.7, 25, 1e-6, True),
+])
+def test_resident_and_streaming_forwards_agree_with_oracle(B, M, N, tau, T, tol, nonuni, monkeypatch):
+    """The register-resident forward (one cooperative launch, lagged on-device
+    stop test) and the streaming sweeps against the oracle, each at its own
+    iteration count.  The two fp32 paths stop within one iteration of each
+    other; the float64 oracle may stop earlier, where the fp32 change of u sits
+    at its rounding floor near tol (|u| ~ 10 has an ulp of 1e-6)."""
+    rng = np.random.default_rng(B * M + N)
+    C = rng.random((B, M, N)).astype(np.float32)
+    lga = np.log(_dirichlet(rng, B, M)) if nonuni else None
+    lgb = np.log(_dirichlet(rng, B, N)) if nonuni else None
+    args = (_t(-C), tau, T, tol, None if lga is None else _t(lga), None if lgb is None else _t(lgb))
+    res = _both_paths(monkeypatch, lambda: _ops.sinkhorn_dual_forward(*args))
+    counts = {mode: int(r[1]) for mode, r in res.items()}
+    assert abs(counts["1"] - counts["0"]) <= 1, counts
+    for mode, (P, used, conv) in res.items():
+        used = int(used)
+        assert int(conv) == (1 if tol > 0 and used < T else 0) or (tol > 0 and used == T), (mode, used)
+        Po = osk.dual_forward(-C, tau, used, log_a=lga, log_b=lgb).P
+        assert rel_err(P, Po) < FWD_TOL, mode
+    if counts["1"] == counts["0"]:
+        assert rel_err(res["1"][0], res["0"][0].cpu().numpy()) < 1e-5
+
+
+def test_resident_forward_outputs_cost_log_and_history(monkeypatch):
+    """Cost-kind scores with the transport cost, log-plan output and the
+    per-iteration history of the unrolled mode, resident against streaming."""
+    rng = np.random.default_rng(11)
+    B, M, N, tau, T = 6, 200, 136, 0.25, 30
+    C = _t(rng.random((B, M, N)).astype(np.float32))
+    lga = _t(np.log(_dirichlet(rng, B, M)))
+    fused = lambda: _ops.fused.sinkhorn_forward(C, -1, tau, T, 0.0, lga, None, True, True)
+    res = _both_paths(monkeypatch, fused)
+    for i, name in enumerate(("plan", "cost", "counts", "u_hist", "v_hist")):
+        a, b = res["1"][i], res["0"][i]
+        if name == "counts":
+            assert a.tolist() == b.tolist() == [T, 0]
+        else:
+            assert rel_err(a, b.cpu().numpy()) < 1e-5, name
+    o = osk.dual_forward(-C.cpu().numpy(), tau, T, log_a=lga.cpu().numpy(), keep_history=True)
+    assert rel_err(res["1"][0], o.P) < FWD_TOL
+    assert rel_err(res["1"][1], osk.transport_cost(o.P, C.cpu().numpy())) < FWD_TOL
+    # dual potentials are log-domain: an absolute error e is a relative error e of P
+    for i, hist in ((3, o.u_hist), (4, o.v_hist)):
+        for mode in ("1", "0"):
+            assert np.abs(res[mode][i].cpu().numpy() - hist).max() < FWD_TOL, (i, mode)
+    logP = _both_paths(monkeypatch, lambda: _ops.sinkhorn_dual_forward(-C, tau, T, 0.0, lga, None, True))
+    assert (logP["1"][0] - logP["0"][0]).abs().max().item() < 1e-4
+
+
+def test_resident_forward_exact_column_fallback(monkeypatch):
+    """A column far costlier than the rest underflows the shared-exponential
+    column sum at small reg; both paths take the exact max-shifted LSE for it."""
+    rng = np.random.default_rng(5)
+    B, M, N, tau, T = 4, 160, 96, 0.01, 15
+    C = (0.1 * rng.random((B, M, N))).astype(np.float32)
+    C[:, :, 7] = 0.7   # exp(K - row max) <= exp(-60): the column sum is exactly 0 in fp32
+    C[1, :, 50] = 0.8
+    res = _both_paths(monkeypatch, lambda: _ops.sinkhorn_dual_forward(_t(-C), tau, T, 0.0))
+    Po = osk.dual_forward(-C, tau, T).P
+    for mode, (P, used, _) in res.items():
+        assert int(used) == T
+        assert torch.isfinite(P).all(), mode
+        assert rel_err(P, Po) < FWD_TOL, mode
