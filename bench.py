@@ -331,6 +331,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="approximate CPU time of each CPU-baseline sample")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="only run 20 device copies of MIB MiB each (calibrates rocprofv3 "
+                         "FETCH_SIZE / WRITE_SIZE against a known byte count) and exit")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -343,6 +346,17 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs a HIP device", file=sys.stderr)
         sys.exit(1)
+    if args.copy_probe:
+        n = args.copy_probe * (1 << 20) // 4
+        src = torch.rand(n, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(20):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_probe_bytes_read": 4 * n, "copy_probe_bytes_written": 4 * n,
+                          "copies": 20}), flush=True)
+        return
+
     sys.path.insert(0, ROOT)
     import dot_amd
     from dot_amd import profiler

@@ -129,54 +129,227 @@ __device__ __forceinline__ void tree_combine(float (&acc)[VEC * CH], float* lds,
     }
 }
 
+// Lane exchange across the two 32-lane halves (lane ^ 32).
+__device__ __forceinline__ float xor32(float x) {
+    const int lane = threadIdx.x % kWave;
+    return __builtin_bit_cast(
+        float, __builtin_amdgcn_ds_bpermute((lane ^ 32) << 2, __builtin_bit_cast(int, x)));
+}
+
+// Partner patterns of the transposed reduction, in the order they are used:
+// row mirror (lane ^ 15), half-row mirror (lane ^ 7), quad xor 2, quad xor 1.
+// Each flips the lane bit that step s selects on (3 - s) and none of the
+// bits selected on by earlier steps, so partners always hold the same rows.
+template <int S>
+__device__ __forceinline__ float tstep_move(float x) {
+    if constexpr (S == 0) return dpp_move<kDppRowMirror>(x);
+    else if constexpr (S == 1) return dpp_move<kDppRowHalfMirror>(x);
+    else if constexpr (S == 2) return dpp_move<kDppQuadXor2>(x);
+    else return dpp_move<kDppQuadXor1>(x);
+}
+
+constexpr int ilog2(int x) { return x <= 1 ? 0 : 1 + ilog2(x / 2); }
+
+template <int N, int S>
+__device__ __forceinline__ float tsum_level(const float* v, int lane) {
+    if constexpr (N == 1) {
+        float x = v[0];
+        if constexpr (S <= 0) x += tstep_move<0>(x);
+        if constexpr (S <= 1) x += tstep_move<1>(x);
+        if constexpr (S <= 2) x += tstep_move<2>(x);
+        if constexpr (S <= 3) x += tstep_move<3>(x);
+        x += swizzle_xor16(x);
+        return x + xor32(x);
+    } else {
+        constexpr int H = N / 2;
+        const bool upper = (lane >> (3 - S)) & 1;
+        float w[H];
+#pragma unroll
+        for (int j = 0; j < H; ++j) {
+            const float keep = upper ? v[j + H] : v[j];
+            const float send = upper ? v[j] : v[j + H];
+            w[j] = keep + tstep_move<S>(send);
+        }
+        return tsum_level<H, S + 1>(w, lane);
+    }
+}
+
+// Wave sums of RPW per-lane values at once (RPW a power of two <= 16): at each
+// butterfly step the two partner lanes trade halves of their remaining rows,
+// so step s moves RPW / 2^(s+1) values instead of RPW.  Every lane returns the
+// wave total of row slot_of_lane(lane); the four lanes that share a slot
+// return the same bits.
+template <int RPW>
+__device__ __forceinline__ float transposed_sum(const float (&v)[RPW]) {
+    static_assert(RPW >= 1 && RPW <= 16 && (RPW & (RPW - 1)) == 0, "RPW must be 1, 2, 4, 8 or 16");
+    return tsum_level<RPW, 0>(v, threadIdx.x % kWave);
+}
+
+template <int RPW>
+__device__ __forceinline__ int slot_of_lane(int lane) {
+    return (lane & 15) >> (4 - ilog2(RPW));
+}
+
+template <int RPW>
+__device__ __forceinline__ int lane_of_slot(int k) {
+    return k << (4 - ilog2(RPW));
+}
+
+constexpr int kColsPerThread = (1024 + kThreads - 1) / kThreads;  // N <= 1024
+
+// Batch-element column totals for this thread's columns j = tid + q*kThreads.
+// `part` holds one row of N per wave; the workgroup's sum of column j is the
+// sum of those rows in wave order, published with tag t into slot row
+// blockIdx.x; the total adds the W workgroups' sums of the element in
+// workgroup order (every workgroup of the element gets the same bits).
+// f(j, total) consumes each total; totals are NaN after a timeout.
+template <class F>
+__device__ __forceinline__ void exchange_columns(const float* part, unsigned long long* slot, int N,
+                                                 int b, int W, int w, unsigned t, int spin_limit,
+                                                 int* status, bool& dead, F&& f) {
+    float own[kColsPerThread];
+#pragma unroll
+    for (int q = 0; q < kColsPerThread; ++q) {
+        const int j = threadIdx.x + q * kThreads;
+        own[q] = 0.0f;
+        if (j < N) {
+            float s = 0.0f;
+#pragma unroll
+            for (int v = 0; v < kWaves; ++v) s += part[v * N + j];
+            own[q] = s;
+            publish(slot + size_t(blockIdx.x) * N + j, s, t);
+        }
+    }
+#pragma unroll 1
+    for (int q = 0; q < kColsPerThread; ++q) {
+        const int j = threadIdx.x + q * kThreads;
+        if (j >= N) continue;
+        unsigned long long* base = slot + size_t(b) * W * N + j;
+        float got[kMaxGroup];
+        for (int spins = 0; !dead; ++spins) {
+            bool ready = true;
+#pragma unroll
+            for (int g = 0; g < kMaxGroup; ++g) {
+                got[g] = 0.0f;
+                if (g < W && g != w) {
+                    const unsigned long long x =
+                        __hip_atomic_load(base + size_t(g) * N, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    ready = ready && static_cast<unsigned>(x >> 32) == t;
+                    got[g] = __uint_as_float(static_cast<unsigned>(x));
+                }
+            }
+            if (ready) break;
+            if (((spins & 255) == 255 &&
+                 __hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) ||
+                spins >= spin_limit) {
+                if (spins >= spin_limit) atomicOr(status, 1);
+                dead = true;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+        float tot = 0.0f;
+#pragma unroll
+        for (int g = 0; g < kMaxGroup; ++g)
+            if (g < W) tot += (g == w) ? own[q] : got[g];
+        f(j, dead ? __builtin_nanf("") : tot);
+    }
+}
+
 struct ImpResArgs {
-    const float* X;        // scores (for the gradient's log_alpha and the cost-path G)
+    const float* X;            // scores
     int scores_kind;
-    const float* gP;       // [B,M,N] or null
-    const float* gC;       // [B] or null
-    const float* P;        // [B,M,N]
-    const float* r;        // [B,M] sum_k P G
-    const float* rs;       // [B,M] sum_k P
-    const float* c;        // [B,N] sum_i P G
-    const float* cs;       // [B,N] sum_i P
-    unsigned long long* xchg;  // [2,B,W,N] tagged partials
-    float* grad;           // [B,M,N]
-    float* tau_partial;    // [B*W]
+    const float* gP;           // [B,M,N] or null
+    const float* gC;           // [B] or null
+    const float* P;            // [B,M,N]
+    unsigned long long* xchg;  // [2, G, N] tagged sweep column sums
+    unsigned long long* pro;   // [2, G, N] tagged prologue column sums (P G, then P)
+    float* grad;               // [B,M,N]
+    float* tau_partial;        // [G]
     int* status;
     float inv_tau;
     int M, N, W, R, iters, spin_limit;
 };
 
-// The implicit adjoint (kernels.cu:965-1098) with P held in registers.
-// Per iteration: lambda_i = (r_i - sum_k P mu_k) / max(rs_i, 1e-12) for the
-// workgroup's rows, the workgroup's column sums of P lambda, one tagged
-// exchange with the batch element's other workgroups, then
-// mu_k = (c_k - sum_i P lambda) / max(cs_k, 1e-12).  The final phase streams
-// G and writes grad = P (G - lambda - mu) / tau (cost path: grad_cost P - that).
+// Upstream gradient of one row: G = grad_plan + grad_cost[b] * C, C = csign * scores.
+template <int VEC, int CH>
+__device__ __forceinline__ void upstream_row(const ImpResArgs& a, size_t off, int lane, float gc,
+                                             float csign, float (&x)[VEC * CH], float (&G)[VEC * CH]) {
+    using R = Row<VEC, CH>;
+    R::load(a.X + off, lane, a.N, x, 0.0f);
+    if (a.gP) {
+        R::load(a.gP + off, lane, a.N, G, 0.0f);
+    } else {
+#pragma unroll
+        for (int e = 0; e < R::PL; ++e) G[e] = 0.0f;
+    }
+    if (a.gC) {
+#pragma unroll
+        for (int e = 0; e < R::PL; ++e) G[e] += gc * (csign * x[e]);
+    }
+}
+
+// The implicit adjoint (kernels.cu:965-1098) with P held in registers, in one
+// launch.  Prologue: r_i = sum_k P G, rs_i = sum_k P for this workgroup's rows
+// and, through one exchange each, c_k = sum_i P G and cs_k = sum_i P over the
+// batch element.  Each of the `iters` Gauss-Seidel sweeps (from lambda = mu = 0):
+//   lambda_i = (r_i - sum_k P mu_k) / max(rs_i, 1e-12)   (all rows of a wave at once)
+//   mu_k = (c_k - sum_i P lambda_i) / max(cs_k, 1e-12)   (one exchange)
+// Final phase: grad = P (G - lambda - mu) / tau (cost kind: grad_cost P - that;
+// log-alpha kind: that - grad_cost P) and this workgroup's share of
+// sum(grad * log_alpha) for grad_tau.
 template <int VEC, int CH, int RPW>
 __global__ __launch_bounds__(kThreads) void implicit_adjoint(ImpResArgs a) {
     using R = Row<VEC, CH>;
     constexpr int PL = R::PL;
-    constexpr int ROWS = kWaves * RPW;  // rows per workgroup
-    // LDS: tree 8N | mu N | c N | cs N | r ROWS | 1/rs ROWS | lambda ROWS | scratch 16
+    // LDS: one row of N per wave | mu N | scratch kWaves
     extern __shared__ float lds[];
-    float* lds_mu = lds + 8 * a.N;
-    float* lds_c = lds_mu + a.N;
-    float* lds_cs = lds_c + a.N;
-    float* lds_r = lds_cs + a.N;
-    float* lds_rs = lds_r + ROWS;
-    float* lds_lam = lds_rs + ROWS;
-    float* scratch = lds_lam + ROWS;
+    float* part = lds;
+    float* lds_mu = lds + kWaves * a.N;
+    float* scratch = lds_mu + a.N;
     const int lane = threadIdx.x % kWave;
     const int wave = threadIdx.x / kWave;
+    const int G = gridDim.x;
     const int b = blockIdx.x / a.W;
     const int w = blockIdx.x % a.W;
     const int row0 = w * a.R;
     const int rend = min(row0 + a.R, a.M);
     const size_t bM = size_t(b) * a.M;
-    const size_t bN = size_t(b) * a.N;
+    const bool cost_kind = a.scores_kind < 0;
+    const float gc = a.gC ? a.gC[b] : 0.0f;
+    const float csign = cost_kind ? 1.0f : -1.0f;  // C = csign * scores
+    bool dead = false;
 
-    // local row index l = wave + kWaves * k  <->  global row row0 + l
+    // Prologue, streamed (one row at a time, nothing kept): row sums r and rs
+    // of this lane's row slot and the workgroup's column partials of P G and P.
+    float cg[PL], cp[PL];
+    float r_l = 0.0f, rs_l = 0.0f;
+#pragma unroll
+    for (int e = 0; e < PL; ++e) cg[e] = cp[e] = 0.0f;
+#pragma unroll 1
+    for (int k = 0; k < RPW; ++k) {
+        const int i = row0 + wave + kWaves * k;
+        if (i >= rend) break;
+        const size_t off = (bM + i) * a.N;
+        float pr[PL], x[PL], Gr[PL];
+        R::load(a.P + off, lane, a.N, pr, 0.0f);
+        upstream_row<VEC, CH>(a, off, lane, gc, csign, x, Gr);
+        float sg = 0.0f, sp = 0.0f;
+#pragma unroll
+        for (int e = 0; e < PL; ++e) {
+            sg = fmaf(pr[e], Gr[e], sg);
+            sp += pr[e];
+            cg[e] = fmaf(pr[e], Gr[e], cg[e]);
+            cp[e] += pr[e];
+        }
+        sg = wave_sum(sg);
+        sp = wave_sum(sp);
+        if (slot_of_lane<RPW>(lane) == k) {
+            r_l = sg;
+            rs_l = sp;
+        }
+    }
+    // The strip of P, held in registers from here on (a second read of the rows).
     float p[RPW][PL];
 #pragma unroll
     for (int k = 0; k < RPW; ++k) {
@@ -188,102 +361,70 @@ __global__ __launch_bounds__(kThreads) void implicit_adjoint(ImpResArgs a) {
             for (int e = 0; e < PL; ++e) p[k][e] = 0.0f;
         }
     }
-    for (int l = threadIdx.x; l < ROWS; l += kThreads) {
-        const int i = row0 + l;
-        const bool ok = i < rend;
-        lds_r[l] = ok ? a.r[bM + i] : 0.0f;
-        lds_rs[l] = ok ? fmaxf(a.rs[bM + i], 1.0e-12f) : 1.0f;
-        lds_lam[l] = 0.0f;
-    }
-    for (int j = threadIdx.x; j < a.N; j += kThreads) {
-        lds_c[j] = a.c[bN + j];
-        lds_cs[j] = fmaxf(a.cs[bN + j], 1.0e-12f);
-    }
+    const float inv_rs = 1.0f / fmaxf(rs_l, sk::kSumFloor);
+    float c_own[kColsPerThread], cs_own[kColsPerThread];
+    R::store(part + wave * a.N, lane, a.N, cg);
     __syncthreads();
+    exchange_columns(part, a.pro, a.N, b, a.W, w, 1u, a.spin_limit, a.status, dead,
+                     [&](int j, float tot) { c_own[(j - threadIdx.x) / kThreads] = tot; });
+    __syncthreads();
+    R::store(part + wave * a.N, lane, a.N, cp);
+    __syncthreads();
+    exchange_columns(part, a.pro + size_t(G) * a.N, a.N, b, a.W, w, 1u, a.spin_limit, a.status, dead,
+                     [&](int j, float tot) { cs_own[(j - threadIdx.x) / kThreads] = fmaxf(tot, sk::kSumFloor); });
+
+    // Sweeps.
     float mu[PL];
 #pragma unroll
     for (int e = 0; e < PL; ++e) mu[e] = 0.0f;
-    bool dead = false;
-
+    float lam_l = 0.0f;
     for (int t = 1; t <= a.iters; ++t) {
+        float d[RPW];  // one dependent chain per row; the rows give the parallelism
+#pragma unroll
+        for (int k = 0; k < RPW; ++k) {
+            d[k] = 0.0f;
+#pragma unroll
+            for (int e = 0; e < PL; ++e) d[k] = fmaf(p[k][e], mu[e], d[k]);
+        }
+        lam_l = (r_l - transposed_sum<RPW>(d)) * inv_rs;
         float acc[PL];
 #pragma unroll
         for (int e = 0; e < PL; ++e) acc[e] = 0.0f;
 #pragma unroll
         for (int k = 0; k < RPW; ++k) {
-            const int l = wave + kWaves * k;
-            float d0 = 0.0f, d1 = 0.0f;
+            const float lk = read_lane(lam_l, lane_of_slot<RPW>(k));
 #pragma unroll
-            for (int e = 0; e < PL; e += 2) {
-                d0 = fmaf(p[k][e], mu[e], d0);
-                if (e + 1 < PL) d1 = fmaf(p[k][e + 1], mu[e + 1], d1);
-            }
-            const float dot = wave_sum(d0 + d1);
-            const float lam = (lds_r[l] - dot) / lds_rs[l];
-#pragma unroll
-            for (int e = 0; e < PL; ++e) acc[e] = fmaf(p[k][e], lam, acc[e]);
-            if (lane == 0) lds_lam[l] = lam;
+            for (int e = 0; e < PL; ++e) acc[e] = fmaf(p[k][e], lk, acc[e]);
         }
-        tree_combine<VEC, CH>(acc, lds, a.N);
-        // Exchange: wave 0 publishes this workgroup's column sums; waves 0..W-1 each
-        // collect one workgroup's row into LDS (all loads of a wave in flight at once).
-        unsigned long long* slot = a.xchg + size_t(t & 1) * gridDim.x * a.N;
-        if (wave == 0) {
-            unsigned long long* mine = slot + size_t(blockIdx.x) * a.N;
-#pragma unroll
-            for (int k = 0; k < CH; ++k) {
-#pragma unroll
-                for (int v = 0; v < VEC; ++v) {
-                    const int col = R::col(lane, k) + v;
-                    if (col < a.N) publish(mine + col, acc[k * VEC + v], unsigned(t));
-                }
-            }
-        }
-        __syncthreads();  // the tree area is reused for the collected rows
-        unsigned long long* batch = slot + size_t(b) * a.W * a.N;
-        for (int w2 = wave; w2 < a.W; w2 += kWaves) {
-            float got[PL];
-            collect_row<VEC, CH>(batch + size_t(w2) * a.N, unsigned(t), a.N, a.spin_limit, a.status,
-                                 dead, got);
-            R::store(lds + w2 * a.N, lane, a.N, got);  // W <= kMaxGroup rows fit the tree area
-        }
+        __syncthreads();  // previous readers of part and lds_mu are done
+        R::store(part + wave * a.N, lane, a.N, acc);
         __syncthreads();
-        for (int j = threadIdx.x; j < a.N; j += kThreads) {
-            float s = 0.0f;
-            for (int w2 = 0; w2 < a.W; ++w2) s += lds[w2 * a.N + j];
-            lds_mu[j] = (lds_c[j] - s) / lds_cs[j];
-        }
+        exchange_columns(part, a.xchg + size_t(t & 1) * G * a.N, a.N, b, a.W, w, unsigned(t),
+                         a.spin_limit, a.status, dead, [&](int j, float tot) {
+                             const int q = (j - threadIdx.x) / kThreads;
+                             lds_mu[j] = (c_own[q] - tot) / cs_own[q];
+                         });
         __syncthreads();
         R::load(lds_mu, lane, a.N, mu, 0.0f);
     }
 
-    // Final phase: stream G and write the gradient of this workgroup's rows.
-    const bool cost_kind = a.scores_kind < 0;
-    const float gc = (cost_kind && a.gC) ? a.gC[b] : 0.0f;
+    // Final phase: stream G again and write this workgroup's gradient rows.
     const bool failed = __hip_atomic_load(a.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
     float tacc = 0.0f;
 #pragma unroll
     for (int k = 0; k < RPW; ++k) {
-        const int l = wave + kWaves * k;
-        const int i = row0 + l;
+        const int i = row0 + wave + kWaves * k;
+        const float lam = read_lane(lam_l, lane_of_slot<RPW>(k));
         if (i >= rend) continue;
-        const float lam = lds_lam[l];
         const size_t off = (bM + i) * a.N;
-        float x[PL], G[PL];
-        R::load(a.X + off, lane, a.N, x, 0.0f);
-        if (a.gP) R::load(a.gP + off, lane, a.N, G, 0.0f);
-        else {
-#pragma unroll
-            for (int e = 0; e < PL; ++e) G[e] = 0.0f;
-        }
-        float o[PL];
+        float x[PL], Gr[PL], o[PL];
+        upstream_row<VEC, CH>(a, off, lane, gc, csign, x, Gr);
 #pragma unroll
         for (int e = 0; e < PL; ++e) {
-            if (a.gC) G[e] += gc * (cost_kind ? x[e] : -x[e]);
-            const float gl = (p[k][e] * ((G[e] - lam) - mu[e])) * a.inv_tau;
+            const float gl = (p[k][e] * ((Gr[e] - lam) - mu[e])) * a.inv_tau;
             const float la = cost_kind ? -x[e] : x[e];
             if (R::valid(lane, e, a.N)) tacc = fmaf(gl, la, tacc);
-            o[e] = failed ? __builtin_nanf("") : (cost_kind ? gc * p[k][e] - gl : gl);
+            o[e] = failed ? __builtin_nanf("") : (cost_kind ? gc * p[k][e] - gl : gl - gc * p[k][e]);
         }
         R::store(a.grad + off, lane, a.N, o);
     }
@@ -293,7 +434,6 @@ __global__ __launch_bounds__(kThreads) void implicit_adjoint(ImpResArgs a) {
 
 }  // namespace res
 }  // namespace dot_amd
-
 
 namespace dot_amd {
 namespace res {

@@ -86,8 +86,9 @@ FwdLayout fwd_layout(void* ws, int B, int M, int N, int max_iter) {
 
 struct ImpLayout {
     float *r, *rs, *lam, *c, *cs, *mu, *partA, *partB, *tau_partial;
-    unsigned long long* xchg;  // resident path: [2, B*W, N] tagged partials, then status
+    unsigned long long* xchg;  // resident path: tagged exchange slots, then status
     int* status;
+    size_t groups;             // workgroups the slots are laid out for
     size_t xchg_words;         // 32-bit words to clear (slots and status)
     int rows, nstrips;
     size_t bytes;
@@ -109,9 +110,11 @@ ImpLayout imp_layout(void* ws, int B, int M, int N) {
     L.tau_partial = c.take<float>(size_t(B) * std::max(L.nstrips, 64));
     // The resident path runs at most one workgroup per CU and only for N <= 1024.
     const size_t groups = resident_groups_max(B, M, N);
-    L.xchg = c.take<unsigned long long>(2 * groups * size_t(N) + 1);
-    L.status = reinterpret_cast<int*>(L.xchg ? L.xchg + 2 * groups * size_t(N) : nullptr);
-    L.xchg_words = (2 * groups * size_t(N) + 1) * 2;
+    // [2, G, N] sweep slots, [2, G, N] prologue slots, then the status word
+    L.groups = groups;
+    L.xchg = c.take<unsigned long long>(4 * groups * size_t(N) + 1);
+    L.status = reinterpret_cast<int*>(L.xchg ? L.xchg + 4 * groups * size_t(N) : nullptr);
+    L.xchg_words = (4 * groups * size_t(N) + 1) * 2;
     L.bytes = c.used();
     return L;
 }
@@ -521,37 +524,34 @@ namespace {
 
 // Cooperative launch of the register-resident adjoint; false when this shape or
 // device cannot host it (the caller then runs the streaming sweeps).
-bool launch_resident_adjoint(const dot_sinkhorn_bwd_args* a, const sk::ImpArgs& x,
-                             const ImpLayout& L, const ResidentCfg& rc, hipStream_t stream) {
+bool launch_resident_adjoint(const dot_sinkhorn_bwd_args* a, const ImpLayout& L, const ResidentCfg& rc,
+                             float inv_tau, hipStream_t stream) {
+    const int groups = a->B * rc.W;
+    if (!L.xchg || size_t(groups) > L.groups) return false;
     res::ImpResArgs r{};
     r.X = a->scores;
     r.scores_kind = a->scores_kind;
     r.gP = a->grad_plan;
     r.gC = a->grad_cost;
     r.P = a->plan;
-    r.r = x.r;
-    r.rs = x.rs;
-    r.c = x.c;
-    r.cs = x.cs;
     r.xchg = L.xchg;
+    r.pro = L.xchg + 2 * size_t(groups) * a->N;
     r.grad = a->grad_scores;
     r.tau_partial = L.tau_partial;
     r.status = L.status;
-    r.inv_tau = x.inv_tau;
+    r.inv_tau = inv_tau;
     r.M = a->M;
     r.N = a->N;
     r.W = rc.W;
     r.R = rc.R;
     r.iters = a->iters;
     r.spin_limit = kSpinLimit;
-    const int groups = a->B * rc.W;
-    if (size_t(groups) * size_t(a->N) * 2 + 1 > L.xchg_words / 2) return false;
     bool ok = false;
     dispatch_resident<false>(rc, [&](auto vc, auto cc, auto rr) {
         constexpr int V = decltype(vc)::value;
         constexpr int C = decltype(cc)::value;
         constexpr int RPW = decltype(rr)::value;
-        const size_t lds = (size_t(11) * a->N + 3 * res::kWaves * RPW + 16) * sizeof(float);
+        const size_t lds = (size_t(res::kWaves + 1) * a->N + res::kWaves) * sizeof(float);
         auto kernel = res::implicit_adjoint<V, C, RPW>;
         int per_cu = 0;
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, res::kThreads, lds) != hipSuccess ||
@@ -567,7 +567,7 @@ bool launch_resident_adjoint(const dot_sinkhorn_bwd_args* a, const sk::ImpArgs& 
     if (!ok) return false;
     ProfScope prof("sk_batch_sum", stream);
     hipLaunchKernelGGL(sk::batch_sum, dim3(a->B), dim3(kWave), 0, stream, L.tau_partial, rc.W,
-                       -x.inv_tau, a->grad_tau);
+                       -inv_tau, a->grad_tau);
     return true;
 }
 
@@ -609,6 +609,9 @@ extern "C" int dot_sinkhorn_backward_implicit(const dot_sinkhorn_bwd_args* a, do
     const size_t lds = lds_bytes(N);
     const dim3 strips(L.nstrips, B);
     const ResidentCfg rc = resident_config<false>(B, M, N, bwd_vec4(a));
+    if (rc.ok && launch_resident_adjoint(a, L, rc, inv_tau, stream))
+        return check_launch("dot_sinkhorn_backward_implicit");
+    (void)hipGetLastError();  // a refused cooperative launch falls back to the sweeps
     bool launched = dispatch_row(N, bwd_vec4(a), [&](auto vc, auto cc) {
         constexpr int V = decltype(vc)::value;
         constexpr int C = decltype(cc)::value;
@@ -620,8 +623,6 @@ extern "C" int dot_sinkhorn_backward_implicit(const dot_sinkhorn_bwd_args* a, do
             ProfScope prof("sk_imp_prep_combine", stream);
             hipLaunchKernelGGL(sk::imp_prep_combine, column_grid(N, B), dim3(kBlock), 0, stream, x);
         }
-        if (rc.ok && launch_resident_adjoint(a, x, L, rc, stream)) return;
-        (void)hipGetLastError();  // a refused cooperative launch falls back to the sweeps
         for (int it = 0; it < a->iters; ++it) {
             {
                 ProfScope prof("sk_imp_sweep", stream);

@@ -420,7 +420,7 @@ __global__ __launch_bounds__(kBlock) void imp_final(ImpArgs a) {
     const int r1 = min(r0 + a.rows, a.M);
     const size_t bM = size_t(b) * a.M;
     const bool cost_kind = a.g.scores_kind < 0;
-    const float gc = (cost_kind && a.g.gC) ? a.g.gC[b] : 0.0f;
+    const float gc = a.g.gC ? a.g.gC[b] : 0.0f;
     float mu[R::PL];
     R::load(a.mu + size_t(b) * a.N, lane, a.N, mu, 0.0f);
     float tacc = 0.0f;
@@ -436,7 +436,7 @@ __global__ __launch_bounds__(kBlock) void imp_final(ImpArgs a) {
             const float gl = (p[e] * ((G[e] - lam) - mu[e])) * a.inv_tau;
             const float la = cost_kind ? -x[e] : x[e];
             if (R::valid(lane, e, a.N)) tacc = fmaf(gl, la, tacc);
-            o[e] = cost_kind ? gc * p[e] - gl : gl;
+            o[e] = cost_kind ? gc * p[e] - gl : gl - gc * p[e];
         }
         R::store(a.grad + off, lane, a.N, o);
     }
@@ -471,14 +471,14 @@ __device__ __forceinline__ void unr_epilogue(const UnrArgs& a, int b, size_t off
                                              const float (&x)[VEC * CH], float& tacc) {
     using R = Row<VEC, CH>;
     const bool cost_kind = a.g.scores_kind < 0;
-    const float gc = (cost_kind && a.g.gC) ? a.g.gC[b] : 0.0f;
+    const float gc = a.g.gC ? a.g.gC[b] : 0.0f;
     float o[R::PL];
 #pragma unroll
     for (int e = 0; e < R::PL; ++e) {
         const float gl = gam[e] * a.inv_tau;               // kernels.cu:926-936
         const float la = cost_kind ? -x[e] : x[e];
         if (R::valid(lane, e, a.N)) tacc = fmaf(gam[e], la, tacc);  // kernels.cu:938-963
-        o[e] = cost_kind ? gc * p[e] - gl : gl;
+        o[e] = cost_kind ? gc * p[e] - gl : gl - gc * p[e];
     }
     R::store(a.grad + off, lane, a.N, o);
 }

@@ -96,6 +96,9 @@ class _SinkhornFusedFunction(torch.autograd.Function):
         ctx.mark_non_differentiable(counts)
         if not want_cost:
             ctx.mark_non_differentiable(cost)
+        # An unused plan or cost reaches backward as None, not as a zero-filled
+        # [B, M, N] tensor the adjoint would have to read.
+        ctx.set_materialize_grads(False)
         ctx.save_for_backward(scores, P, counts, u_hist, v_hist)
         ctx.tau = tau_value
         ctx.tau_is_tensor = torch.is_tensor(tau)
@@ -110,6 +113,8 @@ class _SinkhornFusedFunction(torch.autograd.Function):
         scores, P, counts, u_hist, v_hist = ctx.saved_tensors
         if grad_cost is not None and grad_cost.numel() == 0:
             grad_cost = None
+        if grad_P is None and grad_cost is None:
+            return (torch.zeros_like(scores), None, None, None, None, None, None, None, None, None)
         if ctx.mode == _MODE_UNROLLED:
             iters = int(counts[0].item())
             uh, vh = u_hist, v_hist

@@ -87,11 +87,13 @@ int dot_sinkhorn_forward(const dot_sinkhorn_fwd_args* args, dot_stream_t stream)
 /* ---------------------------------------------------------------------- */
 /* Sinkhorn backward                                                       */
 /* ---------------------------------------------------------------------- */
-/* Upstream gradient G of the plan: G = grad_plan + grad_cost[b] * C, either
- * term optional.  Output when scores_kind == DOT_SCORES_LOG_ALPHA:
- * grad_scores = dL/dlog_alpha.  When scores_kind == DOT_SCORES_COST:
- * grad_scores = dL/dC = grad_cost[b] * P - dL/dlog_alpha (the direct term of
- * cost = sum(P * C) plus the path through the plan). */
+/* L = sum(grad_plan * P) + grad_cost[b] * cost[b], cost = sum(P * C), with
+ * C = scores for DOT_SCORES_COST and C = -scores for DOT_SCORES_LOG_ALPHA;
+ * either term optional.  The plan's upstream gradient is G = grad_plan +
+ * grad_cost[b] * C and, with g = the gradient through the plan w.r.t.
+ * log_alpha:  DOT_SCORES_LOG_ALPHA: grad_scores = g - grad_cost[b] * P;
+ * DOT_SCORES_COST: grad_scores = grad_cost[b] * P - g (the direct term of the
+ * cost plus the path through the plan). */
 typedef struct {
     const float* scores;      /* [B,M,N] */
     int scores_kind;
