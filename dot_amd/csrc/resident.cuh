@@ -196,13 +196,26 @@ __device__ __forceinline__ int lane_of_slot(int k) {
 }
 
 constexpr int kColsPerThread = (1024 + kThreads - 1) / kThreads;  // N <= 1024
+constexpr int kXcds = 8;  // MI355X dispatches consecutive workgroups round-robin over 8 XCDs
+
+// Logical index of this workgroup, b * W + w.  When the grid splits evenly,
+// the W workgroups of a batch element are given blocks on one XCD, where an
+// exchange round trip is ~0.9 us instead of ~1.25 us; any bijection is correct.
+__device__ __forceinline__ int logical_group(int W) {
+    const int G = gridDim.x;
+    const int per = G / kXcds;
+    if (G % kXcds == 0 && per % W == 0) return (blockIdx.x % kXcds) * per + blockIdx.x / kXcds;
+    return blockIdx.x;
+}
 
 // Batch-element column totals for this thread's columns j = tid + q*kThreads.
 // `part` holds one row of N per wave; the workgroup's sum of column j is the
-// sum of those rows in wave order, published with tag t into slot row
-// blockIdx.x; the total adds the W workgroups' sums of the element in
+// sum of those rows in wave order, published with tag t into slot row `gid`
+// (= b * W + w); the total adds the W workgroups' sums of the element in
 // workgroup order (every workgroup of the element gets the same bits).
-// f(j, total) consumes each total; totals are NaN after a timeout.
+// Every lane polls its own values (a separate "ready" word would add a
+// second memory round trip).  f(j, total) consumes each total; totals are
+// NaN after a timeout.
 template <class F>
 __device__ __forceinline__ void exchange_columns(const float* part, unsigned long long* slot, int N,
                                                  int b, int W, int w, unsigned t, int spin_limit,
@@ -217,14 +230,14 @@ __device__ __forceinline__ void exchange_columns(const float* part, unsigned lon
 #pragma unroll
             for (int v = 0; v < kWaves; ++v) s += part[v * N + j];
             own[q] = s;
-            publish(slot + size_t(blockIdx.x) * N + j, s, t);
+            publish(slot + (size_t(b) * W + w) * N + j, s, t);
         }
     }
+    unsigned long long* base = slot + size_t(b) * W * N;
 #pragma unroll 1
     for (int q = 0; q < kColsPerThread; ++q) {
         const int j = threadIdx.x + q * kThreads;
         if (j >= N) continue;
-        unsigned long long* base = slot + size_t(b) * W * N + j;
         float got[kMaxGroup];
         for (int spins = 0; !dead; ++spins) {
             bool ready = true;
@@ -232,8 +245,8 @@ __device__ __forceinline__ void exchange_columns(const float* part, unsigned lon
             for (int g = 0; g < kMaxGroup; ++g) {
                 got[g] = 0.0f;
                 if (g < W && g != w) {
-                    const unsigned long long x =
-                        __hip_atomic_load(base + size_t(g) * N, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    const unsigned long long x = __hip_atomic_load(base + size_t(g) * N + j, __ATOMIC_RELAXED,
+                                                                   __HIP_MEMORY_SCOPE_AGENT);
                     ready = ready && static_cast<unsigned>(x >> 32) == t;
                     got[g] = __uint_as_float(static_cast<unsigned>(x));
                 }
@@ -265,7 +278,7 @@ struct ImpResArgs {
     unsigned long long* xchg;  // [2, G, N] tagged sweep column sums
     unsigned long long* pro;   // [2, G, N] tagged prologue column sums (P G, then P)
     float* grad;               // [B,M,N]
-    float* tau_partial;        // [G]
+    float* tau_partial;        // [G] by logical workgroup b * W + w
     int* status;
     float inv_tau;
     int M, N, W, R, iters, spin_limit;
@@ -310,8 +323,9 @@ __global__ __launch_bounds__(kThreads) void implicit_adjoint(ImpResArgs a) {
     const int lane = threadIdx.x % kWave;
     const int wave = threadIdx.x / kWave;
     const int G = gridDim.x;
-    const int b = blockIdx.x / a.W;
-    const int w = blockIdx.x % a.W;
+    const int gid = logical_group(a.W);
+    const int b = gid / a.W;
+    const int w = gid % a.W;
     const int row0 = w * a.R;
     const int rend = min(row0 + a.R, a.M);
     const size_t bM = size_t(b) * a.M;
@@ -429,7 +443,7 @@ __global__ __launch_bounds__(kThreads) void implicit_adjoint(ImpResArgs a) {
         R::store(a.grad + off, lane, a.N, o);
     }
     const float tsum = block_reduce<kWaves>(wave_sum(tacc), scratch, OpSum{});
-    if (threadIdx.x == 0) a.tau_partial[blockIdx.x] = failed ? __builtin_nanf("") : tsum;
+    if (threadIdx.x == 0) a.tau_partial[gid] = failed ? __builtin_nanf("") : tsum;
 }
 
 }  // namespace res
