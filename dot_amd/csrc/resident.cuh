@@ -150,16 +150,16 @@ __device__ __forceinline__ float tstep_move(float x) {
 
 constexpr int ilog2(int x) { return x <= 1 ? 0 : 1 + ilog2(x / 2); }
 
-template <int N, int S>
-__device__ __forceinline__ float tsum_level(const float* v, int lane) {
+template <int N, int S, class Op>
+__device__ __forceinline__ float treduce_level(const float* v, int lane, Op op) {
     if constexpr (N == 1) {
         float x = v[0];
-        if constexpr (S <= 0) x += tstep_move<0>(x);
-        if constexpr (S <= 1) x += tstep_move<1>(x);
-        if constexpr (S <= 2) x += tstep_move<2>(x);
-        if constexpr (S <= 3) x += tstep_move<3>(x);
-        x += swizzle_xor16(x);
-        return x + xor32(x);
+        if constexpr (S <= 0) x = op(x, tstep_move<0>(x));
+        if constexpr (S <= 1) x = op(x, tstep_move<1>(x));
+        if constexpr (S <= 2) x = op(x, tstep_move<2>(x));
+        if constexpr (S <= 3) x = op(x, tstep_move<3>(x));
+        x = op(x, swizzle_xor16(x));
+        return op(x, xor32(x));
     } else {
         constexpr int H = N / 2;
         const bool upper = (lane >> (3 - S)) & 1;
@@ -168,21 +168,26 @@ __device__ __forceinline__ float tsum_level(const float* v, int lane) {
         for (int j = 0; j < H; ++j) {
             const float keep = upper ? v[j + H] : v[j];
             const float send = upper ? v[j] : v[j + H];
-            w[j] = keep + tstep_move<S>(send);
+            w[j] = op(keep, tstep_move<S>(send));
         }
-        return tsum_level<H, S + 1>(w, lane);
+        return treduce_level<H, S + 1>(w, lane, op);
     }
 }
 
-// Wave sums of RPW per-lane values at once (RPW a power of two <= 16): at each
-// butterfly step the two partner lanes trade halves of their remaining rows,
-// so step s moves RPW / 2^(s+1) values instead of RPW.  Every lane returns the
-// wave total of row slot_of_lane(lane); the four lanes that share a slot
-// return the same bits.
+// Wave reductions of RPW per-lane values at once (RPW a power of two <= 16):
+// at each butterfly step the two partner lanes trade halves of their
+// remaining rows, so step s moves RPW / 2^(s+1) values instead of RPW.  Every
+// lane returns the wave total of row slot_of_lane(lane); the four lanes that
+// share a slot return the same bits.
+template <int RPW, class Op>
+__device__ __forceinline__ float transposed_reduce(const float (&v)[RPW], Op op) {
+    static_assert(RPW >= 1 && RPW <= 16 && (RPW & (RPW - 1)) == 0, "RPW must be 1, 2, 4, 8 or 16");
+    return treduce_level<RPW, 0>(v, threadIdx.x % kWave, op);
+}
+
 template <int RPW>
 __device__ __forceinline__ float transposed_sum(const float (&v)[RPW]) {
-    static_assert(RPW >= 1 && RPW <= 16 && (RPW & (RPW - 1)) == 0, "RPW must be 1, 2, 4, 8 or 16");
-    return tsum_level<RPW, 0>(v, threadIdx.x % kWave);
+    return transposed_reduce<RPW>(v, OpSum{});
 }
 
 template <int RPW>
@@ -472,7 +477,7 @@ struct FwdResArgs {
     int max_iter;
     int return_log;
     float* plan;          // [B,M,N] or null
-    float* cost_partial;  // [B*W] or null
+    float* cost_partial;  // [B*W] by logical workgroup, or null
     float* u_out;         // [B,M] or null
     float* v_out;         // [B,N] or null
     float* u_hist;        // [T,B,M] or null
@@ -511,33 +516,41 @@ __device__ __forceinline__ float global_delta(const FwdResArgs& a, int t, float*
 // of this workgroup's rows held in registers for all iterations.
 // Iteration t: the row update of sk::fwd_sweep from v_{t-1}, whose shared
 // exponentials also give this workgroup's column sums of exp(K + u_t + v_{t-1});
-// one tagged exchange of those sums inside the batch element; then every
-// workgroup of the element forms v_t = log b + v_{t-1} - log colsum in the same
-// fixed order.  Columns whose sum is below the floor take the exact max-shifted
-// LSE (kernels.cu:629-671) through two more exchanges (column max, then sum);
-// the decision is the same in every workgroup of the element because they all
-// hold the same sums.  The batch-global stop test (torch_cuda.cpp:225-237) of
-// iteration t-1 is evaluated during iteration t from every workgroup's
-// published delta, so no grid-wide wait sits on the critical path; when it
-// fires, iteration t is discarded and (u_{t-1}, v_{t-1}) are the result.
+// one exchange of those sums inside the batch element (exchange_columns); then
+// every workgroup of the element forms v_t = log b + v_{t-1} - log colsum with
+// the same bits.  Columns whose sum is below the floor take the exact
+// max-shifted LSE (kernels.cu:629-671) through two more exchanges (column max,
+// then sum); the decision is the same in every workgroup of the element
+// because they all hold the same sums.  The batch-global stop test
+// (torch_cuda.cpp:225-237) of iteration t-1 is evaluated during iteration t:
+// wave 0 issues the loads of every workgroup's delta of t-1 before the row
+// update and reads them after the exchange, so the test costs no wait of its
+// own; when it fires, iteration t is discarded and (u_{t-1}, v_{t-1}) are the
+// result.
+constexpr int kDeltaPrefetch = 4;  // delta loads in flight per lane of wave 0 (covers 256 workgroups)
+
 template <int VEC, int CH, int RPW>
 __global__ __launch_bounds__(kThreads) void forward(FwdResArgs a) {
     using R = Row<VEC, CH>;
     constexpr int PL = R::PL;
     constexpr int ROWS = kWaves * RPW;
-    // LDS: tree 8N | v 2N | log b N | column max N | u 2*ROWS | log a ROWS | scratch 32
+    constexpr int GR = RPW < 4 ? RPW : 4;  // rows per reduction group
+    constexpr float kLn2 = 0.69314718055994531f;
+    // LDS: wave rows 8N | v 2N | log b N | column max N | u 2*ROWS | log a ROWS | scratch 32
     extern __shared__ float lds[];
-    float* lds_v = lds + 8 * a.N;
+    float* part = lds;
+    float* lds_v = lds + kWaves * a.N;
     float* lds_lb = lds_v + 2 * a.N;
     float* lds_mx = lds_lb + a.N;
     float* lds_u = lds_mx + a.N;
     float* lds_la = lds_u + 2 * ROWS;
-    float* scratch = lds_la + ROWS;
+    float* scratch = lds_la + ROWS;  // [0] global delta, [1..kWaves] wave deltas, [16..] reductions
     const int lane = threadIdx.x % kWave;
     const int wave = threadIdx.x / kWave;
     const int G = gridDim.x;
-    const int b = blockIdx.x / a.W;
-    const int w = blockIdx.x % a.W;
+    const int gid = logical_group(a.W);
+    const int b = gid / a.W;
+    const int w = gid % a.W;
     const int row0 = w * a.R;
     const int rend = min(row0 + a.R, a.M);
     const size_t bM = size_t(b) * a.M;
@@ -575,46 +588,81 @@ __global__ __launch_bounds__(kThreads) void forward(FwdResArgs a) {
     float v[PL];
 #pragma unroll
     for (int e = 0; e < PL; ++e) v[e] = 0.0f;
+    // log a of the row this lane takes in each group of GR rows
+    float lga_slot[RPW / GR];
+#pragma unroll
+    for (int g = 0; g < RPW / GR; ++g) lga_slot[g] = lds_la[wave + kWaves * (g * GR + slot_of_lane<GR>(lane))];
+    const float kscale2 = a.kscale * kLog2E;
     bool dead = false;
     int used = a.max_iter;
     int conv = 0;
 
     for (int t = 1; t <= a.max_iter; ++t) {
         const int cur = t & 1, prev = cur ^ 1;
-        // Row update (kernels.cu:503-545) and the shared-exponential column sums.
-        float acc[PL];
+        const bool test = check && t >= 2;
+        unsigned long long* ds = a.dxchg + size_t((t - 1) % kDeltaSlots) * G;
+        unsigned long long dpre[kDeltaPrefetch];
+        if (test && wave == 0) {
 #pragma unroll
-        for (int e = 0; e < PL; ++e) acc[e] = 0.0f;
+            for (int q = 0; q < kDeltaPrefetch; ++q) {
+                const int g = lane + q * kWave;
+                dpre[q] = g < G ? __hip_atomic_load(ds + g, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                : tag_pack(0.0f, unsigned(t - 1));
+            }
+        }
+        // Row update (kernels.cu:503-545) and the shared-exponential column sums,
+        // in base 2: y = K log2(e) + v log2(e), m = max_j y, s = sum_j 2^(y - m),
+        // u = log a - ln2 (m + log2 s), and the column sums take 2^(y - m) a / s.
+        // Rows go in groups of GR: their maxima and sums are reduced across the
+        // wave together (transposed butterfly), and each lane then takes the
+        // logarithm for one row of the group.
+        float acc[PL], v2[PL];
+#pragma unroll
+        for (int e = 0; e < PL; ++e) {
+            acc[e] = 0.0f;
+            v2[e] = v[e] * kLog2E;
+        }
         float uk[RPW];  // this wave's new u values; stored after the loop, which keeps it branch-free
 #pragma unroll
-        for (int k = 0; k < RPW; ++k) {
-            const int l = wave + kWaves * k;
-            float y[PL];
-            float ml = -FLT_MAX;
+        for (int g0 = 0; g0 < RPW; g0 += GR) {
+            float y[GR][PL], lm[GR];
 #pragma unroll
-            for (int e = 0; e < PL; ++e) {
-                y[e] = fmaf(x[k][e], a.kscale, v[e]);
-                ml = fmaxf(ml, y[e]);
+            for (int r = 0; r < GR; ++r) {
+                lm[r] = -FLT_MAX;
+#pragma unroll
+                for (int e = 0; e < PL; ++e) {
+                    y[r][e] = fmaf(x[g0 + r][e], kscale2, v2[e]);
+                    lm[r] = fmaxf(lm[r], y[r][e]);
+                }
             }
-            const float m = wave_max(ml);
-            float sl = 0.0f;
+            const float m_l = transposed_reduce<GR>(lm, OpMax{});
+            float ls[GR], mr[GR];
 #pragma unroll
-            for (int e = 0; e < PL; ++e) {
-                y[e] = fast_exp(y[e] - m);
-                sl += y[e];
+            for (int r = 0; r < GR; ++r) {
+                mr[r] = read_lane(m_l, lane_of_slot<GR>(r));
+                ls[r] = 0.0f;
+#pragma unroll
+                for (int e = 0; e < PL; ++e) {
+                    y[r][e] = __builtin_amdgcn_exp2f(y[r][e] - mr[r]);
+                    ls[r] += y[r][e];
+                }
             }
-            const float ssum = wave_sum(sl);
-            const float lga = lds_la[l];
-            const float ls = logf(fmaxf(ssum, sk::kSumFloor));
-            const float u = lga - (m + ls);
-            const float wgt = fast_exp(lga - ls);
+            const float s_l = fmaxf(transposed_sum<GR>(ls), sk::kSumFloor);
+            const float lga_l = lga_slot[g0 / GR];
+            const float lg2 = __builtin_amdgcn_logf(s_l);  // log2
+            const float u_l = lga_l - kLn2 * (m_l + lg2);
+            const float w_l = __builtin_amdgcn_exp2f(fmaf(lga_l, kLog2E, -lg2));  // a / s
 #pragma unroll
-            for (int e = 0; e < PL; ++e) acc[e] = fmaf(y[e], wgt, acc[e]);
-            // Materialise acc here: left alone, the compiler postpones every row's
-            // update to the end of the loop and keeps all rows' exponentials live.
+            for (int r = 0; r < GR; ++r) {
+                const float wr = read_lane(w_l, lane_of_slot<GR>(r));
+                uk[g0 + r] = read_lane(u_l, lane_of_slot<GR>(r));
+#pragma unroll
+                for (int e = 0; e < PL; ++e) acc[e] = fmaf(y[r][e], wr, acc[e]);
+            }
+            // Materialise acc here: left alone, the compiler postpones the updates
+            // to the end of the loop and keeps every group's exponentials live.
 #pragma unroll
             for (int e = 0; e < PL; ++e) asm volatile("" : "+v"(acc[e]));
-            uk[k] = u;
         }
         float dmax = 0.0f;
 #pragma unroll
@@ -629,41 +677,42 @@ __global__ __launch_bounds__(kThreads) void forward(FwdResArgs a) {
                 }
             }
         }
-        tree_combine<VEC, CH>(acc, lds, a.N);
-        const float wg_delta = check ? block_reduce<kWaves>(dmax, scratch + 1, OpMax{}) : 0.0f;
-        unsigned long long* slot = a.xchg + size_t(cur) * G * a.N;
-        if (wave == 0) {
-            unsigned long long* mine = slot + size_t(blockIdx.x) * a.N;
+        __syncthreads();  // previous readers of part are done
+        R::store(part + wave * a.N, lane, a.N, acc);
+        if (lane == 0) scratch[1 + wave] = dmax;
+        __syncthreads();
+        if (check && threadIdx.x == 0) {
+            float d = scratch[1];
 #pragma unroll
-            for (int k = 0; k < CH; ++k) {
+            for (int q = 1; q < kWaves; ++q) d = fmaxf(d, scratch[1 + q]);
+            publish(a.dxchg + size_t(t % kDeltaSlots) * G + gid, d, unsigned(t));
+        }
+        int low = 0;
+        exchange_columns(part, a.xchg + size_t(cur) * G * a.N, a.N, b, a.W, w, unsigned(t), a.spin_limit,
+                         a.status, dead, [&](int j, float cs) {
+                             if (cs >= sk::kColSumFloor && cs <= FLT_MAX) {
+                                 lds_v[cur * a.N + j] = lds_lb[j] + lds_v[prev * a.N + j] - logf(cs);
+                             } else {
+                                 lds_v[cur * a.N + j] = __builtin_nanf("");  // exact LSE below
+                                 low = 1;
+                             }
+                         });
+        if (test && wave == 0) {
+            float gmax = 0.0f;
 #pragma unroll
-                for (int q = 0; q < VEC; ++q) {
-                    const int col = R::col(lane, k) + q;
-                    if (col < a.N) publish(mine + col, acc[k * VEC + q], unsigned(t));
+            for (int q = 0; q < kDeltaPrefetch; ++q) {
+                const int g = lane + q * kWave;
+                if (g < G) {
+                    float d = __uint_as_float(static_cast<unsigned>(dpre[q]));
+                    if (static_cast<unsigned>(dpre[q] >> 32) != unsigned(t - 1))
+                        d = collect(ds + g, unsigned(t - 1), a.spin_limit, a.status, dead);
+                    gmax = OpMaxNan{}(gmax, d);
                 }
             }
-            if (check && lane == 0)
-                publish(a.dxchg + size_t(t % kDeltaSlots) * G + blockIdx.x, wg_delta, unsigned(t));
-        }
-        __syncthreads();  // the tree area now receives the collected rows
-        unsigned long long* batch = slot + size_t(b) * a.W * a.N;
-        for (int w2 = wave; w2 < a.W; w2 += kWaves) {
-            float got[PL];
-            collect_row<VEC, CH>(batch + size_t(w2) * a.N, unsigned(t), a.N, a.spin_limit, a.status,
-                                 dead, got);
-            R::store(lds + w2 * a.N, lane, a.N, got);
-        }
-        __syncthreads();
-        int low = 0;
-        for (int j = threadIdx.x; j < a.N; j += kThreads) {
-            float cs = 0.0f;
-            for (int w2 = 0; w2 < a.W; ++w2) cs += lds[w2 * a.N + j];
-            if (cs >= sk::kColSumFloor && cs <= FLT_MAX) {
-                lds_v[cur * a.N + j] = lds_lb[j] + lds_v[prev * a.N + j] - logf(cs);
-            } else {
-                lds_v[cur * a.N + j] = __builtin_nanf("");  // marks the column for the exact LSE
-                low = 1;
-            }
+            for (int g = lane + kDeltaPrefetch * kWave; g < G; g += kWave)
+                gmax = OpMaxNan{}(gmax, collect(ds + g, unsigned(t - 1), a.spin_limit, a.status, dead));
+            gmax = wave_reduce(gmax, OpMaxNan{});
+            if (lane == 0) scratch[0] = gmax;
         }
         if (__syncthreads_or(low)) {
             // Exact column LSE of K + u_t over the element's rows: max, then sum.
@@ -679,10 +728,10 @@ __global__ __launch_bounds__(kThreads) void forward(FwdResArgs a) {
                 for (int e = 0; e < PL; ++e)
                     if (R::valid(lane, e, a.N)) cm[e] = fmaxf(cm[e], fmaf(x[k][e], a.kscale, u));
             }
-            tree_combine<VEC, CH>(cm, lds, a.N, OpMax{});
+            tree_combine<VEC, CH>(cm, part, a.N, OpMax{});
             unsigned long long* fslot = a.fxchg + size_t(cur) * 2 * G * a.N;
             if (wave == 0) {
-                unsigned long long* mine = fslot + size_t(blockIdx.x) * a.N;
+                unsigned long long* mine = fslot + size_t(gid) * a.N;
 #pragma unroll
                 for (int k = 0; k < CH; ++k)
 #pragma unroll
@@ -696,12 +745,12 @@ __global__ __launch_bounds__(kThreads) void forward(FwdResArgs a) {
                 float got[PL];
                 collect_row<VEC, CH>(fslot + (size_t(b) * a.W + w2) * a.N, unsigned(t), a.N,
                                      a.spin_limit, a.status, dead, got);
-                R::store(lds + w2 * a.N, lane, a.N, got);
+                R::store(part + w2 * a.N, lane, a.N, got);
             }
             __syncthreads();
             for (int j = threadIdx.x; j < a.N; j += kThreads) {
                 float mx = -FLT_MAX;
-                for (int w2 = 0; w2 < a.W; ++w2) mx = fmaxf(mx, lds[w2 * a.N + j]);
+                for (int w2 = 0; w2 < a.W; ++w2) mx = fmaxf(mx, part[w2 * a.N + j]);
                 lds_mx[j] = mx;
             }
             __syncthreads();
@@ -718,10 +767,10 @@ __global__ __launch_bounds__(kThreads) void forward(FwdResArgs a) {
                 for (int e = 0; e < PL; ++e)
                     if (R::valid(lane, e, a.N)) sm[e] += safe_exp(fmaf(x[k][e], a.kscale, u) - mxl[e]);
             }
-            tree_combine<VEC, CH>(sm, lds, a.N);
+            tree_combine<VEC, CH>(sm, part, a.N);
             unsigned long long* sslot = fslot + size_t(G) * a.N;
             if (wave == 0) {
-                unsigned long long* mine = sslot + size_t(blockIdx.x) * a.N;
+                unsigned long long* mine = sslot + size_t(gid) * a.N;
 #pragma unroll
                 for (int k = 0; k < CH; ++k)
 #pragma unroll
@@ -735,30 +784,26 @@ __global__ __launch_bounds__(kThreads) void forward(FwdResArgs a) {
                 float got[PL];
                 collect_row<VEC, CH>(sslot + (size_t(b) * a.W + w2) * a.N, unsigned(t), a.N,
                                      a.spin_limit, a.status, dead, got);
-                R::store(lds + w2 * a.N, lane, a.N, got);
+                R::store(part + w2 * a.N, lane, a.N, got);
             }
             __syncthreads();
             for (int j = threadIdx.x; j < a.N; j += kThreads) {
                 const float vj = lds_v[cur * a.N + j];
                 if (vj != vj) {
                     float s = 0.0f;
-                    for (int w2 = 0; w2 < a.W; ++w2) s += lds[w2 * a.N + j];
+                    for (int w2 = 0; w2 < a.W; ++w2) s += part[w2 * a.N + j];
                     lds_v[cur * a.N + j] = lds_lb[j] - (lds_mx[j] + logf(fmaxf(s, sk::kSumFloor)));
                 }
             }
+            __syncthreads();
         }
-        __syncthreads();
         if (a.v_hist && w == 0)
             for (int j = threadIdx.x; j < a.N; j += kThreads)
                 a.v_hist[(size_t(t - 1) * a.B + b) * a.N + j] = lds_v[cur * a.N + j];
-        // Lagged stop test on iteration t-1.
-        if (check && t >= 2) {
-            const float g = global_delta(a, t - 1, scratch, dead);
-            if (g < a.tol) {
-                used = t - 1;
-                conv = 1;
-                break;
-            }
+        if (test && scratch[0] < a.tol) {  // the stop test of iteration t-1 fired
+            used = t - 1;
+            conv = 1;
+            break;
         }
         R::load(lds_v + cur * a.N, lane, a.N, v, 0.0f);
     }
@@ -793,8 +838,8 @@ __global__ __launch_bounds__(kThreads) void forward(FwdResArgs a) {
         if (a.plan) R::store(a.plan + (bM + i) * a.N, lane, a.N, pv);
     }
     if (a.cost_partial) {
-        const float cs = block_reduce<kWaves>(wave_sum(cacc), scratch + 1, OpSum{});
-        if (threadIdx.x == 0) a.cost_partial[blockIdx.x] = failed ? __builtin_nanf("") : cs;
+        const float cs = block_reduce<kWaves>(wave_sum(cacc), scratch + 16, OpSum{});
+        if (threadIdx.x == 0) a.cost_partial[gid] = failed ? __builtin_nanf("") : cs;
     }
     if (blockIdx.x == 0 && threadIdx.x == 0) {
         *a.iters_used = failed ? -1 : used;  // -1: an exchange timed out, the outputs are NaN
