@@ -7,13 +7,18 @@
 // strip, merged across strips) and a write sweep.  The backward is two sweeps
 // too: row and column dot products of q = d * r * c, then the gradient.
 // Statistics are stored as planes: row_stats [B, 2, L1] (max plane, then sum
-// plane) and col_stats [B, 2, L2].
+// plane) and col_stats [B, 2, L2], maxima in base-2 units (see below).
 #pragma once
 
 #include <cfloat>
 #include <cstdint>
 
 #include "row.cuh"
+
+// No automatic FMA contraction here: every kernel forms y2 = sim * sc with the
+// same rounding, so the entry that attains a stored maximum gives exactly
+// 2^(y2 - max) = 1; a contracted fma(sim, sc, -max) would not.
+#pragma clang fp contract(off)
 
 namespace dot_amd {
 namespace bidi {
@@ -26,22 +31,14 @@ __device__ __forceinline__ void valid_extent(const int32_t* lengths, int b, int 
     l2 = min(max(lengths[2 * b + 1], 0), L2);
 }
 
-// Online log-sum-exp state (m, s) meaning sum = s * exp(m); one exponential per update.
-__device__ __forceinline__ void lse_push(float& m, float& s, float y) {
-    const float d = y - m;
-    const float e = fast_exp(-fabsf(d));
-    const bool gt = d > 0.0f;
-    s = gt ? fmaf(s, e, 1.0f) : s + e;
-    m = gt ? y : m;
-}
-
-__device__ __forceinline__ void lse_merge(float& m, float& s, float m2, float s2) {
+// Merge of two column states kept in base 2 (sum = s * 2^m).
+__device__ __forceinline__ void lse_merge2(float& m, float& s, float m2, float s2) {
     const float M = fmaxf(m, m2);
-    s = s * fast_exp(m - M) + s2 * fast_exp(m2 - M);
+    s = s * __builtin_amdgcn_exp2f(m - M) + s2 * __builtin_amdgcn_exp2f(m2 - M);
     m = M;
 }
 
-// Fold the (m, s) column states of the 4 waves into wave 0 in the fixed order
+// Fold the base-2 (m, s) column states of the 4 waves into wave 0 in the fixed order
 // (w0 + w2) + (w1 + w3).  `lds` holds 2*N floats; every thread must call it.
 template <int VEC, int CH>
 __device__ __forceinline__ void block_column_combine_lse(float (&m)[VEC * CH], float (&s)[VEC * CH],
@@ -64,7 +61,7 @@ __device__ __forceinline__ void block_column_combine_lse(float (&m)[VEC * CH], f
             R::load(lds, lane, N, m2, -FLT_MAX);
             R::load(lds + N, lane, N, s2, 0.0f);
 #pragma unroll
-            for (int e = 0; e < R::PL; ++e) lse_merge(m[e], s[e], m2[e], s2[e]);
+            for (int e = 0; e < R::PL; ++e) lse_merge2(m[e], s[e], m2[e], s2[e]);
         }
     }
 }
@@ -83,6 +80,18 @@ struct FwdArgs {
     float* col_sm;       // or null
 };
 
+// Exponentials run in base 2 on y2 = sim * (inv_T * log2(e)): exp(y - m) =
+// 2^(y2 - m2).  The statistics keep the maxima in that unit (m2 = max y2) and
+// the sums unchanged (sum of exp(y - max)); every kernel forms y2 with the
+// same expression, so the entry that attains a maximum gives exactly 2^0 = 1.
+
+// Lanes past the valid columns hold -inf (their exponentials are 0).  `full`
+// (every lane of every chunk is a valid column) lets the loops skip the test.
+template <class R>
+__device__ __forceinline__ float masked(float y2, bool full, int lane, int e, int l2) {
+    return (full || R::valid(lane, e, l2)) ? y2 : -INFINITY;
+}
+
 // Row statistics (kernels.cu:90-139: max of sim*inv_T, sum of safe_exp(y - max))
 // and per-strip column statistics (kernels.cu:153-202) in one read of sim.
 template <int VEC, int CH>
@@ -95,9 +104,11 @@ __global__ __launch_bounds__(kBlock) void fwd_stats(FwdArgs a) {
     const int b = blockIdx.y;
     int l1, l2;
     valid_extent(a.lengths, b, a.L1, a.L2, l1, l2);
+    const bool full = l2 == kWave * R::PL;
+    const float sc = a.inv_T * kLog2E;
     const int r0 = st * a.rows;
     const int r1 = min(r0 + a.rows, l1);
-    float cm[R::PL], cs[R::PL];
+    float cm[R::PL], cs[R::PL];  // column state in base 2: sum = cs * 2^cm
 #pragma unroll
     for (int e = 0; e < R::PL; ++e) {
         cm[e] = -FLT_MAX;
@@ -111,14 +122,19 @@ __global__ __launch_bounds__(kBlock) void fwd_stats(FwdArgs a) {
         float ml = -FLT_MAX;
 #pragma unroll
         for (int e = 0; e < R::PL; ++e) {
-            y[e] = R::valid(lane, e, l2) ? y[e] * a.inv_T : -INFINITY;
+            y[e] = masked<R>(y[e] * sc, full, lane, e, l2);
             ml = fmaxf(ml, y[e]);
-            lse_push(cm[e], cs[e], y[e]);
+            // online column state: one exponential per element
+            const float d = y[e] - cm[e];
+            const float x = __builtin_amdgcn_exp2f(-fabsf(d));
+            const bool gt = d > 0.0f;
+            cs[e] = gt ? fmaf(cs[e], x, 1.0f) : cs[e] + x;
+            cm[e] = gt ? y[e] : cm[e];
         }
         const float rm = wave_max(ml);
         float sl = 0.0f;
 #pragma unroll
-        for (int e = 0; e < R::PL; ++e) sl += fast_exp(y[e] - rm);
+        for (int e = 0; e < R::PL; ++e) sl += __builtin_amdgcn_exp2f(y[e] - rm);
         const float rs = wave_sum(sl);
         if (lane == 0) {
             rmax[i] = rm;
@@ -133,6 +149,7 @@ __global__ __launch_bounds__(kBlock) void fwd_stats(FwdArgs a) {
     }
 }
 
+// Column statistics: merge the strips' base-2 states.
 __global__ __launch_bounds__(kBlock) void fwd_col_combine(FwdArgs a) {
     const int b = blockIdx.y;
     const int j = blockIdx.x * kBlock + threadIdx.x;
@@ -140,7 +157,7 @@ __global__ __launch_bounds__(kBlock) void fwd_col_combine(FwdArgs a) {
     const size_t base = size_t(b) * a.nstrips * a.L2 + j;
     float m = -FLT_MAX, s = 0.0f;
     for (int k = 0; k < a.nstrips; ++k)
-        lse_merge(m, s, a.part_m[base + size_t(k) * a.L2], a.part_s[base + size_t(k) * a.L2]);
+        lse_merge2(m, s, a.part_m[base + size_t(k) * a.L2], a.part_s[base + size_t(k) * a.L2]);
     float* cmax = a.col_stats + size_t(b) * 2 * a.L2;
     cmax[j] = m;
     cmax[a.L2 + j] = s;
@@ -156,6 +173,8 @@ __global__ __launch_bounds__(kBlock) void fwd_write(FwdArgs a) {
     const int b = blockIdx.y;
     int l1, l2;
     valid_extent(a.lengths, b, a.L1, a.L2, l1, l2);
+    const bool full = l2 == kWave * R::PL;
+    const float sc = a.inv_T * kLog2E;
     const int r0 = blockIdx.x * a.rows;
     const int r1 = min(r0 + a.rows, a.L1);
     const float* cstat = a.col_stats + size_t(b) * 2 * a.L2;
@@ -176,11 +195,11 @@ __global__ __launch_bounds__(kBlock) void fwd_write(FwdArgs a) {
             const float irs = rsv > 0.0f ? 1.0f / rsv : 0.0f;
 #pragma unroll
             for (int e = 0; e < R::PL; ++e) {
-                const bool ok = R::valid(lane, e, l2);
-                const float yy = y[e] * a.inv_T;
-                rr[e] = ok ? fast_exp(yy - rm) * irs : 0.0f;
-                cc[e] = ok ? fast_exp(yy - cm[e]) * ics[e] : 0.0f;
-                o[e] = ok ? sqrtf(kEps + rr[e] * cc[e]) : 0.0f;
+                const bool ok = full || R::valid(lane, e, l2);
+                const float y2 = y[e] * sc;
+                rr[e] = ok ? __builtin_amdgcn_exp2f(y2 - rm) * irs : 0.0f;
+                cc[e] = ok ? __builtin_amdgcn_exp2f(y2 - cm[e]) * ics[e] : 0.0f;
+                o[e] = ok ? __builtin_amdgcn_sqrtf(fmaf(rr[e], cc[e], kEps)) : 0.0f;
             }
         } else {
 #pragma unroll
@@ -210,13 +229,18 @@ struct BwdArgs {
     float* tau_partial;    // [B,gridDim.x]
 };
 
-// Per-row view of r, c and out for one row, from buffers or recomputed.
+// For one row: r, c and d = g / (2 out) (kernels.cu:249-274), from the
+// forward's buffers or recomputed from the statistics; 0 outside the valid
+// region.  In recompute mode out >= sqrt(1e-9) > 1e-9, so the reference's
+// out > 1e-9 test always passes.
 template <int VEC, int CH, bool RECOMPUTE>
 struct BwdRow {
     using R = Row<VEC, CH>;
     float cm[R::PL], ics[R::PL];
+    float sc;
 
     __device__ void init(const BwdArgs& a, int b, int lane) {
+        sc = a.inv_T * kLog2E;
         if constexpr (RECOMPUTE) {
             const float* cstat = a.col_stats + size_t(b) * 2 * a.L2;
             R::load(cstat, lane, a.L2, cm, 0.0f);
@@ -226,11 +250,11 @@ struct BwdRow {
         }
     }
 
-    // Fills r, c, o for row i (valid region only; other lanes get 0).
-    __device__ void get(const BwdArgs& a, int b, int i, size_t off, int lane, int l2,
-                        float (&r)[R::PL], float (&c)[R::PL], float (&o)[R::PL],
-                        float (&y)[R::PL]) const {
+    __device__ void get(const BwdArgs& a, int b, int i, size_t off, int lane, int l2, bool full,
+                        float (&r)[R::PL], float (&c)[R::PL], float (&d)[R::PL], float (&y)[R::PL]) const {
+        float g[R::PL];
         R::load(a.sim + off, lane, a.L2, y, 0.0f);
+        R::load(a.grad_out + off, lane, a.L2, g, 0.0f);
         if constexpr (RECOMPUTE) {
             const float* rstat = a.row_stats + size_t(b) * 2 * a.L1;
             const float rm = rstat[i];
@@ -238,22 +262,29 @@ struct BwdRow {
             const float irs = rsv > 0.0f ? 1.0f / rsv : 0.0f;
 #pragma unroll
             for (int e = 0; e < R::PL; ++e) {
-                const bool ok = R::valid(lane, e, l2);
-                const float yy = y[e] * a.inv_T;
-                r[e] = ok ? fast_exp(yy - rm) * irs : 0.0f;
-                c[e] = ok ? fast_exp(yy - cm[e]) * ics[e] : 0.0f;
-                o[e] = ok ? sqrtf(kEps + r[e] * c[e]) : 0.0f;
+                const bool ok = full || R::valid(lane, e, l2);
+                const float y2 = y[e] * sc;
+                r[e] = ok ? __builtin_amdgcn_exp2f(y2 - rm) * irs : 0.0f;
+                c[e] = ok ? __builtin_amdgcn_exp2f(y2 - cm[e]) * ics[e] : 0.0f;
+                const float o = __builtin_amdgcn_sqrtf(fmaf(r[e], c[e], kEps));
+                d[e] = ok ? (g[e] * 0.5f) * __builtin_amdgcn_rcpf(o) : 0.0f;
             }
         } else {
+            float o[R::PL];
             R::load(a.row_sm + off, lane, a.L2, r, 0.0f);
             R::load(a.col_sm + off, lane, a.L2, c, 0.0f);
             R::load(a.out + off, lane, a.L2, o, 0.0f);
+#pragma unroll
+            for (int e = 0; e < R::PL; ++e) {
+                const bool ok = (full || R::valid(lane, e, l2)) && o[e] > kEps;
+                d[e] = ok ? (g[e] * 0.5f) * __builtin_amdgcn_rcpf(o[e]) : 0.0f;
+            }
         }
     }
 };
 
-// d = g * 0.5 / out (kernels.cu:249-274), d_r = d c, d_c = d r (:363-376);
-// row dots sum_j d_r r and column partials of d_c c (:277-311, :320-354).
+// Row dots sum_j (d c) r and column partials of (d r) c over the strip
+// (kernels.cu:277-354).
 template <int VEC, int CH, bool RECOMPUTE>
 __global__ __launch_bounds__(kBlock) void bwd_dots(BwdArgs a) {
     using R = Row<VEC, CH>;
@@ -264,6 +295,7 @@ __global__ __launch_bounds__(kBlock) void bwd_dots(BwdArgs a) {
     const int b = blockIdx.y;
     int l1, l2;
     valid_extent(a.lengths, b, a.L1, a.L2, l1, l2);
+    const bool full = l2 == kWave * R::PL;
     const int r0 = st * a.rows;
     const int r1 = min(r0 + a.rows, l1);
     BwdRow<VEC, CH, RECOMPUTE> src;
@@ -273,16 +305,13 @@ __global__ __launch_bounds__(kBlock) void bwd_dots(BwdArgs a) {
     for (int e = 0; e < R::PL; ++e) acc[e] = 0.0f;
     for (int i = r0 + wave; i < r1; i += kWavesPerBlock) {
         const size_t off = (size_t(b) * a.L1 + i) * a.L2;
-        float r[R::PL], c[R::PL], o[R::PL], y[R::PL], g[R::PL];
-        src.get(a, b, i, off, lane, l2, r, c, o, y);
-        R::load(a.grad_out + off, lane, a.L2, g, 0.0f);
+        float r[R::PL], c[R::PL], d[R::PL], y[R::PL];
+        src.get(a, b, i, off, lane, l2, full, r, c, d, y);
         float dl = 0.0f;
 #pragma unroll
         for (int e = 0; e < R::PL; ++e) {
-            const bool ok = R::valid(lane, e, l2) && o[e] > kEps;
-            const float d = ok ? (g[e] * 0.5f) / o[e] : 0.0f;
-            dl += (d * c[e]) * r[e];
-            acc[e] += (d * r[e]) * c[e];
+            dl = fmaf(d[e] * c[e], r[e], dl);
+            acc[e] = fmaf(d[e] * r[e], c[e], acc[e]);
         }
         const float dr = wave_sum(dl);
         if (lane == 0) a.dot_r[size_t(b) * a.L1 + i] = dr;
@@ -291,8 +320,8 @@ __global__ __launch_bounds__(kBlock) void bwd_dots(BwdArgs a) {
     if (wave == 0) R::store(a.partial + (size_t(b) * a.nstrips + st) * a.L2, lane, a.L2, acc);
 }
 
-// grad = ((d_r - dot_r) r) / tau + ((d_c - dot_c) c) / tau in the valid region,
-// 0 elsewhere; per-block sums of grad * sim for grad_tau (kernels.cu:379-411).
+// grad = ((d c - dot_r) r + (d r - dot_c) c) / tau in the valid region, 0
+// elsewhere; per-block sums of grad * sim for grad_tau (kernels.cu:379-411).
 template <int VEC, int CH, bool RECOMPUTE>
 __global__ __launch_bounds__(kBlock) void bwd_write(BwdArgs a) {
     using R = Row<VEC, CH>;
@@ -302,6 +331,7 @@ __global__ __launch_bounds__(kBlock) void bwd_write(BwdArgs a) {
     const int b = blockIdx.y;
     int l1, l2;
     valid_extent(a.lengths, b, a.L1, a.L2, l1, l2);
+    const bool full = l2 == kWave * R::PL;
     const int r0 = blockIdx.x * a.rows;
     const int r1 = min(r0 + a.rows, a.L1);
     BwdRow<VEC, CH, RECOMPUTE> src;
@@ -313,19 +343,15 @@ __global__ __launch_bounds__(kBlock) void bwd_write(BwdArgs a) {
         const size_t off = (size_t(b) * a.L1 + i) * a.L2;
         float gs[R::PL];
         if (i < l1) {
-            float r[R::PL], c[R::PL], o[R::PL], y[R::PL], g[R::PL];
-            src.get(a, b, i, off, lane, l2, r, c, o, y);
-            R::load(a.grad_out + off, lane, a.L2, g, 0.0f);
+            float r[R::PL], c[R::PL], d[R::PL], y[R::PL];
+            src.get(a, b, i, off, lane, l2, full, r, c, d, y);
             const float dr = a.dot_r[size_t(b) * a.L1 + i];
 #pragma unroll
             for (int e = 0; e < R::PL; ++e) {
-                const bool valid = R::valid(lane, e, l2);
-                const bool ok = valid && o[e] > kEps;
-                const float d = ok ? (g[e] * 0.5f) / o[e] : 0.0f;
-                const float row_term = ((d * c[e] - dr) * r[e]) * a.inv_T;
-                const float col_term = ((d * r[e] - dc[e]) * c[e]) * a.inv_T;
-                gs[e] = valid ? row_term + col_term : 0.0f;
-                if (valid) tacc = fmaf(gs[e], y[e], tacc);
+                const bool valid = full || R::valid(lane, e, l2);
+                const float t = (d[e] * c[e] - dr) * r[e] + (d[e] * r[e] - dc[e]) * c[e];
+                gs[e] = valid ? t * a.inv_T : 0.0f;
+                tacc = valid ? fmaf(gs[e], y[e], tacc) : tacc;
             }
         } else {
 #pragma unroll

@@ -142,6 +142,9 @@ typedef struct {
     float* out;               /* [B,L1,L2] sqrt(1e-9 + r*c) in the valid region, else 0 */
     float* row_sm;            /* [B,L1,L2] row softmax r, or NULL */
     float* col_sm;            /* [B,L1,L2] column softmax c, or NULL */
+    /* Statistics, with y2 = sim * (1/tau) * log2(e): the max plane holds max y2
+     * over the row (column), the sum plane sum exp2(y2 - max) (the softmax
+     * denominator).  Only the backward of this library reads them back. */
     float* row_stats;         /* [B,2,L1] row max plane then row sum plane, or NULL */
     float* col_stats;         /* [B,2,L2] column max plane then column sum plane, or NULL */
     void* workspace;
