@@ -205,7 +205,8 @@ def bench_sinkhorn(args, torch, dot_amd, profiler):
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
-    sweeps = ["sk_fwd_sweep", "sk_imp_sweep", "sk_fwd_resident", "sk_imp_resident"]
+    sweeps = ["sk_fwd_sweep", "sk_imp_sweep", "sk_fwd_resident", "sk_imp_resident", "sk_fwd_persistent",
+              "sk_imp_persistent"]
     profiler.reset()
     profiler.enable(True, kernels=sweeps)
     torch.cuda.synchronize()
@@ -230,15 +231,17 @@ def bench_sinkhorn(args, torch, dot_amd, profiler):
         # One fp32 read of the [B,M,N] matrix per sweep.  The resident kernels run all
         # their sweeps in one launch with the matrix held in registers, so their bytes
         # are HBM-equivalent: what the same sweeps would stream.
-        sweeps_per_launch = {"sk_imp_resident": T_b, "sk_fwd_resident": T_f}.get(dominant, 1)
+        sweeps_per_launch = {"sk_imp_resident": T_b, "sk_fwd_resident": T_f, "sk_imp_persistent": T_b,
+                             "sk_fwd_persistent": T_f}.get(dominant, 1)
         bytes_per_launch = 4.0 * E * sweeps_per_launch
         achieved = bytes_per_launch / (stats[dominant]["avg_us"] * 1e-6) / 1e9
         roofline = {"bound": "hbm", "kernel": dominant, "achieved": round(achieved, 1),
                     "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
                     "traffic": _pmc_traffic(dominant, args.workload),
                     "bytes_per_launch": bytes_per_launch,
-                    "tier": "register-resident (HBM-equivalent bytes)" if sweeps_per_launch > 1
-                            else "streaming"}
+                    "tier": ("register-resident (HBM-equivalent bytes)" if "resident" in dominant else
+                             "persistent streaming (one launch; the matrix is re-read every sweep)"
+                             if "persistent" in dominant else "streaming sweeps")}
     algo_bytes = 4.0 * E * (T_f + T_b) + 20.0 * E
     return {
         "value": value,

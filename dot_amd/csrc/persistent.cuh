@@ -1,0 +1,627 @@
+// Persistent streaming kernels: one cooperative launch for all iterations
+// when a batch element's rows do not fit the registers of its workgroups.
+//
+// Each batch element gets W workgroups (one per CU, 8 waves), each owning a
+// strip of rows that it streams from HBM / the Infinity Cache once per
+// iteration, exactly like a streaming sweep, but without a kernel boundary
+// between iterations.  The per-column sums go through a reduce-scatter and an
+// all-gather of tagged words (see resident.cuh for the tag protocol):
+//   1. the workgroup's column sums (fixed-order fold of its waves) are
+//      published as one tagged row;
+//   2. workgroup w owns the column slice [w N / W, (w+1) N / W): it reads the
+//      W rows for its slice (every value in flight at once), adds them in
+//      workgroup order and publishes the slice's results (v or mu);
+//   3. every workgroup reads the N results of its element.
+// Two memory round trips per iteration and 2 N + N / W tagged reads per
+// workgroup, whatever W is.  Slots alternate by iteration parity; a workgroup
+// cannot reach iteration t+2 before every owner has consumed iteration t.
+#pragma once
+
+#include <cfloat>
+#include <cstdint>
+
+#include "resident.cuh"
+
+namespace dot_amd {
+namespace pst {
+
+using res::kThreads;
+using res::kWaves;
+using res::publish;
+using res::tag_pack;
+
+constexpr int kMaxGroups = 64;                                   // workgroups per batch element
+constexpr int kMaxCols = kMaxRowLen;                             // 4096
+constexpr int kLoadsPerThread = (kMaxCols + kMaxGroups + kThreads - 1) / kThreads;  // 9
+
+// The lane index behind an empty asm: addresses and masks computed from it
+// are recomputed where they are used instead of being hoisted out of the
+// iteration loop (64-float rows would otherwise pin dozens of registers).
+__device__ __forceinline__ int opaque_lane() {
+    int lane = threadIdx.x % kWave;
+    asm volatile("" : "+v"(lane));
+    return lane;
+}
+
+__device__ __forceinline__ int slice_begin(int w, int W, int N) {
+    return static_cast<int>(static_cast<long long>(w) * N / W);
+}
+
+// Polls `n` tagged words at base[idx(r)] (r < n <= kLoadsPerThread, all in flight)
+// until each carries tag t; returns false after a timeout (values then NaN).
+template <class Idx>
+__device__ __forceinline__ bool poll_many(const unsigned long long* base, int n, Idx idx, unsigned t,
+                                          int spin_limit, int* status, bool& dead,
+                                          float (&out)[kLoadsPerThread]) {
+    if (dead) {
+#pragma unroll
+        for (int r = 0; r < kLoadsPerThread; ++r) out[r] = __builtin_nanf("");
+        return false;
+    }
+    for (int spins = 0;; ++spins) {
+        bool ready = true;
+#pragma unroll
+        for (int r = 0; r < kLoadsPerThread; ++r) {
+            if (r < n) {
+                const unsigned long long x = __hip_atomic_load(
+                    const_cast<unsigned long long*>(base + idx(r)), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                ready = ready && static_cast<unsigned>(x >> 32) == t;
+                out[r] = __uint_as_float(static_cast<unsigned>(x));
+            }
+        }
+        if (ready) return true;
+        if (((spins & 255) == 255 &&
+             __hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) ||
+            spins >= spin_limit) {
+            if (spins >= spin_limit) atomicOr(status, 1);
+            dead = true;
+#pragma unroll
+            for (int r = 0; r < kLoadsPerThread; ++r) out[r] = __builtin_nanf("");
+            return false;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+}
+
+// Per-column vectors (v, mu) as the row loops use them: rows of up to 32
+// floats per lane keep the vector in registers; longer rows (N > 2048) read
+// it from LDS one chunk at a time, which leaves the registers to the row and
+// the column accumulator.
+template <int VEC, int CH>
+struct ColVec {
+    static constexpr bool kLds = VEC * CH > 32;
+    float reg[kLds ? 1 : VEC * CH];
+    const float* lds;
+
+    __device__ __forceinline__ void bind(const float* v, int lane, int N) {
+        lds = v;
+        if constexpr (!kLds) Row<VEC, CH>::load(v, lane, N, reg, 0.0f);
+    }
+    // columns k*64*VEC + lane*VEC + [0, VEC) of the vector (0 past N)
+    __device__ __forceinline__ void chunk(int lane, int k, int N, float (&out)[VEC]) const {
+        if constexpr (kLds) {
+            const int c = Row<VEC, CH>::col(lane, k);
+            if constexpr (VEC == 4) {  // N % 4 == 0: a chunk is all in or all out
+                float4 t = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                if (c < N) t = *reinterpret_cast<const float4*>(lds + c);
+                out[0] = t.x;
+                out[1] = t.y;
+                out[2] = t.z;
+                out[3] = t.w;
+            } else {
+                out[0] = c < N ? lds[c] : 0.0f;
+            }
+        } else {
+#pragma unroll
+            for (int q = 0; q < VEC; ++q) out[q] = reg[k * VEC + q];
+        }
+    }
+};
+
+// Step 1: fold the waves' per-lane column sums (tree through `tree`, 4 N
+// floats) and publish the workgroup's row with tag t at slot_row.
+template <int VEC, int CH>
+__device__ __forceinline__ void publish_row(float (&acc)[VEC * CH], float* tree, int N,
+                                            unsigned long long* slot_row, unsigned t) {
+    using R = Row<VEC, CH>;
+    res::tree_combine<VEC, CH>(acc, tree, N);
+    if (threadIdx.x < kWave) {
+        const int lane = threadIdx.x;
+#pragma unroll
+        for (int k = 0; k < CH; ++k)
+#pragma unroll
+            for (int q = 0; q < VEC; ++q) {
+                const int col = R::col(lane, k) + q;
+                if (col < N) publish(slot_row + col, acc[k * VEC + q], t);
+            }
+    }
+}
+
+// Step 2: the owner's sums over the element's W rows for its slice [c0, c1),
+// in workgroup order.  `red` holds W * (c1 - c0) floats.  f(j, total) is called
+// once per owned column by one thread.  Contains barriers.
+template <class F>
+__device__ __forceinline__ void reduce_slice(const unsigned long long* rows, int N, int W, int c0, int c1,
+                                             unsigned t, float* red, int spin_limit, int* status,
+                                             bool& dead, F&& f) {
+    // An opaque copy of the thread index keeps the compiler from hoisting these
+    // address computations out of the caller's iteration loop, where they
+    // would hold registers through the whole row phase.
+    int tid = threadIdx.x;
+    asm volatile("" : "+v"(tid));
+    const int S = c1 - c0;
+    const int n = W * S;
+    const int mine = n > tid ? (n - 1 - tid) / kThreads + 1 : 0;
+    float got[kLoadsPerThread];
+    poll_many(rows, mine,
+              [&](int r) {
+                  const int q = tid + r * kThreads;  // q = g * S + jj
+                  return unsigned(q / S) * unsigned(N) + unsigned(c0 + q % S);
+              },
+              t, spin_limit, status, dead, got);
+#pragma unroll
+    for (int r = 0; r < kLoadsPerThread; ++r)
+        if (r < mine) red[tid + r * kThreads] = got[r];
+    __syncthreads();
+    for (int jj = threadIdx.x; jj < S; jj += kThreads) {
+        float s = 0.0f;
+        for (int g = 0; g < W; ++g) s += red[g * S + jj];
+        f(c0 + jj, dead ? __builtin_nanf("") : s);
+    }
+}
+
+// Step 3: read the element's N published results into `out` (LDS).  The
+// caller synchronises before reading `out`.
+__device__ __forceinline__ void gather(const unsigned long long* res_row, int N, unsigned t, float* out,
+                                       int spin_limit, int* status, bool& dead) {
+    int tid = threadIdx.x;  // opaque, as in reduce_slice
+    asm volatile("" : "+v"(tid));
+    const int mine = N > tid ? (N - 1 - tid) / kThreads + 1 : 0;
+    float got[kLoadsPerThread];
+    poll_many(res_row, mine, [&](int r) { return unsigned(tid + r * kThreads); }, t, spin_limit, status, dead,
+              got);
+#pragma unroll
+    for (int r = 0; r < kLoadsPerThread; ++r)
+        if (r < mine) out[tid + r * kThreads] = got[r];
+}
+
+// ---------------------------------------------------------------------------
+// Forward
+// ---------------------------------------------------------------------------
+struct FwdArgs {
+    const float* X;       // scores [B,M,N]
+    float kscale;         // K = X * kscale
+    int scores_kind;      // +1 log_alpha, -1 cost
+    const float* log_a;   // [B,M] or null
+    const float* log_b;   // [B,N] or null
+    float log_a_default, log_b_default;
+    float tol;
+    int max_iter;
+    int return_log;
+    float* plan;          // [B,M,N] or null
+    float* cost_partial;  // [G] by logical workgroup, or null
+    float* u_out;         // [B,M] or null
+    float* v_out;         // [B,N] or null
+    float* u_hist;        // [T,B,M] or null
+    float* v_hist;        // [T,B,N] or null
+    int32_t* iters_used;
+    int32_t* converged;
+    unsigned long long* part;   // [2, G, N] tagged workgroup column sums
+    unsigned long long* res;    // [2, B, N] tagged new v
+    unsigned long long* uslot;  // [2, B, M] tagged u (read by the exact column LSE)
+    unsigned long long* dxchg;  // [kDeltaSlots, G] tagged per-workgroup deltas
+    int* status;
+    int B, M, N, W, R, spin_limit;
+};
+
+// Dual Sinkhorn forward (torch_cuda.cpp:147-264), streaming each workgroup's
+// strip once per iteration.  Row update in base 2 as in res::forward (one
+// wave per row), the shared-exponential column sums, reduce-scatter to the
+// slice owners, who form v_j = log b_j + v_j - log colsum_j (or the exact
+// max-shifted LSE of column j over all M rows when colsum underflows,
+// kernels.cu:629-671), all-gather of v.  The batch-global stop test of
+// iteration t-1 is read during iteration t, as in res::forward.
+template <int VEC, int CH>
+__global__ __launch_bounds__(kThreads) void forward(FwdArgs a) {
+    using R = Row<VEC, CH>;
+    constexpr int PL = R::PL;
+    constexpr float kLn2 = 0.69314718055994531f;
+    // LDS: tree 4N | v N | v log2(e) N | log b N | red N + W (padded to 4) | u 2R | log a R | scratch 32
+    extern __shared__ float lds[];
+    float* tree = lds;
+    float* lds_v = tree + (kWaves / 2) * a.N;
+    float* lds_v2 = lds_v + a.N;
+    float* lds_lb = lds_v2 + a.N;
+    float* red = lds_lb + a.N;
+    float* lds_u = red + ((a.N + a.W + 3) & ~3);
+    float* lds_la = lds_u + 2 * a.R;
+    float* scratch = lds_la + a.R;  // [0] global delta, [1..kWaves] wave deltas, [16..] reductions
+    const int lane = threadIdx.x % kWave;
+    const int wave = threadIdx.x / kWave;
+    const int G = gridDim.x;
+    const int gid = res::logical_group(a.W);
+    const int b = gid / a.W;
+    const int w = gid % a.W;
+    const int row0 = w * a.R;
+    const int rend = min(row0 + a.R, a.M);
+    const int c0 = slice_begin(w, a.W, a.N), c1 = slice_begin(w + 1, a.W, a.N);
+    const size_t bM = size_t(b) * a.M;
+    const size_t bN = size_t(b) * a.N;
+    const bool check = a.tol > 0.0f;
+    const float kscale2 = a.kscale * kLog2E;
+
+    for (int l = threadIdx.x; l < a.R; l += kThreads) {
+        const int i = row0 + l;
+        lds_la[l] = (i < rend && a.log_a) ? a.log_a[bM + i] : a.log_a_default;
+        lds_u[l] = 0.0f;
+        lds_u[a.R + l] = 0.0f;
+    }
+    for (int j = threadIdx.x; j < a.N; j += kThreads) {
+        lds_lb[j] = a.log_b ? a.log_b[bN + j] : a.log_b_default;
+        lds_v[j] = 0.0f;
+        lds_v2[j] = 0.0f;
+    }
+    __syncthreads();
+    bool dead = false;
+    int used = a.max_iter;
+    int conv = 0;
+
+    for (int t = 1; t <= a.max_iter; ++t) {
+        const int cur = t & 1, prev = cur ^ 1;
+        const bool test = check && t >= 2;
+        unsigned long long* ds = a.dxchg + size_t((t - 1) % res::kDeltaSlots) * G;
+        unsigned long long dpre[res::kDeltaPrefetch];
+        if (test && wave == 0) {
+#pragma unroll
+            for (int q = 0; q < res::kDeltaPrefetch; ++q) {
+                const int g = lane + q * kWave;
+                dpre[q] = g < G ? __hip_atomic_load(ds + g, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                : tag_pack(0.0f, unsigned(t - 1));
+            }
+        }
+        ColVec<VEC, CH> v2;
+        v2.bind(lds_v2, lane, a.N);
+        float acc[PL];
+#pragma unroll
+        for (int e = 0; e < PL; ++e) acc[e] = 0.0f;
+        float dmax = 0.0f;
+        for (int l = wave; row0 + l < rend; l += kWaves) {
+            const int i = row0 + l;
+            const int ln = opaque_lane();
+            float y[PL];
+            R::load(a.X + (bM + i) * a.N, ln, a.N, y, 0.0f);
+            float ml = -FLT_MAX;
+#pragma unroll
+            for (int k = 0; k < CH; ++k) {
+                float vv[VEC];
+                v2.chunk(ln, k, a.N, vv);
+#pragma unroll
+                for (int q = 0; q < VEC; ++q) {
+                    const int e = k * VEC + q;
+                    y[e] = R::valid(ln, e, a.N) ? fmaf(y[e], kscale2, vv[q]) : -INFINITY;
+                    ml = fmaxf(ml, y[e]);
+                }
+            }
+            const float m = wave_max(ml);
+            float sl = 0.0f;
+#pragma unroll
+            for (int e = 0; e < PL; ++e) {
+                y[e] = __builtin_amdgcn_exp2f(y[e] - m);
+                sl += y[e];
+            }
+            const float s = fmaxf(wave_sum(sl), sk::kSumFloor);
+            const float lga = lds_la[l];
+            const float lg2 = __builtin_amdgcn_logf(s);
+            const float u = lga - kLn2 * (m + lg2);
+            const float wgt = __builtin_amdgcn_exp2f(fmaf(lga, kLog2E, -lg2));
+#pragma unroll
+            for (int e = 0; e < PL; ++e) acc[e] = fmaf(y[e], wgt, acc[e]);
+#pragma unroll
+            for (int e = 0; e < PL; ++e) asm volatile("" : "+v"(acc[e]));  // keep the update here
+            dmax = fmaxf(dmax, fabsf(u - lds_u[prev * a.R + l]));
+            if (lane == 0) {
+                lds_u[cur * a.R + l] = u;
+                publish(a.uslot + size_t(cur) * a.B * a.M + bM + i, u, unsigned(t));
+                if (a.u_hist) a.u_hist[(size_t(t - 1) * a.B + b) * a.M + i] = u;
+            }
+        }
+        if (lane == 0) scratch[1 + wave] = dmax;
+        publish_row<VEC, CH>(acc, tree, a.N, a.part + (size_t(cur) * G + gid) * a.N, unsigned(t));
+        if (check && threadIdx.x == 0) {
+            float d = scratch[1];
+#pragma unroll
+            for (int q = 1; q < kWaves; ++q) d = fmaxf(d, scratch[1 + q]);
+            publish(a.dxchg + size_t(t % res::kDeltaSlots) * G + gid, d, unsigned(t));
+        }
+        unsigned long long* res_row = a.res + (size_t(cur) * a.B + b) * a.N;
+        const unsigned long long* urow = a.uslot + size_t(cur) * a.B * a.M + bM;
+        reduce_slice(a.part + size_t(cur) * G * a.N + size_t(b) * a.W * a.N, a.N, a.W, c0, c1, unsigned(t),
+                     red, a.spin_limit, a.status, dead, [&](int j, float cs) {
+                         float vn;
+                         if (cs >= sk::kColSumFloor && cs <= FLT_MAX) {
+                             vn = lds_lb[j] + lds_v[j] - logf(cs);
+                         } else {
+                             // exact max-shifted LSE over the column (kernels.cu:629-671)
+                             const float* col = a.X + bM * a.N + j;
+                             float mx = -FLT_MAX;
+                             for (int i = 0; i < a.M; ++i) {
+                                 const float ui = res::collect(const_cast<unsigned long long*>(urow + i), unsigned(t),
+                                                               a.spin_limit, a.status, dead);
+                                 mx = fmaxf(mx, col[size_t(i) * a.N] * a.kscale + ui);
+                             }
+                             float sm = 0.0f;
+                             for (int i = 0; i < a.M; ++i) {
+                                 const float ui = __uint_as_float(static_cast<unsigned>(__hip_atomic_load(
+                                     const_cast<unsigned long long*>(urow + i), __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT)));
+                                 sm += safe_exp(col[size_t(i) * a.N] * a.kscale + ui - mx);
+                             }
+                             vn = lds_lb[j] - (mx + logf(fmaxf(sm, sk::kSumFloor)));
+                         }
+                         publish(res_row + j, vn, unsigned(t));
+                         if (a.v_hist) a.v_hist[(size_t(t - 1) * a.B + b) * a.N + j] = vn;
+                     });
+        __syncthreads();  // the owners have read lds_v (v_{t-1}); it now receives v_t
+        gather(res_row, a.N, unsigned(t), lds_v, a.spin_limit, a.status, dead);
+        for (int j = threadIdx.x; j < a.N; j += kThreads) lds_v2[j] = lds_v[j] * kLog2E;  // own writes
+        if (test && wave == 0) {
+            float gmax = 0.0f;
+#pragma unroll
+            for (int q = 0; q < res::kDeltaPrefetch; ++q) {
+                const int g = lane + q * kWave;
+                if (g < G) {
+                    float d = __uint_as_float(static_cast<unsigned>(dpre[q]));
+                    if (static_cast<unsigned>(dpre[q] >> 32) != unsigned(t - 1))
+                        d = res::collect(ds + g, unsigned(t - 1), a.spin_limit, a.status, dead);
+                    gmax = res::OpMaxNan{}(gmax, d);
+                }
+            }
+            for (int g = lane + res::kDeltaPrefetch * kWave; g < G; g += kWave)
+                gmax = res::OpMaxNan{}(gmax, res::collect(ds + g, unsigned(t - 1), a.spin_limit, a.status, dead));
+            gmax = wave_reduce(gmax, res::OpMaxNan{});
+            if (lane == 0) scratch[0] = gmax;
+        }
+        __syncthreads();
+        if (test && scratch[0] < a.tol) {  // the stop test of iteration t-1 fired: back to v_{t-1}
+            used = t - 1;
+            conv = 1;
+            __syncthreads();
+            gather(a.res + (size_t(prev) * a.B + b) * a.N, a.N, unsigned(t - 1), lds_v, a.spin_limit,
+                   a.status, dead);
+            __syncthreads();
+            break;
+        }
+    }
+    if (check && conv == 0 && a.max_iter >= 1) {
+        // the last iteration's deltas decide `converged`
+        const unsigned T = unsigned(a.max_iter);
+        unsigned long long* ds = a.dxchg + size_t(a.max_iter % res::kDeltaSlots) * G;
+        if (wave == 0) {
+            float m = 0.0f;
+            for (int g = lane; g < G; g += kWave)
+                m = res::OpMaxNan{}(m, res::collect(ds + g, T, a.spin_limit, a.status, dead));
+            m = wave_reduce(m, res::OpMaxNan{});
+            if (lane == 0) scratch[0] = m;
+        }
+        __syncthreads();
+        conv = scratch[0] < a.tol ? 1 : 0;
+    }
+
+    // P = safe_exp(K + u + v) (kernels.cu:755-775) and this workgroup's share of sum(P C).
+    const int par = used & 1;
+    const bool failed = __hip_atomic_load(a.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
+    ColVec<VEC, CH> vf;
+    vf.bind(lds_v, lane, a.N);
+    if (a.v_out && w == 0)
+        for (int j = threadIdx.x; j < a.N; j += kThreads) a.v_out[bN + j] = lds_v[j];
+    const float csign = a.scores_kind < 0 ? 1.0f : -1.0f;  // C = -log_alpha
+    float cacc = 0.0f;
+    for (int l = wave; row0 + l < rend; l += kWaves) {
+        const int i = row0 + l;
+        const float ui = lds_u[par * a.R + l];
+        if (a.u_out && lane == 0) a.u_out[bM + i] = ui;
+        const int ln = opaque_lane();
+        float x[PL];
+        R::load(a.X + (bM + i) * a.N, ln, a.N, x, 0.0f);
+#pragma unroll
+        for (int k = 0; k < CH; ++k) {
+            float vv[VEC];
+            vf.chunk(ln, k, a.N, vv);
+#pragma unroll
+            for (int q = 0; q < VEC; ++q) {
+                const int e = k * VEC + q;
+                const float lp = (x[e] * a.kscale + ui) + vv[q];
+                const float pe = a.return_log ? lp : safe_exp(lp);
+                if (a.cost_partial && R::valid(ln, e, a.N)) cacc = fmaf(pe, csign * x[e], cacc);
+                x[e] = failed ? __builtin_nanf("") : pe;
+            }
+        }
+        if (a.plan) R::store(a.plan + (bM + i) * a.N, ln, a.N, x);
+    }
+    if (a.cost_partial) {
+        const float cs = block_reduce<kWaves>(wave_sum(cacc), scratch + 16, OpSum{});
+        if (threadIdx.x == 0) a.cost_partial[gid] = failed ? __builtin_nanf("") : cs;
+    }
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        *a.iters_used = failed ? -1 : used;  // -1: an exchange timed out, the outputs are NaN
+        *a.converged = conv;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Implicit adjoint
+// ---------------------------------------------------------------------------
+struct ImpArgs {
+    const float* X;
+    int scores_kind;
+    const float* gP;      // [B,M,N] or null
+    const float* gC;      // [B] or null
+    const float* P;       // [B,M,N]
+    unsigned long long* part;  // [2, G, N] tagged workgroup column sums
+    unsigned long long* res;   // [2, B, N] tagged mu
+    unsigned long long* pro;   // [2, G, N] tagged prologue sums (P G, P)
+    float* grad;
+    float* tau_partial;   // [G] by logical workgroup
+    int* status;
+    float inv_tau;
+    int B, M, N, W, R, iters, spin_limit;
+};
+
+template <int VEC, int CH>
+__device__ __forceinline__ void upstream(const ImpArgs& a, size_t off, int lane, float gc, float csign,
+                                         float (&x)[VEC * CH], float (&G)[VEC * CH]) {
+    using R = Row<VEC, CH>;
+    R::load(a.X + off, lane, a.N, x, 0.0f);
+    if (a.gP) {
+        R::load(a.gP + off, lane, a.N, G, 0.0f);
+    } else {
+#pragma unroll
+        for (int e = 0; e < R::PL; ++e) G[e] = 0.0f;
+    }
+    if (a.gC) {
+#pragma unroll
+        for (int e = 0; e < R::PL; ++e) G[e] += gc * (csign * x[e]);
+    }
+}
+
+// The implicit adjoint (kernels.cu:965-1098) streaming P once per sweep:
+// prologue r, rs (rows) and c, cs (slice owners); per sweep lambda_i for the
+// workgroup's rows, column sums of P lambda, reduce-scatter to the owners who
+// form mu_k = (c_k - sum) / max(cs_k, 1e-12), all-gather of mu; final phase
+// grad = P (G - lambda - mu) / tau (log-alpha kind: that - grad_cost P; cost
+// kind: grad_cost P - that) and the workgroup's share of sum(grad * log_alpha).
+template <int VEC, int CH>
+__global__ __launch_bounds__(kThreads) void implicit_adjoint(ImpArgs a) {
+    using R = Row<VEC, CH>;
+    constexpr int PL = R::PL;
+    // LDS: tree 4N | mu N | red N + W | r R | 1/rs R | lambda R | c S | cs S | scratch 16
+    extern __shared__ float lds[];
+    const int lane = threadIdx.x % kWave;
+    const int wave = threadIdx.x / kWave;
+    const int G = gridDim.x;
+    const int gid = res::logical_group(a.W);
+    const int b = gid / a.W;
+    const int w = gid % a.W;
+    const int row0 = w * a.R;
+    const int rend = min(row0 + a.R, a.M);
+    const int c0 = slice_begin(w, a.W, a.N), c1 = slice_begin(w + 1, a.W, a.N);
+    const int S = (a.N + a.W - 1) / a.W;
+    float* tree = lds;
+    float* lds_mu = tree + (kWaves / 2) * a.N;
+    float* red = lds_mu + a.N;
+    float* lds_r = red + a.N + a.W;
+    float* lds_irs = lds_r + a.R;
+    float* lds_lam = lds_irs + a.R;
+    float* lds_c = lds_lam + a.R;
+    float* lds_cs = lds_c + S;
+    float* scratch = lds_cs + S;
+    const size_t bM = size_t(b) * a.M;
+    const bool cost_kind = a.scores_kind < 0;
+    const float gc = a.gC ? a.gC[b] : 0.0f;
+    const float csign = cost_kind ? 1.0f : -1.0f;  // C = csign * scores
+    bool dead = false;
+
+    // Prologue: row sums of P G and P; column sums to the slice owners.
+    float cg[PL], cp[PL];
+#pragma unroll
+    for (int e = 0; e < PL; ++e) cg[e] = cp[e] = 0.0f;
+    for (int l = wave; row0 + l < rend; l += kWaves) {
+        const size_t off = (bM + row0 + l) * a.N;
+        const int ln = opaque_lane();
+        float p[PL], x[PL], Gr[PL];
+        R::load(a.P + off, ln, a.N, p, 0.0f);
+        upstream<VEC, CH>(a, off, ln, gc, csign, x, Gr);
+        float sg = 0.0f, sp = 0.0f;
+#pragma unroll
+        for (int e = 0; e < PL; ++e) {
+            sg = fmaf(p[e], Gr[e], sg);
+            sp += p[e];
+            cg[e] = fmaf(p[e], Gr[e], cg[e]);
+            cp[e] += p[e];
+        }
+        sg = wave_sum(sg);
+        sp = wave_sum(sp);
+        if (lane == 0) {
+            lds_r[l] = sg;
+            lds_irs[l] = 1.0f / fmaxf(sp, sk::kSumFloor);
+            lds_lam[l] = 0.0f;
+        }
+    }
+    publish_row<VEC, CH>(cg, tree, a.N, a.pro + size_t(gid) * a.N, 1u);
+    publish_row<VEC, CH>(cp, tree, a.N, a.pro + (size_t(G) + gid) * a.N, 1u);
+    reduce_slice(a.pro + size_t(b) * a.W * a.N, a.N, a.W, c0, c1, 1u, red, a.spin_limit, a.status, dead,
+                 [&](int j, float tot) { lds_c[j - c0] = tot; });
+    __syncthreads();
+    reduce_slice(a.pro + (size_t(G) + size_t(b) * a.W) * a.N, a.N, a.W, c0, c1, 1u, red, a.spin_limit,
+                 a.status, dead, [&](int j, float tot) { lds_cs[j - c0] = fmaxf(tot, sk::kSumFloor); });
+    for (int j = threadIdx.x; j < a.N; j += kThreads) lds_mu[j] = 0.0f;
+    __syncthreads();
+
+    // Sweeps.
+    for (int t = 1; t <= a.iters; ++t) {
+        const int cur = t & 1;
+        ColVec<VEC, CH> mu;
+        mu.bind(lds_mu, lane, a.N);
+        float acc[PL];
+#pragma unroll
+        for (int e = 0; e < PL; ++e) acc[e] = 0.0f;
+        for (int l = wave; row0 + l < rend; l += kWaves) {
+            const int ln = opaque_lane();
+            float p[PL];
+            R::load(a.P + (bM + row0 + l) * a.N, ln, a.N, p, 0.0f);
+            float d = 0.0f;
+#pragma unroll
+            for (int k = 0; k < CH; ++k) {
+                float mm[VEC];
+                mu.chunk(ln, k, a.N, mm);
+#pragma unroll
+                for (int q = 0; q < VEC; ++q) d = fmaf(p[k * VEC + q], mm[q], d);
+            }
+            const float lam = (lds_r[l] - wave_sum(d)) * lds_irs[l];
+#pragma unroll
+            for (int e = 0; e < PL; ++e) acc[e] = fmaf(p[e], lam, acc[e]);
+            if (lane == 0) lds_lam[l] = lam;
+        }
+        publish_row<VEC, CH>(acc, tree, a.N, a.part + (size_t(cur) * G + gid) * a.N, unsigned(t));
+        unsigned long long* res_row = a.res + (size_t(cur) * a.B + b) * a.N;
+        reduce_slice(a.part + size_t(cur) * G * a.N + size_t(b) * a.W * a.N, a.N, a.W, c0, c1, unsigned(t),
+                     red, a.spin_limit, a.status, dead, [&](int j, float tot) {
+                         publish(res_row + j, (lds_c[j - c0] - tot) / lds_cs[j - c0], unsigned(t));
+                     });
+        gather(res_row, a.N, unsigned(t), lds_mu, a.spin_limit, a.status, dead);
+        __syncthreads();
+    }
+
+    // Final phase: stream P and G again and write this workgroup's gradient rows.
+    const bool failed = __hip_atomic_load(a.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
+    ColVec<VEC, CH> mu;
+    mu.bind(lds_mu, lane, a.N);
+    float tacc = 0.0f;
+    for (int l = wave; row0 + l < rend; l += kWaves) {
+        const size_t off = (bM + row0 + l) * a.N;
+        const float lam = lds_lam[l];
+        const int ln = opaque_lane();
+        float p[PL], x[PL], Gr[PL];
+        R::load(a.P + off, ln, a.N, p, 0.0f);
+        upstream<VEC, CH>(a, off, ln, gc, csign, x, Gr);
+#pragma unroll
+        for (int k = 0; k < CH; ++k) {
+            float mm[VEC];
+            mu.chunk(ln, k, a.N, mm);
+#pragma unroll
+            for (int q = 0; q < VEC; ++q) {
+                const int e = k * VEC + q;
+                const float gl = (p[e] * ((Gr[e] - lam) - mm[q])) * a.inv_tau;
+                const float la = cost_kind ? -x[e] : x[e];
+                if (R::valid(ln, e, a.N)) tacc = fmaf(gl, la, tacc);
+                p[e] = failed ? __builtin_nanf("") : (cost_kind ? gc * p[e] - gl : gl - gc * p[e]);
+            }
+        }
+        R::store(a.grad + off, ln, a.N, p);
+    }
+    const float tsum = block_reduce<kWaves>(wave_sum(tacc), scratch, OpSum{});
+    if (threadIdx.x == 0) a.tau_partial[gid] = failed ? __builtin_nanf("") : tsum;
+}
+
+}  // namespace pst
+}  // namespace dot_amd

@@ -7,6 +7,7 @@
 #include <string>
 
 #include "host.hpp"
+#include "persistent.cuh"
 #include "resident.cuh"
 #include "sinkhorn_kernels.cuh"
 
@@ -41,6 +42,13 @@ size_t resident_groups_max(int B, int M, int N) {
     return std::min<size_t>(size_t(B) * per_b, 1024);
 }
 
+// Upper bound on the workgroups of a persistent streaming launch (at most
+// pst::kMaxGroups per batch element, at most 1024 in all).
+size_t pst_groups_max(int B, int M, int N) {
+    if (N > kMaxRowLen || N < 1 || M < 1) return 0;
+    return std::min<size_t>(size_t(B) * size_t(std::min(M, pst::kMaxGroups)), 1024);
+}
+
 struct FwdLayout {
     uint32_t* delta;
     float* ubuf;
@@ -55,6 +63,8 @@ struct FwdLayout {
     int* status;
     size_t groups;
     size_t res_words;           // 32-bit words from xchg through status
+    unsigned long long* pst;    // persistent streaming path: tagged slots, laid out per launch
+    size_t pst_groups;
     int rows, nstrips;
     size_t bytes;
 };
@@ -69,7 +79,8 @@ FwdLayout fwd_layout(void* ws, int B, int M, int N, int max_iter) {
     L.rows = strip_rows(B, M);
     L.nstrips = (M + L.rows - 1) / L.rows;
     L.partial = c.take<float>(size_t(B) * L.nstrips * N);
-    L.cost_partial = c.take<float>(size_t(B) * std::max(L.nstrips, res::kMaxGroup));
+    L.pst_groups = pst_groups_max(B, M, N);
+    L.cost_partial = c.take<float>(std::max(size_t(B) * std::max(L.nstrips, res::kMaxGroup), L.pst_groups));
     L.groups = resident_groups_max(B, M, N);
     const size_t gn = L.groups * size_t(N);
     const size_t words = 6 * gn + res::kDeltaSlots * L.groups + 1;
@@ -80,6 +91,10 @@ FwdLayout fwd_layout(void* ws, int B, int M, int N, int max_iter) {
         L.status = reinterpret_cast<int*>(L.dxchg + res::kDeltaSlots * L.groups);
     }
     L.res_words = 2 * words;
+    // [2, G, N] partial rows | [2, B, N] v | [2, B, M] u | deltas [kDeltaSlots, G] | status
+    L.pst = c.take<unsigned long long>(L.pst_groups ? 2 * L.pst_groups * size_t(N) + 2 * size_t(B) * N +
+                                                          2 * size_t(B) * M + res::kDeltaSlots * L.pst_groups + 1
+                                                    : 0);
     L.bytes = c.used();
     return L;
 }
@@ -90,6 +105,8 @@ struct ImpLayout {
     int* status;
     size_t groups;             // workgroups the slots are laid out for
     size_t xchg_words;         // 32-bit words to clear (slots and status)
+    unsigned long long* pst;   // persistent streaming path: tagged slots, laid out per launch
+    size_t pst_groups;
     int rows, nstrips;
     size_t bytes;
 };
@@ -107,7 +124,7 @@ ImpLayout imp_layout(void* ws, int B, int M, int N) {
     L.mu = c.take<float>(size_t(B) * N);
     L.partA = c.take<float>(size_t(B) * L.nstrips * N);
     L.partB = c.take<float>(size_t(B) * L.nstrips * N);
-    L.tau_partial = c.take<float>(size_t(B) * std::max(L.nstrips, 64));
+    L.tau_partial = c.take<float>(size_t(B) * std::max(L.nstrips, pst::kMaxGroups));
     // The resident path runs at most one workgroup per CU and only for N <= 1024.
     const size_t groups = resident_groups_max(B, M, N);
     // [2, G, N] sweep slots, [2, G, N] prologue slots, then the status word
@@ -115,6 +132,9 @@ ImpLayout imp_layout(void* ws, int B, int M, int N) {
     L.xchg = c.take<unsigned long long>(4 * groups * size_t(N) + 1);
     L.status = reinterpret_cast<int*>(L.xchg ? L.xchg + 4 * groups * size_t(N) : nullptr);
     L.xchg_words = (4 * groups * size_t(N) + 1) * 2;
+    // [2, G, N] sweep rows | [2, B, N] mu | [2, G, N] prologue rows | status
+    L.pst_groups = pst_groups_max(B, M, N);
+    L.pst = c.take<unsigned long long>(L.pst_groups ? 4 * L.pst_groups * size_t(N) + 2 * size_t(B) * N + 1 : 0);
     L.bytes = c.used();
     return L;
 }
@@ -265,6 +285,96 @@ bool dispatch_resident(const ResidentCfg& c, F&& f) {
 
 constexpr int kSpinLimit = 1 << 20;  // ~1-2 s of polling before a resident kernel gives up
 
+// Persistent streaming configuration: W workgroups per batch element (as many
+// as the CUs allow, at most pst::kMaxGroups and M), R rows each.
+struct StreamCfg {
+    bool ok = false;
+    int W = 1, R = 1;
+};
+
+StreamCfg stream_config(int B, int M, int N) {
+    StreamCfg c;
+    const char* env = std::getenv("DOT_AMD_PERSISTENT");
+    if (env && env[0] == '0') return c;
+    if (N < 1 || N > kMaxRowLen || M < 1 || B < 1) return c;
+    const int cus = device_cus();
+    if (cus <= 0 || B > cus) return c;
+    c.W = std::min({cus / B, pst::kMaxGroups, M});
+    if (int64_t(B) * c.W > 1024) return c;
+    c.R = (M + c.W - 1) / c.W;
+    c.ok = true;
+    return c;
+}
+
+// One cooperative launch `kernel(args)` of G workgroups with `lds` bytes, if
+// the device can hold them all at once.
+template <class K, class A>
+bool launch_cooperative(K kernel, A& args, int G, size_t lds, hipStream_t stream) {
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, res::kThreads, lds) != hipSuccess ||
+        per_cu < 1 || int64_t(per_cu) * device_cus() < G)
+        return false;
+    void* params[] = {&args};
+    return hipLaunchCooperativeKernel(reinterpret_cast<const void*>(kernel), dim3(G), dim3(res::kThreads),
+                                      params, static_cast<unsigned>(lds), stream) == hipSuccess;
+}
+
+bool launch_stream_forward(const dot_sinkhorn_fwd_args* a, const FwdLayout& L, const StreamCfg& sc,
+                           float kscale, float log_a_default, float log_b_default, bool keep, bool ret_log,
+                           bool vec4, hipStream_t stream) {
+    const int B = a->B, M = a->M, N = a->N, G = B * sc.W;
+    if (!L.pst || size_t(G) > L.pst_groups) return false;
+    pst::FwdArgs r{};
+    r.X = a->scores;
+    r.kscale = kscale;
+    r.scores_kind = a->scores_kind;
+    r.log_a = a->log_a;
+    r.log_b = a->log_b;
+    r.log_a_default = log_a_default;
+    r.log_b_default = log_b_default;
+    r.tol = a->tol;
+    r.max_iter = a->max_iter;
+    r.return_log = ret_log ? 1 : 0;
+    r.plan = a->plan;
+    r.cost_partial = a->cost ? L.cost_partial : nullptr;
+    r.u_out = a->u_out;
+    r.v_out = a->v_out;
+    r.u_hist = keep ? a->u_hist : nullptr;
+    r.v_hist = keep ? a->v_hist : nullptr;
+    r.iters_used = a->iters_used;
+    r.converged = a->converged;
+    r.part = L.pst;
+    r.res = r.part + 2 * size_t(G) * N;
+    r.uslot = r.res + 2 * size_t(B) * N;
+    r.dxchg = r.uslot + 2 * size_t(B) * M;
+    r.status = reinterpret_cast<int*>(r.dxchg + res::kDeltaSlots * size_t(G));
+    r.B = B;
+    r.M = M;
+    r.N = N;
+    r.W = sc.W;
+    r.R = sc.R;
+    r.spin_limit = kSpinLimit;
+    const size_t words = size_t(reinterpret_cast<unsigned long long*>(r.status) - L.pst) + 1;
+    const size_t lds =
+        (size_t(8) * N + ((size_t(N) + sc.W + 3) & ~size_t(3)) - N + 3 * size_t(sc.R) + res::kFwdScratch) *
+        sizeof(float);
+    bool ok = false;
+    dispatch_row(N, vec4, [&](auto vc, auto cc) {
+        constexpr int V = decltype(vc)::value;
+        constexpr int C = decltype(cc)::value;
+        launch_fill_zero(L.pst, 2 * words, stream);
+        ProfScope prof("sk_fwd_persistent", stream);
+        ok = launch_cooperative(pst::forward<V, C>, r, G, lds, stream);
+    });
+    if (!ok) return false;
+    if (a->cost) {
+        ProfScope prof("sk_batch_sum", stream);
+        hipLaunchKernelGGL(sk::batch_sum, dim3(B), dim3(kWave), 0, stream, L.cost_partial, sc.W, 1.0f,
+                           a->cost);
+    }
+    return true;
+}
+
 // Cooperative launch of the register-resident forward; false when this shape or
 // device cannot host it (the caller then runs the streaming sweeps).
 bool launch_resident_forward(const dot_sinkhorn_fwd_args* a, const FwdLayout& L, const ResidentCfg& rc,
@@ -388,7 +498,12 @@ extern "C" int dot_sinkhorn_forward(const dot_sinkhorn_fwd_args* a, dot_stream_t
     if (rc.ok && launch_resident_forward(a, L, rc, kscale, log_a_default, log_b_default, keep, ret_log,
                                          stream))
         return check_launch("dot_sinkhorn_forward");
-    (void)hipGetLastError();  // a refused cooperative launch falls back to the sweeps
+    (void)hipGetLastError();  // a refused cooperative launch falls back to the next tier
+    const StreamCfg sc = stream_config(B, M, N);
+    if (sc.ok && launch_stream_forward(a, L, sc, kscale, log_a_default, log_b_default, keep, ret_log, vec4,
+                                       stream))
+        return check_launch("dot_sinkhorn_forward");
+    (void)hipGetLastError();
 
     launch_fill_zero(a->workspace, L.zero_words, stream);
 
@@ -571,6 +686,48 @@ bool launch_resident_adjoint(const dot_sinkhorn_bwd_args* a, const ImpLayout& L,
     return true;
 }
 
+bool launch_stream_adjoint(const dot_sinkhorn_bwd_args* a, const ImpLayout& L, const StreamCfg& sc,
+                           float inv_tau, bool vec4, hipStream_t stream) {
+    const int B = a->B, N = a->N, G = B * sc.W;
+    if (!L.pst || size_t(G) > L.pst_groups) return false;
+    pst::ImpArgs r{};
+    r.X = a->scores;
+    r.scores_kind = a->scores_kind;
+    r.gP = a->grad_plan;
+    r.gC = a->grad_cost;
+    r.P = a->plan;
+    r.part = L.pst;
+    r.res = r.part + 2 * size_t(G) * N;
+    r.pro = r.res + 2 * size_t(B) * N;
+    r.status = reinterpret_cast<int*>(r.pro + 2 * size_t(G) * N);
+    r.grad = a->grad_scores;
+    r.tau_partial = L.tau_partial;
+    r.inv_tau = inv_tau;
+    r.B = B;
+    r.M = a->M;
+    r.N = N;
+    r.W = sc.W;
+    r.R = sc.R;
+    r.iters = a->iters;
+    r.spin_limit = kSpinLimit;
+    const size_t words = size_t(reinterpret_cast<unsigned long long*>(r.status) - L.pst) + 1;
+    const size_t S = (size_t(N) + sc.W - 1) / sc.W;
+    const size_t lds = (size_t(6) * N + sc.W + 3 * size_t(sc.R) + 2 * S + 16) * sizeof(float);
+    bool ok = false;
+    dispatch_row(N, vec4, [&](auto vc, auto cc) {
+        constexpr int V = decltype(vc)::value;
+        constexpr int C = decltype(cc)::value;
+        launch_fill_zero(L.pst, 2 * words, stream);
+        ProfScope prof("sk_imp_persistent", stream);
+        ok = launch_cooperative(pst::implicit_adjoint<V, C>, r, G, lds, stream);
+    });
+    if (!ok) return false;
+    ProfScope prof("sk_batch_sum", stream);
+    hipLaunchKernelGGL(sk::batch_sum, dim3(B), dim3(kWave), 0, stream, L.tau_partial, sc.W, -inv_tau,
+                       a->grad_tau);
+    return true;
+}
+
 }  // namespace
 
 extern "C" size_t dot_sinkhorn_backward_implicit_workspace_bytes(int B, int M, int N) {
@@ -611,7 +768,11 @@ extern "C" int dot_sinkhorn_backward_implicit(const dot_sinkhorn_bwd_args* a, do
     const ResidentCfg rc = resident_config<false>(B, M, N, bwd_vec4(a));
     if (rc.ok && launch_resident_adjoint(a, L, rc, inv_tau, stream))
         return check_launch("dot_sinkhorn_backward_implicit");
-    (void)hipGetLastError();  // a refused cooperative launch falls back to the sweeps
+    (void)hipGetLastError();  // a refused cooperative launch falls back to the next tier
+    const StreamCfg sc = stream_config(B, M, N);
+    if (sc.ok && launch_stream_adjoint(a, L, sc, inv_tau, bwd_vec4(a), stream))
+        return check_launch("dot_sinkhorn_backward_implicit");
+    (void)hipGetLastError();
     bool launched = dispatch_row(N, bwd_vec4(a), [&](auto vc, auto cc) {
         constexpr int V = decltype(vc)::value;
         constexpr int C = decltype(cc)::value;

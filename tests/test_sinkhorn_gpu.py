@@ -603,3 +603,65 @@ def test_resident_forward_exact_column_fallback(monkeypatch):
         assert int(used) == T
         assert torch.isfinite(P).all(), mode
         assert rel_err(P, Po) < FWD_TOL, mode
+
+
+def _three_paths(monkeypatch, fn):
+    """fn() on the persistent streaming kernels ("persistent", the register-
+    resident tier switched off) and on the per-iteration sweeps ("sweeps")."""
+    out = {}
+    for name, env in (("persistent", {"DOT_AMD_RESIDENT": "0"}),
+                      ("sweeps", {"DOT_AMD_RESIDENT": "0", "DOT_AMD_PERSISTENT": "0"})):
+        for k, v in env.items():
+            monkeypatch.setenv(k, v)
+        out[name] = fn()
+        for k in env:
+            monkeypatch.delenv(k)
+    return out
+
+
+@pytest.mark.parametrize("B,M,N,tau,T,tol,nonuni", [
+    (2, 300, 2048, 0.3, 30, 0.0, False),
+    (3, 130, 4096, 0.5, 12, 0.0, True),
+    (4, 257, 1000, 0.2, 300, 1e-5, True),
+    (5, 64, 64, 1.0, 50, 0.0, False),
+    (1, 7, 3, 0.7, 25, 1e-6, True),
+])
+def test_persistent_and_sweeps_agree_with_oracle(B, M, N, tau, T, tol, nonuni, monkeypatch):
+    """Forward and implicit adjoint of the persistent streaming tier (one
+    cooperative launch, reduce-scatter/all-gather exchange) and of the
+    per-iteration sweeps, each against the oracle at its own iteration count."""
+    rng = np.random.default_rng(7 * B + M + N)
+    C = rng.random((B, M, N)).astype(np.float32)
+    G = rng.standard_normal((B, M, N)).astype(np.float32)
+    lga = np.log(_dirichlet(rng, B, M)) if nonuni else None
+    lgb = np.log(_dirichlet(rng, B, N)) if nonuni else None
+    lt = lambda x: None if x is None else _t(x)
+    fwd = _three_paths(monkeypatch, lambda: _ops.sinkhorn_dual_forward(_t(-C), tau, T, tol, lt(lga), lt(lgb)))
+    counts = {k: int(v[1]) for k, v in fwd.items()}
+    assert abs(counts["persistent"] - counts["sweeps"]) <= 1, counts
+    for name, (P, used, conv) in fwd.items():
+        Po = osk.dual_forward(-C, tau, int(used), log_a=lga, log_b=lgb).P
+        assert rel_err(P, Po) < FWD_TOL, name
+    bwd = _three_paths(monkeypatch, lambda: _ops.sinkhorn_with_grads_implicit(
+        _t(-C), _t(G), tau, min(T, 40), min(T, 40), lt(lga), lt(lgb)))
+    Po, go, gto = osk.with_grads_implicit(-C, G, tau, min(T, 40), min(T, 40), lga, lgb)
+    for name, (P, g, gt) in bwd.items():
+        assert rel_err(P, Po) < FWD_TOL, name
+        assert rel_err(g, go) < GRAD_TOL, name
+        assert sum_err(gt, gto, go * -C / tau) < GRAD_TOL, name
+
+
+def test_persistent_exact_column_fallback(monkeypatch):
+    """The underflowing-column case of test_resident_forward_exact_column_fallback
+    on the persistent tier, with a row longer than the resident limit."""
+    rng = np.random.default_rng(9)
+    B, M, N, tau, T = 2, 96, 1536, 0.01, 10
+    C = (0.1 * rng.random((B, M, N))).astype(np.float32)
+    C[:, :, 7] = 0.7
+    C[1, :, 1500] = 0.8
+    fwd = _three_paths(monkeypatch, lambda: _ops.sinkhorn_dual_forward(_t(-C), tau, T, 0.0))
+    Po = osk.dual_forward(-C, tau, T).P
+    for name, (P, used, _) in fwd.items():
+        assert int(used) == T
+        assert torch.isfinite(P).all(), name
+        assert rel_err(P, Po) < FWD_TOL, name
