@@ -64,15 +64,6 @@ BwdLayout bwd_layout(void* ws, int B, int L1, int L2) {
     return L;
 }
 
-__global__ void column_fold(const float* partial, int nstrips, int N, float* out) {
-    const int b = blockIdx.y;
-    const int j = blockIdx.x * kBlock + threadIdx.x;
-    if (j >= N) return;
-    const size_t base = size_t(b) * nstrips * N + j;
-    float s = 0.0f;
-    for (int k = 0; k < nstrips; ++k) s += partial[base + size_t(k) * N];
-    out[size_t(b) * N + j] = s;
-}
 
 __global__ void batch_sum(const float* partial, int nblk, float scale, float* out) {
     const int b = blockIdx.x;
@@ -148,7 +139,7 @@ extern "C" int dot_bidisoftmax_forward(const dot_bidisoftmax_fwd_args* a, dot_st
         }
         {
             ProfScope prof("bidi_fwd_col_combine", stream);
-            hipLaunchKernelGGL(bidi::fwd_col_combine, dim3((L2 + kBlock - 1) / kBlock, B),
+            hipLaunchKernelGGL(bidi::fwd_col_combine, dim3((L2 + bidi::kFoldCols - 1) / bidi::kFoldCols, B),
                                dim3(kBlock), 0, stream, x);
         }
         {
@@ -218,7 +209,8 @@ extern "C" int dot_bidisoftmax_backward(const dot_bidisoftmax_bwd_args* a, dot_s
             }
             {
                 ProfScope prof("bidi_bwd_fold", stream);
-                hipLaunchKernelGGL(column_fold, dim3((L2 + kBlock - 1) / kBlock, B), dim3(kBlock), 0,
+                hipLaunchKernelGGL(bidi::column_fold, dim3((L2 + bidi::kFoldCols - 1) / bidi::kFoldCols, B),
+                                   dim3(kBlock), 0,
                                    stream, L.partial, L.nstrips, L2, L.dot_c);
             }
             {

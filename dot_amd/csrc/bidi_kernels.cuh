@@ -149,18 +149,66 @@ __global__ __launch_bounds__(kBlock) void fwd_stats(FwdArgs a) {
     }
 }
 
-// Column statistics: merge the strips' base-2 states.
+// Column statistics: merge the strips' base-2 states.  A block takes
+// kFoldCols columns; its kFoldLanes lanes per column merge strips
+// lane, lane + kFoldLanes, ... in order, then a fixed halving tree in LDS
+// merges the lanes, so every column sees the same order on every run.
+constexpr int kFoldCols = 16;
+constexpr int kFoldLanes = kBlock / kFoldCols;  // 16
+
 __global__ __launch_bounds__(kBlock) void fwd_col_combine(FwdArgs a) {
+    __shared__ float sm_m[kFoldLanes][kFoldCols], sm_s[kFoldLanes][kFoldCols];
     const int b = blockIdx.y;
-    const int j = blockIdx.x * kBlock + threadIdx.x;
-    if (j >= a.L2) return;
-    const size_t base = size_t(b) * a.nstrips * a.L2 + j;
+    const int jj = threadIdx.x % kFoldCols;
+    const int sl = threadIdx.x / kFoldCols;
+    const int j = blockIdx.x * kFoldCols + jj;
     float m = -FLT_MAX, s = 0.0f;
-    for (int k = 0; k < a.nstrips; ++k)
-        lse_merge2(m, s, a.part_m[base + size_t(k) * a.L2], a.part_s[base + size_t(k) * a.L2]);
-    float* cmax = a.col_stats + size_t(b) * 2 * a.L2;
-    cmax[j] = m;
-    cmax[a.L2 + j] = s;
+    if (j < a.L2) {
+        const size_t base = size_t(b) * a.nstrips * a.L2 + j;
+        for (int k = sl; k < a.nstrips; k += kFoldLanes)
+            lse_merge2(m, s, a.part_m[base + size_t(k) * a.L2], a.part_s[base + size_t(k) * a.L2]);
+    }
+    sm_m[sl][jj] = m;
+    sm_s[sl][jj] = s;
+#pragma unroll
+    for (int half = kFoldLanes / 2; half >= 1; half /= 2) {
+        __syncthreads();
+        if (sl < half) {
+            lse_merge2(m, s, sm_m[sl + half][jj], sm_s[sl + half][jj]);
+            sm_m[sl][jj] = m;
+            sm_s[sl][jj] = s;
+        }
+    }
+    if (sl == 0 && j < a.L2) {
+        float* cmax = a.col_stats + size_t(b) * 2 * a.L2;
+        cmax[j] = m;
+        cmax[a.L2 + j] = s;
+    }
+}
+
+// Column sums of the strips' partial rows, in the same fixed order as
+// fwd_col_combine.
+__global__ __launch_bounds__(kBlock) void column_fold(const float* partial, int nstrips, int N, float* out) {
+    __shared__ float sm[kFoldLanes][kFoldCols];
+    const int b = blockIdx.y;
+    const int jj = threadIdx.x % kFoldCols;
+    const int sl = threadIdx.x / kFoldCols;
+    const int j = blockIdx.x * kFoldCols + jj;
+    float s = 0.0f;
+    if (j < N) {
+        const size_t base = size_t(b) * nstrips * N + j;
+        for (int k = sl; k < nstrips; k += kFoldLanes) s += partial[base + size_t(k) * N];
+    }
+    sm[sl][jj] = s;
+#pragma unroll
+    for (int half = kFoldLanes / 2; half >= 1; half /= 2) {
+        __syncthreads();
+        if (sl < half) {
+            s += sm[sl + half][jj];
+            sm[sl][jj] = s;
+        }
+    }
+    if (sl == 0 && j < N) out[size_t(b) * N + j] = s;
 }
 
 // r = exp(y - rmax) / rsum, c = exp(y - cmax) / csum, out = sqrt(1e-9 + r c);
@@ -205,9 +253,9 @@ __global__ __launch_bounds__(kBlock) void fwd_write(FwdArgs a) {
 #pragma unroll
             for (int e = 0; e < R::PL; ++e) o[e] = rr[e] = cc[e] = 0.0f;
         }
-        R::store(a.out + off, lane, a.L2, o);
-        if (a.row_sm) R::store(a.row_sm + off, lane, a.L2, rr);
-        if (a.col_sm) R::store(a.col_sm + off, lane, a.L2, cc);
+        R::store_stream(a.out + off, lane, a.L2, o);
+        if (a.row_sm) R::store_stream(a.row_sm + off, lane, a.L2, rr);
+        if (a.col_sm) R::store_stream(a.col_sm + off, lane, a.L2, cc);
     }
 }
 
@@ -357,7 +405,7 @@ __global__ __launch_bounds__(kBlock) void bwd_write(BwdArgs a) {
 #pragma unroll
             for (int e = 0; e < R::PL; ++e) gs[e] = 0.0f;
         }
-        R::store(a.grad_sim + off, lane, a.L2, gs);
+        R::store_stream(a.grad_sim + off, lane, a.L2, gs);
     }
     const float t = block_reduce<kWavesPerBlock>(wave_sum(tacc), scratch, OpSum{});
     if (threadIdx.x == 0) a.tau_partial[size_t(b) * gridDim.x + blockIdx.x] = t;

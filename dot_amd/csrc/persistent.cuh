@@ -617,7 +617,7 @@ __global__ __launch_bounds__(kThreads) void implicit_adjoint(ImpArgs a) {
                 p[e] = failed ? __builtin_nanf("") : (cost_kind ? gc * p[e] - gl : gl - gc * p[e]);
             }
         }
-        R::store(a.grad + off, ln, a.N, p);
+        R::store_stream(a.grad + off, ln, a.N, p);
     }
     const float tsum = block_reduce<kWaves>(wave_sum(tacc), scratch, OpSum{});
     if (threadIdx.x == 0) a.tau_partial[gid] = failed ? __builtin_nanf("") : tsum;

@@ -445,7 +445,7 @@ __global__ __launch_bounds__(kThreads) void implicit_adjoint(ImpResArgs a) {
             if (R::valid(lane, e, a.N)) tacc = fmaf(gl, la, tacc);
             o[e] = failed ? __builtin_nanf("") : (cost_kind ? gc * p[k][e] - gl : gl - gc * p[k][e]);
         }
-        R::store(a.grad + off, lane, a.N, o);
+        R::store_stream(a.grad + off, lane, a.N, o);
     }
     const float tsum = block_reduce<kWaves>(wave_sum(tacc), scratch, OpSum{});
     if (threadIdx.x == 0) a.tau_partial[gid] = failed ? __builtin_nanf("") : tsum;

@@ -65,6 +65,25 @@ struct Row {
         }
     }
 
+    // Store of a row that nothing reads back soon (outputs): non-temporal, so
+    // the stream does not evict inputs that are read again from the caches.
+    __device__ static __forceinline__ void store_stream(float* __restrict__ row, int lane, int N,
+                                                        const float (&x)[PL]) {
+#pragma unroll
+        for (int k = 0; k < CH; ++k) {
+            const int c = col(lane, k);
+            if (c < N) {
+                if constexpr (VEC == 4) {
+                    typedef float v4f __attribute__((ext_vector_type(4)));
+                    const v4f v = {x[4 * k + 0], x[4 * k + 1], x[4 * k + 2], x[4 * k + 3]};
+                    __builtin_nontemporal_store(v, reinterpret_cast<v4f*>(row + c));
+                } else {
+                    __builtin_nontemporal_store(x[k], row + c);
+                }
+            }
+        }
+    }
+
     // true when element e of this lane is a real column (< N)
     __device__ static __forceinline__ bool valid(int lane, int e, int N) {
         return col(lane, e / VEC) + (e % VEC) < N;

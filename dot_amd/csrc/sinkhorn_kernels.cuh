@@ -438,7 +438,7 @@ __global__ __launch_bounds__(kBlock) void imp_final(ImpArgs a) {
             if (R::valid(lane, e, a.N)) tacc = fmaf(gl, la, tacc);
             o[e] = cost_kind ? gc * p[e] - gl : gl - gc * p[e];
         }
-        R::store(a.grad + off, lane, a.N, o);
+        R::store_stream(a.grad + off, lane, a.N, o);
     }
     const float t = block_reduce<kWavesPerBlock>(wave_sum(tacc), scratch, OpSum{});
     if (threadIdx.x == 0) a.tau_partial[size_t(b) * gridDim.x + blockIdx.x] = t;
@@ -480,7 +480,7 @@ __device__ __forceinline__ void unr_epilogue(const UnrArgs& a, int b, size_t off
         if (R::valid(lane, e, a.N)) tacc = fmaf(gam[e], la, tacc);  // kernels.cu:938-963
         o[e] = cost_kind ? gc * p[e] - gl : gl - gc * p[e];
     }
-    R::store(a.grad + off, lane, a.N, o);
+    R::store_stream(a.grad + off, lane, a.N, o);
 }
 
 // Gamma = G * P (kernels.cu:844-854) with its column partial sums; when there
