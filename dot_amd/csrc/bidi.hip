@@ -144,7 +144,8 @@ extern "C" int dot_bidisoftmax_forward(const dot_bidisoftmax_fwd_args* a, dot_st
         }
         {
             ProfScope prof("bidi_fwd_write", stream);
-            hipLaunchKernelGGL((bidi::fwd_write<V, C>), strips, dim3(kBlock), 0, stream, x);
+            hipLaunchKernelGGL((bidi::fwd_write<V, C>), strips, dim3(kBlock), 2 * L2 * sizeof(float), stream,
+                               x);
         }
     });
     if (!launched) return fail(DOT_ERR_UNSUPPORTED, "row length outside the supported range");
@@ -204,8 +205,8 @@ extern "C" int dot_bidisoftmax_backward(const dot_bidisoftmax_bwd_args* a, dot_s
             constexpr bool RC = decltype(recompute)::value;
             {
                 ProfScope prof("bidi_bwd_dots", stream);
-                hipLaunchKernelGGL((bidi::bwd_dots<V, C, RC>), strips, dim3(kBlock), lds_bytes(L2),
-                                   stream, x);
+                hipLaunchKernelGGL((bidi::bwd_dots<V, C, RC>), strips, dim3(kBlock),
+                                   2 * L2 * sizeof(float) + lds_bytes(L2), stream, x);
             }
             {
                 ProfScope prof("bidi_bwd_fold", stream);
@@ -215,7 +216,8 @@ extern "C" int dot_bidisoftmax_backward(const dot_bidisoftmax_bwd_args* a, dot_s
             }
             {
                 ProfScope prof("bidi_bwd_write", stream);
-                hipLaunchKernelGGL((bidi::bwd_write<V, C, RC>), strips, dim3(kBlock), 0, stream, x);
+                hipLaunchKernelGGL((bidi::bwd_write<V, C, RC>), strips, dim3(kBlock), 3 * L2 * sizeof(float),
+                                   stream, x);
             }
         };
         if (buffers) run(std::false_type{});

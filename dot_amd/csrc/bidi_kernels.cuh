@@ -97,7 +97,7 @@ __device__ __forceinline__ float masked(float y2, bool full, int lane, int e, in
 template <int VEC, int CH>
 __global__ __launch_bounds__(kBlock) void fwd_stats(FwdArgs a) {
     using R = Row<VEC, CH>;
-    extern __shared__ float lds[];
+    extern __shared__ __align__(16) float lds[];
     const int lane = threadIdx.x % kWave;
     const int wave = threadIdx.x / kWave;
     const int st = blockIdx.x;
@@ -211,11 +211,23 @@ __global__ __launch_bounds__(kBlock) void column_fold(const float* partial, int 
     if (sl == 0 && j < N) out[size_t(b) * N + j] = s;
 }
 
+// Column max and reciprocal column sum of one batch element into LDS, shared
+// by the block's waves (registers would hold them for the whole kernel and cost
+// occupancy).  The caller places the barrier before the first read.
+__device__ __forceinline__ void load_col_stats(const float* cstat, int L2, float* lcm, float* lics) {
+    for (int j = threadIdx.x; j < L2; j += kBlock) {
+        lcm[j] = cstat[j];
+        const float cs = cstat[L2 + j];
+        lics[j] = cs > 0.0f ? 1.0f / cs : 0.0f;
+    }
+}
+
 // r = exp(y - rmax) / rsum, c = exp(y - cmax) / csum, out = sqrt(1e-9 + r c);
 // zeros outside the valid region (kernels.cu:143-149, :206-212, :216-242).
 template <int VEC, int CH>
 __global__ __launch_bounds__(kBlock) void fwd_write(FwdArgs a) {
     using R = Row<VEC, CH>;
+    extern __shared__ __align__(16) float lds[];  // column max (base 2) L2 | 1 / column sum L2
     const int lane = threadIdx.x % kWave;
     const int wave = threadIdx.x / kWave;
     const int b = blockIdx.y;
@@ -225,12 +237,10 @@ __global__ __launch_bounds__(kBlock) void fwd_write(FwdArgs a) {
     const float sc = a.inv_T * kLog2E;
     const int r0 = blockIdx.x * a.rows;
     const int r1 = min(r0 + a.rows, a.L1);
-    const float* cstat = a.col_stats + size_t(b) * 2 * a.L2;
-    float cm[R::PL], ics[R::PL];
-    R::load(cstat, lane, a.L2, cm, 0.0f);
-    R::load(cstat + a.L2, lane, a.L2, ics, 0.0f);
-#pragma unroll
-    for (int e = 0; e < R::PL; ++e) ics[e] = ics[e] > 0.0f ? 1.0f / ics[e] : 0.0f;
+    float* lcm = lds;
+    float* lics = lds + a.L2;
+    load_col_stats(a.col_stats + size_t(b) * 2 * a.L2, a.L2, lcm, lics);
+    __syncthreads();
     const float* rstat = a.row_stats + size_t(b) * 2 * a.L1;
     for (int i = r0 + wave; i < r1; i += kWavesPerBlock) {
         const size_t off = (size_t(b) * a.L1 + i) * a.L2;
@@ -242,12 +252,19 @@ __global__ __launch_bounds__(kBlock) void fwd_write(FwdArgs a) {
             const float rsv = rstat[a.L1 + i];
             const float irs = rsv > 0.0f ? 1.0f / rsv : 0.0f;
 #pragma unroll
-            for (int e = 0; e < R::PL; ++e) {
-                const bool ok = full || R::valid(lane, e, l2);
-                const float y2 = y[e] * sc;
-                rr[e] = ok ? __builtin_amdgcn_exp2f(y2 - rm) * irs : 0.0f;
-                cc[e] = ok ? __builtin_amdgcn_exp2f(y2 - cm[e]) * ics[e] : 0.0f;
-                o[e] = ok ? __builtin_amdgcn_sqrtf(fmaf(rr[e], cc[e], kEps)) : 0.0f;
+            for (int k = 0; k < CH; ++k) {
+                float cm[VEC], ics[VEC];
+                R::chunk(lcm, lane, k, a.L2, cm);
+                R::chunk(lics, lane, k, a.L2, ics);
+#pragma unroll
+                for (int q = 0; q < VEC; ++q) {
+                    const int e = k * VEC + q;
+                    const bool ok = full || R::valid(lane, e, l2);
+                    const float y2 = y[e] * sc;
+                    rr[e] = ok ? __builtin_amdgcn_exp2f(y2 - rm) * irs : 0.0f;
+                    cc[e] = ok ? __builtin_amdgcn_exp2f(y2 - cm[q]) * ics[q] : 0.0f;
+                    o[e] = ok ? __builtin_amdgcn_sqrtf(fmaf(rr[e], cc[e], kEps)) : 0.0f;
+                }
             }
         } else {
 #pragma unroll
@@ -284,18 +301,16 @@ struct BwdArgs {
 template <int VEC, int CH, bool RECOMPUTE>
 struct BwdRow {
     using R = Row<VEC, CH>;
-    float cm[R::PL], ics[R::PL];
+    const float* lcm;   // LDS: column max (base 2), L2 floats
+    const float* lics;  // LDS: 1 / column sum
     float sc;
 
-    __device__ void init(const BwdArgs& a, int b, int lane) {
+    // `lds` holds 2 * L2 floats; the caller places the barrier before the first get().
+    __device__ void init(const BwdArgs& a, int b, float* lds) {
         sc = a.inv_T * kLog2E;
-        if constexpr (RECOMPUTE) {
-            const float* cstat = a.col_stats + size_t(b) * 2 * a.L2;
-            R::load(cstat, lane, a.L2, cm, 0.0f);
-            R::load(cstat + a.L2, lane, a.L2, ics, 0.0f);
-#pragma unroll
-            for (int e = 0; e < R::PL; ++e) ics[e] = ics[e] > 0.0f ? 1.0f / ics[e] : 0.0f;
-        }
+        lcm = lds;
+        lics = lds + a.L2;
+        if constexpr (RECOMPUTE) load_col_stats(a.col_stats + size_t(b) * 2 * a.L2, a.L2, lds, lds + a.L2);
     }
 
     __device__ void get(const BwdArgs& a, int b, int i, size_t off, int lane, int l2, bool full,
@@ -309,13 +324,20 @@ struct BwdRow {
             const float rsv = rstat[a.L1 + i];
             const float irs = rsv > 0.0f ? 1.0f / rsv : 0.0f;
 #pragma unroll
-            for (int e = 0; e < R::PL; ++e) {
-                const bool ok = full || R::valid(lane, e, l2);
-                const float y2 = y[e] * sc;
-                r[e] = ok ? __builtin_amdgcn_exp2f(y2 - rm) * irs : 0.0f;
-                c[e] = ok ? __builtin_amdgcn_exp2f(y2 - cm[e]) * ics[e] : 0.0f;
-                const float o = __builtin_amdgcn_sqrtf(fmaf(r[e], c[e], kEps));
-                d[e] = ok ? (g[e] * 0.5f) * __builtin_amdgcn_rcpf(o) : 0.0f;
+            for (int k = 0; k < CH; ++k) {
+                float cm[VEC], ics[VEC];
+                R::chunk(lcm, lane, k, a.L2, cm);
+                R::chunk(lics, lane, k, a.L2, ics);
+#pragma unroll
+                for (int q = 0; q < VEC; ++q) {
+                    const int e = k * VEC + q;
+                    const bool ok = full || R::valid(lane, e, l2);
+                    const float y2 = y[e] * sc;
+                    r[e] = ok ? __builtin_amdgcn_exp2f(y2 - rm) * irs : 0.0f;
+                    c[e] = ok ? __builtin_amdgcn_exp2f(y2 - cm[q]) * ics[q] : 0.0f;
+                    const float o = __builtin_amdgcn_sqrtf(fmaf(r[e], c[e], kEps));
+                    d[e] = ok ? (g[e] * 0.5f) * __builtin_amdgcn_rcpf(o) : 0.0f;
+                }
             }
         } else {
             float o[R::PL];
@@ -336,7 +358,7 @@ struct BwdRow {
 template <int VEC, int CH, bool RECOMPUTE>
 __global__ __launch_bounds__(kBlock) void bwd_dots(BwdArgs a) {
     using R = Row<VEC, CH>;
-    extern __shared__ float lds[];
+    extern __shared__ __align__(16) float lds[];
     const int lane = threadIdx.x % kWave;
     const int wave = threadIdx.x / kWave;
     const int st = blockIdx.x;
@@ -347,7 +369,9 @@ __global__ __launch_bounds__(kBlock) void bwd_dots(BwdArgs a) {
     const int r0 = st * a.rows;
     const int r1 = min(r0 + a.rows, l1);
     BwdRow<VEC, CH, RECOMPUTE> src;
-    src.init(a, b, lane);
+    src.init(a, b, lds);
+    __syncthreads();
+    float* comb = lds + 2 * a.L2;  // block_column_combine's 2 * L2 floats
     float acc[R::PL];
 #pragma unroll
     for (int e = 0; e < R::PL; ++e) acc[e] = 0.0f;
@@ -364,7 +388,7 @@ __global__ __launch_bounds__(kBlock) void bwd_dots(BwdArgs a) {
         const float dr = wave_sum(dl);
         if (lane == 0) a.dot_r[size_t(b) * a.L1 + i] = dr;
     }
-    block_column_combine<VEC, CH>(acc, lds, a.L2);
+    block_column_combine<VEC, CH>(acc, comb, a.L2);
     if (wave == 0) R::store(a.partial + (size_t(b) * a.nstrips + st) * a.L2, lane, a.L2, acc);
 }
 
@@ -374,6 +398,7 @@ template <int VEC, int CH, bool RECOMPUTE>
 __global__ __launch_bounds__(kBlock) void bwd_write(BwdArgs a) {
     using R = Row<VEC, CH>;
     __shared__ float scratch[kWavesPerBlock];
+    extern __shared__ __align__(16) float lds[];  // column stats 2 * L2 | column dots L2
     const int lane = threadIdx.x % kWave;
     const int wave = threadIdx.x / kWave;
     const int b = blockIdx.y;
@@ -382,10 +407,11 @@ __global__ __launch_bounds__(kBlock) void bwd_write(BwdArgs a) {
     const bool full = l2 == kWave * R::PL;
     const int r0 = blockIdx.x * a.rows;
     const int r1 = min(r0 + a.rows, a.L1);
+    float* ldc = lds + 2 * a.L2;
+    for (int j = threadIdx.x; j < a.L2; j += kBlock) ldc[j] = a.dot_c[size_t(b) * a.L2 + j];
     BwdRow<VEC, CH, RECOMPUTE> src;
-    src.init(a, b, lane);
-    float dc[R::PL];
-    R::load(a.dot_c + size_t(b) * a.L2, lane, a.L2, dc, 0.0f);
+    src.init(a, b, lds);
+    __syncthreads();
     float tacc = 0.0f;
     for (int i = r0 + wave; i < r1; i += kWavesPerBlock) {
         const size_t off = (size_t(b) * a.L1 + i) * a.L2;
@@ -395,11 +421,17 @@ __global__ __launch_bounds__(kBlock) void bwd_write(BwdArgs a) {
             src.get(a, b, i, off, lane, l2, full, r, c, d, y);
             const float dr = a.dot_r[size_t(b) * a.L1 + i];
 #pragma unroll
-            for (int e = 0; e < R::PL; ++e) {
-                const bool valid = full || R::valid(lane, e, l2);
-                const float t = (d[e] * c[e] - dr) * r[e] + (d[e] * r[e] - dc[e]) * c[e];
-                gs[e] = valid ? t * a.inv_T : 0.0f;
-                tacc = valid ? fmaf(gs[e], y[e], tacc) : tacc;
+            for (int k = 0; k < CH; ++k) {
+                float dc[VEC];
+                R::chunk(ldc, lane, k, a.L2, dc);
+#pragma unroll
+                for (int q = 0; q < VEC; ++q) {
+                    const int e = k * VEC + q;
+                    const bool valid = full || R::valid(lane, e, l2);
+                    const float t = (d[e] * c[e] - dr) * r[e] + (d[e] * r[e] - dc[q]) * c[e];
+                    gs[e] = valid ? t * a.inv_T : 0.0f;
+                    tacc = valid ? fmaf(gs[e], y[e], tacc) : tacc;
+                }
             }
         } else {
 #pragma unroll

@@ -84,6 +84,22 @@ struct Row {
         }
     }
 
+    // This lane's VEC values of chunk k from an LDS (or any) array of N floats;
+    // 0 past N.  VEC = 4 requires N % 4 == 0 and a 16-byte aligned array.
+    __device__ static __forceinline__ void chunk(const float* v, int lane, int k, int N, float (&out)[VEC]) {
+        const int c = col(lane, k);
+        if constexpr (VEC == 4) {
+            float4 t = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if (c < N) t = *reinterpret_cast<const float4*>(v + c);
+            out[0] = t.x;
+            out[1] = t.y;
+            out[2] = t.z;
+            out[3] = t.w;
+        } else {
+            out[0] = c < N ? v[c] : 0.0f;
+        }
+    }
+
     // true when element e of this lane is a real column (< N)
     __device__ static __forceinline__ bool valid(int lane, int e, int N) {
         return col(lane, e / VEC) + (e % VEC) < N;
