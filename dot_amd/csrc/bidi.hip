@@ -144,8 +144,8 @@ extern "C" int dot_bidisoftmax_forward(const dot_bidisoftmax_fwd_args* a, dot_st
         }
         {
             ProfScope prof("bidi_fwd_write", stream);
-            hipLaunchKernelGGL((bidi::fwd_write<V, C>), strips, dim3(kBlock), 2 * L2 * sizeof(float), stream,
-                               x);
+            hipLaunchKernelGGL((bidi::fwd_write<V, C>), strips, dim3(kBlock),
+                               (2 * size_t(L2) + 2 * L.rows) * sizeof(float), stream, x);
         }
     });
     if (!launched) return fail(DOT_ERR_UNSUPPORTED, "row length outside the supported range");
@@ -206,7 +206,7 @@ extern "C" int dot_bidisoftmax_backward(const dot_bidisoftmax_bwd_args* a, dot_s
             {
                 ProfScope prof("bidi_bwd_dots", stream);
                 hipLaunchKernelGGL((bidi::bwd_dots<V, C, RC>), strips, dim3(kBlock),
-                                   2 * L2 * sizeof(float) + lds_bytes(L2), stream, x);
+                                   (2 * size_t(L2) + 2 * L.rows) * sizeof(float) + lds_bytes(L2), stream, x);
             }
             {
                 ProfScope prof("bidi_bwd_fold", stream);
@@ -216,8 +216,8 @@ extern "C" int dot_bidisoftmax_backward(const dot_bidisoftmax_bwd_args* a, dot_s
             }
             {
                 ProfScope prof("bidi_bwd_write", stream);
-                hipLaunchKernelGGL((bidi::bwd_write<V, C, RC>), strips, dim3(kBlock), 3 * L2 * sizeof(float),
-                                   stream, x);
+                hipLaunchKernelGGL((bidi::bwd_write<V, C, RC>), strips, dim3(kBlock),
+                                   (3 * size_t(L2) + 3 * L.rows) * sizeof(float), stream, x);
             }
         };
         if (buffers) run(std::false_type{});

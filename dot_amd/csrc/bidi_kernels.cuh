@@ -45,7 +45,7 @@ __device__ __forceinline__ void block_column_combine_lse(float (&m)[VEC * CH], f
                                                          float* lds, int N) {
     using R = Row<VEC, CH>;
     const int lane = threadIdx.x % kWave;
-    const int wave = threadIdx.x / kWave;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);  // wave-uniform: scalar row loads
     // (source wave, destination wave) per round
     constexpr int kRounds[3][2] = {{3, 1}, {2, 0}, {1, 0}};
 #pragma unroll
@@ -99,7 +99,7 @@ __global__ __launch_bounds__(kBlock) void fwd_stats(FwdArgs a) {
     using R = Row<VEC, CH>;
     extern __shared__ __align__(16) float lds[];
     const int lane = threadIdx.x % kWave;
-    const int wave = threadIdx.x / kWave;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);  // wave-uniform: scalar row loads
     const int st = blockIdx.x;
     const int b = blockIdx.y;
     int l1, l2;
@@ -116,9 +116,13 @@ __global__ __launch_bounds__(kBlock) void fwd_stats(FwdArgs a) {
     }
     float* rmax = a.row_stats + size_t(b) * 2 * a.L1;
     float* rsum = rmax + a.L1;
-    for (int i = r0 + wave; i < r1; i += kWavesPerBlock) {
-        float y[R::PL];
-        R::load(a.sim + (size_t(b) * a.L1 + i) * a.L2, lane, a.L2, y, 0.0f);
+    const float* base = a.sim + size_t(b) * a.L1 * a.L2;
+    struct Buf {
+        float v[R::PL];
+    };
+    auto load = [&](int i, Buf& t) { R::load_clamped(base + size_t(i) * a.L2, lane, a.L2, t.v, 0.0f); };
+    pipelined_rows<Buf>(r0 + wave, r1, kWavesPerBlock, load, [&](int i, Buf& t) {
+        float(&y)[R::PL] = t.v;
         float ml = -FLT_MAX;
 #pragma unroll
         for (int e = 0; e < R::PL; ++e) {
@@ -136,11 +140,11 @@ __global__ __launch_bounds__(kBlock) void fwd_stats(FwdArgs a) {
 #pragma unroll
         for (int e = 0; e < R::PL; ++e) sl += __builtin_amdgcn_exp2f(y[e] - rm);
         const float rs = wave_sum(sl);
-        if (lane == 0) {
-            rmax[i] = rm;
-            rsum[i] = rs;
-        }
-    }
+        // every lane stores the same value: no branch, so the look-ahead's
+        // wait counts stay exact
+        rmax[i] = rm;
+        rsum[i] = rs;
+    });
     block_column_combine_lse<VEC, CH>(cm, cs, lds, a.L2);
     if (wave == 0) {
         const size_t off = (size_t(b) * a.nstrips + st) * a.L2;
@@ -156,7 +160,7 @@ __global__ __launch_bounds__(kBlock) void fwd_stats(FwdArgs a) {
 constexpr int kFoldCols = 16;
 constexpr int kFoldLanes = kBlock / kFoldCols;  // 16
 
-__global__ __launch_bounds__(kBlock) void fwd_col_combine(FwdArgs a) {
+static __global__ __launch_bounds__(kBlock) void fwd_col_combine(FwdArgs a) {
     __shared__ float sm_m[kFoldLanes][kFoldCols], sm_s[kFoldLanes][kFoldCols];
     const int b = blockIdx.y;
     const int jj = threadIdx.x % kFoldCols;
@@ -188,7 +192,7 @@ __global__ __launch_bounds__(kBlock) void fwd_col_combine(FwdArgs a) {
 
 // Column sums of the strips' partial rows, in the same fixed order as
 // fwd_col_combine.
-__global__ __launch_bounds__(kBlock) void column_fold(const float* partial, int nstrips, int N, float* out) {
+static __global__ __launch_bounds__(kBlock) void column_fold(const float* partial, int nstrips, int N, float* out) {
     __shared__ float sm[kFoldLanes][kFoldCols];
     const int b = blockIdx.y;
     const int jj = threadIdx.x % kFoldCols;
@@ -222,14 +226,32 @@ __device__ __forceinline__ void load_col_stats(const float* cstat, int L2, float
     }
 }
 
+// Row max and reciprocal row sum of the strip's valid rows [r0, r1) into LDS
+// (read there, per-row global loads would queue behind the rows loaded ahead).
+// The caller places the barrier before the first read.
+__device__ __forceinline__ void load_row_stats(const float* rstat, int L1, int r0, int r1, float* lrm,
+                                               float* lirs) {
+    for (int t = threadIdx.x; t < r1 - r0; t += kBlock) {
+        lrm[t] = rstat[r0 + t];
+        const float rs = rstat[L1 + r0 + t];
+        lirs[t] = rs > 0.0f ? 1.0f / rs : 0.0f;
+    }
+}
+
+template <class R>
+struct RowBuf {
+    float v[R::PL];
+};
+
 // r = exp(y - rmax) / rsum, c = exp(y - cmax) / csum, out = sqrt(1e-9 + r c);
 // zeros outside the valid region (kernels.cu:143-149, :206-212, :216-242).
 template <int VEC, int CH>
 __global__ __launch_bounds__(kBlock) void fwd_write(FwdArgs a) {
     using R = Row<VEC, CH>;
-    extern __shared__ __align__(16) float lds[];  // column max (base 2) L2 | 1 / column sum L2
+    // LDS: column max (base 2) L2 | 1 / column sum L2 | row max rows | 1 / row sum rows
+    extern __shared__ __align__(16) float lds[];
     const int lane = threadIdx.x % kWave;
-    const int wave = threadIdx.x / kWave;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const int b = blockIdx.y;
     int l1, l2;
     valid_extent(a.lengths, b, a.L1, a.L2, l1, l2);
@@ -237,43 +259,50 @@ __global__ __launch_bounds__(kBlock) void fwd_write(FwdArgs a) {
     const float sc = a.inv_T * kLog2E;
     const int r0 = blockIdx.x * a.rows;
     const int r1 = min(r0 + a.rows, a.L1);
+    const int rv = min(r1, l1);  // end of the valid rows
     float* lcm = lds;
     float* lics = lds + a.L2;
+    float* lrm = lds + 2 * a.L2;
+    float* lirs = lrm + a.rows;
     load_col_stats(a.col_stats + size_t(b) * 2 * a.L2, a.L2, lcm, lics);
+    load_row_stats(a.row_stats + size_t(b) * 2 * a.L1, a.L1, r0, rv, lrm, lirs);
     __syncthreads();
-    const float* rstat = a.row_stats + size_t(b) * 2 * a.L1;
-    for (int i = r0 + wave; i < r1; i += kWavesPerBlock) {
+    auto write = [&](int i, const float(&o)[R::PL], const float(&rr)[R::PL], const float(&cc)[R::PL]) {
         const size_t off = (size_t(b) * a.L1 + i) * a.L2;
-        float o[R::PL], rr[R::PL], cc[R::PL];
-        if (i < l1) {
-            float y[R::PL];
-            R::load(a.sim + off, lane, a.L2, y, 0.0f);
-            const float rm = rstat[i];
-            const float rsv = rstat[a.L1 + i];
-            const float irs = rsv > 0.0f ? 1.0f / rsv : 0.0f;
-#pragma unroll
-            for (int k = 0; k < CH; ++k) {
-                float cm[VEC], ics[VEC];
-                R::chunk(lcm, lane, k, a.L2, cm);
-                R::chunk(lics, lane, k, a.L2, ics);
-#pragma unroll
-                for (int q = 0; q < VEC; ++q) {
-                    const int e = k * VEC + q;
-                    const bool ok = full || R::valid(lane, e, l2);
-                    const float y2 = y[e] * sc;
-                    rr[e] = ok ? __builtin_amdgcn_exp2f(y2 - rm) * irs : 0.0f;
-                    cc[e] = ok ? __builtin_amdgcn_exp2f(y2 - cm[q]) * ics[q] : 0.0f;
-                    o[e] = ok ? __builtin_amdgcn_sqrtf(fmaf(rr[e], cc[e], kEps)) : 0.0f;
-                }
-            }
-        } else {
-#pragma unroll
-            for (int e = 0; e < R::PL; ++e) o[e] = rr[e] = cc[e] = 0.0f;
-        }
         R::store_stream(a.out + off, lane, a.L2, o);
         if (a.row_sm) R::store_stream(a.row_sm + off, lane, a.L2, rr);
         if (a.col_sm) R::store_stream(a.col_sm + off, lane, a.L2, cc);
-    }
+    };
+    // rows of the valid region, then the zero rows past it
+    auto load = [&](int i, RowBuf<R>& t) {
+        R::load_clamped(a.sim + (size_t(b) * a.L1 + i) * a.L2, lane, a.L2, t.v, 0.0f);
+    };
+    pipelined_rows<RowBuf<R>>(r0 + wave, rv, kWavesPerBlock, load, [&](int i, RowBuf<R>& t) {
+        const float rm = lrm[i - r0];
+        const float irs = lirs[i - r0];
+        float o[R::PL], rr[R::PL], cc[R::PL];
+#pragma unroll
+        for (int k = 0; k < CH; ++k) {
+            float cm[VEC], ics[VEC];
+            R::chunk(lcm, lane, k, a.L2, cm);
+            R::chunk(lics, lane, k, a.L2, ics);
+#pragma unroll
+            for (int q = 0; q < VEC; ++q) {
+                const int e = k * VEC + q;
+                const bool ok = full || R::valid(lane, e, l2);
+                const float y2 = t.v[e] * sc;
+                rr[e] = ok ? __builtin_amdgcn_exp2f(y2 - rm) * irs : 0.0f;
+                cc[e] = ok ? __builtin_amdgcn_exp2f(y2 - cm[q]) * ics[q] : 0.0f;
+                o[e] = ok ? __builtin_amdgcn_sqrtf(fmaf(rr[e], cc[e], kEps)) : 0.0f;
+            }
+        }
+        write(i, o, rr, cc);
+    });
+    float z[R::PL];
+#pragma unroll
+    for (int e = 0; e < R::PL; ++e) z[e] = 0.0f;
+    for (int i = r0 + wave; i < r1; i += kWavesPerBlock)
+        if (i >= l1) write(i, z, z, z);
 }
 
 struct BwdArgs {
@@ -297,32 +326,58 @@ struct BwdArgs {
 // For one row: r, c and d = g / (2 out) (kernels.cu:249-274), from the
 // forward's buffers or recomputed from the statistics; 0 outside the valid
 // region.  In recompute mode out >= sqrt(1e-9) > 1e-9, so the reference's
-// out > 1e-9 test always passes.
+// out > 1e-9 test always passes.  A row's inputs are loaded into a Buf first
+// (sim and grad_out; plus the three buffers in buffer mode), so the kernels can
+// load rows ahead.
 template <int VEC, int CH, bool RECOMPUTE>
 struct BwdRow {
     using R = Row<VEC, CH>;
+    static constexpr int kBufPL = RECOMPUTE ? 1 : R::PL;
+    struct Buf {
+        float y[R::PL], g[R::PL];
+        float r[kBufPL], c[kBufPL], o[kBufPL];
+    };
     const float* lcm;   // LDS: column max (base 2), L2 floats
     const float* lics;  // LDS: 1 / column sum
+    const float* lrm;   // LDS: row max (base 2) of the strip's rows
+    const float* lirs;  // LDS: 1 / row sum
+    int r0;
     float sc;
 
-    // `lds` holds 2 * L2 floats; the caller places the barrier before the first get().
-    __device__ void init(const BwdArgs& a, int b, float* lds) {
+    // `lds` holds 2 * L2 + 2 * rows floats; the caller places the barrier
+    // before the first get().  [r0, rv) are the strip's valid rows.
+    __device__ void init(const BwdArgs& a, int b, float* lds, int r0_, int rv) {
         sc = a.inv_T * kLog2E;
-        lcm = lds;
-        lics = lds + a.L2;
-        if constexpr (RECOMPUTE) load_col_stats(a.col_stats + size_t(b) * 2 * a.L2, a.L2, lds, lds + a.L2);
+        r0 = r0_;
+        float* cm = lds;
+        float* ics = lds + a.L2;
+        float* rm = lds + 2 * a.L2;
+        float* irs = rm + a.rows;
+        lcm = cm;
+        lics = ics;
+        lrm = rm;
+        lirs = irs;
+        if constexpr (RECOMPUTE) {
+            load_col_stats(a.col_stats + size_t(b) * 2 * a.L2, a.L2, cm, ics);
+            load_row_stats(a.row_stats + size_t(b) * 2 * a.L1, a.L1, r0, rv, rm, irs);
+        }
     }
 
-    __device__ void get(const BwdArgs& a, int b, int i, size_t off, int lane, int l2, bool full,
-                        float (&r)[R::PL], float (&c)[R::PL], float (&d)[R::PL], float (&y)[R::PL]) const {
-        float g[R::PL];
-        R::load(a.sim + off, lane, a.L2, y, 0.0f);
-        R::load(a.grad_out + off, lane, a.L2, g, 0.0f);
+    __device__ void load(const BwdArgs& a, size_t off, int lane, Buf& t) const {
+        R::load_clamped(a.sim + off, lane, a.L2, t.y, 0.0f);
+        R::load_clamped(a.grad_out + off, lane, a.L2, t.g, 0.0f);
+        if constexpr (!RECOMPUTE) {
+            R::load(a.row_sm + off, lane, a.L2, t.r, 0.0f);
+            R::load(a.col_sm + off, lane, a.L2, t.c, 0.0f);
+            R::load(a.out + off, lane, a.L2, t.o, 0.0f);
+        }
+    }
+
+    __device__ void get(const BwdArgs& a, int i, int lane, int l2, bool full, const Buf& t,
+                        float (&r)[R::PL], float (&c)[R::PL], float (&d)[R::PL]) const {
         if constexpr (RECOMPUTE) {
-            const float* rstat = a.row_stats + size_t(b) * 2 * a.L1;
-            const float rm = rstat[i];
-            const float rsv = rstat[a.L1 + i];
-            const float irs = rsv > 0.0f ? 1.0f / rsv : 0.0f;
+            const float rm = lrm[i - r0];
+            const float irs = lirs[i - r0];
 #pragma unroll
             for (int k = 0; k < CH; ++k) {
                 float cm[VEC], ics[VEC];
@@ -332,35 +387,54 @@ struct BwdRow {
                 for (int q = 0; q < VEC; ++q) {
                     const int e = k * VEC + q;
                     const bool ok = full || R::valid(lane, e, l2);
-                    const float y2 = y[e] * sc;
+                    const float y2 = t.y[e] * sc;
                     r[e] = ok ? __builtin_amdgcn_exp2f(y2 - rm) * irs : 0.0f;
                     c[e] = ok ? __builtin_amdgcn_exp2f(y2 - cm[q]) * ics[q] : 0.0f;
                     const float o = __builtin_amdgcn_sqrtf(fmaf(r[e], c[e], kEps));
-                    d[e] = ok ? (g[e] * 0.5f) * __builtin_amdgcn_rcpf(o) : 0.0f;
+                    d[e] = ok ? (t.g[e] * 0.5f) * __builtin_amdgcn_rcpf(o) : 0.0f;
                 }
             }
         } else {
-            float o[R::PL];
-            R::load(a.row_sm + off, lane, a.L2, r, 0.0f);
-            R::load(a.col_sm + off, lane, a.L2, c, 0.0f);
-            R::load(a.out + off, lane, a.L2, o, 0.0f);
 #pragma unroll
             for (int e = 0; e < R::PL; ++e) {
-                const bool ok = (full || R::valid(lane, e, l2)) && o[e] > kEps;
-                d[e] = ok ? (g[e] * 0.5f) * __builtin_amdgcn_rcpf(o[e]) : 0.0f;
+                r[e] = t.r[e];
+                c[e] = t.c[e];
+                const bool ok = (full || R::valid(lane, e, l2)) && t.o[e] > kEps;
+                d[e] = ok ? (t.g[e] * 0.5f) * __builtin_amdgcn_rcpf(t.o[e]) : 0.0f;
             }
         }
     }
 };
+
+// Visits the rows of `src` with loads ahead in recompute mode (two row buffers
+// of sim and grad_out); buffer mode, with five arrays per row, visits them
+// one at a time.
+template <bool RECOMPUTE, class Src, class Body>
+__device__ __forceinline__ void bwd_rows(const BwdArgs& a, const Src& src, int b, int i0, int r1, int lane,
+                                         Body&& body) {
+    using Buf = typename Src::Buf;
+    auto load = [&](int i, Buf& t) { src.load(a, (size_t(b) * a.L1 + i) * a.L2, lane, t); };
+    if constexpr (RECOMPUTE) {
+        pipelined_rows<Buf>(i0, r1, kWavesPerBlock, load, body);
+    } else {
+        for (int i = i0; i < r1; i += kWavesPerBlock) {
+            Buf t;
+            load(i, t);
+            body(i, t);
+        }
+    }
+}
 
 // Row dots sum_j (d c) r and column partials of (d r) c over the strip
 // (kernels.cu:277-354).
 template <int VEC, int CH, bool RECOMPUTE>
 __global__ __launch_bounds__(kBlock) void bwd_dots(BwdArgs a) {
     using R = Row<VEC, CH>;
+    using Src = BwdRow<VEC, CH, RECOMPUTE>;
+    // LDS: statistics 2 * L2 + 2 * rows | block_column_combine's 2 * L2 + 8
     extern __shared__ __align__(16) float lds[];
     const int lane = threadIdx.x % kWave;
-    const int wave = threadIdx.x / kWave;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const int st = blockIdx.x;
     const int b = blockIdx.y;
     int l1, l2;
@@ -368,17 +442,16 @@ __global__ __launch_bounds__(kBlock) void bwd_dots(BwdArgs a) {
     const bool full = l2 == kWave * R::PL;
     const int r0 = st * a.rows;
     const int r1 = min(r0 + a.rows, l1);
-    BwdRow<VEC, CH, RECOMPUTE> src;
-    src.init(a, b, lds);
+    Src src;
+    src.init(a, b, lds, r0, r1);
     __syncthreads();
-    float* comb = lds + 2 * a.L2;  // block_column_combine's 2 * L2 floats
+    float* comb = lds + 2 * a.L2 + 2 * a.rows;
     float acc[R::PL];
 #pragma unroll
     for (int e = 0; e < R::PL; ++e) acc[e] = 0.0f;
-    for (int i = r0 + wave; i < r1; i += kWavesPerBlock) {
-        const size_t off = (size_t(b) * a.L1 + i) * a.L2;
-        float r[R::PL], c[R::PL], d[R::PL], y[R::PL];
-        src.get(a, b, i, off, lane, l2, full, r, c, d, y);
+    bwd_rows<RECOMPUTE>(a, src, b, r0 + wave, r1, lane, [&](int i, const typename Src::Buf& t) {
+        float r[R::PL], c[R::PL], d[R::PL];
+        src.get(a, i, lane, l2, full, t, r, c, d);
         float dl = 0.0f;
 #pragma unroll
         for (int e = 0; e < R::PL; ++e) {
@@ -386,8 +459,8 @@ __global__ __launch_bounds__(kBlock) void bwd_dots(BwdArgs a) {
             acc[e] = fmaf(d[e] * r[e], c[e], acc[e]);
         }
         const float dr = wave_sum(dl);
-        if (lane == 0) a.dot_r[size_t(b) * a.L1 + i] = dr;
-    }
+        a.dot_r[size_t(b) * a.L1 + i] = dr;  // every lane stores the same value (no branch)
+    });
     block_column_combine<VEC, CH>(acc, comb, a.L2);
     if (wave == 0) R::store(a.partial + (size_t(b) * a.nstrips + st) * a.L2, lane, a.L2, acc);
 }
@@ -397,50 +470,56 @@ __global__ __launch_bounds__(kBlock) void bwd_dots(BwdArgs a) {
 template <int VEC, int CH, bool RECOMPUTE>
 __global__ __launch_bounds__(kBlock) void bwd_write(BwdArgs a) {
     using R = Row<VEC, CH>;
+    using Src = BwdRow<VEC, CH, RECOMPUTE>;
     __shared__ float scratch[kWavesPerBlock];
-    extern __shared__ __align__(16) float lds[];  // column stats 2 * L2 | column dots L2
+    // LDS: statistics 2 * L2 + 2 * rows | column dots L2 | row dots rows
+    extern __shared__ __align__(16) float lds[];
     const int lane = threadIdx.x % kWave;
-    const int wave = threadIdx.x / kWave;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const int b = blockIdx.y;
     int l1, l2;
     valid_extent(a.lengths, b, a.L1, a.L2, l1, l2);
     const bool full = l2 == kWave * R::PL;
     const int r0 = blockIdx.x * a.rows;
     const int r1 = min(r0 + a.rows, a.L1);
-    float* ldc = lds + 2 * a.L2;
+    const int rv = min(r1, l1);
+    float* ldc = lds + 2 * a.L2 + 2 * a.rows;
+    float* ldr = ldc + a.L2;
     for (int j = threadIdx.x; j < a.L2; j += kBlock) ldc[j] = a.dot_c[size_t(b) * a.L2 + j];
-    BwdRow<VEC, CH, RECOMPUTE> src;
-    src.init(a, b, lds);
+    for (int t = threadIdx.x; t < rv - r0; t += kBlock) ldr[t] = a.dot_r[size_t(b) * a.L1 + r0 + t];
+    Src src;
+    src.init(a, b, lds, r0, rv);
     __syncthreads();
     float tacc = 0.0f;
-    for (int i = r0 + wave; i < r1; i += kWavesPerBlock) {
-        const size_t off = (size_t(b) * a.L1 + i) * a.L2;
-        float gs[R::PL];
-        if (i < l1) {
-            float r[R::PL], c[R::PL], d[R::PL], y[R::PL];
-            src.get(a, b, i, off, lane, l2, full, r, c, d, y);
-            const float dr = a.dot_r[size_t(b) * a.L1 + i];
+    auto store = [&](int i, const float(&gs)[R::PL]) {
+        R::store_stream(a.grad_sim + (size_t(b) * a.L1 + i) * a.L2, lane, a.L2, gs);
+    };
+    bwd_rows<RECOMPUTE>(a, src, b, r0 + wave, rv, lane, [&](int i, const typename Src::Buf& t) {
+        float r[R::PL], c[R::PL], d[R::PL], gs[R::PL];
+        src.get(a, i, lane, l2, full, t, r, c, d);
+        const float dr = ldr[i - r0];
 #pragma unroll
-            for (int k = 0; k < CH; ++k) {
-                float dc[VEC];
-                R::chunk(ldc, lane, k, a.L2, dc);
+        for (int k = 0; k < CH; ++k) {
+            float dc[VEC];
+            R::chunk(ldc, lane, k, a.L2, dc);
 #pragma unroll
-                for (int q = 0; q < VEC; ++q) {
-                    const int e = k * VEC + q;
-                    const bool valid = full || R::valid(lane, e, l2);
-                    const float t = (d[e] * c[e] - dr) * r[e] + (d[e] * r[e] - dc[q]) * c[e];
-                    gs[e] = valid ? t * a.inv_T : 0.0f;
-                    tacc = valid ? fmaf(gs[e], y[e], tacc) : tacc;
-                }
+            for (int q = 0; q < VEC; ++q) {
+                const int e = k * VEC + q;
+                const bool valid = full || R::valid(lane, e, l2);
+                const float tt = (d[e] * c[e] - dr) * r[e] + (d[e] * r[e] - dc[q]) * c[e];
+                gs[e] = valid ? tt * a.inv_T : 0.0f;
+                tacc = valid ? fmaf(gs[e], t.y[e], tacc) : tacc;
             }
-        } else {
-#pragma unroll
-            for (int e = 0; e < R::PL; ++e) gs[e] = 0.0f;
         }
-        R::store_stream(a.grad_sim + off, lane, a.L2, gs);
-    }
-    const float t = block_reduce<kWavesPerBlock>(wave_sum(tacc), scratch, OpSum{});
-    if (threadIdx.x == 0) a.tau_partial[size_t(b) * gridDim.x + blockIdx.x] = t;
+        store(i, gs);
+    });
+    float z[R::PL];
+#pragma unroll
+    for (int e = 0; e < R::PL; ++e) z[e] = 0.0f;
+    for (int i = r0 + wave; i < r1; i += kWavesPerBlock)
+        if (i >= l1) store(i, z);
+    const float tsum = block_reduce<kWavesPerBlock>(wave_sum(tacc), scratch, OpSum{});
+    if (threadIdx.x == 0) a.tau_partial[size_t(b) * gridDim.x + blockIdx.x] = tsum;
 }
 
 }  // namespace bidi

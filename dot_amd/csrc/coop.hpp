@@ -1,0 +1,41 @@
+// Host-side helpers shared by the cooperative (one launch, exchange through
+// tagged words) kernels of both operators.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace dot_amd {
+
+// Polls of one exchange word before a cooperative kernel gives up (~1-2 s).
+constexpr int kSpinLimit = 1 << 20;
+
+inline int device_cus() {
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    return cus;
+}
+
+inline int pow2_ceil(int x) {
+    int p = 1;
+    while (p < x) p *= 2;
+    return p;
+}
+
+// Launches `kernel` on G workgroups of `threads` threads only if all of them
+// can be resident at once (the exchange protocol spins on other workgroups);
+// false, with nothing launched, otherwise.
+template <class K, class A>
+bool launch_cooperative(K kernel, A& args, int G, int threads, size_t lds, hipStream_t stream) {
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, lds) != hipSuccess ||
+        per_cu < 1 || int64_t(per_cu) * device_cus() < G)
+        return false;
+    void* params[] = {&args};
+    return hipLaunchCooperativeKernel(reinterpret_cast<const void*>(kernel), dim3(G), dim3(threads), params,
+                                      static_cast<unsigned>(lds), stream) == hipSuccess;
+}
+
+}  // namespace dot_amd

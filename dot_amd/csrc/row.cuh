@@ -49,6 +49,29 @@ struct Row {
         }
     }
 
+    // As load(), but lanes past N load the row's last element(s) (a cache hit)
+    // instead of branching around the load.  With every load unconditional the
+    // compiler's wait counts stay exact, so a row loaded ahead stays in flight
+    // while earlier ones are used (pipelined_rows).
+    __device__ static __forceinline__ void load_clamped(const float* __restrict__ row, int lane, int N,
+                                                        float (&x)[PL], float fill) {
+#pragma unroll
+        for (int k = 0; k < CH; ++k) {
+            const int c = col(lane, k);
+            const bool in = c < N;
+            if constexpr (VEC == 4) {
+                const float4 t = *reinterpret_cast<const float4*>(row + min(c, N - 4));
+                x[4 * k + 0] = in ? t.x : fill;
+                x[4 * k + 1] = in ? t.y : fill;
+                x[4 * k + 2] = in ? t.z : fill;
+                x[4 * k + 3] = in ? t.w : fill;
+            } else {
+                const float t = row[min(c, N - 1)];
+                x[k] = in ? t : fill;
+            }
+        }
+    }
+
     __device__ static __forceinline__ void store(float* __restrict__ row, int lane, int N,
                                                  const float (&x)[PL]) {
 #pragma unroll
@@ -131,6 +154,25 @@ __device__ __forceinline__ void block_column_combine(float (&acc)[VEC * CH], flo
         R::load(lds, lane, N, o, 0.0f);
 #pragma unroll
         for (int e = 0; e < R::PL; ++e) acc[e] += o[e];
+    }
+}
+
+// Visits rows i0, i0 + step, ... (< r1) with each row's load issued one visit
+// ahead, so it is in flight while the previous row is computed: load(i, buf)
+// fills a Buf, body(i, buf) consumes it.  Two buffers alternate (unrolled by
+// two, so no register copy has to wait for a load in flight); the look-ahead
+// past the last row reloads that row, a cache hit, which keeps every load
+// unconditional and the wait counts exact (load with Row::load_clamped).
+template <class Buf, class Load, class Body>
+__device__ __forceinline__ void pipelined_rows(int i0, int r1, int step, Load&& load, Body&& body) {
+    if (i0 >= r1) return;
+    Buf x, y;
+    load(i0, x);
+    for (int i = i0; i < r1; i += 2 * step) {
+        load(min(i + step, r1 - 1), y);
+        body(i, x);
+        load(min(i + 2 * step, r1 - 1), x);
+        if (i + step < r1) body(i + step, y);
     }
 }
 

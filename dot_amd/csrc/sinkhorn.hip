@@ -6,6 +6,7 @@
 #include <cstdlib>
 #include <string>
 
+#include "coop.hpp"
 #include "host.hpp"
 #include "persistent.cuh"
 #include "resident.cuh"
@@ -191,19 +192,6 @@ int check_shape(int B, int M, int N) {
 
 bool valid_tau(float tau) { return std::isfinite(tau) && tau > 0.0f; }
 
-int device_cus() {
-    int dev = 0, cus = 0;
-    if (hipGetDevice(&dev) != hipSuccess) return 0;
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-    return cus;
-}
-
-int pow2_ceil(int x) {
-    int p = 1;
-    while (p < x) p *= 2;
-    return p;
-}
-
 // Register-resident configuration: a batch element's rows split over W
 // workgroups of 8 waves, each wave holding RPW rows of PL floats per lane in
 // VGPRs (PL * RPW <= strip_budget), one workgroup per CU.
@@ -283,8 +271,6 @@ bool dispatch_resident(const ResidentCfg& c, F&& f) {
     return false;
 }
 
-constexpr int kSpinLimit = 1 << 20;  // ~1-2 s of polling before a resident kernel gives up
-
 // Persistent streaming configuration: W workgroups per batch element (as many
 // as the CUs allow, at most pst::kMaxGroups and M), R rows each.
 struct StreamCfg {
@@ -308,16 +294,6 @@ StreamCfg stream_config(int B, int M, int N) {
 
 // One cooperative launch `kernel(args)` of G workgroups with `lds` bytes, if
 // the device can hold them all at once.
-template <class K, class A>
-bool launch_cooperative(K kernel, A& args, int G, size_t lds, hipStream_t stream) {
-    int per_cu = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, res::kThreads, lds) != hipSuccess ||
-        per_cu < 1 || int64_t(per_cu) * device_cus() < G)
-        return false;
-    void* params[] = {&args};
-    return hipLaunchCooperativeKernel(reinterpret_cast<const void*>(kernel), dim3(G), dim3(res::kThreads),
-                                      params, static_cast<unsigned>(lds), stream) == hipSuccess;
-}
 
 bool launch_stream_forward(const dot_sinkhorn_fwd_args* a, const FwdLayout& L, const StreamCfg& sc,
                            float kscale, float log_a_default, float log_b_default, bool keep, bool ret_log,
@@ -364,7 +340,7 @@ bool launch_stream_forward(const dot_sinkhorn_fwd_args* a, const FwdLayout& L, c
         constexpr int C = decltype(cc)::value;
         launch_fill_zero(L.pst, 2 * words, stream);
         ProfScope prof("sk_fwd_persistent", stream);
-        ok = launch_cooperative(pst::forward<V, C>, r, G, lds, stream);
+        ok = launch_cooperative(pst::forward<V, C>, r, G, res::kThreads, lds, stream);
     });
     if (!ok) return false;
     if (a->cost) {
@@ -719,7 +695,7 @@ bool launch_stream_adjoint(const dot_sinkhorn_bwd_args* a, const ImpLayout& L, c
         constexpr int C = decltype(cc)::value;
         launch_fill_zero(L.pst, 2 * words, stream);
         ProfScope prof("sk_imp_persistent", stream);
-        ok = launch_cooperative(pst::implicit_adjoint<V, C>, r, G, lds, stream);
+        ok = launch_cooperative(pst::implicit_adjoint<V, C>, r, G, res::kThreads, lds, stream);
     });
     if (!ok) return false;
     ProfScope prof("sk_batch_sum", stream);

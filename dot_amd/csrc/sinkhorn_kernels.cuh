@@ -134,7 +134,7 @@ struct FwdCombineArgs {
 // Column update v_j = log b_j + v_j - log colsum_j (kernels.cu:629-671 in
 // shared-exponential form); columns whose sum is below kColSumFloor (or not
 // finite) take the reference's exact max-shifted LSE over the column.
-__global__ __launch_bounds__(kBlock) void fwd_combine(FwdCombineArgs a) {
+static __global__ __launch_bounds__(kBlock) void fwd_combine(FwdCombineArgs a) {
     if (stopped_before(a.delta_bits, a.t, a.tol)) return;
     const int b = blockIdx.y;
     const int j = blockIdx.x * kBlock + threadIdx.x;
@@ -162,7 +162,7 @@ __global__ __launch_bounds__(kBlock) void fwd_combine(FwdCombineArgs a) {
 
 // Iterations executed and the converged flag, from the per-iteration deltas
 // (the host loop's break at torch_cuda.cpp:225-237, evaluated after the fact).
-__global__ void fwd_finalize(const unsigned* delta_bits, int max_iter, float tol,
+static __global__ void fwd_finalize(const unsigned* delta_bits, int max_iter, float tol,
                              int32_t* iters_used, int32_t* converged) {
     if (blockIdx.x != 0 || threadIdx.x != 0) return;
     int used = max_iter;
@@ -236,7 +236,7 @@ __global__ __launch_bounds__(kBlock) void materialize(MaterializeArgs a) {
 }
 
 // out[b] = scale * sum_k partial[b, k] in a fixed order; one wave per batch element.
-__global__ void batch_sum(const float* partial, int nblk, float scale, float* out) {
+static __global__ void batch_sum(const float* partial, int nblk, float scale, float* out) {
     const int b = blockIdx.x;
     float s = 0.0f;
     for (int k = threadIdx.x; k < nblk; k += kWave) s += partial[size_t(b) * nblk + k];
@@ -244,7 +244,7 @@ __global__ void batch_sum(const float* partial, int nblk, float scale, float* ou
     if (threadIdx.x == 0) out[b] = s * scale;
 }
 
-__global__ void fill_zero(uint32_t* p, size_t n) {
+static __global__ void fill_zero(uint32_t* p, size_t n) {
     for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
          i += size_t(gridDim.x) * blockDim.x)
         p[i] = 0u;
@@ -345,7 +345,7 @@ __global__ __launch_bounds__(kBlock) void imp_prep(ImpArgs a) {
     if (wave == 0) R::store(a.partB + (size_t(b) * a.nstrips + s) * a.N, lane, a.N, accB);
 }
 
-__global__ __launch_bounds__(kBlock) void imp_prep_combine(ImpArgs a) {
+static __global__ __launch_bounds__(kBlock) void imp_prep_combine(ImpArgs a) {
     const int b = blockIdx.y;
     const int j = blockIdx.x * kBlock + threadIdx.x;
     if (j >= a.N) return;
@@ -396,7 +396,7 @@ __global__ __launch_bounds__(kBlock) void imp_lambda_sweep(ImpArgs a) {
 }
 
 // mu_k = (sum_i P G - sum_i P lambda_i) / max(sum_i P, 1e-12)   (kernels.cu:1007-1047)
-__global__ __launch_bounds__(kBlock) void imp_mu_combine(ImpArgs a) {
+static __global__ __launch_bounds__(kBlock) void imp_mu_combine(ImpArgs a) {
     const int b = blockIdx.y;
     const int j = blockIdx.x * kBlock + threadIdx.x;
     if (j >= a.N) return;
@@ -524,7 +524,7 @@ __global__ __launch_bounds__(kBlock) void unr_init(UnrArgs a) {
 }
 
 // colsum[b, j] = sum over strips of partial (plain sum, fixed order).
-__global__ __launch_bounds__(kBlock) void column_fold(const float* partial, int nstrips, int N,
+static __global__ __launch_bounds__(kBlock) void column_fold(const float* partial, int nstrips, int N,
                                                      float* out) {
     const int b = blockIdx.y;
     const int j = blockIdx.x * kBlock + threadIdx.x;
