@@ -238,11 +238,6 @@ __device__ __forceinline__ void load_row_stats(const float* rstat, int L1, int r
     }
 }
 
-template <class R>
-struct RowBuf {
-    float v[R::PL];
-};
-
 // r = exp(y - rmax) / rsum, c = exp(y - cmax) / csum, out = sqrt(1e-9 + r c);
 // zeros outside the valid region (kernels.cu:143-149, :206-212, :216-242).
 template <int VEC, int CH>

@@ -157,6 +157,12 @@ __device__ __forceinline__ void block_column_combine(float (&acc)[VEC * CH], flo
     }
 }
 
+// One row of a Row<VEC, CH> layout, as a value (row buffers of pipelined_rows).
+template <class R>
+struct RowBuf {
+    float v[R::PL];
+};
+
 // Visits rows i0, i0 + step, ... (< r1) with each row's load issued one visit
 // ahead, so it is in flight while the previous row is computed: load(i, buf)
 // fills a Buf, body(i, buf) consumes it.  Two buffers alternate (unrolled by
