@@ -126,14 +126,18 @@ __device__ __forceinline__ void publish_row(float (&acc)[VEC * CH], float* tree,
     using R = Row<VEC, CH>;
     res::tree_combine<VEC, CH>(acc, tree, N);
     if (threadIdx.x < kWave) {
-        const int lane = threadIdx.x;
+        // Addresses from an opaque lane index, computed here: hoisted out of
+        // the caller's iteration loop they would be spilled, and each spill
+        // reload would wait for every store issued before it.
+        const int lane = opaque_lane();
 #pragma unroll
-        for (int k = 0; k < CH; ++k)
+        for (int k = 0; k < CH; ++k) {
+            const int c = R::col(lane, k);
+            if (VEC == 1 ? c < N : c + VEC <= N) {  // N % 4 == 0 when VEC == 4
 #pragma unroll
-            for (int q = 0; q < VEC; ++q) {
-                const int col = R::col(lane, k) + q;
-                if (col < N) publish(slot_row + col, acc[k * VEC + q], t);
+                for (int q = 0; q < VEC; ++q) publish(slot_row + c + q, acc[k * VEC + q], t);
             }
+        }
     }
 }
 
