@@ -213,6 +213,24 @@ __device__ __forceinline__ int logical_group(int W) {
     return blockIdx.x;
 }
 
+// Element q of a small per-thread array through static indices only (a
+// dynamic index would place the array in scratch memory, and every reload
+// from there waits for all memory operations in flight).
+template <int N>
+__device__ __forceinline__ float pick(const float (&v)[N], int q) {
+    float r = v[0];
+#pragma unroll
+    for (int i = 1; i < N; ++i)
+        if (q == i) r = v[i];
+    return r;
+}
+template <int N>
+__device__ __forceinline__ void put(float (&v)[N], int q, float x) {
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+        if (q == i) v[i] = x;
+}
+
 // Batch-element column totals for this thread's columns j = tid + q*kThreads.
 // `part` holds one row of N per wave; the workgroup's sum of column j is the
 // sum of those rows in wave order, published with tag t into slot row `gid`
@@ -266,10 +284,11 @@ __device__ __forceinline__ void exchange_columns(const float* part, unsigned lon
             }
             __builtin_amdgcn_s_sleep(1);
         }
+        const float mine = pick(own, q);
         float tot = 0.0f;
 #pragma unroll
         for (int g = 0; g < kMaxGroup; ++g)
-            if (g < W) tot += (g == w) ? own[q] : got[g];
+            if (g < W) tot += (g == w) ? mine : got[g];
         f(j, dead ? __builtin_nanf("") : tot);
     }
 }
@@ -385,12 +404,12 @@ __global__ __launch_bounds__(kThreads) void implicit_adjoint(ImpResArgs a) {
     R::store(part + wave * a.N, lane, a.N, cg);
     __syncthreads();
     exchange_columns(part, a.pro, a.N, b, a.W, w, 1u, a.spin_limit, a.status, dead,
-                     [&](int j, float tot) { c_own[(j - threadIdx.x) / kThreads] = tot; });
+                     [&](int j, float tot) { put(c_own, (j - threadIdx.x) / kThreads, tot); });
     __syncthreads();
     R::store(part + wave * a.N, lane, a.N, cp);
     __syncthreads();
     exchange_columns(part, a.pro + size_t(G) * a.N, a.N, b, a.W, w, 1u, a.spin_limit, a.status, dead,
-                     [&](int j, float tot) { cs_own[(j - threadIdx.x) / kThreads] = fmaxf(tot, sk::kSumFloor); });
+                     [&](int j, float tot) { put(cs_own, (j - threadIdx.x) / kThreads, fmaxf(tot, sk::kSumFloor)); });
 
     // Sweeps.
     float mu[PL];
@@ -421,7 +440,7 @@ __global__ __launch_bounds__(kThreads) void implicit_adjoint(ImpResArgs a) {
         exchange_columns(part, a.xchg + size_t(t & 1) * G * a.N, a.N, b, a.W, w, unsigned(t),
                          a.spin_limit, a.status, dead, [&](int j, float tot) {
                              const int q = (j - threadIdx.x) / kThreads;
-                             lds_mu[j] = (c_own[q] - tot) / cs_own[q];
+                             lds_mu[j] = (pick(c_own, q) - tot) / pick(cs_own, q);
                          });
         __syncthreads();
         R::load(lds_mu, lane, a.N, mu, 0.0f);
