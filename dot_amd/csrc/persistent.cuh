@@ -118,11 +118,42 @@ struct ColVec {
     }
 };
 
+// LDS rows of the step-1 fold: all 8 waves' rows at once when a row is at most
+// 32 floats per lane (publish_row_flat), else a halving tree through 4 rows.
+template <int VEC, int CH>
+constexpr int kFoldRows = VEC * CH <= 32 ? kWaves : kWaves / 2;
+
+// Step 1 with every wave's row in LDS: one barrier, then thread t adds
+// columns t, t + 512, ... over the 8 waves in order and publishes them (all
+// 512 threads publish; the tree leaves that to wave 0 alone).  Contains
+// barriers; `rows` holds 8 N floats.
+template <int VEC, int CH>
+__device__ __forceinline__ void publish_row_flat(const float (&acc)[VEC * CH], float* rows, int N,
+                                                 unsigned long long* slot_row, unsigned t) {
+    using R = Row<VEC, CH>;
+    const int wave = threadIdx.x / kWave;
+    __syncthreads();  // earlier readers of `rows` are done
+    R::store(rows + wave * N, opaque_lane(), N, acc);
+    __syncthreads();
+    int tid = threadIdx.x;
+    asm volatile("" : "+v"(tid));
+    for (int j = tid; j < N; j += kThreads) {
+        float s = rows[j];
+#pragma unroll
+        for (int v = 1; v < kWaves; ++v) s += rows[v * N + j];
+        publish(slot_row + j, s, t);
+    }
+}
+
 // Step 1: fold the waves' per-lane column sums (tree through `tree`, 4 N
 // floats) and publish the workgroup's row with tag t at slot_row.
 template <int VEC, int CH>
 __device__ __forceinline__ void publish_row(float (&acc)[VEC * CH], float* tree, int N,
                                             unsigned long long* slot_row, unsigned t) {
+    if constexpr (kFoldRows<VEC, CH> == kWaves) {
+        publish_row_flat<VEC, CH>(acc, tree, N, slot_row, t);
+        return;
+    }
     using R = Row<VEC, CH>;
     res::tree_combine<VEC, CH>(acc, tree, N);
     if (threadIdx.x < kWave) {
@@ -230,10 +261,10 @@ __global__ __launch_bounds__(kThreads) void forward(FwdArgs a) {
     using R = Row<VEC, CH>;
     constexpr int PL = R::PL;
     constexpr float kLn2 = 0.69314718055994531f;
-    // LDS: tree 4N | v N | v log2(e) N | log b N | red N + W (padded to 4) | u 2R | log a R | scratch 32
+    // LDS: fold (kFoldRows) N | v N | v log2(e) N | log b N | red N + W (padded to 4) | u 2R | log a R | scratch 32
     extern __shared__ float lds[];
     float* tree = lds;
-    float* lds_v = tree + (kWaves / 2) * a.N;
+    float* lds_v = tree + kFoldRows<VEC, CH> * a.N;
     float* lds_v2 = lds_v + a.N;
     float* lds_lb = lds_v2 + a.N;
     float* red = lds_lb + a.N;
@@ -498,7 +529,7 @@ template <int VEC, int CH>
 __global__ __launch_bounds__(kThreads) void implicit_adjoint(ImpArgs a) {
     using R = Row<VEC, CH>;
     constexpr int PL = R::PL;
-    // LDS: tree 4N | mu N | red N + W | r R | 1/rs R | lambda R | c S | cs S | scratch 16
+    // LDS: fold (kFoldRows) N | mu N | red N + W | r R | 1/rs R | lambda R | c S | cs S | scratch 16
     extern __shared__ float lds[];
     const int lane = threadIdx.x % kWave;
     const int wave = threadIdx.x / kWave;
@@ -511,7 +542,7 @@ __global__ __launch_bounds__(kThreads) void implicit_adjoint(ImpArgs a) {
     const int c0 = slice_begin(w, a.W, a.N), c1 = slice_begin(w + 1, a.W, a.N);
     const int S = (a.N + a.W - 1) / a.W;
     float* tree = lds;
-    float* lds_mu = tree + (kWaves / 2) * a.N;
+    float* lds_mu = tree + kFoldRows<VEC, CH> * a.N;
     float* red = lds_mu + a.N;
     float* lds_r = red + a.N + a.W;
     float* lds_irs = lds_r + a.R;

@@ -331,13 +331,14 @@ bool launch_stream_forward(const dot_sinkhorn_fwd_args* a, const FwdLayout& L, c
     r.R = sc.R;
     r.spin_limit = kSpinLimit;
     const size_t words = size_t(reinterpret_cast<unsigned long long*>(r.status) - L.pst) + 1;
-    const size_t lds =
-        (size_t(8) * N + ((size_t(N) + sc.W + 3) & ~size_t(3)) - N + 3 * size_t(sc.R) + res::kFwdScratch) *
-        sizeof(float);
     bool ok = false;
     dispatch_row(N, vec4, [&](auto vc, auto cc) {
         constexpr int V = decltype(vc)::value;
         constexpr int C = decltype(cc)::value;
+        // fold rows | v, v log2(e), log b | red (padded to 4) | u 2R, log a R | scratch
+        const size_t lds = (size_t(pst::kFoldRows<V, C> + 3) * N + ((size_t(N) + sc.W + 3) & ~size_t(3)) +
+                            3 * size_t(sc.R) + res::kFwdScratch) *
+                           sizeof(float);
         launch_fill_zero(L.pst, 2 * words, stream);
         ProfScope prof("sk_fwd_persistent", stream);
         ok = launch_cooperative(pst::forward<V, C>, r, G, res::kThreads, lds, stream);
@@ -688,11 +689,13 @@ bool launch_stream_adjoint(const dot_sinkhorn_bwd_args* a, const ImpLayout& L, c
     r.spin_limit = kSpinLimit;
     const size_t words = size_t(reinterpret_cast<unsigned long long*>(r.status) - L.pst) + 1;
     const size_t S = (size_t(N) + sc.W - 1) / sc.W;
-    const size_t lds = (size_t(6) * N + sc.W + 3 * size_t(sc.R) + 2 * S + 16) * sizeof(float);
     bool ok = false;
     dispatch_row(N, vec4, [&](auto vc, auto cc) {
         constexpr int V = decltype(vc)::value;
         constexpr int C = decltype(cc)::value;
+        // fold rows | mu | red N + W | r, 1/rs, lambda R each | c, cs S each | scratch
+        const size_t lds =
+            (size_t(pst::kFoldRows<V, C> + 2) * N + sc.W + 3 * size_t(sc.R) + 2 * S + 16) * sizeof(float);
         launch_fill_zero(L.pst, 2 * words, stream);
         ProfScope prof("sk_imp_persistent", stream);
         ok = launch_cooperative(pst::implicit_adjoint<V, C>, r, G, res::kThreads, lds, stream);
