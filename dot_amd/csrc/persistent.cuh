@@ -124,9 +124,9 @@ template <int VEC, int CH>
 constexpr int kFoldRows = VEC * CH <= 32 ? kWaves : kWaves / 2;
 
 // Step 1 with every wave's row in LDS: one barrier, then thread t adds
-// columns t, t + 512, ... over the 8 waves in order and publishes them (all
-// 512 threads publish; the tree leaves that to wave 0 alone).  Contains
-// barriers; `rows` holds 8 N floats.
+// columns t, t + 512, ... over the 8 waves in order and publishes them, so
+// the stores are spread over all 512 threads.  Contains barriers; `rows`
+// holds 8 N floats.
 template <int VEC, int CH>
 __device__ __forceinline__ void publish_row_flat(const float (&acc)[VEC * CH], float* rows, int N,
                                                  unsigned long long* slot_row, unsigned t) {
@@ -145,31 +145,47 @@ __device__ __forceinline__ void publish_row_flat(const float (&acc)[VEC * CH], f
     }
 }
 
-// Step 1: fold the waves' per-lane column sums (tree through `tree`, 4 N
-// floats) and publish the workgroup's row with tag t at slot_row.
+// Step 1 through 4 LDS rows (rows of 64 floats per lane): waves 4..7 store,
+// waves 0..3 add them to their own rows and store the pairs, then thread t
+// adds columns t, t + 512, ... over the 4 pair rows in order and publishes
+// them.  Contains barriers; `rows` holds 4 N floats.
+template <int VEC, int CH>
+__device__ __forceinline__ void publish_row_pairs(float (&acc)[VEC * CH], float* rows, int N,
+                                                  unsigned long long* slot_row, unsigned t) {
+    using R = Row<VEC, CH>;
+    const int wave = threadIdx.x / kWave;
+    constexpr int H = kWaves / 2;
+    __syncthreads();  // earlier readers of `rows` are done
+    if (wave >= H) R::store(rows + (wave - H) * N, opaque_lane(), N, acc);
+    __syncthreads();
+    if (wave < H) {
+        const int ln = opaque_lane();
+        float o[R::PL];
+        R::load(rows + wave * N, ln, N, o, 0.0f);
+#pragma unroll
+        for (int e = 0; e < R::PL; ++e) acc[e] += o[e];
+        R::store(rows + wave * N, ln, N, acc);
+    }
+    __syncthreads();
+    int tid = threadIdx.x;
+    asm volatile("" : "+v"(tid));
+    for (int j = tid; j < N; j += kThreads) {
+        float s = rows[j];
+#pragma unroll
+        for (int v = 1; v < H; ++v) s += rows[v * N + j];
+        publish(slot_row + j, s, t);
+    }
+}
+
+// Step 1: fold the waves' per-lane column sums in a fixed order and publish
+// the workgroup's row with tag t at slot_row (every thread publishes).
 template <int VEC, int CH>
 __device__ __forceinline__ void publish_row(float (&acc)[VEC * CH], float* tree, int N,
                                             unsigned long long* slot_row, unsigned t) {
-    if constexpr (kFoldRows<VEC, CH> == kWaves) {
+    if constexpr (kFoldRows<VEC, CH> == kWaves)
         publish_row_flat<VEC, CH>(acc, tree, N, slot_row, t);
-        return;
-    }
-    using R = Row<VEC, CH>;
-    res::tree_combine<VEC, CH>(acc, tree, N);
-    if (threadIdx.x < kWave) {
-        // Addresses from an opaque lane index, computed here: hoisted out of
-        // the caller's iteration loop they would be spilled, and each spill
-        // reload would wait for every store issued before it.
-        const int lane = opaque_lane();
-#pragma unroll
-        for (int k = 0; k < CH; ++k) {
-            const int c = R::col(lane, k);
-            if (VEC == 1 ? c < N : c + VEC <= N) {  // N % 4 == 0 when VEC == 4
-#pragma unroll
-                for (int q = 0; q < VEC; ++q) publish(slot_row + c + q, acc[k * VEC + q], t);
-            }
-        }
-    }
+    else
+        publish_row_pairs<VEC, CH>(acc, tree, N, slot_row, t);
 }
 
 // Step 2: the owner's sums over the element's W rows for its slice [c0, c1),
