@@ -189,35 +189,30 @@ std::vector<Tensor> sinkhorn_dual_forward_op(Tensor log_alpha, double tau, int64
     return {o.plan, c[0], c[1]};
 }
 
-// sinkhorn_spectral_preflight (torch_cuda.cpp:559-593; kernel kernels.cu:141-241):
-// the same power iteration on P = softmax_row(log_alpha / tau) with the
-// reference's deterministic sin() start vector, written with ATen batched
-// products.  Not a hand-written kernel: this op is off the hot path.
+// sinkhorn_spectral_preflight (torch_cuda.cpp:559-593; kernel kernels.cu:141-241).
 Tensor sinkhorn_spectral_preflight_op(Tensor log_alpha, double tau, int64_t n_power) {
     check_hip_input(log_alpha, "log_alpha");
     TORCH_CHECK(log_alpha.dim() == 3, "log_alpha must be 3D [B, n, m]");
     TORCH_CHECK(tau > 0.0, "tau must be > 0");
     TORCH_CHECK(n_power >= 1, "n_power must be >= 1");
     c10::OptionalDeviceGuard guard(log_alpha.device());
-    const int64_t B = log_alpha.size(0), m = log_alpha.size(2);
-    Tensor K = f32c(log_alpha) * (1.0f / static_cast<float>(tau));
-    Tensor P = at::exp(K - at::logsumexp(K, {2}, true));
-    auto opts = K.options();
-    Tensor j = at::arange(1, m + 1, opts).unsqueeze(0);
-    Tensor bb = at::arange(1, B + 1, opts).unsqueeze(1);
-    Tensor v = at::sin(j * 12.9898f + bb * 78.233f);
-    auto center = [](const Tensor& x) { return x - x.mean({-1}, true); };
-    auto normalize = [](const Tensor& x) {
-        return x / at::sqrt(at::clamp_min((x * x).sum({-1}, true), 1.0e-12f));
-    };
-    v = normalize(center(v));
-    for (int64_t it = 0; it < n_power; ++it) {
-        Tensor u = center(at::bmm(P, v.unsqueeze(-1)).squeeze(-1));
-        v = normalize(center(at::bmm(P.transpose(1, 2).contiguous(), u.unsqueeze(-1)).squeeze(-1)));
-    }
-    Tensor u = center(at::bmm(P, v.unsqueeze(-1)).squeeze(-1));
-    Tensor est = at::sqrt(at::clamp_min((u * u).sum({-1}), 1.0e-12f));
-    return at::clamp(est, 0.0f, 0.999999f);
+    Tensor X = f32c(log_alpha);
+    const int64_t B = X.size(0), M = X.size(1), N = X.size(2);
+    Tensor tau_est = at::empty({B}, X.options());
+    const size_t ws_bytes = dot_sinkhorn_spectral_preflight_workspace_bytes(int(B), int(M), int(N));
+    Tensor ws = workspace(ws_bytes, X);
+    dot_spectral_preflight_args a{};
+    a.log_alpha = X.data_ptr<float>();
+    a.B = int(B);
+    a.M = int(M);
+    a.N = int(N);
+    a.tau = static_cast<float>(tau);
+    a.n_power = int(n_power);
+    a.tau_est = tau_est.data_ptr<float>();
+    a.workspace = ws.data_ptr();
+    a.workspace_bytes = ws_bytes;
+    check_rc(dot_sinkhorn_spectral_preflight(&a, current_stream(X)), "dot_sinkhorn_spectral_preflight");
+    return tau_est;
 }
 
 std::vector<Tensor> run_backward(bool implicit, const Tensor& scores_f, int kind, const Tensor& plan,

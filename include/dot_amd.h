@@ -131,6 +131,26 @@ int dot_sinkhorn_backward_implicit(const dot_sinkhorn_bwd_args* args, dot_stream
 size_t dot_sinkhorn_backward_unrolled_workspace_bytes(int B, int M, int N);
 int dot_sinkhorn_backward_unrolled(const dot_sinkhorn_bwd_args* args, dot_stream_t stream);
 
+typedef struct {
+    const float* log_alpha;   /* [B,M,N] */
+    int B, M, N;
+    float tau;                /* > 0 */
+    int n_power;              /* power iterations, >= 1 */
+    float* tau_est;           /* [B] out: contraction estimate in [0, 0.999999] */
+    void* workspace;
+    size_t workspace_bytes;
+} dot_spectral_preflight_args;
+
+/* Spectral contraction estimate behind n_iters='auto': with
+ * P = softmax_row(log_alpha / tau), n_power deflated power iterations
+ * u = centre(P v), v = centre_normalise(P^T u) from the reference's
+ * deterministic sin() start vector, then tau_est = ||centre(P v)||.
+ * Replaces sinkhorn_spectral_preflight_cuda (src/sinkhorn/kernels.cuh;
+ * kernels.cu:141-241, :1509-1532) behind sinkhorn_spectral_preflight
+ * (torch_cuda.cpp:559-593; registry.cpp:48). */
+size_t dot_sinkhorn_spectral_preflight_workspace_bytes(int B, int M, int N);
+int dot_sinkhorn_spectral_preflight(const dot_spectral_preflight_args* args, dot_stream_t stream);
+
 /* ---------------------------------------------------------------------- */
 /* Bidirectional softmax                                                   */
 /* ---------------------------------------------------------------------- */

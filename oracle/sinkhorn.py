@@ -31,6 +31,14 @@ and exercised by ``tests/test_oracle.py``:
 * ``unrolled_backward`` — golden vectors of the reference's compiled
   ``sinkhorn_backward_unrolled_cpu`` (autograd cannot pin it: the reference's
   formula is not the exact Jacobian; see ``unrolled_backward``).
+* ``spectral_preflight_tau`` — the deflated power iteration converges to the
+  largest singular value of C_M P C_N (C the centring projector), checked
+  against ``numpy.linalg.svd`` at a large iteration count; a row-constant
+  ``log_alpha`` (P = 1 1^T / N, rank one) gives the 1e-12 floor.  The start
+  vector is restated from the source and not independently pinned: no golden
+  vector of the reference exists for the preflight (its compiled CPU library
+  has none), so the value after 5 or 8 iterations, which still depends on
+  the start vector, is parity unpinned beyond the restated algorithm.
 """
 
 from __future__ import annotations
@@ -223,3 +231,36 @@ def with_grads_unrolled(log_alpha, grad_P, tau, n_iters, log_a=None, log_b=None,
     grad, grad_tau = unrolled_backward(log_alpha, fwd.P, grad_P, fwd.K, fwd.u_hist, fwd.v_hist,
                                        tau, dtype)
     return fwd.P, grad, grad_tau
+
+
+def spectral_preflight_tau(log_alpha, tau: float, n_power: int, dtype=np.float64) -> np.ndarray:
+    """Contraction estimate per batch element (reference dot/sinkhorn.py:878-897,
+    the same math as the GPU kernel src/sinkhorn/kernels.cu:141-241):
+    P = softmax_row(log_alpha / tau); v0_j = sin((j+1) 12.9898 + (b+1) 78.233)
+    (arguments rounded in float32 as the kernel forms them), centred and
+    normalised; n_power times u = centre(P v), v = centre_normalise(P^T u);
+    finally ||centre(P v)||, floored at 1e-12 under the root and clamped to
+    [0, 0.999999] (kernels.cu:238-240)."""
+    X = np.asarray(log_alpha, dtype=dtype)
+    B, M, N = X.shape
+    K = X * (dtype(1.0) / dtype(tau)) if dtype is np.float32 else X / tau
+    lse = np.max(K, axis=2, keepdims=True)
+    s = np.sum(safe_exp(K - lse), axis=2, keepdims=True)
+    P = safe_exp(K - (lse + np.log(np.maximum(s, 1e-12))))
+    j = np.arange(1, N + 1, dtype=np.float32)[None, :] * np.float32(12.9898)
+    bb = np.arange(1, B + 1, dtype=np.float32)[:, None] * np.float32(78.233)
+    v = np.sin((j + bb).astype(np.float32)).astype(dtype)
+
+    def centre(x):
+        return x - x.mean(axis=-1, keepdims=True)
+
+    def normalise(x):
+        return x / np.sqrt(np.maximum((x * x).sum(axis=-1, keepdims=True), 1e-12))
+
+    v = normalise(centre(v))
+    for _ in range(n_power):
+        u = centre(np.einsum("bij,bj->bi", P, v))
+        v = normalise(centre(np.einsum("bij,bi->bj", P, u)))
+    u = centre(np.einsum("bij,bj->bi", P, v))
+    est = np.sqrt(np.maximum((u * u).sum(axis=-1), 1e-12))
+    return np.clip(est, 0.0, 0.999999)

@@ -306,3 +306,37 @@ def test_oracle_vs_compiled_reference(shape, tau, T):
     Pu, gu, gtu = osk.with_grads_unrolled(la, G, tau, min(T, 25), np.log(a), np.log(b))
     assert rel_err(gu, gu_ref) < GRAD_TOL
     assert sum_err(gtu, gtu_ref, gu * la / tau) < GRAD_TOL
+
+
+def _centred_svd_top(log_alpha, tau):
+    """Largest singular value of C_M P C_N (C the centring projector) per batch
+    element, by numpy's SVD in float64."""
+    K = log_alpha / tau
+    P = np.exp(K - np.log(np.exp(K - K.max(-1, keepdims=True)).sum(-1, keepdims=True)) - K.max(-1, keepdims=True))
+    out = []
+    for Pb in P:
+        M, N = Pb.shape
+        CM = np.eye(M) - 1.0 / M
+        CN = np.eye(N) - 1.0 / N
+        out.append(np.linalg.svd(CM @ Pb @ CN, compute_uv=False)[0])
+    return np.array(out)
+
+
+def test_spectral_preflight_converges_to_centred_singular_value():
+    """The deflated power iteration's limit is sigma_max(C_M P C_N): a missing
+    centring step would converge to sigma_max(P) >= 1 instead."""
+    rng = np.random.default_rng(11)
+    X = 0.5 * rng.standard_normal((3, 20, 15))
+    for tau in (0.4, 1.5):
+        est = osk.spectral_preflight_tau(X, tau, 400)
+        ref_sv = _centred_svd_top(X, tau)
+        assert np.all(ref_sv < 0.999)
+        np.testing.assert_allclose(est, ref_sv, rtol=1e-6)
+
+
+def test_spectral_preflight_rank_one_plan_gives_the_floor():
+    """Rows of log_alpha that are constant give P = 1 1^T / N, whose centred
+    image vanishes: the estimate is the 1e-12 floor under the root."""
+    X = np.repeat(np.linspace(-1, 1, 9)[:, None], 7, axis=1)[None].repeat(2, 0)
+    est = osk.spectral_preflight_tau(X, 0.3, 5)
+    np.testing.assert_allclose(est, 1e-6, rtol=1e-9)
