@@ -31,6 +31,14 @@ and exercised by ``tests/test_oracle.py``:
 * ``unrolled_backward`` — golden vectors of the reference's compiled
   ``sinkhorn_backward_unrolled_cpu`` (autograd cannot pin it: the reference's
   formula is not the exact Jacobian; see ``unrolled_backward``).
+* ``dual_forward_method`` (momentum, Adam, Anderson, regularisation
+  schedules) — restated from torch_cuda.cpp:323-557 and :61-84.  Pinned by
+  reductions to the vanilla forward (momentum with omega = 1, an Anderson
+  history of one, a schedule whose start equals the target, each equal to
+  ``dual_forward`` step for step) and by the fixed point: every method that
+  converges reaches the vanilla plan.  The per-iteration values of the
+  accelerated methods between those pins are restated, not independently
+  pinned (the reference ships no fixture for them).
 * ``spectral_preflight_tau`` — the deflated power iteration converges to the
   largest singular value of C_M P C_N (C the centring projector), checked
   against ``numpy.linalg.svd`` at a large iteration count; a row-constant
@@ -264,3 +272,159 @@ def spectral_preflight_tau(log_alpha, tau: float, n_power: int, dtype=np.float64
     u = centre(np.einsum("bij,bj->bi", P, v))
     est = np.sqrt(np.maximum((u * u).sum(axis=-1), 1e-12))
     return np.clip(est, 0.0, 0.999999)
+
+
+SCHEDULE_NONE, SCHEDULE_LINEAR, SCHEDULE_EXPONENTIAL, SCHEDULE_COSINE = 0, 1, 2, 3
+METHOD_VANILLA, METHOD_MOMENTUM, METHOD_ANDERSON, METHOD_ADAM = 0, 1, 2, 3
+
+
+def scheduled_tau(step: int, total: int, tau: float, reg_start: float, schedule: int) -> np.float32:
+    """Regularisation at iteration ``step`` (torch_cuda.cpp:61-84), in float32
+    like the reference's host code: start = reg_start if > 0 else 10 tau;
+    frac = step / (total - 1); linear, cosine or exponential from start to tau."""
+    f = np.float32
+    tau = f(tau)
+    if schedule == SCHEDULE_NONE or total <= 1:
+        return tau
+    start = f(reg_start) if reg_start > 0.0 else f(10.0) * tau
+    frac = f(step) / f(total - 1)
+    if schedule == SCHEDULE_LINEAR:
+        return start * (f(1.0) - frac) + tau * frac
+    if schedule == SCHEDULE_COSINE:
+        return tau + f(0.5) * (start - tau) * (f(1.0) + f(np.cos(f(np.pi) * frac)))
+    if schedule == SCHEDULE_EXPONENTIAL:
+        return tau * f(np.power(start / tau, f(1.0) - frac))
+    return tau
+
+
+def dual_forward_method(log_alpha, tau: float, n_iters: int, tol: float = 0.0, log_a=None, log_b=None,
+                        method: int = METHOD_VANILLA, omega: float = 1.5, anderson_k: int = 5,
+                        mixing_beta: float = 1.0, lr: float = 1.0, beta1: float = 0.9, beta2: float = 0.999,
+                        eps_adam: float = 1e-8, bias_correction: bool = True, reg_start: float = -1.0,
+                        schedule: int = SCHEDULE_NONE, return_log: bool = False, dtype=np.float64):
+    """Accelerated / scheduled dual Sinkhorn of the reference's GPU path.
+
+    method 0 with a schedule is ``sinkhorn_dual_vanilla_cuda`` (torch_cuda.cpp:
+    147-264: K rebuilt from log_alpha at each iteration's tau, the u-only stop
+    test).  Methods 1-3 are ``torch_cuda.cpp:323-557``:
+
+    * momentum: u' = (1 - omega) u + omega u*, kept when the batch-global
+      max|u' - u*| < max|u - u*| (u* the plain row update); the same for v
+      after the column update from the kept u;
+    * Adam: g = u* - u, first/second moments, optional bias correction
+      (beta^(t+1) in float32), u' = u + lr m^ / (sqrt(v^) + eps), kept by the
+      same test;
+    * Anderson: state x = (u, v), x_new = one plain row+column update of x,
+      residual f = x_new - x, the last k (x, f) pairs; with at least two,
+      alpha solves (F^T F + 1e-8 I) alpha = 1 per batch element, normalised
+      by its sum (all elements fall back to x_new when any |sum| < 1e-12 or a
+      solve fails), x = (X + mixing_beta F) alpha.
+
+    Stop test (tol > 0): methods 1 and 3 use max over u and v of the change;
+    Anderson max|x_new - x|; vanilla max|u - u_prev|.  The plan is
+    exp(K + u + v) with K at the target tau.  Returns ForwardResult.
+    """
+    f32 = np.float32
+    la = np.asarray(log_alpha, dtype=np.float32)
+    B, n, m = la.shape
+    lga = default_log_marginal(B, n, dtype) if log_a is None else np.asarray(log_a, np.float32).astype(dtype)
+    lgb = default_log_marginal(B, m, dtype) if log_b is None else np.asarray(log_b, np.float32).astype(dtype)
+
+    def kernel_at(t):
+        return (la * (f32(1.0) / f32(t))).astype(dtype)
+
+    K = kernel_at(scheduled_tau(0, n_iters, tau, reg_start, schedule))
+    u = np.zeros((B, n), dtype)
+    v = np.zeros((B, m), dtype)
+    row = lambda K, v: lga - _lse(K + v[:, None, :], axis=2)
+    col = lambda K, u: lgb - _lse(K + u[:, :, None], axis=1)
+    gmax = lambda x: float(np.abs(x).max()) if x.size else 0.0
+    used, converged = 0, False
+    if method == METHOD_ADAM:
+        mu_u, vu_u = np.zeros_like(u), np.zeros_like(u)
+        mu_v, vu_v = np.zeros_like(v), np.zeros_like(v)
+    if method == METHOD_ANDERSON:
+        state = np.zeros((B, n + m), dtype)
+        hist_x, hist_f = [], []
+    for it in range(n_iters):
+        if schedule != SCHEDULE_NONE:
+            K = kernel_at(scheduled_tau(it, n_iters, tau, reg_start, schedule))
+        if method == METHOD_ANDERSON:
+            un = row(K, state[:, n:])
+            vn = col(K, un)
+            x_new = np.concatenate([un, vn], axis=1)
+            resid = x_new - state
+            delta = gmax(resid) if tol > 0.0 else 0.0
+            hist_x.append(state.copy())
+            hist_f.append(resid)
+            if len(hist_x) > anderson_k:
+                hist_x.pop(0)
+                hist_f.pop(0)
+            if len(hist_x) >= 2:
+                X = np.stack(hist_x, axis=2)
+                F = np.stack(hist_f, axis=2)
+                h = X.shape[2]
+                gram = np.einsum("blp,blq->bpq", F, F) + 1e-8 * np.eye(h)[None]
+                try:
+                    alpha = np.linalg.solve(gram, np.ones((B, h, 1)))[..., 0]
+                    denom = alpha.sum(1, keepdims=True)
+                    if np.abs(denom).min() >= 1e-12:
+                        alpha = alpha / denom
+                        state = np.einsum("blh,bh->bl", X + mixing_beta * F, alpha)
+                    else:
+                        state = x_new
+                except np.linalg.LinAlgError:
+                    state = x_new
+            else:
+                state = x_new
+            used = it + 1
+            if tol > 0.0 and delta < tol:
+                converged = True
+                break
+            continue
+        u_prev = u
+        ut = row(K, v)
+        if method == METHOD_MOMENTUM:
+            un = (1.0 - omega) * u + omega * ut
+            if gmax(un - ut) < gmax(u - ut):
+                ut = un
+        elif method == METHOD_ADAM:
+            g = ut - u
+            mu_u = beta1 * mu_u + (1.0 - beta1) * g
+            vu_u = beta2 * vu_u + (1.0 - beta2) * g * g
+            c1 = float(f32(1.0) - np.power(f32(beta1), f32(it + 1))) if bias_correction else 1.0
+            c2 = float(f32(1.0) - np.power(f32(beta2), f32(it + 1))) if bias_correction else 1.0
+            un = u + lr * (mu_u / c1) / (np.sqrt(vu_u / c2) + eps_adam)
+            if gmax(un - ut) < gmax(u - ut):
+                ut = un
+        vt = col(K, ut)
+        if method == METHOD_MOMENTUM:
+            vn = (1.0 - omega) * v + omega * vt
+            if gmax(vn - vt) < gmax(v - vt):
+                vt = vn
+        elif method == METHOD_ADAM:
+            g = vt - v
+            mu_v = beta1 * mu_v + (1.0 - beta1) * g
+            vu_v = beta2 * vu_v + (1.0 - beta2) * g * g
+            c1 = float(f32(1.0) - np.power(f32(beta1), f32(it + 1))) if bias_correction else 1.0
+            c2 = float(f32(1.0) - np.power(f32(beta2), f32(it + 1))) if bias_correction else 1.0
+            vn = v + lr * (mu_v / c1) / (np.sqrt(vu_v / c2) + eps_adam)
+            if gmax(vn - vt) < gmax(v - vt):
+                vt = vn
+        if method == METHOD_VANILLA:
+            delta = gmax(ut - u_prev)
+        else:
+            delta = max(gmax(ut - u), gmax(vt - v)) if tol > 0.0 else 0.0
+        u, v = ut, vt
+        used = it + 1
+        if tol > 0.0 and delta < tol:
+            converged = True
+            break
+    if method == METHOD_ANDERSON:
+        u, v = state[:, :n], state[:, n:]
+    if schedule != SCHEDULE_NONE:
+        K = kernel_at(tau)
+    logP = K + u[:, :, None] + v[:, None, :]
+    with np.errstate(over="ignore"):
+        P = logP if return_log else np.exp(logP)
+    return ForwardResult(P=P, n_iters_used=used, converged=converged, u=u, v=v, K=K)

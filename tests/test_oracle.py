@@ -340,3 +340,59 @@ def test_spectral_preflight_rank_one_plan_gives_the_floor():
     X = np.repeat(np.linspace(-1, 1, 9)[:, None], 7, axis=1)[None].repeat(2, 0)
     est = osk.spectral_preflight_tau(X, 0.3, 5)
     np.testing.assert_allclose(est, 1e-6, rtol=1e-9)
+
+
+# --- accelerated methods and regularisation schedules (torch_cuda.cpp:323-557) ---
+def _small_problem(seed=0, B=2, n=12, m=10):
+    rng = np.random.default_rng(seed)
+    return -rng.random((B, n, m)).astype(np.float32)
+
+
+def test_momentum_with_unit_omega_is_vanilla_step_for_step():
+    la = _small_problem(1)
+    ref_ = osk.dual_forward_method(la, 0.1, 37, 0.0)
+    mom = osk.dual_forward_method(la, 0.1, 37, 0.0, method=osk.METHOD_MOMENTUM, omega=1.0)
+    np.testing.assert_array_equal(mom.u, ref_.u)
+    np.testing.assert_array_equal(mom.v, ref_.v)
+    # and the method-free path is the vanilla oracle itself
+    van = osk.dual_forward(la, 0.1, 37, 0.0)
+    np.testing.assert_allclose(ref_.u, van.u, rtol=0, atol=0)
+
+
+def test_anderson_with_history_of_one_is_vanilla_step_for_step():
+    la = _small_problem(2)
+    van = osk.dual_forward(la, 0.2, 25, 0.0)
+    aa = osk.dual_forward_method(la, 0.2, 25, 0.0, method=osk.METHOD_ANDERSON, anderson_k=1)
+    np.testing.assert_allclose(aa.u, van.u, rtol=0, atol=1e-12)
+    np.testing.assert_allclose(aa.v, van.v, rtol=0, atol=1e-12)
+
+
+@pytest.mark.parametrize("schedule", [osk.SCHEDULE_COSINE, osk.SCHEDULE_EXPONENTIAL])
+def test_schedule_starting_at_the_target_is_unscheduled(schedule):
+    la = _small_problem(3)
+    van = osk.dual_forward(la, 0.1, 30, 0.0)
+    sch = osk.dual_forward_method(la, 0.1, 30, 0.0, schedule=schedule, reg_start=0.1)
+    np.testing.assert_array_equal(sch.u, van.u)
+
+
+def test_schedule_endpoints_and_shape():
+    for sched in (osk.SCHEDULE_LINEAR, osk.SCHEDULE_COSINE, osk.SCHEDULE_EXPONENTIAL):
+        taus = [float(osk.scheduled_tau(t, 11, 0.01, 0.5, sched)) for t in range(11)]
+        assert abs(taus[0] - 0.5) < 1e-6 and abs(taus[-1] - 0.01) < 1e-7, (sched, taus)
+        assert all(a >= b for a, b in zip(taus, taus[1:])), sched
+    # default start 10 tau; exponential midpoint is the geometric mean
+    assert abs(float(osk.scheduled_tau(0, 5, 0.02, -1.0, osk.SCHEDULE_LINEAR)) - 0.2) < 1e-7
+    mid = float(osk.scheduled_tau(5, 11, 0.01, 1.0, osk.SCHEDULE_EXPONENTIAL))
+    assert abs(mid - 0.1) < 1e-7
+
+
+@pytest.mark.parametrize("method,kw", [
+    (osk.METHOD_MOMENTUM, dict(omega=1.5)),
+    (osk.METHOD_ADAM, dict(lr=0.5)),
+    (osk.METHOD_ANDERSON, dict(anderson_k=5)),
+])
+def test_methods_reach_the_vanilla_fixed_point(method, kw):
+    la = _small_problem(4, B=2, n=12, m=12)
+    van = osk.dual_forward(la, 0.1, 400, 0.0)
+    r = osk.dual_forward_method(la, 0.1, 400, 0.0, method=method, **kw)
+    np.testing.assert_allclose(r.P, van.P, rtol=0, atol=1e-7)
