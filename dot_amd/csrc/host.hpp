@@ -72,4 +72,12 @@ class ProfScope {
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// Rows per workgroup strip of a streaming sweep: the largest power of two in
+// [4, 64] that still yields >= 1024 workgroups (4 per CU on 256 CUs).
+inline int sweep_strip_rows(int B, int M) {
+    int r = 64;
+    while (r > 4 && int64_t(B) * ((M + r - 1) / r) < 1024) r /= 2;
+    return r;
+}
+
 }  // namespace dot_amd

@@ -1,0 +1,383 @@
+// Accelerated / scheduled dual Sinkhorn C ABI: argument checks, workspace
+// layout and the per-iteration launch sequence.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <string>
+
+#include "host.hpp"
+#include "methods.cuh"
+
+namespace dot_amd {
+namespace {
+
+using mth::kMaxHistory;
+using mth::kSlots;
+
+constexpr int kStopCheckEvery = 16;  // iterations between host reads of the stop flag (tol > 0)
+
+struct MethodLayout {
+    unsigned* slots;  // [T, kSlots] flag words
+    int* done;
+    float *u, *v;                 // current potentials (Anderson: the state)
+    float *m1u, *m2u, *m1v, *m2v; // Adam moments
+    size_t zero_bytes;            // from `slots` through the last zeroed buffer
+    float *ut, *vt, *un, *vn;     // plain updates and candidates
+    float *part_m, *part_s, *cost_partial;
+    float *hxu, *hxv, *hfu, *hfv, *gram, *alpha, *denom;
+    int rows, nstrips;
+    size_t bytes;
+};
+
+MethodLayout method_layout(void* ws, int B, int M, int N, int T, int method, int k) {
+    Carver c(ws);
+    MethodLayout L{};
+    L.rows = sweep_strip_rows(B, M);
+    L.nstrips = M > 0 ? (M + L.rows - 1) / L.rows : 0;
+    const size_t BM = size_t(B) * M, BN = size_t(B) * N;
+    L.slots = c.take<unsigned>(size_t(std::max(T, 1)) * kSlots);
+    L.done = c.take<int>(1);
+    L.u = c.take<float>(BM);
+    L.v = c.take<float>(BN);
+    const bool adam = method == DOT_SK_ADAM;
+    L.m1u = c.take<float>(adam ? BM : 0);
+    L.m2u = c.take<float>(adam ? BM : 0);
+    L.m1v = c.take<float>(adam ? BN : 0);
+    L.m2v = c.take<float>(adam ? BN : 0);
+    L.zero_bytes = c.used();
+    L.ut = c.take<float>(BM);
+    L.vt = c.take<float>(BN);
+    const bool cand = method == DOT_SK_MOMENTUM || adam;
+    L.un = c.take<float>(cand ? BM : 0);
+    L.vn = c.take<float>(cand ? BN : 0);
+    L.part_m = c.take<float>(size_t(B) * L.nstrips * N);
+    L.part_s = c.take<float>(size_t(B) * L.nstrips * N);
+    L.cost_partial = c.take<float>(size_t(B) * L.nstrips);
+    const size_t kk = method == DOT_SK_ANDERSON ? size_t(k) : 0;
+    L.hxu = c.take<float>(kk * BM);
+    L.hxv = c.take<float>(kk * BN);
+    L.hfu = c.take<float>(kk * BM);
+    L.hfv = c.take<float>(kk * BN);
+    L.gram = c.take<float>(kk ? size_t(B) * kMaxHistory * kMaxHistory : 0);
+    L.alpha = c.take<float>(kk ? size_t(B) * kMaxHistory : 0);
+    L.denom = c.take<float>(kk ? size_t(B) : 0);
+    L.bytes = c.used();
+    return L;
+}
+
+// tau at iteration `step` of `total` (scheduled_tau_cuda, torch_cuda.cpp:61-84),
+// in float as there.
+float scheduled_tau(int64_t step, int64_t total, float tau, float reg_start, int schedule) {
+    constexpr float kPi = 3.14159265358979323846f;
+    if (schedule == DOT_SK_SCHEDULE_NONE || total <= 1) return tau;
+    const float start = reg_start > 0.0f ? reg_start : 10.0f * tau;
+    const float frac = static_cast<float>(step) / static_cast<float>(total - 1);
+    switch (schedule) {
+        case DOT_SK_SCHEDULE_LINEAR: return start * (1.0f - frac) + tau * frac;
+        case DOT_SK_SCHEDULE_COSINE: return tau + 0.5f * (start - tau) * (1.0f + std::cos(kPi * frac));
+        case DOT_SK_SCHEDULE_EXPONENTIAL: return tau * std::pow(start / tau, 1.0f - frac);
+        default: return tau;
+    }
+}
+
+dim3 vector_grid(size_t n) { return dim3(unsigned(std::max<size_t>(1, std::min<size_t>((n + kBlock - 1) / kBlock, 1024)))); }
+
+__global__ void set_counts_m(int32_t* used, int32_t* converged, int u, int c) {
+    *used = u;
+    *converged = c;
+}
+
+__global__ void fill_value_m(float* p, size_t n, float x) {
+    for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += size_t(gridDim.x) * blockDim.x)
+        p[i] = x;
+}
+
+__global__ void zero_words(uint32_t* p, size_t n) {
+    for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += size_t(gridDim.x) * blockDim.x)
+        p[i] = 0u;
+}
+
+__global__ void batch_sum_m(const float* partial, int n, float* out) {
+    // one wave per batch element; strips summed lane-strided then across the wave
+    const int b = blockIdx.x;
+    float s = 0.0f;
+    for (int k = threadIdx.x; k < n; k += kWave) s += partial[size_t(b) * n + k];
+    s = wave_sum(s);
+    if (threadIdx.x == 0) out[b] = s;
+}
+
+int check_method_args(const dot_sinkhorn_method_args* m) {
+    if (m->method < DOT_SK_VANILLA || m->method > DOT_SK_ADAM)
+        return fail(DOT_ERR_INVALID_ARG, "method must be 0 (vanilla), 1 (momentum), 2 (anderson) or 3 (adam)");
+    if (m->schedule < DOT_SK_SCHEDULE_NONE || m->schedule > DOT_SK_SCHEDULE_COSINE)
+        return fail(DOT_ERR_INVALID_ARG, "schedule must be 0 (none), 1 (linear), 2 (exponential) or 3 (cosine)");
+    if (m->anderson_k < 1) return fail(DOT_ERR_INVALID_ARG, "anderson_k must be >= 1");
+    if (m->method == DOT_SK_ANDERSON && m->anderson_k > kMaxHistory)
+        return fail(DOT_ERR_UNSUPPORTED, "anderson_k above " + std::to_string(kMaxHistory) +
+                                              " is not supported by this build");
+    return DOT_OK;
+}
+
+}  // namespace
+}  // namespace dot_amd
+
+using namespace dot_amd;
+
+extern "C" size_t dot_sinkhorn_forward_method_workspace_bytes(int B, int M, int N, int max_iter, int method,
+                                                              int anderson_k) {
+    if (B < 0 || M < 0 || N < 0 || max_iter < 0 || anderson_k < 0) return 0;
+    return method_layout(nullptr, B, M, N, max_iter, method, std::min(anderson_k, kMaxHistory)).bytes;
+}
+
+extern "C" int dot_sinkhorn_forward_method(const dot_sinkhorn_method_args* m, dot_stream_t stream_) {
+    hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+    if (!m) return fail(DOT_ERR_INVALID_ARG, "args is NULL");
+    const dot_sinkhorn_fwd_args* a = &m->base;
+    const int B = a->B, M = a->M, N = a->N, T = a->max_iter;
+    if (B < 0 || M < 0 || N < 0) return fail(DOT_ERR_INVALID_ARG, "B, M and N must be >= 0");
+    if (B > 65535) return fail(DOT_ERR_UNSUPPORTED, "batch size above 65535 is not supported");
+    if (N > kMaxRowLen)
+        return fail(DOT_ERR_UNSUPPORTED, "rows longer than 4096 columns are not supported by this build (N=" +
+                                             std::to_string(N) + ")");
+    if (!(std::isfinite(a->tau) && a->tau > 0.0f)) return fail(DOT_ERR_INVALID_ARG, "tau must be > 0");
+    if (T < 0) return fail(DOT_ERR_INVALID_ARG, "max_iter must be >= 0");
+    if (a->scores_kind != DOT_SCORES_LOG_ALPHA && a->scores_kind != DOT_SCORES_COST)
+        return fail(DOT_ERR_INVALID_ARG, "scores_kind must be DOT_SCORES_LOG_ALPHA or DOT_SCORES_COST");
+    if (!a->iters_used || !a->converged)
+        return fail(DOT_ERR_INVALID_ARG, "iters_used and converged must be device pointers");
+    if (a->flags & ~DOT_SK_RETURN_LOG)
+        return fail(DOT_ERR_INVALID_ARG, "only DOT_SK_RETURN_LOG is accepted by dot_sinkhorn_forward_method");
+    const bool ret_log = (a->flags & DOT_SK_RETURN_LOG) != 0;
+    if (ret_log && a->cost) return fail(DOT_ERR_INVALID_ARG, "cost is undefined with DOT_SK_RETURN_LOG");
+    if (int rc = check_method_args(m)) return rc;
+    const int method = m->method;
+    const bool sched = m->schedule != DOT_SK_SCHEDULE_NONE;
+    const bool track = a->tol > 0.0f;
+
+    const size_t elems = size_t(B) * M * N;
+    if (elems == 0) {
+        // as the vanilla entry point: an empty delta is 0, so tol > 0 stops at t = 1
+        const bool stop = track && T > 0;
+        hipLaunchKernelGGL(set_counts_m, dim3(1), dim3(1), 0, stream, a->iters_used, a->converged,
+                           stop ? 1 : T, stop ? 1 : 0);
+        if (a->cost && B > 0)
+            hipLaunchKernelGGL(fill_value_m, dim3(1), dim3(kBlock), 0, stream, a->cost, size_t(B), 0.0f);
+        if (a->u_out && size_t(B) * M)
+            hipLaunchKernelGGL(fill_value_m, dim3(1), dim3(kBlock), 0, stream, a->u_out, size_t(B) * M, 0.0f);
+        if (a->v_out && size_t(B) * N)
+            hipLaunchKernelGGL(fill_value_m, dim3(1), dim3(kBlock), 0, stream, a->v_out, size_t(B) * N, 0.0f);
+        return check_launch("dot_sinkhorn_forward_method");
+    }
+    if (!a->scores) return fail(DOT_ERR_INVALID_ARG, "scores is NULL");
+
+    const int k = std::min(m->anderson_k, kMaxHistory);
+    const MethodLayout L = method_layout(a->workspace, B, M, N, T, method, k);
+    if (!a->workspace || a->workspace_bytes < L.bytes)
+        return fail(DOT_ERR_WORKSPACE, "workspace smaller than dot_sinkhorn_forward_method_workspace_bytes()");
+
+    const float tau = a->tau;
+    const float log_a_default = -std::log(static_cast<float>(M));  // torch_cuda.cpp:42
+    const float log_b_default = -std::log(static_cast<float>(N));
+    const float sign = static_cast<float>(a->scores_kind);
+    auto kscale_at = [&](float t) { return sign * (1.0f / t); };  // kernels.cu:1350 (K = log_alpha * (1/tau))
+    const bool vec4 = (N % 4 == 0) && aligned16(a->scores) && (!a->plan || aligned16(a->plan));
+    const size_t BM = size_t(B) * M, BN = size_t(B) * N;
+
+    // capture-safe fill kernel instead of a memset node
+    {
+        const size_t words = L.zero_bytes / sizeof(uint32_t);
+        hipLaunchKernelGGL(zero_words, vector_grid(words), dim3(kBlock), 0, stream,
+                           reinterpret_cast<uint32_t*>(L.slots), words);
+        hipLaunchKernelGGL(mth::reset_counts, dim3(1), dim3(1), 0, stream, a->iters_used, a->converged);
+    }
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &cap) != hipSuccess) cap = hipStreamCaptureStatusNone;
+    (void)hipGetLastError();
+    const bool may_wait = track && cap == hipStreamCaptureStatusNone;
+
+    int rc = DOT_OK;
+    const bool launched = dispatch_row(N, vec4, [&](auto vc, auto cc) {
+        constexpr int V = decltype(vc)::value;
+        constexpr int C = decltype(cc)::value;
+        const dim3 strips(L.nstrips, B);
+        const dim3 cols((N + mth::kFoldCols - 1) / mth::kFoldCols, B);
+        const size_t col_lds = size_t(2) * N * sizeof(float);
+
+        mth::RowArgs ra{};
+        ra.X = a->scores;
+        ra.M = M;
+        ra.N = N;
+        ra.rows = L.rows;
+        ra.log_a = a->log_a;
+        ra.log_a_default = log_a_default;
+        ra.done = L.done;
+        mth::ColArgs ca{};
+        ca.X = a->scores;
+        ca.M = M;
+        ca.N = N;
+        ca.rows = L.rows;
+        ca.nstrips = L.nstrips;
+        ca.part_m = L.part_m;
+        ca.part_s = L.part_s;
+        ca.log_b = a->log_b;
+        ca.log_b_default = log_b_default;
+        ca.done = L.done;
+        auto row_col = [&](float ks, const float* v_in, float* u_out, float* v_out) {
+            ra.kscale = ks;
+            ra.v = v_in;
+            ra.u = u_out;
+            ca.kscale = ks;
+            ca.u = u_out;
+            ca.v = v_out;
+            ProfScope prof("mth_sweeps", stream);
+            hipLaunchKernelGGL((mth::row_update<V, C>), strips, dim3(kBlock), 0, stream, ra);
+            hipLaunchKernelGGL((mth::col_partial<V, C>), strips, dim3(kBlock), col_lds, stream, ca);
+            hipLaunchKernelGGL(mth::col_finish, cols, dim3(kBlock), 0, stream, ca);
+        };
+        // Anderson ring: logical position -> physical slot
+        int ring_head = 0, ring_size = 0;
+
+        float ks = kscale_at(scheduled_tau(0, T, tau, m->reg_start, m->schedule));
+        for (int it = 0; it < T; ++it) {
+            if (sched) ks = kscale_at(scheduled_tau(it, T, tau, m->reg_start, m->schedule));
+            unsigned* slots = L.slots + size_t(it) * kSlots;
+            if (method == DOT_SK_ANDERSON) {
+                // x_new = one plain row + column update of the state (u, v)
+                row_col(ks, L.v, L.ut, L.vt);
+                int slot;
+                if (ring_size < k) {
+                    slot = (ring_head + ring_size) % k;
+                    ++ring_size;
+                } else {
+                    slot = ring_head;
+                    ring_head = (ring_head + 1) % k;
+                }
+                mth::AaArgs aa{};
+                aa.B = B;
+                aa.M = M;
+                aa.N = N;
+                aa.xu = L.u;
+                aa.xv = L.v;
+                aa.nu = L.ut;
+                aa.nv = L.vt;
+                aa.hxu = L.hxu;
+                aa.hxv = L.hxv;
+                aa.hfu = L.hfu;
+                aa.hfv = L.hfv;
+                aa.slot = slot;
+                aa.h = ring_size;
+                for (int c = 0; c < ring_size; ++c) aa.order[c] = (ring_head + c) % k;
+                aa.mixing_beta = m->mixing_beta;
+                aa.gram = L.gram;
+                aa.alpha = L.alpha;
+                aa.denom = L.denom;
+                aa.slots = slots;
+                aa.track_delta = track ? 1 : 0;
+                aa.done = L.done;
+                ProfScope prof("mth_anderson", stream);
+                hipLaunchKernelGGL(mth::aa_push, vector_grid(BM + BN), dim3(kBlock), 0, stream, aa);
+                if (ring_size >= 2) {
+                    hipLaunchKernelGGL(mth::aa_gram, dim3(ring_size, B), dim3(kBlock), 0, stream, aa);
+                    hipLaunchKernelGGL(mth::aa_solve, dim3(B), dim3(kWave), 0, stream, aa);
+                }
+                hipLaunchKernelGGL(mth::aa_update, vector_grid(BM + BN), dim3(kBlock), 0, stream, aa);
+            } else {
+                // u step
+                ra.kscale = ks;
+                ra.v = L.v;
+                ra.u = L.ut;
+                {
+                    ProfScope prof("mth_sweeps", stream);
+                    hipLaunchKernelGGL((mth::row_update<V, C>), strips, dim3(kBlock), 0, stream, ra);
+                }
+                if (method == DOT_SK_MOMENTUM) {
+                    hipLaunchKernelGGL(mth::momentum_candidate, vector_grid(BM), dim3(kBlock), 0, stream, L.u,
+                                       L.ut, L.un, BM, m->omega, slots + mth::kGapU, L.done);
+                } else if (method == DOT_SK_ADAM) {
+                    const float c1 = m->bias_correction
+                                         ? 1.0f - std::pow(m->beta1, static_cast<float>(it + 1)) : 1.0f;
+                    const float c2 = m->bias_correction
+                                         ? 1.0f - std::pow(m->beta2, static_cast<float>(it + 1)) : 1.0f;
+                    hipLaunchKernelGGL(mth::adam_candidate, vector_grid(BM), dim3(kBlock), 0, stream, L.u, L.ut,
+                                       L.un, L.m1u, L.m2u, BM, m->beta1, m->beta2, c1, c2, m->lr, m->eps_adam,
+                                       slots + mth::kGapU, L.done);
+                }
+                if (method != DOT_SK_VANILLA)
+                    hipLaunchKernelGGL(mth::accept_candidate, vector_grid(BM), dim3(kBlock), 0, stream, L.ut,
+                                       L.un, BM, slots + mth::kGapU, L.done);
+                // v step from the kept u
+                ca.kscale = ks;
+                ca.u = L.ut;
+                ca.v = L.vt;
+                {
+                    ProfScope prof("mth_sweeps", stream);
+                    hipLaunchKernelGGL((mth::col_partial<V, C>), strips, dim3(kBlock), col_lds, stream, ca);
+                    hipLaunchKernelGGL(mth::col_finish, cols, dim3(kBlock), 0, stream, ca);
+                }
+                if (method == DOT_SK_MOMENTUM) {
+                    hipLaunchKernelGGL(mth::momentum_candidate, vector_grid(BN), dim3(kBlock), 0, stream, L.v,
+                                       L.vt, L.vn, BN, m->omega, slots + mth::kGapV, L.done);
+                } else if (method == DOT_SK_ADAM) {
+                    const float c1 = m->bias_correction
+                                         ? 1.0f - std::pow(m->beta1, static_cast<float>(it + 1)) : 1.0f;
+                    const float c2 = m->bias_correction
+                                         ? 1.0f - std::pow(m->beta2, static_cast<float>(it + 1)) : 1.0f;
+                    hipLaunchKernelGGL(mth::adam_candidate, vector_grid(BN), dim3(kBlock), 0, stream, L.v, L.vt,
+                                       L.vn, L.m1v, L.m2v, BN, m->beta1, m->beta2, c1, c2, m->lr, m->eps_adam,
+                                       slots + mth::kGapV, L.done);
+                }
+                if (method != DOT_SK_VANILLA)
+                    hipLaunchKernelGGL(mth::accept_candidate, vector_grid(BN), dim3(kBlock), 0, stream, L.vt,
+                                       L.vn, BN, slots + mth::kGapV, L.done);
+                // stop test: vanilla on u alone (torch_cuda.cpp:230-238), the methods on u and v
+                // (:519-524)
+                hipLaunchKernelGGL(mth::commit, vector_grid(BM), dim3(kBlock), 0, stream, L.u, L.ut, BM,
+                                   track ? slots + mth::kDeltaU : nullptr, L.done);
+                hipLaunchKernelGGL(mth::commit, vector_grid(BN), dim3(kBlock), 0, stream, L.v, L.vt, BN,
+                                   track && method != DOT_SK_VANILLA ? slots + mth::kDeltaV : nullptr, L.done);
+            }
+            hipLaunchKernelGGL(mth::finish_iteration, dim3(1), dim3(1), 0, stream, slots, it, a->tol, L.done,
+                               a->iters_used, a->converged);
+            if (may_wait && (it + 1) % kStopCheckEvery == 0 && it + 1 < T) {
+                int h_done = 0;
+                if (hipMemcpyAsync(&h_done, L.done, sizeof(int), hipMemcpyDeviceToHost, stream) != hipSuccess ||
+                    hipStreamSynchronize(stream) != hipSuccess) {
+                    rc = check_launch("dot_sinkhorn_forward_method (stop-flag read)");
+                    if (rc == DOT_OK) rc = fail(DOT_ERR_HIP, "dot_sinkhorn_forward_method: stop-flag read failed");
+                    return;
+                }
+                if (h_done) break;
+            }
+        }
+
+        // plan and cost at the target tau (torch_cuda.cpp:538-552, :242-261)
+        if (a->plan || a->cost) {
+            mth::PlanArgs pa{};
+            pa.X = a->scores;
+            pa.kscale = kscale_at(tau);
+            pa.csign = -sign;  // C = -log_alpha
+            pa.M = M;
+            pa.N = N;
+            pa.rows = L.rows;
+            pa.return_log = ret_log ? 1 : 0;
+            pa.safe = method == DOT_SK_VANILLA ? 1 : 0;
+            pa.u = L.u;
+            pa.v = L.v;
+            pa.plan = a->plan;
+            pa.cost_partial = a->cost ? L.cost_partial : nullptr;
+            ProfScope prof("mth_plan", stream);
+            hipLaunchKernelGGL((mth::plan<V, C>), strips, dim3(kBlock), 0, stream, pa);
+            if (a->cost)
+                hipLaunchKernelGGL(batch_sum_m, dim3(B), dim3(kWave), 0, stream, L.cost_partial, L.nstrips,
+                                   a->cost);
+        }
+    });
+    if (rc != DOT_OK) return rc;
+    if (!launched) return fail(DOT_ERR_UNSUPPORTED, "row length outside the supported range");
+    if (a->u_out && hipMemcpyAsync(a->u_out, L.u, BM * sizeof(float), hipMemcpyDeviceToDevice, stream) != hipSuccess)
+        return check_launch("dot_sinkhorn_forward_method (u_out)");
+    if (a->v_out && hipMemcpyAsync(a->v_out, L.v, BN * sizeof(float), hipMemcpyDeviceToDevice, stream) != hipSuccess)
+        return check_launch("dot_sinkhorn_forward_method (v_out)");
+    return check_launch("dot_sinkhorn_forward_method");
+}

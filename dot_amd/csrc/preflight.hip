@@ -10,14 +10,6 @@
 namespace dot_amd {
 namespace {
 
-// Rows per strip: the largest power of two in [4, 64] that still gives >= 1024
-// workgroups, as for the Sinkhorn sweeps.
-int spf_rows(int B, int M) {
-    int r = 64;
-    while (r > 4 && int64_t(B) * ((M + r - 1) / r) < 1024) r /= 2;
-    return r;
-}
-
 struct SpfLayout {
     float *lse, *u, *upart, *v, *vpart;
     int rows, nstrips;
@@ -27,7 +19,7 @@ struct SpfLayout {
 SpfLayout spf_layout(void* ws, int B, int M, int N) {
     Carver c(ws);
     SpfLayout L{};
-    L.rows = spf_rows(B, M);
+    L.rows = sweep_strip_rows(B, M);
     L.nstrips = (M + L.rows - 1) / L.rows;
     L.lse = c.take<float>(size_t(B) * M);
     L.u = c.take<float>(size_t(B) * M);

@@ -17,18 +17,15 @@ namespace {
 
 using sk::kColSumFloor;
 
-// Rows per workgroup strip: the largest power of two in [4, 64] that still
-// yields >= 1024 workgroups (4 per CU on 256 CUs), so every sweep fills the
-// chip.  DOT_AMD_ROWS overrides it (tuning only).
+// Rows per workgroup strip (sweep_strip_rows); DOT_AMD_ROWS overrides it
+// (tuning only).
 int strip_rows(int B, int M) {
     static const int forced = [] {
         const char* s = std::getenv("DOT_AMD_ROWS");
         return s ? std::atoi(s) : 0;
     }();
     if (forced >= 1) return forced;
-    int r = 64;
-    while (r > 4 && int64_t(B) * ((M + r - 1) / r) < 1024) r /= 2;
-    return r;
+    return sweep_strip_rows(B, M);
 }
 
 size_t lds_bytes(int N) { return (size_t(2) * N + 8) * sizeof(float); }

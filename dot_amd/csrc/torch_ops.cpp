@@ -158,33 +158,91 @@ std::vector<Tensor> counts_to_cpu(const Tensor& counts) {
     return {at::scalar_tensor(int64_t(p[0]), opt), at::scalar_tensor(int64_t(p[1]), opt)};
 }
 
-// sinkhorn_dual_forward (torch_cuda.cpp:266-321): returns [P or log P,
-// used (CPU int64 0-d), converged (CPU int64 0-d)].
+struct MethodParams {
+    int64_t method = 0;
+    double omega = 1.5;
+    int64_t anderson_k = 5;
+    double mixing_beta = 1.0, lr = 1.0, beta1 = 0.9, beta2 = 0.999, eps_adam = 1e-8;
+    bool bias_correction = true;
+    double reg_start = -1.0;
+    int64_t schedule = 0;
+};
+
+// One call of dot_sinkhorn_forward_method (momentum / Anderson / Adam and the
+// regularisation schedules); counts as for run_forward.
+ForwardOut run_forward_method(const Tensor& scores_f, int kind, double tau, int64_t n_iters, double tol,
+                              const optional<Tensor>& log_a_f, const optional<Tensor>& log_b_f,
+                              bool return_log, bool want_cost, const MethodParams& mp) {
+    const int64_t B = scores_f.size(0), M = scores_f.size(1), N = scores_f.size(2);
+    TORCH_CHECK(n_iters <= INT32_MAX, "n_iters too large");
+    TORCH_CHECK(mp.anderson_k <= INT32_MAX, "anderson_k too large");
+    auto opts = scores_f.options().dtype(at::kFloat);
+    ForwardOut o;
+    o.plan = at::empty({B, M, N}, opts);
+    if (want_cost) o.cost = at::empty({B}, opts);
+    o.counts = at::empty({2}, scores_f.options().dtype(at::kInt));
+    const int k = int(std::min<int64_t>(mp.anderson_k, DOT_SK_MAX_ANDERSON));
+    const size_t ws_bytes = dot_sinkhorn_forward_method_workspace_bytes(int(B), int(M), int(N), int(n_iters),
+                                                                        int(mp.method), k);
+    Tensor ws = workspace(ws_bytes, scores_f);
+    dot_sinkhorn_method_args m{};
+    dot_sinkhorn_fwd_args& a = m.base;
+    a.scores = scores_f.data_ptr<float>();
+    a.log_a = ptr_or_null(log_a_f);
+    a.log_b = ptr_or_null(log_b_f);
+    a.B = int(B);
+    a.M = int(M);
+    a.N = int(N);
+    a.scores_kind = kind;
+    a.tau = static_cast<float>(tau);
+    a.max_iter = int(n_iters);
+    a.tol = static_cast<float>(tol);
+    a.flags = return_log ? DOT_SK_RETURN_LOG : 0;
+    a.plan = o.plan.data_ptr<float>();
+    a.cost = want_cost ? o.cost.data_ptr<float>() : nullptr;
+    a.iters_used = o.counts.data_ptr<int32_t>();
+    a.converged = o.counts.data_ptr<int32_t>() + 1;
+    a.workspace = ws.data_ptr();
+    a.workspace_bytes = ws_bytes;
+    m.method = int(mp.method);
+    m.omega = static_cast<float>(mp.omega);
+    m.anderson_k = int(std::min<int64_t>(mp.anderson_k, INT32_MAX));
+    m.mixing_beta = static_cast<float>(mp.mixing_beta);
+    m.lr = static_cast<float>(mp.lr);
+    m.beta1 = static_cast<float>(mp.beta1);
+    m.beta2 = static_cast<float>(mp.beta2);
+    m.eps_adam = static_cast<float>(mp.eps_adam);
+    m.bias_correction = mp.bias_correction ? 1 : 0;
+    m.reg_start = static_cast<float>(mp.reg_start);
+    m.schedule = int(mp.schedule);
+    check_rc(dot_sinkhorn_forward_method(&m, current_stream(scores_f)), "dot_sinkhorn_forward_method");
+    return o;
+}
+
+// sinkhorn_dual_forward (torch_cuda.cpp:266-557): returns [P or log P,
+// used (CPU int64 0-d), converged (CPU int64 0-d)].  method 0 without a
+// schedule is dot_sinkhorn_forward; the methods and schedules are
+// dot_sinkhorn_forward_method.
 std::vector<Tensor> sinkhorn_dual_forward_op(Tensor log_alpha, double tau, int64_t n_iters, double tol,
                                              optional<Tensor> log_a, optional<Tensor> log_b,
                                              bool return_log, int64_t method, double omega,
                                              int64_t anderson_k, double mixing_beta, double lr,
                                              double beta1, double beta2, double eps_adam,
                                              bool bias_correction, double reg_start, int64_t schedule) {
-    (void)omega;
-    (void)mixing_beta;
-    (void)lr;
-    (void)beta1;
-    (void)beta2;
-    (void)eps_adam;
-    (void)bias_correction;
-    (void)reg_start;
     check_common(log_alpha, tau, n_iters);
     TORCH_CHECK(anderson_k >= 1, "anderson_k must be >= 1");
-    TORCH_CHECK(method == 0,
-                "sinkhorn_dual_forward: method ", method,
-                " (momentum/anderson/adam) is not implemented by dot_amd; only method=0 (vanilla)");
-    TORCH_CHECK(schedule == 0,
-                "sinkhorn_dual_forward: regularisation schedules are not implemented by dot_amd");
     check_marginals(log_a, log_b, log_alpha.size(0), log_alpha.size(1), log_alpha.size(2));
     c10::OptionalDeviceGuard guard(log_alpha.device());
-    ForwardOut o = run_forward(f32c(log_alpha), DOT_SCORES_LOG_ALPHA, tau, n_iters, tol,
-                               f32c_opt(log_a), f32c_opt(log_b), return_log, true, false, false);
+    ForwardOut o;
+    if (method == 0 && schedule == 0) {
+        o = run_forward(f32c(log_alpha), DOT_SCORES_LOG_ALPHA, tau, n_iters, tol, f32c_opt(log_a),
+                        f32c_opt(log_b), return_log, true, false, false);
+    } else {
+        MethodParams mp{method, omega, anderson_k, mixing_beta, lr, beta1, beta2, eps_adam,
+                        bias_correction, reg_start, schedule};
+        o = run_forward_method(f32c(log_alpha), DOT_SCORES_LOG_ALPHA, tau, n_iters, tol, f32c_opt(log_a),
+                               f32c_opt(log_b), return_log, false, mp);
+    }
     std::vector<Tensor> c = counts_to_cpu(o.counts);
     return {o.plan, c[0], c[1]};
 }
@@ -396,6 +454,27 @@ std::vector<Tensor> fused_forward_op(Tensor scores, int64_t scores_kind, double 
     return {o.plan, or_empty(o.cost), o.counts, or_empty(o.u_hist), or_empty(o.v_hist)};
 }
 
+// -> [plan, cost (B,) or empty, counts int32 [2]]
+std::vector<Tensor> fused_forward_method_op(Tensor scores, int64_t scores_kind, double tau, int64_t n_iters,
+                                            double tol, optional<Tensor> log_a, optional<Tensor> log_b,
+                                            int64_t method, double omega, int64_t anderson_k,
+                                            double mixing_beta, double lr, double beta1, double beta2,
+                                            double eps_adam, bool bias_correction, double reg_start,
+                                            int64_t schedule, bool want_cost) {
+    check_common(scores, tau, n_iters);
+    TORCH_CHECK(scores_kind == DOT_SCORES_LOG_ALPHA || scores_kind == DOT_SCORES_COST,
+                "scores_kind must be 1 (log_alpha) or -1 (cost)");
+    TORCH_CHECK(anderson_k >= 1, "anderson_k must be >= 1");
+    check_marginals(log_a, log_b, scores.size(0), scores.size(1), scores.size(2));
+    c10::OptionalDeviceGuard guard(scores.device());
+    MethodParams mp{method, omega, anderson_k, mixing_beta, lr, beta1, beta2, eps_adam,
+                    bias_correction, reg_start, schedule};
+    ForwardOut o = run_forward_method(f32c(scores), int(scores_kind), tau, n_iters, tol, f32c_opt(log_a),
+                                      f32c_opt(log_b), false, want_cost, mp);
+    Tensor cost = o.cost.defined() ? o.cost : at::empty({0}, scores.options().dtype(at::kFloat));
+    return {o.plan, cost, o.counts};
+}
+
 // -> [grad_scores, grad_tau (B,)]; mode 0 implicit (iters = adjoint sweeps), 1 unrolled (iters = T).
 std::vector<Tensor> fused_backward_op(Tensor scores, int64_t scores_kind, Tensor plan,
                                       optional<Tensor> grad_plan, optional<Tensor> grad_cost,
@@ -494,6 +573,7 @@ TORCH_LIBRARY_IMPL(dot, CUDA, m) {
 
 TORCH_LIBRARY(dot_amd, m) {
     m.def("sinkhorn_forward(Tensor scores, int scores_kind, float tau, int n_iters, float tol, Tensor? log_a, Tensor? log_b, bool want_cost, bool keep_history) -> Tensor[]");
+    m.def("sinkhorn_forward_method(Tensor scores, int scores_kind, float tau, int n_iters, float tol, Tensor? log_a, Tensor? log_b, int method, float omega, int anderson_k, float mixing_beta, float lr, float beta1, float beta2, float eps_adam, bool bias_correction, float reg_start, int schedule, bool want_cost) -> Tensor[]");
     m.def("sinkhorn_backward(Tensor scores, int scores_kind, Tensor plan, Tensor? grad_plan, Tensor? grad_cost, float tau, int mode, int iters, Tensor? u_hist, Tensor? v_hist) -> Tensor[]");
     m.def("bidirectional_softmax_forward(Tensor sim, float tau, Tensor lengths) -> Tensor[]");
     m.def("bidirectional_softmax_backward(Tensor sim, Tensor grad_output, Tensor row_stats, Tensor col_stats, float tau, Tensor lengths) -> Tensor[]");
@@ -501,6 +581,7 @@ TORCH_LIBRARY(dot_amd, m) {
 
 TORCH_LIBRARY_IMPL(dot_amd, CUDA, m) {
     m.impl("sinkhorn_forward", fused_forward_op);
+    m.impl("sinkhorn_forward_method", fused_forward_method_op);
     m.impl("sinkhorn_backward", fused_backward_op);
     m.impl("bidirectional_softmax_forward", bidi_forward_op);
     m.impl("bidirectional_softmax_backward", bidi_backward_op);

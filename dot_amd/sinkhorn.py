@@ -18,11 +18,17 @@ On HIP tensors the forward and backward run as fused dot_amd operators:
   unrolled reverse pass over the ``n_iters_used`` recorded potentials, with the
   cost's direct gradient ``grad_cost * P`` folded in.
 
+On HIP tensors with ``dual=True`` and the implicit backward, the momentum,
+Anderson and Adam solvers and the linear / exponential / cosine
+regularisation schedules run as the ``dot_sinkhorn_forward_method`` operator,
+as on the reference's CUDA path (sinkhorn.py:1393-1530); their backward is the
+reference's: the implicit adjoint of the vanilla plan recomputed at
+``n_iters_used`` iterations.
+
 On CPU tensors the reference's CPU path is followed through the
-``torch.ops.dot`` CPU operators.  The alternative solvers (momentum, Anderson,
-Adam, Newton, Muon) and regularisation schedules are not implemented; asking
-for one raises ``NotImplementedError`` unless the reference itself would fall
-back to the vanilla solver (sinkhorn.py:1378-1390).
+``torch.ops.dot`` CPU operators.  The reference's pure-PyTorch solvers (its
+CPU and ``dual=False`` paths for momentum, Anderson, Adam, Newton, Muon and the
+schedules) are not implemented: asking for one raises ``NotImplementedError``.
 """
 
 from __future__ import annotations
@@ -153,6 +159,85 @@ def _run_fused(scores, reg, scores_kind, n_iters, backward_iters, log_a, log_b, 
     return P, cost, used, bool(conv)
 
 
+_METHOD_CODES = {"vanilla": 0, "momentum": 1, "anderson": 2, "adam": 3}
+_SCHEDULE_CODES = {None: 0, "linear": 1, "exponential": 2, "cosine": 3}
+
+
+class _SinkhornMethodFunction(torch.autograd.Function):
+    """Momentum / Anderson / Adam / scheduled dual Sinkhorn on HIP tensors.
+
+    The reference's _SinkhornCudaDualImplicitFunction (sinkhorn.py:155-240)
+    with the transport cost sum(P * C) of sinkhorn.py:1702 fused into the
+    forward.  Outputs ``(P, cost, counts)`` like _SinkhornFusedFunction.
+    Backward, as the reference's: the implicit adjoint (``backward_iters``
+    sweeps) of the vanilla plan recomputed at ``n_iters_used`` iterations
+    (its sinkhorn_with_grads_implicit), with the cost's upstream gradient
+    folded into the plan's, G = grad_P + grad_cost * C, and the cost's direct
+    term grad_cost * P taken from this forward's plan.
+    """
+
+    @staticmethod
+    def forward(ctx, scores, tau, scores_kind, n_iters, backward_iters, log_a, log_b, tol, params,
+                want_cost):
+        _check_tau_tensor(tau)
+        tau_value = _tau_value(tau)
+        P, cost, counts = _ops.fused.sinkhorn_forward_method(
+            scores, scores_kind, tau_value, n_iters, tol, log_a, log_b, *params, want_cost)
+        ctx.mark_non_differentiable(counts)
+        if not want_cost:
+            ctx.mark_non_differentiable(cost)
+        ctx.set_materialize_grads(False)
+        ctx.save_for_backward(scores, P, counts,
+                              log_a if log_a is not None else torch.Tensor(),
+                              log_b if log_b is not None else torch.Tensor())
+        ctx.has_log_a, ctx.has_log_b = log_a is not None, log_b is not None
+        ctx.tau = tau_value
+        ctx.tau_is_tensor = torch.is_tensor(tau)
+        ctx.scores_kind = scores_kind
+        ctx.backward_iters = backward_iters
+        ctx.scores_dtype = scores.dtype
+        return P, cost, counts
+
+    @staticmethod
+    def backward(ctx, grad_P, grad_cost, _grad_counts):
+        scores, P, counts, log_a, log_b = ctx.saved_tensors
+        log_a = log_a if ctx.has_log_a else None
+        log_b = log_b if ctx.has_log_b else None
+        none = (None,) * 9
+        if grad_cost is not None and grad_cost.numel() == 0:
+            grad_cost = None
+        if grad_P is None and grad_cost is None:
+            return (torch.zeros_like(scores),) + none
+        used = int(counts[0].item())
+        P_vanilla = _ops.fused.sinkhorn_forward(scores, ctx.scores_kind, ctx.tau, used, 0.0, log_a, log_b,
+                                                False, False)[0]
+        grad_scores, grad_tau = _ops.fused.sinkhorn_backward(
+            scores, ctx.scores_kind, P_vanilla,
+            grad_P.contiguous() if grad_P is not None else None,
+            grad_cost.contiguous() if grad_cost is not None else None,
+            ctx.tau, _MODE_IMPLICIT, ctx.backward_iters, None, None)
+        if grad_cost is not None:
+            # the fused backward's direct cost term used P_vanilla; the cost was
+            # computed from this forward's plan (d sum(P C)/dC = P, C = -log_alpha)
+            grad_scores = grad_scores.add_(grad_cost.view(-1, 1, 1) * (P - P_vanilla),
+                                           alpha=float(-ctx.scores_kind))
+        tau_grad = None
+        if ctx.tau_is_tensor and ctx.needs_input_grad[1]:
+            tau_grad = grad_tau.sum()
+        return (grad_scores.to(ctx.scores_dtype), tau_grad) + none[1:]
+
+
+def _run_method(scores, reg, scores_kind, n_iters, backward_iters, log_a, log_b, tol, params, want_cost):
+    tau_arg = reg
+    if torch.is_tensor(reg):
+        tau_arg = reg.reshape(()).to(device=scores.device)
+    P, cost, counts = _SinkhornMethodFunction.apply(
+        scores, tau_arg, scores_kind, int(n_iters), int(backward_iters), log_a, log_b, float(tol), params,
+        want_cost)
+    used, conv = (int(x) for x in counts.tolist())
+    return P, cost, used, bool(conv)
+
+
 # ---------------------------------------------------------------------------
 # CPU: the reference's autograd functions over the CPU operators
 # ---------------------------------------------------------------------------
@@ -243,6 +328,7 @@ def _effective_method(method, schedule, reg_start, omega, tau_value, lr, beta1, 
         method = "newton" if size[0] <= 100 and size[1] <= 100 else "vanilla"
     effective = method
     eff_schedule = schedule
+    eff_reg_start = reg_start
     if dual and on_gpu and backward_mode == "implicit":
         if effective == "momentum" and omega is None:
             effective = "vanilla"
@@ -251,12 +337,14 @@ def _effective_method(method, schedule, reg_start, omega, tau_value, lr, beta1, 
                 effective = "vanilla"
             elif tau_value <= 0.01:
                 eff_schedule = "exponential"
+                if eff_reg_start is None:
+                    eff_reg_start = 10.0 * tau_value
         elif effective == "adam" and eff_schedule is None:
             is_default_adam = (lr == 1.0 and beta1 == 0.9 and beta2 == 0.999 and eps_adam == 1e-8
                                and bias_correction)
             if tau_value >= 0.05 or is_default_adam:
                 effective = "vanilla"
-    return method, effective, eff_schedule
+    return method, effective, eff_schedule, eff_reg_start
 
 
 _METHODS = ("vanilla", "momentum", "anderson", "adam", "newton", "muon", "auto")
@@ -294,8 +382,12 @@ def sinkhorn(
         backward_mode: 'implicit' (adjoint, default) or 'unrolled'
         backward_iters: Adjoint sweeps of the implicit backward (default: n_iters)
         a, b: Optional source/target marginals, shape (B, n)/(n,) and (B, m)/(m,)
-        method: Solver; only 'vanilla' (and the cases the reference maps to it)
-            is implemented
+        method: Solver: 'vanilla', or on HIP tensors with dual=True and the
+            implicit backward 'momentum' (omega), 'anderson' (anderson_k,
+            mixing_beta) or 'adam' (lr, beta1, beta2, eps_adam,
+            bias_correction); 'auto' picks 'newton' up to 100x100
+        schedule: 'linear', 'exponential' or 'cosine' annealing of reg from
+            reg_start (default 10 * reg) over the iterations (HIP dual path)
         tol: Stop after the first iteration with max|u_t - u_{t-1}| < tol over
             the whole batch (HIP tensors); 0 forces all iterations
         dual: Prefer the dual-state device path (HIP tensors)
@@ -333,17 +425,35 @@ def sinkhorn(
         backward_iters = n_iters
 
     on_gpu = cost_matrix.is_cuda
-    method, effective, eff_schedule = _effective_method(
+    method, effective, eff_schedule, eff_reg_start = _effective_method(
         method, schedule, reg_start, omega, tau_value, lr, beta1, beta2, eps_adam, bias_correction,
         backward_mode, on_gpu, dual, (cost_matrix.size(-2), cost_matrix.size(-1)))
-    if effective != "vanilla":
+    plain = effective == "vanilla" and eff_schedule is None
+    # the reference's use_cuda_dual (sinkhorn.py:1393-1400)
+    cuda_dual = on_gpu and dual and (
+        (backward_mode == "implicit" and effective in _METHOD_CODES)
+        or (backward_mode == "unrolled" and plain))
+    if not cuda_dual and not plain:
+        # the reference's PyTorch solver branches (sinkhorn.py:1531-1693)
+        if method != "vanilla" and backward_mode != "implicit":
+            raise ValueError(f"method='{method}' only supports implicit backward")
+        if method == "vanilla" and backward_mode == "unrolled" and schedule is not None:
+            raise ValueError("schedule is only supported with implicit backward")
         raise NotImplementedError(
-            f"method={effective!r} is not implemented by dot_amd; use method='vanilla'")
-    if eff_schedule is not None:
-        raise NotImplementedError("regularisation schedules are not implemented by dot_amd")
+            f"method={effective!r} (schedule={eff_schedule!r}) outside the HIP dual path (CUDA/HIP tensors, "
+            "dual=True, backward_mode='implicit') is not implemented by dot_amd")
 
     mode = _MODE_UNROLLED if backward_mode == "unrolled" else _MODE_IMPLICIT
-    if on_gpu:
+    if cuda_dual and not plain:
+        params = (_METHOD_CODES[effective], float(omega) if omega is not None else 1.4, int(anderson_k),
+                  float(mixing_beta), float(lr), float(beta1), float(beta2), float(eps_adam),
+                  bool(bias_correction), -1.0 if eff_reg_start is None else float(eff_reg_start),
+                  _SCHEDULE_CODES[eff_schedule])
+        P, cost, used, conv = _run_method(cost_matrix, reg, SCORES_COST, n_iters, backward_iters, log_a, log_b,
+                                          tol, params, True)
+        converged = conv if tol > 0 else True
+        cost = cost.to(torch.result_type(P, cost_matrix))
+    elif on_gpu:
         # dual=False is the reference's full-matrix path: it ignores tol and
         # always runs n_iters (sinkhorn.py:1693 with torch_cuda.cpp:599-656).
         run_tol = tol if dual else 0.0

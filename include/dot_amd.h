@@ -84,6 +84,53 @@ typedef struct {
 size_t dot_sinkhorn_forward_workspace_bytes(int B, int M, int N, int max_iter, int flags);
 int dot_sinkhorn_forward(const dot_sinkhorn_fwd_args* args, dot_stream_t stream);
 
+/* Solver of dot_sinkhorn_method_args.method (the reference's method codes). */
+#define DOT_SK_VANILLA 0
+#define DOT_SK_MOMENTUM 1
+#define DOT_SK_ANDERSON 2
+#define DOT_SK_ADAM 3
+/* Regularisation schedule of dot_sinkhorn_method_args.schedule. */
+#define DOT_SK_SCHEDULE_NONE 0
+#define DOT_SK_SCHEDULE_LINEAR 1
+#define DOT_SK_SCHEDULE_EXPONENTIAL 2
+#define DOT_SK_SCHEDULE_COSINE 3
+#define DOT_SK_MAX_ANDERSON 16  /* longest Anderson history this build supports */
+
+typedef struct {
+    dot_sinkhorn_fwd_args base;  /* as for dot_sinkhorn_forward; DOT_SK_KEEP_HISTORY is not
+                                    accepted (u_hist, v_hist unused) */
+    int method;                  /* DOT_SK_VANILLA .. DOT_SK_ADAM */
+    float omega;                 /* momentum over-relaxation */
+    int anderson_k;              /* Anderson history, 1 .. DOT_SK_MAX_ANDERSON */
+    float mixing_beta;           /* Anderson mixing */
+    float lr, beta1, beta2, eps_adam;
+    int bias_correction;         /* Adam: nonzero divides the moments by 1 - beta^t */
+    float reg_start;             /* schedule start; <= 0 means 10 * tau */
+    int schedule;                /* DOT_SK_SCHEDULE_* */
+} dot_sinkhorn_method_args;
+
+/* Accelerated and scheduled dual Sinkhorn: the reference's momentum (relaxed
+ * u and v steps kept when the batch-wide max distance to the plain update
+ * shrinks), Adam (moment-scaled steps, same acceptance test) and Anderson
+ * (mixing of the last anderson_k (state, residual) pairs of x = (u, v), per
+ * batch element) iterations, and the vanilla iteration under a linear,
+ * exponential or cosine schedule of tau from reg_start to tau.  Every
+ * acceptance and stopping decision is taken on the device.  With tol > 0 the
+ * call waits on `stream` every 16 iterations to stop launching once the test
+ * has fired (not while the stream is being captured).  The plan is
+ * exp(K + u + v) at the target tau (the vanilla method: safe_exp).
+ * Replaces sinkhorn_dual_forward_cuda_impl's method and schedule branches
+ * (src/sinkhorn/torch_cuda.cpp:266-557: sinkhorn_dual_vanilla_cuda with a
+ * schedule, :147-264; the method loop, :323-536; scheduled_tau_cuda, :61-84;
+ * dual_fixed_point_map_cuda, :98-145) behind sinkhorn_dual_forward
+ * (registry.cpp:31-36).  The reference's Anderson map hands a strided view of
+ * v to a kernel that indexes it densely (torch_cuda.cpp:116-117 with
+ * kernels.cu:518), so for B > 1 its iterates mix batch elements; this entry
+ * point runs the per-element map (the two agree at B = 1). */
+size_t dot_sinkhorn_forward_method_workspace_bytes(int B, int M, int N, int max_iter, int method,
+                                                   int anderson_k);
+int dot_sinkhorn_forward_method(const dot_sinkhorn_method_args* args, dot_stream_t stream);
+
 /* ---------------------------------------------------------------------- */
 /* Sinkhorn backward                                                       */
 /* ---------------------------------------------------------------------- */

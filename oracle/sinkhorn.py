@@ -322,9 +322,18 @@ def dual_forward_method(log_alpha, tau: float, n_iters: int, tol: float = 0.0, l
 
     Stop test (tol > 0): methods 1 and 3 use max over u and v of the change;
     Anderson max|x_new - x|; vanilla max|u - u_prev|.  The plan is
-    exp(K + u + v) with K at the target tau.  Returns ForwardResult.
+    exp(K + u + v) with K at the target tau (safe_exp for the vanilla loop).
+    Anderson's map is per batch element: the reference's CUDA map reads v
+    through a strided view as if dense (torch_cuda.cpp:116-117 with
+    kernels.cu:518), which mixes batch elements when B > 1; the two agree at
+    B = 1.  Returns ForwardResult.
     """
     f32 = np.float32
+    # the reference passes every hyperparameter as float (static_cast<float>,
+    # torch_cuda.cpp:470-530): 1 - beta2 for beta2 = 0.999 differs from its
+    # double by 1.3e-5 relative, which the moments carry into every step
+    omega, mixing_beta, lr, beta1, beta2, eps_adam = (
+        float(f32(x)) for x in (omega, mixing_beta, lr, beta1, beta2, eps_adam))
     la = np.asarray(log_alpha, dtype=np.float32)
     B, n, m = la.shape
     lga = default_log_marginal(B, n, dtype) if log_a is None else np.asarray(log_a, np.float32).astype(dtype)
@@ -364,9 +373,9 @@ def dual_forward_method(log_alpha, tau: float, n_iters: int, tol: float = 0.0, l
                 X = np.stack(hist_x, axis=2)
                 F = np.stack(hist_f, axis=2)
                 h = X.shape[2]
-                gram = np.einsum("blp,blq->bpq", F, F) + 1e-8 * np.eye(h)[None]
+                gram = np.einsum("blp,blq->bpq", F, F) + np.asarray(1e-8, dtype) * np.eye(h, dtype=dtype)[None]
                 try:
-                    alpha = np.linalg.solve(gram, np.ones((B, h, 1)))[..., 0]
+                    alpha = np.linalg.solve(gram, np.ones((B, h, 1), dtype))[..., 0]
                     denom = alpha.sum(1, keepdims=True)
                     if np.abs(denom).min() >= 1e-12:
                         alpha = alpha / denom
@@ -385,13 +394,13 @@ def dual_forward_method(log_alpha, tau: float, n_iters: int, tol: float = 0.0, l
         u_prev = u
         ut = row(K, v)
         if method == METHOD_MOMENTUM:
-            un = (1.0 - omega) * u + omega * ut
+            un = float(f32(1.0) - f32(omega)) * u + omega * ut
             if gmax(un - ut) < gmax(u - ut):
                 ut = un
         elif method == METHOD_ADAM:
             g = ut - u
-            mu_u = beta1 * mu_u + (1.0 - beta1) * g
-            vu_u = beta2 * vu_u + (1.0 - beta2) * g * g
+            mu_u = beta1 * mu_u + float(f32(1.0) - f32(beta1)) * g
+            vu_u = beta2 * vu_u + float(f32(1.0) - f32(beta2)) * g * g
             c1 = float(f32(1.0) - np.power(f32(beta1), f32(it + 1))) if bias_correction else 1.0
             c2 = float(f32(1.0) - np.power(f32(beta2), f32(it + 1))) if bias_correction else 1.0
             un = u + lr * (mu_u / c1) / (np.sqrt(vu_u / c2) + eps_adam)
@@ -399,13 +408,13 @@ def dual_forward_method(log_alpha, tau: float, n_iters: int, tol: float = 0.0, l
                 ut = un
         vt = col(K, ut)
         if method == METHOD_MOMENTUM:
-            vn = (1.0 - omega) * v + omega * vt
+            vn = float(f32(1.0) - f32(omega)) * v + omega * vt
             if gmax(vn - vt) < gmax(v - vt):
                 vt = vn
         elif method == METHOD_ADAM:
             g = vt - v
-            mu_v = beta1 * mu_v + (1.0 - beta1) * g
-            vu_v = beta2 * vu_v + (1.0 - beta2) * g * g
+            mu_v = beta1 * mu_v + float(f32(1.0) - f32(beta1)) * g
+            vu_v = beta2 * vu_v + float(f32(1.0) - f32(beta2)) * g * g
             c1 = float(f32(1.0) - np.power(f32(beta1), f32(it + 1))) if bias_correction else 1.0
             c2 = float(f32(1.0) - np.power(f32(beta2), f32(it + 1))) if bias_correction else 1.0
             vn = v + lr * (mu_v / c1) / (np.sqrt(vu_v / c2) + eps_adam)
@@ -425,6 +434,8 @@ def dual_forward_method(log_alpha, tau: float, n_iters: int, tol: float = 0.0, l
     if schedule != SCHEDULE_NONE:
         K = kernel_at(tau)
     logP = K + u[:, :, None] + v[:, None, :]
-    with np.errstate(over="ignore"):
-        P = logP if return_log else np.exp(logP)
+    # the vanilla loop materialises with safe_exp (kernels.cu:755-772), the
+    # methods with torch's exp (torch_cuda.cpp:550-551)
+    with np.errstate(over="ignore", under="ignore"):
+        P = logP if return_log else (safe_exp(logP) if method == METHOD_VANILLA else np.exp(logP))
     return ForwardResult(P=P, n_iters_used=used, converged=converged, u=u, v=v, K=K)

@@ -91,5 +91,10 @@ def test_validation_errors_before_any_kernel():
         dot.sinkhorn(C, method="momentum", omega=1.5)
     with pytest.raises(NotImplementedError, match="schedule"):
         dot.sinkhorn(C, schedule="linear")
+    # the reference's solver branches reject the unrolled backward (sinkhorn.py:1533-1690)
+    with pytest.raises(ValueError, match="only supports implicit backward"):
+        dot.sinkhorn(C, method="anderson", backward_mode="unrolled")
+    with pytest.raises(ValueError, match="schedule is only supported with implicit backward"):
+        dot.sinkhorn(C, schedule="cosine", backward_mode="unrolled")
     with pytest.raises(ValueError, match="spectral_preflight requires tol > 0"):
         dot.spectral_preflight(-C, 0.1, tol=0)

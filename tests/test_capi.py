@@ -100,3 +100,47 @@ def test_forward_rejects_bad_arguments_on_the_host(lib):
 def test_version_string(lib):
     lib.dot_version.restype = ctypes.c_char_p
     assert lib.dot_version().decode().startswith("dot_amd")
+
+
+class MethodArgs(ctypes.Structure):
+    _fields_ = [("base", FwdArgs), ("method", ctypes.c_int), ("omega", ctypes.c_float),
+                ("anderson_k", ctypes.c_int), ("mixing_beta", ctypes.c_float), ("lr", ctypes.c_float),
+                ("beta1", ctypes.c_float), ("beta2", ctypes.c_float), ("eps_adam", ctypes.c_float),
+                ("bias_correction", ctypes.c_int), ("reg_start", ctypes.c_float), ("schedule", ctypes.c_int)]
+
+
+def test_method_forward_rejects_bad_arguments_on_the_host(lib):
+    f = lib.dot_sinkhorn_forward_method
+    f.argtypes = [ctypes.POINTER(MethodArgs), ctypes.c_void_p]
+    q = lib.dot_sinkhorn_forward_method_workspace_bytes
+    q.restype = ctypes.c_size_t
+    # Anderson keeps anderson_k (state, residual) pairs: the query grows with it
+    assert q(2, 64, 64, 50, 2, 8) > q(2, 64, 64, 50, 2, 2) > q(2, 64, 64, 50, 0, 2) > 0
+    assert q(2, 64, 64, 50, 3, 5) > q(2, 64, 64, 50, 1, 5)  # Adam's moments
+    assert q(-1, 64, 64, 50, 0, 5) == 0
+    assert f(None, None) == DOT_ERR_INVALID_ARG
+    dummy = ctypes.c_int(0)
+    m = MethodArgs(base=FwdArgs(B=2, M=8, N=8, scores_kind=1, tau=1.0, max_iter=10),
+                   method=1, omega=1.5, anderson_k=5, schedule=0)
+    m.base.iters_used = m.base.converged = ctypes.addressof(dummy)
+    for field, value, code, text in (("method", 4, DOT_ERR_INVALID_ARG, "method"),
+                                     ("schedule", 9, DOT_ERR_INVALID_ARG, "schedule"),
+                                     ("anderson_k", 0, DOT_ERR_INVALID_ARG, "anderson_k")):
+        good = getattr(m, field)
+        setattr(m, field, value)
+        assert f(ctypes.byref(m), None) == code
+        assert text in _last_error(lib)
+        setattr(m, field, good)
+    m.method, m.anderson_k = 2, 17
+    assert f(ctypes.byref(m), None) == DOT_ERR_UNSUPPORTED
+    assert "anderson_k" in _last_error(lib)
+    m.anderson_k = 5
+    m.base.flags = 0x2  # history is not kept by the accelerated solvers
+    assert f(ctypes.byref(m), None) == DOT_ERR_INVALID_ARG
+    m.base.flags = 0
+    m.base.tau = -1.0
+    assert f(ctypes.byref(m), None) == DOT_ERR_INVALID_ARG
+    m.base.tau = 1.0
+    m.base.scores = ctypes.addressof(dummy)
+    m.base.workspace, m.base.workspace_bytes = ctypes.addressof(dummy), 4
+    assert f(ctypes.byref(m), None) == DOT_ERR_WORKSPACE

@@ -181,8 +181,8 @@ def test_op_argument_errors():
         _ops.sinkhorn(x, 1.0, 5, torch.zeros(2, 5, device=DEV))
     with pytest.raises(RuntimeError, match="grad_P must match"):
         _ops.sinkhorn_with_grads_implicit(x, torch.zeros(2, 4, 5, device=DEV), 1.0, 5, 5)
-    with pytest.raises(RuntimeError, match="not implemented"):
-        _ops.sinkhorn_dual_forward(x, 1.0, 5, 0.0, None, None, False, 2)
+    with pytest.raises(RuntimeError, match="anderson_k"):
+        _ops.sinkhorn_dual_forward(x, 1.0, 5, 0.0, None, None, False, 2, 1.5, 0)
     with pytest.raises(RuntimeError, match="4096"):
         _ops.sinkhorn(torch.rand(1, 2, 4097, device=DEV), 1.0, 1)
 
@@ -303,7 +303,9 @@ def test_api_errors():
     with pytest.raises(ValueError, match="n_iters must be an int"):
         dot_amd.sinkhorn(C, n_iters="many")
     with pytest.raises(NotImplementedError):
-        dot_amd.sinkhorn(C, reg=0.02, method="adam", lr=0.5)
+        dot_amd.sinkhorn(C, reg=0.02, method="newton")
+    with pytest.raises(NotImplementedError):
+        dot_amd.sinkhorn(C, reg=0.02, method="adam", lr=0.5, dual=False)
     with pytest.raises(ValueError):
         dot_amd.sinkhorn(C, backward_mode="sideways")
 
