@@ -2,6 +2,7 @@
 """Benchmark of the dot_amd hot path on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c3|c1|c4|c5]
+                    [--method vanilla|momentum|anderson|adam] [--schedule linear|exponential|cosine]
 
 One "step" is one pass of the hot path over one batch of synthetic input, as
 the reference's users run it: ``result = dot.sinkhorn(C, reg, n_iters)``
@@ -24,6 +25,13 @@ and T_b = adjoint sweeps executed.  The same line carries
   one host core, or the numpy oracle when oracle/_ref is absent;
 * ``bidirectional_softmax`` — config C2 (B=32, 1024x1024, fwd+bwd) in GB/s of
   algorithmic traffic (20 bytes per element), with its own roofline.
+
+``--method`` / ``--schedule`` (with ``--omega``, ``--lr``, ``--anderson-k``,
+``--reg-start``) time the accelerated solvers instead, on the same workload and
+through the same public call; the line's ``config`` names the method the
+reference's resolution rules select (sinkhorn.py:1362-1390).  Their backward
+recomputes the plain forward at ``n_iters_used`` iterations, as the
+reference's does; ``value`` still counts E * (T_f + T_b).
 """
 
 from __future__ import annotations
@@ -196,17 +204,25 @@ def bench_sinkhorn(args, torch, dot_amd, profiler):
     E = B * M * N
     reg, n_iters, tol = cfg["reg"], cfg["n_iters"], cfg["tol"]
 
+    solver = dict(method=args.method, schedule=args.schedule, omega=args.omega, lr=args.lr,
+                  anderson_k=args.anderson_k, reg_start=args.reg_start)
+
     def step():
         leaf = C.detach().requires_grad_(True)
-        res = dot_amd.sinkhorn(leaf, reg=reg, n_iters=n_iters, tol=tol, a=a, b=b)
+        res = dot_amd.sinkhorn(leaf, reg=reg, n_iters=n_iters, tol=tol, a=a, b=b, **solver)
         res.cost.sum().backward()
         return res.n_iters_used
+
+    from dot_amd.sinkhorn import _effective_method
+    _, effective, eff_schedule, _ = _effective_method(
+        args.method, args.schedule, args.reg_start, args.omega, reg, args.lr, 0.9, 0.999, 1e-8, True,
+        "implicit", True, True, (M, N))
 
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
     sweeps = ["sk_fwd_sweep", "sk_imp_sweep", "sk_fwd_resident", "sk_imp_resident", "sk_fwd_persistent",
-              "sk_imp_persistent"]
+              "sk_imp_persistent", "mth_sweep", "mth_vfinish"]
     profiler.reset()
     profiler.enable(True, kernels=sweeps)
     torch.cuda.synchronize()
@@ -250,7 +266,10 @@ def bench_sinkhorn(args, torch, dot_amd, profiler):
         "T_f": T_f,
         "T_b": T_b,
         "config": {"workload": f"{args.workload}: sinkhorn fwd+bwd B={B} M={M} N={N} reg={reg} "
-                               f"n_iters={n_iters} tol={tol}",
+                               f"n_iters={n_iters} tol={tol}"
+                               + ("" if effective == "vanilla" and eff_schedule is None else
+                                  f" method={effective} schedule={eff_schedule}"),
+                   "method": effective, "schedule": eff_schedule,
                    "B": B, "M": M, "N": N, "reg": reg, "n_iters": n_iters, "tol": tol,
                    "n_iters_used": used[-1], "backward_iters": T_b},
         "algorithmic_GBps": algo_bytes / sec_per_step / 1e9,
@@ -330,6 +349,12 @@ def main():
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--workload", default="c3", choices=sorted(WORKLOADS))
+    ap.add_argument("--method", default="vanilla", choices=["vanilla", "momentum", "anderson", "adam"])
+    ap.add_argument("--schedule", default=None, choices=["linear", "exponential", "cosine"])
+    ap.add_argument("--omega", type=float, default=None)
+    ap.add_argument("--lr", type=float, default=1.0)
+    ap.add_argument("--anderson-k", type=int, default=5)
+    ap.add_argument("--reg-start", type=float, default=None)
     ap.add_argument("--no-bidi", action="store_true", help="skip the bidirectional-softmax leg")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,

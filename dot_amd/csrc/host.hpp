@@ -6,6 +6,7 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <cstdlib>
 #include <string>
 
 #include "../../include/dot_amd.h"
@@ -78,6 +79,15 @@ inline int sweep_strip_rows(int B, int M) {
     int r = 64;
     while (r > 4 && int64_t(B) * ((M + r - 1) / r) < 1024) r /= 2;
     return r;
+}
+
+// sweep_strip_rows, or the value of DOT_AMD_ROWS when set (tuning only).
+inline int tuned_strip_rows(int B, int M) {
+    static const int forced = [] {
+        const char* s = std::getenv("DOT_AMD_ROWS");
+        return s ? std::atoi(s) : 0;
+    }();
+    return forced >= 1 ? forced : sweep_strip_rows(B, M);
 }
 
 }  // namespace dot_amd

@@ -2,18 +2,26 @@
 // and regularisation schedules, src/sinkhorn/torch_cuda.cpp:61-84, :147-264,
 // :323-557).
 //
-// These methods modify u between the row and the column update (momentum and
-// Adam keep a candidate only when it moves closer to the plain update, a
-// batch-global test), and Anderson mixes whole (u, v) states, so a row update
-// cannot share its exponentials with the next column update as the vanilla
-// sweeps do: each iteration is a row-update sweep, a column log-sum-exp
-// sweep over row strips (online max/sum per column, strips merged in a fixed
-// order) and small vector kernels.  Every decision the reference takes on the
-// host after a device-to-host copy (candidate tests, the stop test, Anderson's
-// fallback) is a device flag here; iterations after the stop test fired are
-// no-ops.  Batch-global maxima of non-negative values go through atomicMax on
-// their bit patterns (order-preserving for non-negative floats), so they are
-// exact and independent of the order of arrival.
+// One iteration is one pass over the matrix (sweep) and a per-column kernel
+// (vfinish):
+//   sweep     row update u*_i = log a_i - LSE_j(K_ij + v_j) for a strip of rows,
+//             the method's candidate u'_i (momentum: (1 - w) u + w u*;
+//             Adam: moment-scaled step), and per-strip column sums of
+//             exp(K_ij + u_i + v_j) for BOTH u = u* and u = u': they share the
+//             row's exponentials, e_ij w_i and e_ij w_i exp(u'_i - u*_i), so
+//             keeping either candidate costs no second pass;
+//   vfinish   the column update from whichever sum the batch-global test kept
+//             (v*_j = log b_j + v_j - log colsum_j), the v candidate, and its test.
+// The reference decides each test on the host after a device-to-host copy;
+// here every decision is a word of the iteration's flag block, read by the
+// kernels that need it: the sweep of iteration t takes the u and v that
+// iteration t-1 kept, and returns at once when iteration t-1 met the stop
+// test.  An iteration that did not run leaves its flag words zero, which
+// reads as met, so the stop carries forward with no extra state.  Anderson
+// runs the plain sweep and mixes the (u, v) state with small vector kernels.
+// Batch-global maxima of non-negative values are atomicMax over their bit
+// patterns (order-preserving for non-negative floats): exact and independent
+// of the order of arrival.
 #pragma once
 
 #include <cfloat>
@@ -24,193 +32,352 @@
 namespace dot_amd {
 namespace mth {
 
-constexpr float kFloor = 1.0e-12f;  // kernels.cu:523-538, :649-664
-constexpr int kMaxHistory = 16;     // longest Anderson history (anderson_k) supported
+constexpr float kSumFloor = 1.0e-12f;     // log(max(sum, 1e-12)), kernels.cu:523-538, :649-664
+constexpr float kColSumFloor = 1.0e-20f;  // smaller column sums take the exact column LSE
+constexpr int kMaxHistory = 16;           // longest Anderson history (anderson_k) supported
 
-// Natural-log merge of two column states (sum = s * e^m).
-__device__ __forceinline__ void lse_merge(float& m, float& s, float m2, float s2) {
-    const float M = fmaxf(m, m2);
-    s = s * expf(m - M) + s2 * expf(m2 - M);
-    m = M;
+// Solver codes (the reference's method codes); Anderson runs the plain sweep.
+constexpr int kPlain = 0, kMomentum = 1, kAnderson = 2, kAdam = 3;
+
+// Flag words of one iteration (zeroed once per call).  Each word is striped
+// over kStripes addresses: a workgroup reduces its values first and adds them
+// with one atomicMax on the stripe of its index, so no address sees more than
+// a few dozen atomics per launch; readers take the max over the stripes with
+// one wave-wide load.
+constexpr int kStripes = kWave;
+constexpr int kGapU = 0;    // [0] max|u' - u*|, [1] max|u - u*| (the change when u* is kept)
+constexpr int kGapV = 2;    // the same for v
+constexpr int kMoveU = 4;   // max|u' - u| (the change when u' is kept)
+constexpr int kMoveV = 5;
+constexpr int kAaDelta = 6; // Anderson: max|x_new - x|
+constexpr int kAaMin = 7;   // Anderson: kInfBits - bits(min |sum alpha|), ordered as a float
+constexpr int kAaFail = 8;  // Anderson: a solve failed
+constexpr int kWords = 9;
+constexpr int kIterWords = kWords * kStripes;
+constexpr unsigned kInfBits = 0x7f800000u;
+
+// Word k of an iteration's flag block; every lane of the wave must call it.
+__device__ __forceinline__ float flag(const unsigned* s, int k) {
+    return wave_max(__uint_as_float(s[k * kStripes + threadIdx.x % kWave]));
 }
 
-__device__ __forceinline__ void atomic_max_nonneg(unsigned* p, float x) {
-    atomicMax(p, __float_as_uint(x));
+inline float host_flag(const unsigned* s, int k) {
+    float m = 0.0f;
+    for (int i = 0; i < kStripes; ++i) {
+        const float x = __builtin_bit_cast(float, s[k * kStripes + i]);
+        m = x > m ? x : m;
+    }
+    return m;
 }
 
-// ---------------------------------------------------------------------------
-// Row update: u_i = log a_i - (max + log max(sum safe_exp(K_ij + v_j - max), 1e-12)),
-// K = X * kscale (kernels.cu:503-545).
-// ---------------------------------------------------------------------------
-struct RowArgs {
-    const float* X;
-    float kscale;
-    int M, N, rows;
-    const float* log_a;  // [B,M] or null
-    float log_a_default;
-    const float* v;      // [B,N]
-    float* u;            // [B,M] out
-    const int* done;
+// What an iteration decided: candidate tests (candidate_improves_cuda,
+// torch_cuda.cpp:86-96) and the stop test's change (torch_cuda.cpp:230-238
+// vanilla, u only; :519-524 momentum/Adam, u and v after the tests; :400
+// Anderson).  An iteration that did not run reads as all zero.
+struct Decision {
+    bool keep_u, keep_v;
+    float delta;
 };
 
-template <int VEC, int CH>
-__global__ __launch_bounds__(kBlock) void row_update(RowArgs a) {
-    using R = Row<VEC, CH>;
-    if (*a.done) return;
-    const int lane = threadIdx.x % kWave;
-    const int wave = threadIdx.x / kWave;
-    const int b = blockIdx.y;
-    const int r0 = blockIdx.x * a.rows;
-    const int r1 = min(r0 + a.rows, a.M);
-    float v[R::PL];
-    R::load(a.v + size_t(b) * a.N, lane, a.N, v, 0.0f);
-    for (int i = r0 + wave; i < r1; i += kWavesPerBlock) {
-        float y[R::PL];
-        R::load(a.X + (size_t(b) * a.M + i) * a.N, lane, a.N, y, 0.0f);
-        float mx = -FLT_MAX;
-#pragma unroll
-        for (int e = 0; e < R::PL; ++e) {
-            y[e] = y[e] * a.kscale + v[e];
-            if (R::valid(lane, e, a.N)) mx = fmaxf(mx, y[e]);
-        }
-        const float m = wave_max(mx);
-        float s = 0.0f;
-#pragma unroll
-        for (int e = 0; e < R::PL; ++e)
-            if (R::valid(lane, e, a.N)) s += safe_exp(y[e] - m);
-        s = wave_sum(s);
-        if (lane == 0) {
-            const float la = a.log_a ? a.log_a[size_t(b) * a.M + i] : a.log_a_default;
-            a.u[size_t(b) * a.M + i] = la - (m + logf(fmaxf(s, kFloor)));
-        }
+template <class Flag>
+__host__ __device__ inline Decision decide(Flag f, int method) {
+    Decision d{false, false, 0.0f};
+    if (method == kAnderson) {
+        d.delta = f(kAaDelta);
+        return d;
     }
+    const float g1 = f(kGapU + 1);
+    if (method == kPlain) {
+        d.delta = g1;
+        return d;
+    }
+    d.keep_u = f(kGapU) < g1;
+    const float h1 = f(kGapV + 1);
+    d.keep_v = f(kGapV) < h1;
+    const float du = d.keep_u ? f(kMoveU) : g1;
+    const float dv = d.keep_v ? f(kMoveV) : h1;
+    d.delta = du > dv ? du : dv;
+    return d;
+}
+
+__device__ __forceinline__ Decision decide_dev(const unsigned* s, int method) {
+    return decide([&](int k) { return flag(s, k); }, method);
+}
+
+inline Decision decide_host(const unsigned* s, int method) {
+    return decide([&](int k) { return host_flag(s, k); }, method);
+}
+
+// The previous iteration's decision (prev null before the first) and whether
+// the stop test fired at or before it.  Every lane of the wave must call it.
+struct Prev {
+    Decision d;
+    bool stop;
+};
+
+__device__ __forceinline__ Prev previous(const unsigned* prev, int method, float tol) {
+    Prev p{{false, false, 0.0f}, false};
+    if (prev) {
+        p.d = decide_dev(prev, method);
+        p.stop = tol > 0.0f && p.d.delta < tol;
+    }
+    return p;
+}
+
+__device__ __forceinline__ void atomic_max_nonneg(unsigned* p, float x) { atomicMax(p, __float_as_uint(x)); }
+
+// Workgroup max of one value per thread, added to word k's stripe for this
+// workgroup.  Every thread must call it; `red` holds kWavesPerBlock floats.
+__device__ __forceinline__ void block_flag_max(unsigned* s, int k, float x, float* red) {
+    const float m = block_reduce<kWavesPerBlock>(wave_max(x), red, OpMax{});
+    const unsigned blk = blockIdx.x + blockIdx.y * gridDim.x;
+    if (threadIdx.x == 0) atomic_max_nonneg(s + k * kStripes + (blk % kStripes), m);
 }
 
 // ---------------------------------------------------------------------------
-// Column update: v_j = log b_j - LSE_i(K_ij + u_i) (kernels.cu:629-671), as
-// per-strip online (max, sum) states merged in strip order.
+// Sweep
 // ---------------------------------------------------------------------------
-struct ColArgs {
+struct SweepArgs {
     const float* X;
-    float kscale;
+    float kscale;               // K = X * kscale at this iteration's tau
     int M, N, rows, nstrips;
-    const float* u;      // [B,M]
-    float* part_m;       // [B,nstrips,N]
-    float* part_s;
-    const float* log_b;  // [B,N] or null
-    float log_b_default;
-    float* v;            // [B,N] out (col_finish)
-    const int* done;
+    const float* log_a;         // [B,M] or null
+    float log_a_default;
+    const float* u_prev[2];     // [B,M] u* and u' of the previous iteration (null: zeros)
+    const float* v_prev[2];     // [B,N]
+    const unsigned* prev;       // flag words of the previous iteration, null at the first
+    unsigned* slots;            // this iteration's
+    int method;                 // for the stop test
+    float tol;
+    int track;                  // write the change words (tol > 0)
+    float* ut;                  // [B,M] out: u*
+    float* un;                  // [B,M] out: u'
+    float* m1;                  // [B,M] Adam moments (in place)
+    float* m2;
+    float omega, lr, beta1, beta2, c1, c2, eps;
+    float* part_t;              // [B,nstrips,N] column sums with u*
+    float* part_n;              // [B,nstrips,N] column sums with u'
+    int t;                      // iteration
+    int32_t* used;              // iterations executed (written by every sweep that runs)
+    int32_t* converged;         // set by the first sweep that finds the stop test met
 };
 
-template <int VEC, int CH>
-__global__ __launch_bounds__(kBlock) void col_partial(ColArgs a) {
+template <int VEC, int CH, int MODE>
+__global__ __launch_bounds__(kBlock) void sweep(SweepArgs a) {
+    // the candidates round each operation of the reference's tensor
+    // expressions on its own; the row arithmetic uses explicit fmaf
+#pragma clang fp contract(off)
     using R = Row<VEC, CH>;
-    extern __shared__ __align__(16) float lds[];  // 2 N floats
-    if (*a.done) return;
+    extern __shared__ __align__(16) float lds[];  // 2 N floats + kWavesPerBlock
+    const Prev pv = previous(a.prev, a.method, a.tol);
+    const bool first_block = blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0;
+    if (pv.stop) {
+        if (first_block) *a.converged = 1;
+        return;
+    }
+    if (first_block) *a.used = a.t + 1;
     const int lane = threadIdx.x % kWave;
     const int wave = threadIdx.x / kWave;
-    const int st = blockIdx.x;
+    const int s = blockIdx.x;
     const int b = blockIdx.y;
-    const int r0 = st * a.rows;
+    const int r0 = s * a.rows;
     const int r1 = min(r0 + a.rows, a.M);
-    float cm[R::PL], cs[R::PL];
+    const size_t bM = size_t(b) * a.M;
+    const float* uc = a.u_prev[MODE != kPlain && pv.d.keep_u ? 1 : 0];
+    const float* vc = a.v_prev[MODE != kPlain && pv.d.keep_v ? 1 : 0];
+
+    float v[R::PL];
+    if (vc) {
+        R::load(vc + size_t(b) * a.N, lane, a.N, v, 0.0f);
+    } else {
 #pragma unroll
-    for (int e = 0; e < R::PL; ++e) {
-        cm[e] = -FLT_MAX;
-        cs[e] = 0.0f;
+        for (int e = 0; e < R::PL; ++e) v[e] = 0.0f;
     }
+    float acc_t[R::PL], acc_n[R::PL];
+#pragma unroll
+    for (int e = 0; e < R::PL; ++e) acc_t[e] = acc_n[e] = 0.0f;
+    float gap0 = 0.0f, gap1 = 0.0f, move = 0.0f;
+
     for (int i = r0 + wave; i < r1; i += kWavesPerBlock) {
-        float y[R::PL];
-        R::load(a.X + (size_t(b) * a.M + i) * a.N, lane, a.N, y, 0.0f);
-        const float ui = a.u[size_t(b) * a.M + i];
+        float x[R::PL];
+        R::load(a.X + (bM + i) * a.N, lane, a.N, x, 0.0f);
+        float mloc = -FLT_MAX;
 #pragma unroll
         for (int e = 0; e < R::PL; ++e) {
-            const float t = y[e] * a.kscale + ui;
-            const float d = t - cm[e];
-            const float x = expf(-fabsf(d));
-            const bool gt = d > 0.0f;
-            cs[e] = gt ? fmaf(cs[e], x, 1.0f) : cs[e] + x;
-            cm[e] = gt ? t : cm[e];
+            x[e] = R::valid(lane, e, a.N) ? fmaf(x[e], a.kscale, v[e]) : -INFINITY;
+            mloc = fmaxf(mloc, x[e]);
+        }
+        const float m = wave_max(mloc);
+        float sloc = 0.0f;
+#pragma unroll
+        for (int e = 0; e < R::PL; ++e) {
+            x[e] = fast_exp(x[e] - m);
+            sloc += x[e];
+        }
+        const float ssum = wave_sum(sloc);
+        const float lga = a.log_a ? a.log_a[bM + i] : a.log_a_default;
+        const float ls = logf(fmaxf(ssum, kSumFloor));
+        const float ut = lga - (m + ls);
+        const float w = fast_exp(lga - ls);  // e_ij w = exp(K_ij + v_j + u*_i)
+#pragma unroll
+        for (int e = 0; e < R::PL; ++e) acc_t[e] = fmaf(x[e], w, acc_t[e]);
+        const float ucur = uc ? uc[bM + i] : 0.0f;
+        if constexpr (MODE == kPlain) {
+            gap1 = fmaxf(gap1, fabsf(ucur - ut));
+            if (lane == 0) a.ut[bM + i] = ut;
+        } else {
+            float un;
+            if constexpr (MODE == kMomentum) {
+                un = (1.0f - a.omega) * ucur + a.omega * ut;  // torch_cuda.cpp:470-474
+            } else {
+                // torch_cuda.cpp:475-484: the moments advance whether or not u' is kept
+                const float g = ut - ucur;
+                const float mm = a.beta1 * a.m1[bM + i] + (1.0f - a.beta1) * g;
+                const float vv = a.beta2 * a.m2[bM + i] + (1.0f - a.beta2) * (g * g);
+                if (lane == 0) {
+                    a.m1[bM + i] = mm;
+                    a.m2[bM + i] = vv;
+                }
+                un = ucur + a.lr * (mm / a.c1) / (sqrtf(vv / a.c2) + a.eps);
+            }
+            const float w2 = w * fast_exp(un - ut);  // e_ij w2 = exp(K_ij + v_j + u'_i)
+#pragma unroll
+            for (int e = 0; e < R::PL; ++e) acc_n[e] = fmaf(x[e], w2, acc_n[e]);
+            gap0 = fmaxf(gap0, fabsf(un - ut));
+            gap1 = fmaxf(gap1, fabsf(ucur - ut));
+            move = fmaxf(move, fabsf(un - ucur));
+            if (lane == 0) {
+                a.ut[bM + i] = ut;
+                a.un[bM + i] = un;
+            }
         }
     }
-    // fold the 4 waves in the order (w0 + w2) + (w1 + w3)
-    constexpr int kRounds[3][2] = {{3, 1}, {2, 0}, {1, 0}};
-#pragma unroll
-    for (int r = 0; r < 3; ++r) {
-        __syncthreads();
-        if (wave == kRounds[r][0]) {
-            R::store(lds, lane, a.N, cm);
-            R::store(lds + a.N, lane, a.N, cs);
-        }
-        __syncthreads();
-        if (wave == kRounds[r][1]) {
-            float m2[R::PL], s2[R::PL];
-            R::load(lds, lane, a.N, m2, -FLT_MAX);
-            R::load(lds + a.N, lane, a.N, s2, 0.0f);
-#pragma unroll
-            for (int e = 0; e < R::PL; ++e) lse_merge(cm[e], cs[e], m2[e], s2[e]);
-        }
+
+    const size_t off = (size_t(b) * a.nstrips + s) * a.N;
+    block_column_combine<VEC, CH>(acc_t, lds, a.N);
+    if (wave == 0) R::store(a.part_t + off, lane, a.N, acc_t);
+    if constexpr (MODE != kPlain) {
+        block_column_combine<VEC, CH>(acc_n, lds, a.N);
+        if (wave == 0) R::store(a.part_n + off, lane, a.N, acc_n);
     }
-    if (wave == 0) {
-        const size_t off = (size_t(b) * a.nstrips + st) * a.N;
-        R::store(a.part_m + off, lane, a.N, cm);
-        R::store(a.part_s + off, lane, a.N, cs);
+    // every lane holds its wave's maxima (wave-uniform values)
+    float* red = lds + 2 * a.N;
+    if (MODE != kPlain || a.track) block_flag_max(a.slots, kGapU + 1, gap1, red);
+    if constexpr (MODE != kPlain) {
+        block_flag_max(a.slots, kGapU, gap0, red);
+        block_flag_max(a.slots, kMoveU, move, red);
     }
 }
+
+// ---------------------------------------------------------------------------
+// Column update and the v candidate: 16 columns per workgroup, 16 threads
+// per column summing its strips (lane-strided, then a fixed halving tree).
+// ---------------------------------------------------------------------------
+struct VfinishArgs {
+    const float* X;
+    float kscale;
+    int M, N, nstrips;
+    const float* log_b;         // [B,N] or null
+    float log_b_default;
+    const float* v_prev[2];     // as SweepArgs
+    const float* ut;            // [B,M] this iteration's u* and u' (exact fallback)
+    const float* un;
+    const unsigned* prev;
+    unsigned* slots;            // this iteration's (the u test decided by the sweep)
+    int method;
+    float tol;
+    const float* part_t;
+    const float* part_n;
+    float* vt;                  // [B,N] out: v*
+    float* vn;                  // [B,N] out: v'
+    float* m1;                  // [B,N] Adam moments
+    float* m2;
+    float omega, lr, beta1, beta2, c1, c2, eps;
+};
 
 constexpr int kFoldCols = 16;
 constexpr int kFoldLanes = kBlock / kFoldCols;  // 16
 
-// Strips merged per column: lanes take strips lane, lane + 16, ... in order,
-// then a fixed halving tree; v_j = log b_j - (m + log max(s, 1e-12)).
-static __global__ __launch_bounds__(kBlock) void col_finish(ColArgs a) {
-    __shared__ float sm_m[kFoldLanes][kFoldCols], sm_s[kFoldLanes][kFoldCols];
-    if (*a.done) return;
+template <int MODE>
+__global__ __launch_bounds__(kBlock) void vfinish(VfinishArgs a) {
+#pragma clang fp contract(off)
+    __shared__ float fold[kFoldLanes][kFoldCols];
+    __shared__ float red[kWavesPerBlock];
+    const Prev pv = previous(a.prev, a.method, a.tol);
+    if (pv.stop) return;
     const int b = blockIdx.y;
     const int jj = threadIdx.x % kFoldCols;
     const int sl = threadIdx.x / kFoldCols;
     const int j = blockIdx.x * kFoldCols + jj;
-    float m = -FLT_MAX, s = 0.0f;
+    const bool keep = MODE != kPlain && flag(a.slots, kGapU) < flag(a.slots, kGapU + 1);
+    const float* part = keep ? a.part_n : a.part_t;
+    float cs = 0.0f;
     if (j < a.N) {
-        const size_t base = size_t(b) * a.nstrips * a.N + j;
-        for (int k = sl; k < a.nstrips; k += kFoldLanes)
-            lse_merge(m, s, a.part_m[base + size_t(k) * a.N], a.part_s[base + size_t(k) * a.N]);
+        const float* p = part + size_t(b) * a.nstrips * a.N + j;
+        for (int s = sl; s < a.nstrips; s += kFoldLanes) cs += p[size_t(s) * a.N];
     }
-    sm_m[sl][jj] = m;
-    sm_s[sl][jj] = s;
+    fold[sl][jj] = cs;
 #pragma unroll
     for (int half = kFoldLanes / 2; half >= 1; half /= 2) {
         __syncthreads();
         if (sl < half) {
-            lse_merge(m, s, sm_m[sl + half][jj], sm_s[sl + half][jj]);
-            sm_m[sl][jj] = m;
-            sm_s[sl][jj] = s;
+            cs += fold[sl + half][jj];
+            fold[sl][jj] = cs;
         }
     }
+    const float* vc = a.v_prev[MODE != kPlain && pv.d.keep_v ? 1 : 0];
+    float gap0 = 0.0f, gap1 = 0.0f, move = 0.0f;
     if (sl == 0 && j < a.N) {
-        const float lb = a.log_b ? a.log_b[size_t(b) * a.N + j] : a.log_b_default;
-        a.v[size_t(b) * a.N + j] = lb - (m + logf(fmaxf(s, kFloor)));
+        const size_t bj = size_t(b) * a.N + j;
+        const float lgb = a.log_b ? a.log_b[bj] : a.log_b_default;
+        const float vcur = vc ? vc[bj] : 0.0f;
+        float vt;
+        if (cs >= kColSumFloor && cs <= FLT_MAX) {
+            vt = lgb + vcur - logf(cs);
+        } else {
+            // the reference's max-shifted column LSE (kernels.cu:629-671)
+            const float* col = a.X + size_t(b) * a.M * a.N + j;
+            const float* u = (keep ? a.un : a.ut) + size_t(b) * a.M;
+            float mx = -FLT_MAX;
+            for (int i = 0; i < a.M; ++i) mx = fmaxf(mx, fmaf(col[size_t(i) * a.N], a.kscale, u[i]));
+            float sm = 0.0f;
+            for (int i = 0; i < a.M; ++i) sm += safe_exp(fmaf(col[size_t(i) * a.N], a.kscale, u[i]) - mx);
+            vt = lgb - (mx + logf(fmaxf(sm, kSumFloor)));
+        }
+        a.vt[bj] = vt;
+        if constexpr (MODE != kPlain) {
+            float vn;
+            if constexpr (MODE == kMomentum) {
+                vn = (1.0f - a.omega) * vcur + a.omega * vt;
+            } else {
+                const float g = vt - vcur;
+                const float mm = a.beta1 * a.m1[bj] + (1.0f - a.beta1) * g;
+                const float vv = a.beta2 * a.m2[bj] + (1.0f - a.beta2) * (g * g);
+                a.m1[bj] = mm;
+                a.m2[bj] = vv;
+                vn = vcur + a.lr * (mm / a.c1) / (sqrtf(vv / a.c2) + a.eps);
+            }
+            a.vn[bj] = vn;
+            gap0 = fabsf(vn - vt);
+            gap1 = fabsf(vcur - vt);
+            move = fabsf(vn - vcur);
+        }
+    }
+    if constexpr (MODE != kPlain) {
+        block_flag_max(a.slots, kGapV, gap0, red);
+        block_flag_max(a.slots, kGapV + 1, gap1, red);
+        block_flag_max(a.slots, kMoveV, move, red);
     }
 }
 
 // ---------------------------------------------------------------------------
-// Per-iteration flag words (zeroed once per call).  Batch-global maxima of
-// non-negative floats are atomicMax over their bit patterns; Anderson's
-// minimum |sum(alpha)| is the maximum of kInfBits - bits.
+// End of the loop: iterations executed, and the potentials the last one kept.
 // ---------------------------------------------------------------------------
-constexpr int kSlots = 8;
-constexpr int kGapU = 0;     // [0] max|cand - target|, [1] max|cur - target| (u step)
-constexpr int kGapV = 2;     // the same for the v step
-constexpr int kDeltaU = 4;   // stop-test change of u (Anderson: of the state)
-constexpr int kDeltaV = 5;   // stop-test change of v
-constexpr int kAaMin = 0;    // Anderson: kInfBits - bits(min |sum alpha|)
-constexpr int kAaFail = 1;   // Anderson: a solve failed
-constexpr unsigned kInfBits = 0x7f800000u;
-
-__device__ __forceinline__ void wave_flag_max(unsigned* p, float x) {
-    x = wave_max(x);
-    if (threadIdx.x % kWave == 0) atomic_max_nonneg(p, x);
+// The sweeps count the iterations and flag a stop they find; a stop at the
+// last iteration has no later sweep to find it (one wave).
+static __global__ void finalize(const unsigned* last, int method, float tol, int32_t* converged) {
+    const Decision d = decide_dev(last, method);
+    if (threadIdx.x == 0 && tol > 0.0f && d.delta < tol) *converged = 1;
 }
 
 static __global__ void reset_counts(int32_t* used, int32_t* converged) {
@@ -220,84 +387,28 @@ static __global__ void reset_counts(int32_t* used, int32_t* converged) {
     }
 }
 
-// Momentum candidate (torch_cuda.cpp:470-474): nxt = (1 - omega) cur + omega tgt;
-// gaps max|nxt - tgt| -> gap[0], max|cur - tgt| -> gap[1].
-static __global__ __launch_bounds__(kBlock) void momentum_candidate(const float* cur, const float* tgt,
-                                                                    float* nxt, size_t n, float omega,
-                                                                    unsigned* gap, const int* done) {
-    // each operation of the reference's tensor expression rounded on its own
-#pragma clang fp contract(off)
-    if (*done) return;
-    float g0 = 0.0f, g1 = 0.0f;
+struct ResolveArgs {
+    int B, M, N, method;
+    const int32_t* used;
+    const unsigned* slots;
+    const float* ut[2];  // by parity of the iteration
+    const float* un[2];
+    const float* vt[2];
+    const float* vn[2];
+    float* u;            // [B,M] out
+    float* v;            // [B,N] out
+};
+
+static __global__ __launch_bounds__(kBlock) void resolve(ResolveArgs a) {
+    const int T = *a.used;
+    const size_t nu = size_t(a.B) * a.M, n = nu + size_t(a.B) * a.N;
+    const unsigned* s = T > 0 ? a.slots + size_t(T - 1) * kIterWords : nullptr;
+    const int p = (T - 1) & 1;
+    const Decision d = s ? decide_dev(s, a.method) : Decision{false, false, 0.0f};
+    const bool ku = d.keep_u, kv = d.keep_v;
     for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += size_t(gridDim.x) * blockDim.x) {
-        const float c = cur[i], t = tgt[i];
-        const float x = (1.0f - omega) * c + omega * t;
-        nxt[i] = x;
-        g0 = fmaxf(g0, fabsf(x - t));
-        g1 = fmaxf(g1, fabsf(c - t));
-    }
-    wave_flag_max(gap, g0);
-    wave_flag_max(gap + 1, g1);
-}
-
-// Adam candidate (torch_cuda.cpp:475-484): the moments always advance; c1, c2
-// are the bias-correction divisors (1 when it is off).
-static __global__ __launch_bounds__(kBlock) void adam_candidate(const float* cur, const float* tgt, float* nxt,
-                                                                float* m1, float* m2, size_t n, float beta1,
-                                                                float beta2, float c1, float c2, float lr,
-                                                                float eps, unsigned* gap, const int* done) {
-#pragma clang fp contract(off)
-    if (*done) return;
-    float g0 = 0.0f, g1 = 0.0f;
-    for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += size_t(gridDim.x) * blockDim.x) {
-        const float c = cur[i], t = tgt[i];
-        const float g = t - c;
-        const float mm = beta1 * m1[i] + (1.0f - beta1) * g;
-        const float vv = beta2 * m2[i] + (1.0f - beta2) * (g * g);
-        m1[i] = mm;
-        m2[i] = vv;
-        const float x = c + lr * (mm / c1) / (sqrtf(vv / c2) + eps);
-        nxt[i] = x;
-        g0 = fmaxf(g0, fabsf(x - t));
-        g1 = fmaxf(g1, fabsf(c - t));
-    }
-    wave_flag_max(gap, g0);
-    wave_flag_max(gap + 1, g1);
-}
-
-// tgt = nxt when the candidate is strictly closer (candidate_improves_cuda,
-// torch_cuda.cpp:86-96).
-static __global__ __launch_bounds__(kBlock) void accept_candidate(float* tgt, const float* nxt, size_t n,
-                                                                  const unsigned* gap, const int* done) {
-    if (*done) return;
-    if (!(__uint_as_float(gap[0]) < __uint_as_float(gap[1]))) return;
-    for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += size_t(gridDim.x) * blockDim.x)
-        tgt[i] = nxt[i];
-}
-
-// cur = tgt; with `delta` set, max|tgt - cur| -> *delta.
-static __global__ __launch_bounds__(kBlock) void commit(float* cur, const float* tgt, size_t n, unsigned* delta,
-                                                        const int* done) {
-    if (*done) return;
-    float d = 0.0f;
-    for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += size_t(gridDim.x) * blockDim.x) {
-        const float t = tgt[i];
-        d = fmaxf(d, fabsf(t - cur[i]));
-        cur[i] = t;
-    }
-    if (delta) wave_flag_max(delta, d);
-}
-
-// End of iteration `it` (slots of that iteration): count it, and stop when
-// tol > 0 and the larger of the two deltas is below tol.
-static __global__ void finish_iteration(const unsigned* slots, int it, float tol, int* done, int32_t* used,
-                                        int32_t* converged) {
-    if (blockIdx.x != 0 || threadIdx.x != 0 || *done) return;
-    *used = it + 1;
-    const float d = fmaxf(__uint_as_float(slots[kDeltaU]), __uint_as_float(slots[kDeltaV]));
-    if (tol > 0.0f && d < tol) {
-        *converged = 1;
-        *done = 1;
+        if (i < nu) a.u[i] = s ? (ku ? a.un[p] : a.ut[p])[i] : 0.0f;
+        else a.v[i - nu] = s ? (kv ? a.vn[p] : a.vt[p])[i - nu] : 0.0f;
     }
 }
 
@@ -322,9 +433,9 @@ struct AaArgs {
     float* gram;      // [B,kMaxHistory,kMaxHistory]
     float* alpha;     // [B,kMaxHistory]
     float* denom;     // [B]
+    const unsigned* prev;
     unsigned* slots;  // this iteration's flag words
-    int track_delta;
-    const int* done;
+    float tol;
 };
 
 __device__ __forceinline__ float aa_at(const float* hu, const float* hv, int s, size_t nu, size_t nv, int b, int M,
@@ -332,9 +443,10 @@ __device__ __forceinline__ float aa_at(const float* hu, const float* hv, int s, 
     return i < M ? hu[size_t(s) * nu + size_t(b) * M + i] : hv[size_t(s) * nv + size_t(b) * N + (i - M)];
 }
 
-// Push (x, x_new - x) into the ring; the residual's max into the delta slot.
+// Push (x, x_new - x) into the ring; the residual's max into the delta word.
 static __global__ __launch_bounds__(kBlock) void aa_push(AaArgs a) {
-    if (*a.done) return;
+    __shared__ float red[kWavesPerBlock];
+    if (previous(a.prev, kAnderson, a.tol).stop) return;
     const size_t nu = size_t(a.B) * a.M, nv = size_t(a.B) * a.N, n = nu + nv;
     float d = 0.0f;
     for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += size_t(gridDim.x) * blockDim.x) {
@@ -351,14 +463,14 @@ static __global__ __launch_bounds__(kBlock) void aa_push(AaArgs a) {
             d = fmaxf(d, fabsf(f));
         }
     }
-    if (a.track_delta) wave_flag_max(a.slots + kDeltaU, d);
+    block_flag_max(a.slots, kAaDelta, d, red);
 }
 
 // Row p of the Gram matrix F^T F of element b (grid h x B): one pass over the
 // element's M + N residual entries of every history pair.
 static __global__ __launch_bounds__(kBlock) void aa_gram(AaArgs a) {
     __shared__ float red[kWavesPerBlock][kMaxHistory];
-    if (*a.done) return;
+    if (previous(a.prev, kAnderson, a.tol).stop) return;
     const int p = blockIdx.x, b = blockIdx.y, h = a.h;
     const size_t nu = size_t(a.B) * a.M, nv = size_t(a.B) * a.N;
     const int sp = a.order[p];
@@ -393,7 +505,7 @@ static __global__ __launch_bounds__(kBlock) void aa_gram(AaArgs a) {
 static __global__ void aa_solve(AaArgs a) {
     __shared__ float A[kMaxHistory][kMaxHistory + 1];
     __shared__ float x[kMaxHistory];
-    if (*a.done || threadIdx.x != 0) return;
+    if (previous(a.prev, kAnderson, a.tol).stop || threadIdx.x != 0) return;
     const int b = blockIdx.x, h = a.h;
     for (int p = 0; p < h; ++p) {
         for (int q = 0; q < h; ++q)
@@ -438,17 +550,21 @@ static __global__ void aa_solve(AaArgs a) {
     }
     for (int c = 0; c < h; ++c) a.alpha[size_t(b) * kMaxHistory + c] = failed ? 0.0f : x[c];
     a.denom[b] = sum;
-    if (failed) atomicOr(a.slots + kAaFail, 1u);
-    else atomicMax(a.slots + kAaMin, kInfBits - __float_as_uint(fabsf(sum)));
+    unsigned* stripe = a.slots + (b % kStripes);
+    if (failed) atomicMax(stripe + kAaFail * kStripes, 1u);
+    else atomicMax(stripe + kAaMin * kStripes, kInfBits - __float_as_uint(fabsf(sum)));
 }
 
 // x = sum_c (alpha_c / sum) (X_c + beta F_c) when every element's solve
 // succeeded with |sum| >= 1e-12, else x = x_new (torch_cuda.cpp:421-444).
 // With fewer than two pairs, x = x_new.
 static __global__ __launch_bounds__(kBlock) void aa_update(AaArgs a) {
-    if (*a.done) return;
-    const bool mix = a.h >= 2 && a.slots[kAaFail] == 0u &&
-                     __uint_as_float(kInfBits - a.slots[kAaMin]) >= 1.0e-12f;
+    if (previous(a.prev, kAnderson, a.tol).stop) return;
+    // the stripes hold kInfBits - bits(|sum|): their max is the minimum |sum|
+    const float fail = flag(a.slots, kAaFail);
+    const float code = flag(a.slots, kAaMin);
+    const bool mix = a.h >= 2 && fail == 0.0f &&
+                     __uint_as_float(kInfBits - __float_as_uint(code)) >= 1.0e-12f;
     const size_t nu = size_t(a.B) * a.M, nv = size_t(a.B) * a.N, n = nu + nv;
     for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += size_t(gridDim.x) * blockDim.x) {
         const bool isu = i < nu;

@@ -5,6 +5,7 @@
 #include <algorithm>
 #include <cmath>
 #include <string>
+#include <type_traits>
 
 #include "host.hpp"
 #include "methods.cuh"
@@ -13,18 +14,17 @@ namespace dot_amd {
 namespace {
 
 using mth::kMaxHistory;
-using mth::kSlots;
+using mth::kIterWords;
 
 constexpr int kStopCheckEvery = 16;  // iterations between host reads of the stop flag (tol > 0)
 
 struct MethodLayout {
-    unsigned* slots;  // [T, kSlots] flag words
-    int* done;
-    float *u, *v;                 // current potentials (Anderson: the state)
+    unsigned* slots;              // [T, kIterWords] flag words
     float *m1u, *m2u, *m1v, *m2v; // Adam moments
-    size_t zero_bytes;            // from `slots` through the last zeroed buffer
-    float *ut, *vt, *un, *vn;     // plain updates and candidates
-    float *part_m, *part_s, *cost_partial;
+    float *u, *v;                 // final potentials (Anderson: the state)
+    size_t zero_bytes;            // from `slots` through `v`
+    float *ut[2], *un[2], *vt[2], *vn[2];  // per iteration, by parity
+    float *part_t, *part_n, *cost_partial;
     float *hxu, *hxv, *hfu, *hfv, *gram, *alpha, *denom;
     int rows, nstrips;
     size_t bytes;
@@ -33,28 +33,30 @@ struct MethodLayout {
 MethodLayout method_layout(void* ws, int B, int M, int N, int T, int method, int k) {
     Carver c(ws);
     MethodLayout L{};
-    L.rows = sweep_strip_rows(B, M);
+    L.rows = tuned_strip_rows(B, M);
     L.nstrips = M > 0 ? (M + L.rows - 1) / L.rows : 0;
     const size_t BM = size_t(B) * M, BN = size_t(B) * N;
-    L.slots = c.take<unsigned>(size_t(std::max(T, 1)) * kSlots);
-    L.done = c.take<int>(1);
-    L.u = c.take<float>(BM);
-    L.v = c.take<float>(BN);
-    const bool adam = method == DOT_SK_ADAM;
+    const bool adam = method == DOT_SK_ADAM, anderson = method == DOT_SK_ANDERSON;
+    const bool cand = method == DOT_SK_MOMENTUM || adam;
+    L.slots = c.take<unsigned>(size_t(std::max(T, 1)) * kIterWords);
     L.m1u = c.take<float>(adam ? BM : 0);
     L.m2u = c.take<float>(adam ? BM : 0);
     L.m1v = c.take<float>(adam ? BN : 0);
     L.m2v = c.take<float>(adam ? BN : 0);
+    L.u = c.take<float>(BM);
+    L.v = c.take<float>(BN);
     L.zero_bytes = c.used();
-    L.ut = c.take<float>(BM);
-    L.vt = c.take<float>(BN);
-    const bool cand = method == DOT_SK_MOMENTUM || adam;
-    L.un = c.take<float>(cand ? BM : 0);
-    L.vn = c.take<float>(cand ? BN : 0);
-    L.part_m = c.take<float>(size_t(B) * L.nstrips * N);
-    L.part_s = c.take<float>(size_t(B) * L.nstrips * N);
+    const int parities = anderson ? 1 : 2;
+    for (int p = 0; p < 2; ++p) {
+        L.ut[p] = p < parities ? c.take<float>(BM) : L.ut[0];
+        L.vt[p] = p < parities ? c.take<float>(BN) : L.vt[0];
+        L.un[p] = cand ? c.take<float>(BM) : L.ut[p];
+        L.vn[p] = cand ? c.take<float>(BN) : L.vt[p];
+    }
+    L.part_t = c.take<float>(size_t(B) * L.nstrips * N);
+    L.part_n = cand ? c.take<float>(size_t(B) * L.nstrips * N) : L.part_t;
     L.cost_partial = c.take<float>(size_t(B) * L.nstrips);
-    const size_t kk = method == DOT_SK_ANDERSON ? size_t(k) : 0;
+    const size_t kk = anderson ? size_t(k) : 0;
     L.hxu = c.take<float>(kk * BM);
     L.hxv = c.take<float>(kk * BN);
     L.hfu = c.take<float>(kk * BM);
@@ -195,6 +197,7 @@ extern "C" int dot_sinkhorn_forward_method(const dot_sinkhorn_method_args* m, do
     if (hipStreamIsCapturing(stream, &cap) != hipSuccess) cap = hipStreamCaptureStatusNone;
     (void)hipGetLastError();
     const bool may_wait = track && cap == hipStreamCaptureStatusNone;
+    const bool anderson = method == DOT_SK_ANDERSON;
 
     int rc = DOT_OK;
     const bool launched = dispatch_row(N, vec4, [&](auto vc, auto cc) {
@@ -202,153 +205,178 @@ extern "C" int dot_sinkhorn_forward_method(const dot_sinkhorn_method_args* m, do
         constexpr int C = decltype(cc)::value;
         const dim3 strips(L.nstrips, B);
         const dim3 cols((N + mth::kFoldCols - 1) / mth::kFoldCols, B);
-        const size_t col_lds = size_t(2) * N * sizeof(float);
+        const size_t sweep_lds = (size_t(2) * N + 8) * sizeof(float);
+        int ring_head = 0, ring_size = 0;  // Anderson ring: logical position -> physical slot
 
-        mth::RowArgs ra{};
-        ra.X = a->scores;
-        ra.M = M;
-        ra.N = N;
-        ra.rows = L.rows;
-        ra.log_a = a->log_a;
-        ra.log_a_default = log_a_default;
-        ra.done = L.done;
-        mth::ColArgs ca{};
-        ca.X = a->scores;
-        ca.M = M;
-        ca.N = N;
-        ca.rows = L.rows;
-        ca.nstrips = L.nstrips;
-        ca.part_m = L.part_m;
-        ca.part_s = L.part_s;
-        ca.log_b = a->log_b;
-        ca.log_b_default = log_b_default;
-        ca.done = L.done;
-        auto row_col = [&](float ks, const float* v_in, float* u_out, float* v_out) {
-            ra.kscale = ks;
-            ra.v = v_in;
-            ra.u = u_out;
-            ca.kscale = ks;
-            ca.u = u_out;
-            ca.v = v_out;
-            ProfScope prof("mth_sweeps", stream);
-            hipLaunchKernelGGL((mth::row_update<V, C>), strips, dim3(kBlock), 0, stream, ra);
-            hipLaunchKernelGGL((mth::col_partial<V, C>), strips, dim3(kBlock), col_lds, stream, ca);
-            hipLaunchKernelGGL(mth::col_finish, cols, dim3(kBlock), 0, stream, ca);
+        auto iteration = [&](auto mode_c, int t, float ks) {
+            constexpr int MODE = decltype(mode_c)::value;
+            const unsigned* prev = t > 0 ? L.slots + size_t(t - 1) * kIterWords : nullptr;
+            unsigned* cur = L.slots + size_t(t) * kIterWords;
+            const int p = t & 1, q = p ^ 1;
+            float c1 = 1.0f, c2 = 1.0f;
+            if (method == DOT_SK_ADAM && m->bias_correction) {  // torch_cuda.cpp:478-481
+                c1 = 1.0f - std::pow(m->beta1, static_cast<float>(t + 1));
+                c2 = 1.0f - std::pow(m->beta2, static_cast<float>(t + 1));
+            }
+            mth::SweepArgs sa{};
+            sa.X = a->scores;
+            sa.kscale = ks;
+            sa.M = M;
+            sa.N = N;
+            sa.rows = L.rows;
+            sa.nstrips = L.nstrips;
+            sa.log_a = a->log_a;
+            sa.log_a_default = log_a_default;
+            if (anderson) {
+                sa.u_prev[0] = sa.u_prev[1] = L.u;
+                sa.v_prev[0] = sa.v_prev[1] = L.v;
+            } else if (t > 0) {
+                sa.u_prev[0] = L.ut[q];
+                sa.u_prev[1] = L.un[q];
+                sa.v_prev[0] = L.vt[q];
+                sa.v_prev[1] = L.vn[q];
+            }
+            sa.prev = prev;
+            sa.slots = cur;
+            sa.method = method;
+            sa.tol = a->tol;
+            sa.track = track && method == DOT_SK_VANILLA ? 1 : 0;
+            sa.ut = L.ut[p];
+            sa.un = L.un[p];
+            sa.m1 = L.m1u;
+            sa.m2 = L.m2u;
+            sa.omega = m->omega;
+            sa.lr = m->lr;
+            sa.beta1 = m->beta1;
+            sa.beta2 = m->beta2;
+            sa.c1 = c1;
+            sa.c2 = c2;
+            sa.eps = m->eps_adam;
+            sa.part_t = L.part_t;
+            sa.part_n = L.part_n;
+            sa.t = t;
+            sa.used = a->iters_used;
+            sa.converged = a->converged;
+            {
+                ProfScope prof("mth_sweep", stream);
+                hipLaunchKernelGGL((mth::sweep<V, C, MODE>), strips, dim3(kBlock), sweep_lds, stream, sa);
+            }
+            mth::VfinishArgs fa{};
+            fa.X = a->scores;
+            fa.kscale = ks;
+            fa.M = M;
+            fa.N = N;
+            fa.nstrips = L.nstrips;
+            fa.log_b = a->log_b;
+            fa.log_b_default = log_b_default;
+            fa.v_prev[0] = sa.v_prev[0];
+            fa.v_prev[1] = sa.v_prev[1];
+            fa.ut = L.ut[p];
+            fa.un = L.un[p];
+            fa.prev = prev;
+            fa.slots = cur;
+            fa.method = method;
+            fa.tol = a->tol;
+            fa.part_t = L.part_t;
+            fa.part_n = L.part_n;
+            fa.vt = L.vt[p];
+            fa.vn = L.vn[p];
+            fa.m1 = L.m1v;
+            fa.m2 = L.m2v;
+            fa.omega = m->omega;
+            fa.lr = m->lr;
+            fa.beta1 = m->beta1;
+            fa.beta2 = m->beta2;
+            fa.c1 = c1;
+            fa.c2 = c2;
+            fa.eps = m->eps_adam;
+            {
+                ProfScope prof("mth_vfinish", stream);
+                hipLaunchKernelGGL((mth::vfinish<MODE>), cols, dim3(kBlock), 0, stream, fa);
+            }
+            if (!anderson) return;
+            // x_new = (u*, v*); mix the state (torch_cuda.cpp:395-446)
+            int slot;
+            if (ring_size < k) {
+                slot = (ring_head + ring_size) % k;
+                ++ring_size;
+            } else {
+                slot = ring_head;
+                ring_head = (ring_head + 1) % k;
+            }
+            mth::AaArgs aa{};
+            aa.B = B;
+            aa.M = M;
+            aa.N = N;
+            aa.xu = L.u;
+            aa.xv = L.v;
+            aa.nu = L.ut[0];
+            aa.nv = L.vt[0];
+            aa.hxu = L.hxu;
+            aa.hxv = L.hxv;
+            aa.hfu = L.hfu;
+            aa.hfv = L.hfv;
+            aa.slot = slot;
+            aa.h = ring_size;
+            for (int c = 0; c < ring_size; ++c) aa.order[c] = (ring_head + c) % k;
+            aa.mixing_beta = m->mixing_beta;
+            aa.gram = L.gram;
+            aa.alpha = L.alpha;
+            aa.denom = L.denom;
+            aa.prev = prev;
+            aa.slots = cur;
+            aa.tol = a->tol;
+            ProfScope prof("mth_anderson", stream);
+            hipLaunchKernelGGL(mth::aa_push, vector_grid(BM + BN), dim3(kBlock), 0, stream, aa);
+            if (ring_size >= 2) {
+                hipLaunchKernelGGL(mth::aa_gram, dim3(ring_size, B), dim3(kBlock), 0, stream, aa);
+                hipLaunchKernelGGL(mth::aa_solve, dim3(B), dim3(kWave), 0, stream, aa);
+            }
+            hipLaunchKernelGGL(mth::aa_update, vector_grid(BM + BN), dim3(kBlock), 0, stream, aa);
         };
-        // Anderson ring: logical position -> physical slot
-        int ring_head = 0, ring_size = 0;
 
         float ks = kscale_at(scheduled_tau(0, T, tau, m->reg_start, m->schedule));
-        for (int it = 0; it < T; ++it) {
-            if (sched) ks = kscale_at(scheduled_tau(it, T, tau, m->reg_start, m->schedule));
-            unsigned* slots = L.slots + size_t(it) * kSlots;
-            if (method == DOT_SK_ANDERSON) {
-                // x_new = one plain row + column update of the state (u, v)
-                row_col(ks, L.v, L.ut, L.vt);
-                int slot;
-                if (ring_size < k) {
-                    slot = (ring_head + ring_size) % k;
-                    ++ring_size;
-                } else {
-                    slot = ring_head;
-                    ring_head = (ring_head + 1) % k;
-                }
-                mth::AaArgs aa{};
-                aa.B = B;
-                aa.M = M;
-                aa.N = N;
-                aa.xu = L.u;
-                aa.xv = L.v;
-                aa.nu = L.ut;
-                aa.nv = L.vt;
-                aa.hxu = L.hxu;
-                aa.hxv = L.hxv;
-                aa.hfu = L.hfu;
-                aa.hfv = L.hfv;
-                aa.slot = slot;
-                aa.h = ring_size;
-                for (int c = 0; c < ring_size; ++c) aa.order[c] = (ring_head + c) % k;
-                aa.mixing_beta = m->mixing_beta;
-                aa.gram = L.gram;
-                aa.alpha = L.alpha;
-                aa.denom = L.denom;
-                aa.slots = slots;
-                aa.track_delta = track ? 1 : 0;
-                aa.done = L.done;
-                ProfScope prof("mth_anderson", stream);
-                hipLaunchKernelGGL(mth::aa_push, vector_grid(BM + BN), dim3(kBlock), 0, stream, aa);
-                if (ring_size >= 2) {
-                    hipLaunchKernelGGL(mth::aa_gram, dim3(ring_size, B), dim3(kBlock), 0, stream, aa);
-                    hipLaunchKernelGGL(mth::aa_solve, dim3(B), dim3(kWave), 0, stream, aa);
-                }
-                hipLaunchKernelGGL(mth::aa_update, vector_grid(BM + BN), dim3(kBlock), 0, stream, aa);
-            } else {
-                // u step
-                ra.kscale = ks;
-                ra.v = L.v;
-                ra.u = L.ut;
-                {
-                    ProfScope prof("mth_sweeps", stream);
-                    hipLaunchKernelGGL((mth::row_update<V, C>), strips, dim3(kBlock), 0, stream, ra);
-                }
-                if (method == DOT_SK_MOMENTUM) {
-                    hipLaunchKernelGGL(mth::momentum_candidate, vector_grid(BM), dim3(kBlock), 0, stream, L.u,
-                                       L.ut, L.un, BM, m->omega, slots + mth::kGapU, L.done);
-                } else if (method == DOT_SK_ADAM) {
-                    const float c1 = m->bias_correction
-                                         ? 1.0f - std::pow(m->beta1, static_cast<float>(it + 1)) : 1.0f;
-                    const float c2 = m->bias_correction
-                                         ? 1.0f - std::pow(m->beta2, static_cast<float>(it + 1)) : 1.0f;
-                    hipLaunchKernelGGL(mth::adam_candidate, vector_grid(BM), dim3(kBlock), 0, stream, L.u, L.ut,
-                                       L.un, L.m1u, L.m2u, BM, m->beta1, m->beta2, c1, c2, m->lr, m->eps_adam,
-                                       slots + mth::kGapU, L.done);
-                }
-                if (method != DOT_SK_VANILLA)
-                    hipLaunchKernelGGL(mth::accept_candidate, vector_grid(BM), dim3(kBlock), 0, stream, L.ut,
-                                       L.un, BM, slots + mth::kGapU, L.done);
-                // v step from the kept u
-                ca.kscale = ks;
-                ca.u = L.ut;
-                ca.v = L.vt;
-                {
-                    ProfScope prof("mth_sweeps", stream);
-                    hipLaunchKernelGGL((mth::col_partial<V, C>), strips, dim3(kBlock), col_lds, stream, ca);
-                    hipLaunchKernelGGL(mth::col_finish, cols, dim3(kBlock), 0, stream, ca);
-                }
-                if (method == DOT_SK_MOMENTUM) {
-                    hipLaunchKernelGGL(mth::momentum_candidate, vector_grid(BN), dim3(kBlock), 0, stream, L.v,
-                                       L.vt, L.vn, BN, m->omega, slots + mth::kGapV, L.done);
-                } else if (method == DOT_SK_ADAM) {
-                    const float c1 = m->bias_correction
-                                         ? 1.0f - std::pow(m->beta1, static_cast<float>(it + 1)) : 1.0f;
-                    const float c2 = m->bias_correction
-                                         ? 1.0f - std::pow(m->beta2, static_cast<float>(it + 1)) : 1.0f;
-                    hipLaunchKernelGGL(mth::adam_candidate, vector_grid(BN), dim3(kBlock), 0, stream, L.v, L.vt,
-                                       L.vn, L.m1v, L.m2v, BN, m->beta1, m->beta2, c1, c2, m->lr, m->eps_adam,
-                                       slots + mth::kGapV, L.done);
-                }
-                if (method != DOT_SK_VANILLA)
-                    hipLaunchKernelGGL(mth::accept_candidate, vector_grid(BN), dim3(kBlock), 0, stream, L.vt,
-                                       L.vn, BN, slots + mth::kGapV, L.done);
-                // stop test: vanilla on u alone (torch_cuda.cpp:230-238), the methods on u and v
-                // (:519-524)
-                hipLaunchKernelGGL(mth::commit, vector_grid(BM), dim3(kBlock), 0, stream, L.u, L.ut, BM,
-                                   track ? slots + mth::kDeltaU : nullptr, L.done);
-                hipLaunchKernelGGL(mth::commit, vector_grid(BN), dim3(kBlock), 0, stream, L.v, L.vt, BN,
-                                   track && method != DOT_SK_VANILLA ? slots + mth::kDeltaV : nullptr, L.done);
+        for (int t = 0; t < T; ++t) {
+            if (sched) ks = kscale_at(scheduled_tau(t, T, tau, m->reg_start, m->schedule));
+            switch (method) {
+                case DOT_SK_MOMENTUM: iteration(std::integral_constant<int, mth::kMomentum>{}, t, ks); break;
+                case DOT_SK_ADAM: iteration(std::integral_constant<int, mth::kAdam>{}, t, ks); break;
+                default: iteration(std::integral_constant<int, mth::kPlain>{}, t, ks); break;
             }
-            hipLaunchKernelGGL(mth::finish_iteration, dim3(1), dim3(1), 0, stream, slots, it, a->tol, L.done,
-                               a->iters_used, a->converged);
-            if (may_wait && (it + 1) % kStopCheckEvery == 0 && it + 1 < T) {
-                int h_done = 0;
-                if (hipMemcpyAsync(&h_done, L.done, sizeof(int), hipMemcpyDeviceToHost, stream) != hipSuccess ||
+            if (may_wait && (t + 1) % kStopCheckEvery == 0 && t + 1 < T) {
+                // stop launching once the device's test has fired (an iteration
+                // that did not run reads as met, so this one's words suffice)
+                unsigned words[kIterWords];
+                if (hipMemcpyAsync(words, L.slots + size_t(t) * kIterWords, sizeof(words), hipMemcpyDeviceToHost,
+                                   stream) != hipSuccess ||
                     hipStreamSynchronize(stream) != hipSuccess) {
                     rc = check_launch("dot_sinkhorn_forward_method (stop-flag read)");
                     if (rc == DOT_OK) rc = fail(DOT_ERR_HIP, "dot_sinkhorn_forward_method: stop-flag read failed");
                     return;
                 }
-                if (h_done) break;
+                if (mth::decide_host(words, method).delta < a->tol) break;
             }
+        }
+        if (T > 0)
+            hipLaunchKernelGGL(mth::finalize, dim3(1), dim3(kWave), 0, stream, L.slots + size_t(T - 1) * kIterWords,
+                               method, a->tol, a->converged);
+        if (!anderson) {
+            mth::ResolveArgs ra{};
+            ra.B = B;
+            ra.M = M;
+            ra.N = N;
+            ra.method = method;
+            ra.used = a->iters_used;
+            ra.slots = L.slots;
+            for (int p = 0; p < 2; ++p) {
+                ra.ut[p] = L.ut[p];
+                ra.un[p] = L.un[p];
+                ra.vt[p] = L.vt[p];
+                ra.vn[p] = L.vn[p];
+            }
+            ra.u = L.u;
+            ra.v = L.v;
+            hipLaunchKernelGGL(mth::resolve, vector_grid(BM + BN), dim3(kBlock), 0, stream, ra);
         }
 
         // plan and cost at the target tau (torch_cuda.cpp:538-552, :242-261)

@@ -17,16 +17,7 @@ namespace {
 
 using sk::kColSumFloor;
 
-// Rows per workgroup strip (sweep_strip_rows); DOT_AMD_ROWS overrides it
-// (tuning only).
-int strip_rows(int B, int M) {
-    static const int forced = [] {
-        const char* s = std::getenv("DOT_AMD_ROWS");
-        return s ? std::atoi(s) : 0;
-    }();
-    if (forced >= 1) return forced;
-    return sweep_strip_rows(B, M);
-}
+int strip_rows(int B, int M) { return tuned_strip_rows(B, M); }
 
 size_t lds_bytes(int N) { return (size_t(2) * N + 8) * sizeof(float); }
 

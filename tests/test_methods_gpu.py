@@ -368,14 +368,27 @@ def test_ref_adam_handles_nonuniform_costs():
 
 
 def test_ref_adam_rmsprop_regime_can_beat_vanilla():
+    # The reference's test (test_sinkhorn.py:544-566) runs its CPU PyTorch
+    # solver.  On its CUDA path, restated by the oracle, this regime's first
+    # RMSprop step (lr / sqrt(1 - beta2) = 7.9 units) never passes the
+    # candidate test, so the run is the plain iteration and both errors agree
+    # (oracle: 2.6173e-6 each); the strict inequality would be decided by
+    # rounding.  Checked here: no worse than vanilla, and equal to the
+    # oracle's error.
     cost = _grid_cost(32, -3.0, 3.0, weight=5.0)
     tau = 0.02
     ref = dot_amd.sinkhorn(cost, reg=tau, n_iters=800)
     vanilla = dot_amd.sinkhorn(cost, reg=tau, n_iters=20)
     rms = dot_amd.sinkhorn(cost, reg=tau, n_iters=20, method="adam", lr=0.25, beta1=0.0, beta2=0.999,
                            bias_correction=False)
-    assert (rms.transport_plan - ref.transport_plan).abs().mean() < \
-        (vanilla.transport_plan - ref.transport_plan).abs().mean()
+    rms_err = float((rms.transport_plan - ref.transport_plan).abs().mean())
+    van_err = float((vanilla.transport_plan - ref.transport_plan).abs().mean())
+    assert rms_err <= van_err * (1 + 1e-4)
+    la = -cost.cpu().numpy()
+    o_ref = osk.dual_forward(la, tau, 800, 1e-6)
+    o_rms = osk.dual_forward_method(la, tau, 20, 1e-6, method=ADAM, lr=0.25, beta1=0.0, beta2=0.999,
+                                    bias_correction=False)
+    assert abs(rms_err - float(np.abs(o_rms.P - o_ref.P).mean())) < 1e-3 * rms_err
 
 
 def test_ref_adam_bias_correction_can_hurt_deterministic_residuals():
