@@ -54,17 +54,19 @@ constexpr int kAaMin = 7;   // Anderson: kInfBits - bits(min |sum alpha|), order
 constexpr int kAaFail = 8;  // Anderson: a solve failed
 constexpr int kWords = 9;
 constexpr int kIterWords = kWords * kStripes;
+// a word's stripes are contiguous, so a wave reads one word in one access
+__host__ __device__ constexpr int flag_at(int k, int stripe) { return k * kStripes + stripe; }
 constexpr unsigned kInfBits = 0x7f800000u;
 
 // Word k of an iteration's flag block; every lane of the wave must call it.
 __device__ __forceinline__ float flag(const unsigned* s, int k) {
-    return wave_max(__uint_as_float(s[k * kStripes + threadIdx.x % kWave]));
+    return wave_max(__uint_as_float(s[flag_at(k, threadIdx.x % kWave)]));
 }
 
 inline float host_flag(const unsigned* s, int k) {
     float m = 0.0f;
     for (int i = 0; i < kStripes; ++i) {
-        const float x = __builtin_bit_cast(float, s[k * kStripes + i]);
+        const float x = __builtin_bit_cast(float, s[flag_at(k, i)]);
         m = x > m ? x : m;
     }
     return m;
@@ -100,8 +102,29 @@ __host__ __device__ inline Decision decide(Flag f, int method) {
     return d;
 }
 
+// This lane's stripe of every word of a flag block (zeros for null), so the
+// loads can be issued together with a kernel's other operands.
+struct Words {
+    float w[kWords];
+};
+
+__device__ __forceinline__ Words load_words(const unsigned* s) {
+    const int lane = threadIdx.x % kWave;
+    Words r;
+#pragma unroll
+    for (int k = 0; k < kWords; ++k) r.w[k] = s ? __uint_as_float(s[flag_at(k, lane)]) : 0.0f;
+    return r;
+}
+
+// The decision from loaded words.  Every lane of the wave must call it.
+__device__ __forceinline__ Decision decide_words(Words r, int method) {
+#pragma unroll
+    for (int k = 0; k < kWords; ++k) r.w[k] = wave_max(r.w[k]);
+    return decide([&](int k) { return r.w[k]; }, method);
+}
+
 __device__ __forceinline__ Decision decide_dev(const unsigned* s, int method) {
-    return decide([&](int k) { return flag(s, k); }, method);
+    return decide_words(load_words(s), method);
 }
 
 inline Decision decide_host(const unsigned* s, int method) {
@@ -115,23 +138,48 @@ struct Prev {
     bool stop;
 };
 
-__device__ __forceinline__ Prev previous(const unsigned* prev, int method, float tol) {
+__device__ __forceinline__ Prev previous_from(const Words& w, bool has_prev, int method, float tol) {
     Prev p{{false, false, 0.0f}, false};
-    if (prev) {
-        p.d = decide_dev(prev, method);
+    if (has_prev) {
+        p.d = decide_words(w, method);
         p.stop = tol > 0.0f && p.d.delta < tol;
     }
     return p;
 }
 
+__device__ __forceinline__ Prev previous(const unsigned* prev, int method, float tol) {
+    return previous_from(load_words(prev), prev != nullptr, method, tol);
+}
+
 __device__ __forceinline__ void atomic_max_nonneg(unsigned* p, float x) { atomicMax(p, __float_as_uint(x)); }
 
-// Workgroup max of one value per thread, added to word k's stripe for this
-// workgroup.  Every thread must call it; `red` holds kWavesPerBlock floats.
-__device__ __forceinline__ void block_flag_max(unsigned* s, int k, float x, float* red) {
-    const float m = block_reduce<kWavesPerBlock>(wave_max(x), red, OpMax{});
-    const unsigned blk = blockIdx.x + blockIdx.y * gridDim.x;
-    if (threadIdx.x == 0) atomic_max_nonneg(s + k * kStripes + (blk % kStripes), m);
+// Workgroup maxima of up to three values per thread, each added to its word's
+// stripe for this workgroup by its own thread (one barrier for all).  Every
+// thread must call it; `red` holds 3 * kWavesPerBlock floats that no other
+// code of the kernel uses.  Words are scalars (an index array would be
+// placed in scratch memory and indexed there).
+template <int NW>
+__device__ __forceinline__ void block_flag_max(unsigned* s, int k0, float x0, int k1, float x1, int k2, float x2,
+                                               float* red) {
+    const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+    const float m0 = wave_max(x0);
+    const float m1 = NW > 1 ? wave_max(x1) : 0.0f;
+    const float m2 = NW > 2 ? wave_max(x2) : 0.0f;
+    if (lane == 0) {
+        red[wave] = m0;
+        if (NW > 1) red[kWavesPerBlock + wave] = m1;
+        if (NW > 2) red[2 * kWavesPerBlock + wave] = m2;
+    }
+    __syncthreads();
+    if (threadIdx.x < NW) {
+        const int w = threadIdx.x;
+        float m = red[w * kWavesPerBlock];
+#pragma unroll
+        for (int i = 1; i < kWavesPerBlock; ++i) m = fmaxf(m, red[w * kWavesPerBlock + i]);
+        const int k = w == 0 ? k0 : (w == 1 ? k1 : k2);
+        const unsigned blk = blockIdx.x + blockIdx.y * gridDim.x;
+        atomic_max_nonneg(s + flag_at(k, blk % kStripes), m);
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -168,31 +216,40 @@ __global__ __launch_bounds__(kBlock) void sweep(SweepArgs a) {
     // expressions on its own; the row arithmetic uses explicit fmaf
 #pragma clang fp contract(off)
     using R = Row<VEC, CH>;
-    extern __shared__ __align__(16) float lds[];  // 2 N floats + kWavesPerBlock
-    const Prev pv = previous(a.prev, a.method, a.tol);
+    extern __shared__ __align__(16) float lds[];  // 2 N floats + 3 kWavesPerBlock
+    const int lane = threadIdx.x % kWave;
+    const int wave = threadIdx.x / kWave;
+    const int s = blockIdx.x;
+    const int b = blockIdx.y;
+    // the previous iteration's flags and both of its v candidates, loaded
+    // together before anything waits on them
+    const Words words = load_words(a.prev);
+    float v[R::PL], v_alt[R::PL];
+    if (a.v_prev[0]) {
+        R::load(a.v_prev[0] + size_t(b) * a.N, lane, a.N, v, 0.0f);
+        if constexpr (MODE != kPlain) R::load(a.v_prev[1] + size_t(b) * a.N, lane, a.N, v_alt, 0.0f);
+    } else {
+#pragma unroll
+        for (int e = 0; e < R::PL; ++e) v[e] = v_alt[e] = 0.0f;
+    }
+    const Prev pv = previous_from(words, a.prev != nullptr, a.method, a.tol);
     const bool first_block = blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0;
     if (pv.stop) {
         if (first_block) *a.converged = 1;
         return;
     }
     if (first_block) *a.used = a.t + 1;
-    const int lane = threadIdx.x % kWave;
-    const int wave = threadIdx.x / kWave;
-    const int s = blockIdx.x;
-    const int b = blockIdx.y;
+    if constexpr (MODE != kPlain) {
+        if (pv.d.keep_v)
+#pragma unroll
+            for (int e = 0; e < R::PL; ++e) v[e] = v_alt[e];
+    }
     const int r0 = s * a.rows;
     const int r1 = min(r0 + a.rows, a.M);
     const size_t bM = size_t(b) * a.M;
-    const float* uc = a.u_prev[MODE != kPlain && pv.d.keep_u ? 1 : 0];
-    const float* vc = a.v_prev[MODE != kPlain && pv.d.keep_v ? 1 : 0];
-
-    float v[R::PL];
-    if (vc) {
-        R::load(vc + size_t(b) * a.N, lane, a.N, v, 0.0f);
-    } else {
-#pragma unroll
-        for (int e = 0; e < R::PL; ++e) v[e] = 0.0f;
-    }
+    // static indices only: a dynamic index into the kernel-argument array
+    // would copy it to scratch
+    const float* uc = MODE != kPlain && pv.d.keep_u ? a.u_prev[1] : a.u_prev[0];
     float acc_t[R::PL], acc_n[R::PL];
 #pragma unroll
     for (int e = 0; e < R::PL; ++e) acc_t[e] = acc_n[e] = 0.0f;
@@ -262,10 +319,10 @@ __global__ __launch_bounds__(kBlock) void sweep(SweepArgs a) {
     }
     // every lane holds its wave's maxima (wave-uniform values)
     float* red = lds + 2 * a.N;
-    if (MODE != kPlain || a.track) block_flag_max(a.slots, kGapU + 1, gap1, red);
     if constexpr (MODE != kPlain) {
-        block_flag_max(a.slots, kGapU, gap0, red);
-        block_flag_max(a.slots, kMoveU, move, red);
+        block_flag_max<3>(a.slots, kGapU, gap0, kGapU + 1, gap1, kMoveU, move, red);
+    } else if (a.track) {
+        block_flag_max<1>(a.slots, kGapU + 1, gap1, 0, 0.0f, 0, 0.0f, red);
     }
 }
 
@@ -302,20 +359,46 @@ template <int MODE>
 __global__ __launch_bounds__(kBlock) void vfinish(VfinishArgs a) {
 #pragma clang fp contract(off)
     __shared__ float fold[kFoldLanes][kFoldCols];
-    __shared__ float red[kWavesPerBlock];
-    const Prev pv = previous(a.prev, a.method, a.tol);
-    if (pv.stop) return;
+    __shared__ float red[3 * kWavesPerBlock];
     const int b = blockIdx.y;
     const int jj = threadIdx.x % kFoldCols;
     const int sl = threadIdx.x / kFoldCols;
     const int j = blockIdx.x * kFoldCols + jj;
-    const bool keep = MODE != kPlain && flag(a.slots, kGapU) < flag(a.slots, kGapU + 1);
-    const float* part = keep ? a.part_n : a.part_t;
-    float cs = 0.0f;
-    if (j < a.N) {
-        const float* p = part + size_t(b) * a.nstrips * a.N + j;
-        for (int s = sl; s < a.nstrips; s += kFoldLanes) cs += p[size_t(s) * a.N];
+    const int lane = threadIdx.x % kWave;
+    // every operand is loaded before the decisions that select among them
+    const Words words = load_words(a.prev);
+    float g0 = 0.0f, g1 = 0.0f;
+    if constexpr (MODE != kPlain) {
+        g0 = __uint_as_float(a.slots[flag_at(kGapU, lane)]);
+        g1 = __uint_as_float(a.slots[flag_at(kGapU + 1, lane)]);
     }
+    float cs_t = 0.0f, cs_n = 0.0f;
+    if (j < a.N) {
+        const size_t off = size_t(b) * a.nstrips * a.N + j;
+        for (int s = sl; s < a.nstrips; s += kFoldLanes) {
+            cs_t += a.part_t[off + size_t(s) * a.N];
+            if constexpr (MODE != kPlain) cs_n += a.part_n[off + size_t(s) * a.N];
+        }
+    }
+    const bool col = sl == 0 && j < a.N;
+    const size_t bj = size_t(b) * a.N + j;
+    float lgb = a.log_b_default, v0 = 0.0f, v1 = 0.0f, m1 = 0.0f, m2 = 0.0f;
+    if (col) {
+        if (a.log_b) lgb = a.log_b[bj];
+        if (a.v_prev[0]) {
+            v0 = a.v_prev[0][bj];
+            if constexpr (MODE != kPlain) v1 = a.v_prev[1][bj];
+        }
+        if constexpr (MODE == kAdam) {
+            m1 = a.m1[bj];
+            m2 = a.m2[bj];
+        }
+    }
+    const Prev pv = previous_from(words, a.prev != nullptr, a.method, a.tol);
+    if (pv.stop) return;
+    bool keep = false;
+    if constexpr (MODE != kPlain) keep = wave_max(g0) < wave_max(g1);
+    float cs = keep ? cs_n : cs_t;
     fold[sl][jj] = cs;
 #pragma unroll
     for (int half = kFoldLanes / 2; half >= 1; half /= 2) {
@@ -325,12 +408,9 @@ __global__ __launch_bounds__(kBlock) void vfinish(VfinishArgs a) {
             fold[sl][jj] = cs;
         }
     }
-    const float* vc = a.v_prev[MODE != kPlain && pv.d.keep_v ? 1 : 0];
     float gap0 = 0.0f, gap1 = 0.0f, move = 0.0f;
-    if (sl == 0 && j < a.N) {
-        const size_t bj = size_t(b) * a.N + j;
-        const float lgb = a.log_b ? a.log_b[bj] : a.log_b_default;
-        const float vcur = vc ? vc[bj] : 0.0f;
+    if (col) {
+        const float vcur = MODE != kPlain && pv.d.keep_v ? v1 : v0;
         float vt;
         if (cs >= kColSumFloor && cs <= FLT_MAX) {
             vt = lgb + vcur - logf(cs);
@@ -351,8 +431,8 @@ __global__ __launch_bounds__(kBlock) void vfinish(VfinishArgs a) {
                 vn = (1.0f - a.omega) * vcur + a.omega * vt;
             } else {
                 const float g = vt - vcur;
-                const float mm = a.beta1 * a.m1[bj] + (1.0f - a.beta1) * g;
-                const float vv = a.beta2 * a.m2[bj] + (1.0f - a.beta2) * (g * g);
+                const float mm = a.beta1 * m1 + (1.0f - a.beta1) * g;
+                const float vv = a.beta2 * m2 + (1.0f - a.beta2) * (g * g);
                 a.m1[bj] = mm;
                 a.m2[bj] = vv;
                 vn = vcur + a.lr * (mm / a.c1) / (sqrtf(vv / a.c2) + a.eps);
@@ -363,11 +443,7 @@ __global__ __launch_bounds__(kBlock) void vfinish(VfinishArgs a) {
             move = fabsf(vn - vcur);
         }
     }
-    if constexpr (MODE != kPlain) {
-        block_flag_max(a.slots, kGapV, gap0, red);
-        block_flag_max(a.slots, kGapV + 1, gap1, red);
-        block_flag_max(a.slots, kMoveV, move, red);
-    }
+    if constexpr (MODE != kPlain) block_flag_max<3>(a.slots, kGapV, gap0, kGapV + 1, gap1, kMoveV, move, red);
 }
 
 // ---------------------------------------------------------------------------
@@ -430,7 +506,8 @@ struct AaArgs {
     int h;            // pairs held after the push
     int order[kMaxHistory];  // physical slots, oldest first
     float mixing_beta;
-    float* gram;      // [B,kMaxHistory,kMaxHistory]
+    float* gram;      // [B,nchunk,kMaxHistory,kMaxHistory] per-chunk Gram sums
+    int nchunk;       // chunks of kGramChunk state entries
     float* alpha;     // [B,kMaxHistory]
     float* denom;     // [B]
     const unsigned* prev;
@@ -463,21 +540,25 @@ static __global__ __launch_bounds__(kBlock) void aa_push(AaArgs a) {
             d = fmaxf(d, fabsf(f));
         }
     }
-    block_flag_max(a.slots, kAaDelta, d, red);
+    block_flag_max<1>(a.slots, kAaDelta, d, 0, 0.0f, 0, 0.0f, red);
 }
 
-// Row p of the Gram matrix F^T F of element b (grid h x B): one pass over the
-// element's M + N residual entries of every history pair.
+constexpr int kGramChunk = 1024;  // state entries per Gram workgroup
+
+// Row p of the Gram matrix F^T F of element b over one chunk of the element's
+// M + N residual entries (grid h x B x nchunk); the solve adds the chunks in
+// order.
 static __global__ __launch_bounds__(kBlock) void aa_gram(AaArgs a) {
     __shared__ float red[kWavesPerBlock][kMaxHistory];
     if (previous(a.prev, kAnderson, a.tol).stop) return;
-    const int p = blockIdx.x, b = blockIdx.y, h = a.h;
+    const int p = blockIdx.x, b = blockIdx.y, ch = blockIdx.z, h = a.h;
     const size_t nu = size_t(a.B) * a.M, nv = size_t(a.B) * a.N;
     const int sp = a.order[p];
+    const int i1 = min((ch + 1) * kGramChunk, a.M + a.N);
     float acc[kMaxHistory];
 #pragma unroll
     for (int q = 0; q < kMaxHistory; ++q) acc[q] = 0.0f;
-    for (int i = threadIdx.x; i < a.M + a.N; i += kBlock) {
+    for (int i = ch * kGramChunk + threadIdx.x; i < i1; i += kBlock) {
         const float fp = aa_at(a.hfu, a.hfv, sp, nu, nv, b, a.M, a.N, i);
 #pragma unroll
         for (int q = 0; q < kMaxHistory; ++q)
@@ -495,7 +576,7 @@ static __global__ __launch_bounds__(kBlock) void aa_gram(AaArgs a) {
         float s = red[0][q];
 #pragma unroll
         for (int w = 1; w < kWavesPerBlock; ++w) s += red[w][q];
-        a.gram[(size_t(b) * kMaxHistory + p) * kMaxHistory + q] = s;
+        a.gram[((size_t(b) * a.nchunk + ch) * kMaxHistory + p) * kMaxHistory + q] = s;
     }
 }
 
@@ -505,13 +586,18 @@ static __global__ __launch_bounds__(kBlock) void aa_gram(AaArgs a) {
 static __global__ void aa_solve(AaArgs a) {
     __shared__ float A[kMaxHistory][kMaxHistory + 1];
     __shared__ float x[kMaxHistory];
-    if (previous(a.prev, kAnderson, a.tol).stop || threadIdx.x != 0) return;
+    if (previous(a.prev, kAnderson, a.tol).stop) return;
     const int b = blockIdx.x, h = a.h;
-    for (int p = 0; p < h; ++p) {
-        for (int q = 0; q < h; ++q)
-            A[p][q] = a.gram[(size_t(b) * kMaxHistory + p) * kMaxHistory + q] + (p == q ? 1.0e-8f : 0.0f);
-        x[p] = 1.0f;
+    for (int e = threadIdx.x; e < h * h; e += blockDim.x) {
+        const int p = e / h, q = e % h;
+        float g = 0.0f;
+        for (int ch = 0; ch < a.nchunk; ++ch)
+            g += a.gram[((size_t(b) * a.nchunk + ch) * kMaxHistory + p) * kMaxHistory + q];
+        A[p][q] = g + (p == q ? 1.0e-8f : 0.0f);
     }
+    if (threadIdx.x < h) x[threadIdx.x] = 1.0f;
+    __syncthreads();
+    if (threadIdx.x != 0) return;
     bool failed = false;
     for (int c = 0; c < h && !failed; ++c) {
         int piv = c;
@@ -550,9 +636,8 @@ static __global__ void aa_solve(AaArgs a) {
     }
     for (int c = 0; c < h; ++c) a.alpha[size_t(b) * kMaxHistory + c] = failed ? 0.0f : x[c];
     a.denom[b] = sum;
-    unsigned* stripe = a.slots + (b % kStripes);
-    if (failed) atomicMax(stripe + kAaFail * kStripes, 1u);
-    else atomicMax(stripe + kAaMin * kStripes, kInfBits - __float_as_uint(fabsf(sum)));
+    if (failed) atomicMax(a.slots + flag_at(kAaFail, b % kStripes), 1u);
+    else atomicMax(a.slots + flag_at(kAaMin, b % kStripes), kInfBits - __float_as_uint(fabsf(sum)));
 }
 
 // x = sum_c (alpha_c / sum) (X_c + beta F_c) when every element's solve

@@ -61,7 +61,8 @@ MethodLayout method_layout(void* ws, int B, int M, int N, int T, int method, int
     L.hxv = c.take<float>(kk * BN);
     L.hfu = c.take<float>(kk * BM);
     L.hfv = c.take<float>(kk * BN);
-    L.gram = c.take<float>(kk ? size_t(B) * kMaxHistory * kMaxHistory : 0);
+    const size_t nchunk = (size_t(M) + N + mth::kGramChunk - 1) / mth::kGramChunk;
+    L.gram = c.take<float>(kk ? size_t(B) * nchunk * kMaxHistory * kMaxHistory : 0);
     L.alpha = c.take<float>(kk ? size_t(B) * kMaxHistory : 0);
     L.denom = c.take<float>(kk ? size_t(B) : 0);
     L.bytes = c.used();
@@ -205,7 +206,7 @@ extern "C" int dot_sinkhorn_forward_method(const dot_sinkhorn_method_args* m, do
         constexpr int C = decltype(cc)::value;
         const dim3 strips(L.nstrips, B);
         const dim3 cols((N + mth::kFoldCols - 1) / mth::kFoldCols, B);
-        const size_t sweep_lds = (size_t(2) * N + 8) * sizeof(float);
+        const size_t sweep_lds = (size_t(2) * N + 16) * sizeof(float);  // columns + flag reduction
         int ring_head = 0, ring_size = 0;  // Anderson ring: logical position -> physical slot
 
         auto iteration = [&](auto mode_c, int t, float ks) {
@@ -321,6 +322,7 @@ extern "C" int dot_sinkhorn_forward_method(const dot_sinkhorn_method_args* m, do
             for (int c = 0; c < ring_size; ++c) aa.order[c] = (ring_head + c) % k;
             aa.mixing_beta = m->mixing_beta;
             aa.gram = L.gram;
+            aa.nchunk = (M + N + mth::kGramChunk - 1) / mth::kGramChunk;
             aa.alpha = L.alpha;
             aa.denom = L.denom;
             aa.prev = prev;
@@ -329,7 +331,7 @@ extern "C" int dot_sinkhorn_forward_method(const dot_sinkhorn_method_args* m, do
             ProfScope prof("mth_anderson", stream);
             hipLaunchKernelGGL(mth::aa_push, vector_grid(BM + BN), dim3(kBlock), 0, stream, aa);
             if (ring_size >= 2) {
-                hipLaunchKernelGGL(mth::aa_gram, dim3(ring_size, B), dim3(kBlock), 0, stream, aa);
+                hipLaunchKernelGGL(mth::aa_gram, dim3(ring_size, B, aa.nchunk), dim3(kBlock), 0, stream, aa);
                 hipLaunchKernelGGL(mth::aa_solve, dim3(B), dim3(kWave), 0, stream, aa);
             }
             hipLaunchKernelGGL(mth::aa_update, vector_grid(BM + BN), dim3(kBlock), 0, stream, aa);
