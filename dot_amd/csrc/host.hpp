@@ -81,6 +81,12 @@ inline int sweep_strip_rows(int B, int M) {
     return r;
 }
 
+// dot_sinkhorn_forward with an optional per-iteration K scale (a tau
+// schedule): ks_host[t] on the host and ks_dev[t] on the device for
+// t < max_iter, or both null.  Defined in sinkhorn.hip.
+int sinkhorn_forward_scheduled(const dot_sinkhorn_fwd_args* a, const float* ks_host, const float* ks_dev,
+                               hipStream_t stream);
+
 // sweep_strip_rows, or the value of DOT_AMD_ROWS when set (tuning only).
 inline int tuned_strip_rows(int B, int M) {
     static const int forced = [] {

@@ -6,6 +6,7 @@
 #include <cmath>
 #include <string>
 #include <type_traits>
+#include <vector>
 
 #include "host.hpp"
 #include "methods.cuh"
@@ -110,6 +111,24 @@ __global__ void batch_sum_m(const float* partial, int n, float* out) {
     if (threadIdx.x == 0) out[b] = s;
 }
 
+// The per-iteration K scales of a schedule reach the device as kernel
+// arguments, kTableChunk at a time (no host buffer has to outlive the call).
+constexpr int kTableChunk = 256;
+struct TableChunk {
+    float v[kTableChunk];
+};
+
+__global__ void fill_table(float* dst, TableChunk c, int n) {
+    if (blockIdx.x != 0 || threadIdx.x != 0) return;
+#pragma unroll
+    for (int i = 0; i < kTableChunk; ++i)
+        if (i < n) dst[i] = c.v[i];
+}
+
+// Workspace of the vanilla method (plain or scheduled): the K-scale table,
+// then dot_sinkhorn_forward's workspace.
+size_t vanilla_table_bytes(int T) { return (size_t(T) * sizeof(float) + 255) & ~size_t(255); }
+
 int check_method_args(const dot_sinkhorn_method_args* m) {
     if (m->method < DOT_SK_VANILLA || m->method > DOT_SK_ADAM)
         return fail(DOT_ERR_INVALID_ARG, "method must be 0 (vanilla), 1 (momentum), 2 (anderson) or 3 (adam)");
@@ -130,6 +149,8 @@ using namespace dot_amd;
 extern "C" size_t dot_sinkhorn_forward_method_workspace_bytes(int B, int M, int N, int max_iter, int method,
                                                               int anderson_k) {
     if (B < 0 || M < 0 || N < 0 || max_iter < 0 || anderson_k < 0) return 0;
+    if (method == DOT_SK_VANILLA)
+        return vanilla_table_bytes(max_iter) + dot_sinkhorn_forward_workspace_bytes(B, M, N, max_iter, 0);
     return method_layout(nullptr, B, M, N, max_iter, method, std::min(anderson_k, kMaxHistory)).bytes;
 }
 
@@ -174,16 +195,41 @@ extern "C" int dot_sinkhorn_forward_method(const dot_sinkhorn_method_args* m, do
     }
     if (!a->scores) return fail(DOT_ERR_INVALID_ARG, "scores is NULL");
 
+    const float tau = a->tau;
+    const float sign = static_cast<float>(a->scores_kind);
+    auto kscale_at = [&](float t) { return sign * (1.0f / t); };  // kernels.cu:1350 (K = log_alpha * (1/tau))
+
+    if (method == DOT_SK_VANILLA) {
+        // The plain iteration, scheduled or not, runs on dot_sinkhorn_forward's
+        // tiers with each iteration's K scale (sinkhorn_dual_vanilla_cuda,
+        // torch_cuda.cpp:147-264: K rebuilt at every iteration's tau).
+        const size_t tb = vanilla_table_bytes(sched ? T : 0);
+        if (!a->workspace || a->workspace_bytes < tb)
+            return fail(DOT_ERR_WORKSPACE, "workspace smaller than dot_sinkhorn_forward_method_workspace_bytes()");
+        dot_sinkhorn_fwd_args f = *a;
+        f.workspace = static_cast<char*>(a->workspace) + tb;
+        f.workspace_bytes = a->workspace_bytes - tb;
+        if (!sched) return sinkhorn_forward_scheduled(&f, nullptr, nullptr, stream);
+        std::vector<float> ks(static_cast<size_t>(T));
+        for (int t = 0; t < T; ++t) ks[t] = kscale_at(scheduled_tau(t, T, tau, m->reg_start, m->schedule));
+        float* table = static_cast<float*>(a->workspace);
+        for (int t0 = 0; t0 < T; t0 += kTableChunk) {
+            TableChunk c{};
+            const int n = std::min(kTableChunk, T - t0);
+            std::copy(ks.begin() + t0, ks.begin() + t0 + n, c.v);
+            hipLaunchKernelGGL(fill_table, dim3(1), dim3(kWave), 0, stream, table + t0, c, n);
+        }
+        if (int rc = check_launch("dot_sinkhorn_forward_method (K-scale table)")) return rc;
+        return sinkhorn_forward_scheduled(&f, ks.data(), table, stream);
+    }
+
     const int k = std::min(m->anderson_k, kMaxHistory);
     const MethodLayout L = method_layout(a->workspace, B, M, N, T, method, k);
     if (!a->workspace || a->workspace_bytes < L.bytes)
         return fail(DOT_ERR_WORKSPACE, "workspace smaller than dot_sinkhorn_forward_method_workspace_bytes()");
 
-    const float tau = a->tau;
     const float log_a_default = -std::log(static_cast<float>(M));  // torch_cuda.cpp:42
     const float log_b_default = -std::log(static_cast<float>(N));
-    const float sign = static_cast<float>(a->scores_kind);
-    auto kscale_at = [&](float t) { return sign * (1.0f / t); };  // kernels.cu:1350 (K = log_alpha * (1/tau))
     const bool vec4 = (N % 4 == 0) && aligned16(a->scores) && (!a->plan || aligned16(a->plan));
     const size_t BM = size_t(B) * M, BN = size_t(B) * N;
 

@@ -241,7 +241,8 @@ __device__ __forceinline__ void gather(const unsigned long long* res_row, int N,
 // ---------------------------------------------------------------------------
 struct FwdArgs {
     const float* X;       // scores [B,M,N]
-    float kscale;         // K = X * kscale
+    float kscale;         // K = X * kscale (the plan's; every iteration's unless scheduled)
+    const float* kscale_t;  // [max_iter] K scale of each iteration (tau schedule), SCHED kernels
     int scores_kind;      // +1 log_alpha, -1 cost
     const float* log_a;   // [B,M] or null
     const float* log_b;   // [B,N] or null
@@ -272,7 +273,7 @@ struct FwdArgs {
 // max-shifted LSE of column j over all M rows when colsum underflows,
 // kernels.cu:629-671), all-gather of v.  The batch-global stop test of
 // iteration t-1 is read during iteration t, as in res::forward.
-template <int VEC, int CH>
+template <int VEC, int CH, bool SCHED = false>
 __global__ __launch_bounds__(kThreads) void forward(FwdArgs a) {
     using R = Row<VEC, CH>;
     constexpr int PL = R::PL;
@@ -299,7 +300,10 @@ __global__ __launch_bounds__(kThreads) void forward(FwdArgs a) {
     const size_t bM = size_t(b) * a.M;
     const size_t bN = size_t(b) * a.N;
     const bool check = a.tol > 0.0f;
-    const float kscale2 = a.kscale * kLog2E;
+    float kscale2 = a.kscale * kLog2E;
+    // scheduled runs: this iteration's scale, and the next one's already in flight
+    float ks_it = a.kscale;
+    float ks_next = (SCHED && a.max_iter > 0) ? a.kscale_t[0] : a.kscale;
 
     for (int l = threadIdx.x; l < a.R; l += kThreads) {
         const int i = row0 + l;
@@ -320,6 +324,11 @@ __global__ __launch_bounds__(kThreads) void forward(FwdArgs a) {
     for (int t = 1; t <= a.max_iter; ++t) {
         const int cur = t & 1, prev = cur ^ 1;
         const bool test = check && t >= 2;
+        if constexpr (SCHED) {
+            ks_it = ks_next;
+            kscale2 = ks_it * kLog2E;
+            if (t < a.max_iter) ks_next = a.kscale_t[t];
+        }
         unsigned long long* ds = a.dxchg + size_t((t - 1) % res::kDeltaSlots) * G;
         unsigned long long dpre[res::kDeltaPrefetch];
         if (test && wave == 0) {
@@ -398,14 +407,14 @@ __global__ __launch_bounds__(kThreads) void forward(FwdArgs a) {
                              for (int i = 0; i < a.M; ++i) {
                                  const float ui = res::collect(const_cast<unsigned long long*>(urow + i), unsigned(t),
                                                                a.spin_limit, a.status, dead);
-                                 mx = fmaxf(mx, col[size_t(i) * a.N] * a.kscale + ui);
+                                 mx = fmaxf(mx, col[size_t(i) * a.N] * ks_it + ui);
                              }
                              float sm = 0.0f;
                              for (int i = 0; i < a.M; ++i) {
                                  const float ui = __uint_as_float(static_cast<unsigned>(__hip_atomic_load(
                                      const_cast<unsigned long long*>(urow + i), __ATOMIC_RELAXED,
                                      __HIP_MEMORY_SCOPE_AGENT)));
-                                 sm += safe_exp(col[size_t(i) * a.N] * a.kscale + ui - mx);
+                                 sm += safe_exp(col[size_t(i) * a.N] * ks_it + ui - mx);
                              }
                              vn = lds_lb[j] - (mx + logf(fmaxf(sm, sk::kSumFloor)));
                          }

@@ -487,7 +487,8 @@ struct OpMaxNan {  // max that keeps a NaN (a timed-out poll) instead of droppin
 
 struct FwdResArgs {
     const float* X;       // scores [B,M,N]
-    float kscale;         // K = X * kscale
+    float kscale;         // K = X * kscale (the plan's; every iteration's unless scheduled)
+    const float* kscale_t;  // [max_iter] K scale of each iteration (tau schedule), SCHED kernels
     int scores_kind;      // +1 log_alpha, -1 cost
     const float* log_a;   // [B,M] or null
     const float* log_b;   // [B,N] or null
@@ -548,7 +549,7 @@ __device__ __forceinline__ float global_delta(const FwdResArgs& a, int t, float*
 // result.
 constexpr int kDeltaPrefetch = 4;  // delta loads in flight per lane of wave 0 (covers 256 workgroups)
 
-template <int VEC, int CH, int RPW>
+template <int VEC, int CH, int RPW, bool SCHED = false>
 __global__ __launch_bounds__(kThreads) void forward(FwdResArgs a) {
     using R = Row<VEC, CH>;
     constexpr int PL = R::PL;
@@ -611,7 +612,10 @@ __global__ __launch_bounds__(kThreads) void forward(FwdResArgs a) {
     float lga_slot[RPW / GR];
 #pragma unroll
     for (int g = 0; g < RPW / GR; ++g) lga_slot[g] = lds_la[wave + kWaves * (g * GR + slot_of_lane<GR>(lane))];
-    const float kscale2 = a.kscale * kLog2E;
+    float kscale2 = a.kscale * kLog2E;
+    // scheduled runs: this iteration's scale, and the next one's already in flight
+    float ks_it = a.kscale;
+    float ks_next = (SCHED && a.max_iter > 0) ? a.kscale_t[0] : a.kscale;
     bool dead = false;
     int used = a.max_iter;
     int conv = 0;
@@ -619,6 +623,11 @@ __global__ __launch_bounds__(kThreads) void forward(FwdResArgs a) {
     for (int t = 1; t <= a.max_iter; ++t) {
         const int cur = t & 1, prev = cur ^ 1;
         const bool test = check && t >= 2;
+        if constexpr (SCHED) {
+            ks_it = ks_next;
+            kscale2 = ks_it * kLog2E;
+            if (t < a.max_iter) ks_next = a.kscale_t[t];
+        }
         unsigned long long* ds = a.dxchg + size_t((t - 1) % kDeltaSlots) * G;
         unsigned long long dpre[kDeltaPrefetch];
         if (test && wave == 0) {
@@ -745,7 +754,7 @@ __global__ __launch_bounds__(kThreads) void forward(FwdResArgs a) {
                 const float u = lds_u[cur * ROWS + l];
 #pragma unroll
                 for (int e = 0; e < PL; ++e)
-                    if (R::valid(lane, e, a.N)) cm[e] = fmaxf(cm[e], fmaf(x[k][e], a.kscale, u));
+                    if (R::valid(lane, e, a.N)) cm[e] = fmaxf(cm[e], fmaf(x[k][e], ks_it, u));
             }
             tree_combine<VEC, CH>(cm, part, a.N, OpMax{});
             unsigned long long* fslot = a.fxchg + size_t(cur) * 2 * G * a.N;
@@ -784,7 +793,7 @@ __global__ __launch_bounds__(kThreads) void forward(FwdResArgs a) {
                 const float u = lds_u[cur * ROWS + l];
 #pragma unroll
                 for (int e = 0; e < PL; ++e)
-                    if (R::valid(lane, e, a.N)) sm[e] += safe_exp(fmaf(x[k][e], a.kscale, u) - mxl[e]);
+                    if (R::valid(lane, e, a.N)) sm[e] += safe_exp(fmaf(x[k][e], ks_it, u) - mxl[e]);
             }
             tree_combine<VEC, CH>(sm, part, a.N);
             unsigned long long* sslot = fslot + size_t(G) * a.N;

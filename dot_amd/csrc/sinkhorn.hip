@@ -284,13 +284,14 @@ StreamCfg stream_config(int B, int M, int N) {
 // the device can hold them all at once.
 
 bool launch_stream_forward(const dot_sinkhorn_fwd_args* a, const FwdLayout& L, const StreamCfg& sc,
-                           float kscale, float log_a_default, float log_b_default, bool keep, bool ret_log,
-                           bool vec4, hipStream_t stream) {
+                           float kscale, const float* ks_dev, float log_a_default, float log_b_default,
+                           bool keep, bool ret_log, bool vec4, hipStream_t stream) {
     const int B = a->B, M = a->M, N = a->N, G = B * sc.W;
     if (!L.pst || size_t(G) > L.pst_groups) return false;
     pst::FwdArgs r{};
     r.X = a->scores;
     r.kscale = kscale;
+    r.kscale_t = ks_dev;
     r.scores_kind = a->scores_kind;
     r.log_a = a->log_a;
     r.log_b = a->log_b;
@@ -329,7 +330,8 @@ bool launch_stream_forward(const dot_sinkhorn_fwd_args* a, const FwdLayout& L, c
                            sizeof(float);
         launch_fill_zero(L.pst, 2 * words, stream);
         ProfScope prof("sk_fwd_persistent", stream);
-        ok = launch_cooperative(pst::forward<V, C>, r, G, res::kThreads, lds, stream);
+        ok = ks_dev ? launch_cooperative(pst::forward<V, C, true>, r, G, res::kThreads, lds, stream)
+                    : launch_cooperative(pst::forward<V, C>, r, G, res::kThreads, lds, stream);
     });
     if (!ok) return false;
     if (a->cost) {
@@ -343,13 +345,14 @@ bool launch_stream_forward(const dot_sinkhorn_fwd_args* a, const FwdLayout& L, c
 // Cooperative launch of the register-resident forward; false when this shape or
 // device cannot host it (the caller then runs the streaming sweeps).
 bool launch_resident_forward(const dot_sinkhorn_fwd_args* a, const FwdLayout& L, const ResidentCfg& rc,
-                             float kscale, float log_a_default, float log_b_default, bool keep,
-                             bool ret_log, hipStream_t stream) {
+                             float kscale, const float* ks_dev, float log_a_default, float log_b_default,
+                             bool keep, bool ret_log, hipStream_t stream) {
     const int groups = a->B * rc.W;
     if (!L.xchg || size_t(groups) > L.groups) return false;
     res::FwdResArgs r{};
     r.X = a->scores;
     r.kscale = kscale;
+    r.kscale_t = ks_dev;
     r.scores_kind = a->scores_kind;
     r.log_a = a->log_a;
     r.log_b = a->log_b;
@@ -384,7 +387,7 @@ bool launch_resident_forward(const dot_sinkhorn_fwd_args* a, const FwdLayout& L,
         constexpr int RPW = decltype(rr)::value;
         const size_t lds =
             (size_t(12) * a->N + 3 * res::kWaves * RPW + res::kFwdScratch) * sizeof(float);
-        auto kernel = res::forward<V, C, RPW>;
+        auto kernel = ks_dev ? res::forward<V, C, RPW, true> : res::forward<V, C, RPW>;
         int per_cu = 0;
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, res::kThreads, lds) != hipSuccess ||
             per_cu < 1 || int64_t(per_cu) * device_cus() < groups)
@@ -417,7 +420,13 @@ extern "C" size_t dot_sinkhorn_forward_workspace_bytes(int B, int M, int N, int 
 }
 
 extern "C" int dot_sinkhorn_forward(const dot_sinkhorn_fwd_args* a, dot_stream_t stream_) {
-    hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+    return dot_amd::sinkhorn_forward_scheduled(a, nullptr, nullptr, reinterpret_cast<hipStream_t>(stream_));
+}
+
+// The forward with an optional per-iteration K scale (a tau schedule):
+// ks_host[t] and its device copy ks_dev[t] for t < max_iter, or both null.
+int dot_amd::sinkhorn_forward_scheduled(const dot_sinkhorn_fwd_args* a, const float* ks_host,
+                                        const float* ks_dev, hipStream_t stream) {
     if (!a) return fail(DOT_ERR_INVALID_ARG, "args is NULL");
     if (int rc = check_shape(a->B, a->M, a->N)) return rc;
     if (!valid_tau(a->tau)) return fail(DOT_ERR_INVALID_ARG, "tau must be > 0");
@@ -460,13 +469,13 @@ extern "C" int dot_sinkhorn_forward(const dot_sinkhorn_fwd_args* a, dot_stream_t
     const size_t lds = lds_bytes(N);
 
     const ResidentCfg rc = resident_config<true>(B, M, N, vec4);
-    if (rc.ok && launch_resident_forward(a, L, rc, kscale, log_a_default, log_b_default, keep, ret_log,
+    if (rc.ok && launch_resident_forward(a, L, rc, kscale, ks_dev, log_a_default, log_b_default, keep, ret_log,
                                          stream))
         return check_launch("dot_sinkhorn_forward");
     (void)hipGetLastError();  // a refused cooperative launch falls back to the next tier
     const StreamCfg sc = stream_config(B, M, N);
-    if (sc.ok && launch_stream_forward(a, L, sc, kscale, log_a_default, log_b_default, keep, ret_log, vec4,
-                                       stream))
+    if (sc.ok && launch_stream_forward(a, L, sc, kscale, ks_dev, log_a_default, log_b_default, keep, ret_log,
+                                       vec4, stream))
         return check_launch("dot_sinkhorn_forward");
     (void)hipGetLastError();
 
@@ -477,9 +486,10 @@ extern "C" int dot_sinkhorn_forward(const dot_sinkhorn_fwd_args* a, dot_stream_t
         constexpr int C = decltype(cc)::value;
         for (int t = 1; t <= T; ++t) {
             const int cur = t & 1, prev = (t - 1) & 1;
+            const float ks = ks_host ? ks_host[t - 1] : kscale;
             sk::FwdSweepArgs s{};
             s.X = a->scores;
-            s.kscale = kscale;
+            s.kscale = ks;
             s.log_a = a->log_a;
             s.log_a_default = log_a_default;
             s.v_old = L.vbuf + size_t(prev) * B * N;
@@ -503,7 +513,7 @@ extern "C" int dot_sinkhorn_forward(const dot_sinkhorn_fwd_args* a, dot_stream_t
             cb.partial = L.partial;
             cb.nstrips = L.nstrips;
             cb.X = a->scores;
-            cb.kscale = kscale;
+            cb.kscale = ks;
             cb.u_new = s.u_new;
             cb.log_b = a->log_b;
             cb.log_b_default = log_b_default;

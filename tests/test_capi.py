@@ -115,8 +115,12 @@ def test_method_forward_rejects_bad_arguments_on_the_host(lib):
     q = lib.dot_sinkhorn_forward_method_workspace_bytes
     q.restype = ctypes.c_size_t
     # Anderson keeps anderson_k (state, residual) pairs: the query grows with it
-    assert q(2, 64, 64, 50, 2, 8) > q(2, 64, 64, 50, 2, 2) > q(2, 64, 64, 50, 0, 2) > 0
+    assert q(2, 64, 64, 50, 2, 8) > q(2, 64, 64, 50, 2, 2) > 0
     assert q(2, 64, 64, 50, 3, 5) > q(2, 64, 64, 50, 1, 5)  # Adam's moments
+    # the plain method runs on dot_sinkhorn_forward's workspace after a table of T scales
+    fq = lib.dot_sinkhorn_forward_workspace_bytes
+    fq.restype = ctypes.c_size_t
+    assert q(2, 64, 64, 50, 0, 5) == fq(2, 64, 64, 50, 0) + 256
     assert q(-1, 64, 64, 50, 0, 5) == 0
     assert f(None, None) == DOT_ERR_INVALID_ARG
     dummy = ctypes.c_int(0)

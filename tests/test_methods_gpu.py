@@ -82,6 +82,31 @@ def test_schedule_matches_oracle(schedule, shape):
         assert rel_err(P, ref.P) < FWD_TOL, (T, reg_start)
 
 
+TIERS = {"resident": {}, "persistent": {"DOT_AMD_RESIDENT": "0"},
+         "sweeps": {"DOT_AMD_RESIDENT": "0", "DOT_AMD_PERSISTENT": "0"}}
+
+
+@pytest.mark.parametrize("tier", sorted(TIERS))
+@pytest.mark.parametrize("shape", [(2, 40, 56), (1, 37, 29), (3, 64, 256), (1, 130, 1030)])
+def test_scheduled_plain_iteration_on_every_tier(tier, shape, monkeypatch):
+    # the plain method runs on the vanilla forward's tiers with a per-iteration K scale
+    for k, v in TIERS[tier].items():
+        monkeypatch.setenv(k, v)
+    B, M, N = shape
+    la, lga, lgb = _case(17 + N, B, M, N, marginals=True)
+    for schedule, T in ((LIN, 1), (COS, 9), (EXP, 25)):
+        print(f"tier={tier} shape={shape} schedule={schedule} T={T}", flush=True)
+        P, used, conv = _gpu(la, 0.1, T, 0.0, lga, lgb, schedule=schedule, reg_start=0.4)
+        ref = _oracle(la, 0.1, T, 0.0, lga, lgb, schedule=schedule, reg_start=0.4)
+        assert used == T and conv == 0
+        assert rel_err(P, ref.P) < FWD_TOL, (schedule, T)
+    # the device stop test under a schedule
+    P, used, conv = _gpu(la, 0.1, 150, 1e-3, lga, lgb, schedule=COS, reg_start=0.15)
+    ref = _oracle(la, 0.1, 150, 1e-3, lga, lgb, schedule=COS, reg_start=0.15)
+    assert conv == int(ref.converged) and used == ref.n_iters_used
+    assert rel_err(P, ref.P) < FWD_TOL
+
+
 def test_schedule_with_start_equal_to_target_is_the_plain_iteration():
     la, _, _ = _case(3, 2, 48, 40)
     P_plain, _, _ = _gpu(la, 0.1, 30)
