@@ -491,7 +491,12 @@ static __global__ __launch_bounds__(kBlock) void resolve(ResolveArgs a) {
 // ---------------------------------------------------------------------------
 // Anderson mixing (torch_cuda.cpp:395-446) on the state x = (u, v) of each
 // batch element, with a ring of up to kMaxHistory (x, f = x_new - x) pairs.
+// The Gram matrix F^T F of the ring is kept across iterations: a push adds
+// the new residual's products with every pair in the ring (the others'
+// products are unchanged), so an iteration reads the history once.
 // ---------------------------------------------------------------------------
+constexpr int kGramChunk = kBlock;  // state entries per push workgroup (one per thread)
+
 struct AaArgs {
     int B, M, N;
     float* xu;        // [B,M] state
@@ -504,10 +509,11 @@ struct AaArgs {
     float* hfv;       // [k,B,N]
     int slot;         // physical slot of the newest pair
     int h;            // pairs held after the push
-    int order[kMaxHistory];  // physical slots, oldest first
+    int order[kMaxHistory];  // physical slots, oldest first (the newest is order[h-1] = slot)
     float mixing_beta;
-    float* gram;      // [B,nchunk,kMaxHistory,kMaxHistory] per-chunk Gram sums
+    float* dots;      // [B,nchunk,kMaxHistory] per-chunk products of the new residual with order[q]
     int nchunk;       // chunks of kGramChunk state entries
+    float* gram;      // [B,kMaxHistory,kMaxHistory] by physical slot, kept across iterations
     float* alpha;     // [B,kMaxHistory]
     float* denom;     // [B]
     const unsigned* prev;
@@ -515,122 +521,134 @@ struct AaArgs {
     float tol;
 };
 
-__device__ __forceinline__ float aa_at(const float* hu, const float* hv, int s, size_t nu, size_t nv, int b, int M,
-                                       int N, int i) {
-    return i < M ? hu[size_t(s) * nu + size_t(b) * M + i] : hv[size_t(s) * nv + size_t(b) * N + (i - M)];
-}
-
-// Push (x, x_new - x) into the ring; the residual's max into the delta word.
+// Push (x, x_new - x) into the ring for one chunk of one element's state
+// (grid nchunk x B), with the chunk's products of the new residual and every
+// residual in the ring, and the residual's max into the delta word.
 static __global__ __launch_bounds__(kBlock) void aa_push(AaArgs a) {
-    __shared__ float red[kWavesPerBlock];
+    __shared__ float red[3 * kWavesPerBlock];
+    __shared__ float dred[kWavesPerBlock][kMaxHistory];
     if (previous(a.prev, kAnderson, a.tol).stop) return;
-    const size_t nu = size_t(a.B) * a.M, nv = size_t(a.B) * a.N, n = nu + nv;
-    float d = 0.0f;
-    for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += size_t(gridDim.x) * blockDim.x) {
-        if (i < nu) {
-            const float x = a.xu[i], f = a.nu[i] - x;
-            a.hxu[size_t(a.slot) * nu + i] = x;
-            a.hfu[size_t(a.slot) * nu + i] = f;
-            d = fmaxf(d, fabsf(f));
-        } else {
-            const size_t k = i - nu;
-            const float x = a.xv[k], f = a.nv[k] - x;
-            a.hxv[size_t(a.slot) * nv + k] = x;
-            a.hfv[size_t(a.slot) * nv + k] = f;
-            d = fmaxf(d, fabsf(f));
-        }
-    }
-    block_flag_max<1>(a.slots, kAaDelta, d, 0, 0.0f, 0, 0.0f, red);
-}
-
-constexpr int kGramChunk = 1024;  // state entries per Gram workgroup
-
-// Row p of the Gram matrix F^T F of element b over one chunk of the element's
-// M + N residual entries (grid h x B x nchunk); the solve adds the chunks in
-// order.
-static __global__ __launch_bounds__(kBlock) void aa_gram(AaArgs a) {
-    __shared__ float red[kWavesPerBlock][kMaxHistory];
-    if (previous(a.prev, kAnderson, a.tol).stop) return;
-    const int p = blockIdx.x, b = blockIdx.y, ch = blockIdx.z, h = a.h;
+    const int ch = blockIdx.x, b = blockIdx.y, h = a.h;
     const size_t nu = size_t(a.B) * a.M, nv = size_t(a.B) * a.N;
-    const int sp = a.order[p];
     const int i1 = min((ch + 1) * kGramChunk, a.M + a.N);
     float acc[kMaxHistory];
 #pragma unroll
     for (int q = 0; q < kMaxHistory; ++q) acc[q] = 0.0f;
+    float d = 0.0f;
     for (int i = ch * kGramChunk + threadIdx.x; i < i1; i += kBlock) {
-        const float fp = aa_at(a.hfu, a.hfv, sp, nu, nv, b, a.M, a.N, i);
+        const bool isu = i < a.M;
+        const size_t k = isu ? size_t(b) * a.M + i : size_t(b) * a.N + (i - a.M);
+        const size_t st = isu ? nu : nv;
+        const float x = isu ? a.xu[k] : a.xv[k];
+        const float f = (isu ? a.nu[k] : a.nv[k]) - x;
+        (isu ? a.hxu : a.hxv)[size_t(a.slot) * st + k] = x;
+        (isu ? a.hfu : a.hfv)[size_t(a.slot) * st + k] = f;
+        d = fmaxf(d, fabsf(f));
+        const float* hf = isu ? a.hfu : a.hfv;
 #pragma unroll
         for (int q = 0; q < kMaxHistory; ++q)
-            if (q < h) acc[q] = fmaf(fp, aa_at(a.hfu, a.hfv, a.order[q], nu, nv, b, a.M, a.N, i), acc[q]);
+            if (q < h) acc[q] = fmaf(f, q == h - 1 ? f : hf[size_t(a.order[q]) * st + k], acc[q]);
     }
     const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
 #pragma unroll
     for (int q = 0; q < kMaxHistory; ++q) {
         const float s = wave_sum(acc[q]);
-        if (lane == 0) red[wave][q] = s;
+        if (lane == 0) dred[wave][q] = s;
     }
-    __syncthreads();
+    block_flag_max<1>(a.slots, kAaDelta, d, 0, 0.0f, 0, 0.0f, red);  // barrier for dred too
     if (threadIdx.x < h) {
         const int q = threadIdx.x;
-        float s = red[0][q];
+        float s = dred[0][q];
 #pragma unroll
-        for (int w = 1; w < kWavesPerBlock; ++w) s += red[w][q];
-        a.gram[((size_t(b) * a.nchunk + ch) * kMaxHistory + p) * kMaxHistory + q] = s;
+        for (int w = 1; w < kWavesPerBlock; ++w) s += dred[w][q];
+        a.dots[(size_t(b) * a.nchunk + ch) * kMaxHistory + q] = s;
     }
 }
 
-// (G + 1e-8 I) alpha = 1 for element b by Gaussian elimination with partial
-// pivoting (one thread; h <= kMaxHistory), then sum(alpha); a zero or
-// non-finite pivot or sum marks the iteration's solve as failed.
+// One workgroup per element: fold the new products (chunks in order) into
+// the kept Gram matrix, then (G + 1e-8 I) alpha = 1 over the ring (oldest
+// first) by Gaussian elimination with partial pivoting (the updates of a
+// column in parallel, one thread per entry; h <= kMaxHistory) and sum(alpha); a zero or non-finite pivot or sum marks the
+// iteration's solve as failed.  With fewer than two pairs only the Gram
+// matrix is updated.
 static __global__ void aa_solve(AaArgs a) {
     __shared__ float A[kMaxHistory][kMaxHistory + 1];
     __shared__ float x[kMaxHistory];
+    __shared__ float fresh[kMaxHistory];  // the new residual's products, by ring position
     if (previous(a.prev, kAnderson, a.tol).stop) return;
     const int b = blockIdx.x, h = a.h;
+    float* G = a.gram + size_t(b) * kMaxHistory * kMaxHistory;
+    if (threadIdx.x < h) {
+        const int q = threadIdx.x;
+        float s = 0.0f;
+        for (int ch = 0; ch < a.nchunk; ++ch) s += a.dots[(size_t(b) * a.nchunk + ch) * kMaxHistory + q];
+        fresh[q] = s;
+        const int pq = a.order[q];
+        G[a.slot * kMaxHistory + pq] = s;  // kept for later iterations
+        G[pq * kMaxHistory + a.slot] = s;
+    }
+    __syncthreads();
+    if (h < 2) return;
+    // the newest pair is ring position h - 1; its products come from LDS, the
+    // others' from the kept matrix (written by earlier launches)
     for (int e = threadIdx.x; e < h * h; e += blockDim.x) {
         const int p = e / h, q = e % h;
-        float g = 0.0f;
-        for (int ch = 0; ch < a.nchunk; ++ch)
-            g += a.gram[((size_t(b) * a.nchunk + ch) * kMaxHistory + p) * kMaxHistory + q];
+        const float g = p == h - 1 ? fresh[q]
+                        : q == h - 1 ? fresh[p]
+                                     : G[a.order[p] * kMaxHistory + a.order[q]];
         A[p][q] = g + (p == q ? 1.0e-8f : 0.0f);
     }
     if (threadIdx.x < h) x[threadIdx.x] = 1.0f;
-    __syncthreads();
-    if (threadIdx.x != 0) return;
-    bool failed = false;
-    for (int c = 0; c < h && !failed; ++c) {
-        int piv = c;
-        for (int r = c + 1; r < h; ++r)
-            if (fabsf(A[r][c]) > fabsf(A[piv][c])) piv = r;
-        const float pv = A[piv][c];
-        if (pv == 0.0f || !(fabsf(pv) <= FLT_MAX)) {
-            failed = true;
-            break;
+    __shared__ float fr[kMaxHistory];
+    __shared__ int piv_sh, fail_sh;
+    const int tr = threadIdx.x / kMaxHistory, tq = threadIdx.x % kMaxHistory;  // (row, column) of this thread
+    // forward elimination: per column, the pivot by one thread, then the row
+    // swap and the updates of the rows below by one thread per entry
+    for (int c = 0; c < h; ++c) {
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            int piv = c;
+            for (int r = c + 1; r < h; ++r)
+                if (fabsf(A[r][c]) > fabsf(A[piv][c])) piv = r;
+            const float pv = A[piv][c];
+            piv_sh = piv;
+            fail_sh = (pv == 0.0f || !(fabsf(pv) <= FLT_MAX)) ? 1 : 0;
         }
+        __syncthreads();
+        if (fail_sh) break;
+        const int piv = piv_sh;
         if (piv != c) {
-            for (int q = 0; q < h; ++q) {
-                const float t = A[c][q];
-                A[c][q] = A[piv][q];
-                A[piv][q] = t;
+            if (threadIdx.x < h) {
+                const float t = A[c][threadIdx.x];
+                A[c][threadIdx.x] = A[piv][threadIdx.x];
+                A[piv][threadIdx.x] = t;
+            } else if (threadIdx.x == kMaxHistory) {
+                const float t = x[c];
+                x[c] = x[piv];
+                x[piv] = t;
             }
-            const float t = x[c];
-            x[c] = x[piv];
-            x[piv] = t;
+            __syncthreads();
         }
-        for (int r = c + 1; r < h; ++r) {
-            const float f = A[r][c] / A[c][c];
-            for (int q = c; q < h; ++q) A[r][q] -= f * A[c][q];
-            x[r] -= f * x[c];
+        if (threadIdx.x > c && threadIdx.x < h) fr[threadIdx.x] = A[threadIdx.x][c] / A[c][c];
+        __syncthreads();
+        if (tr > c && tr < h && tq >= c && tq < h) A[tr][tq] -= fr[tr] * A[c][tq];
+        if (threadIdx.x > c && threadIdx.x < h) x[threadIdx.x] -= fr[threadIdx.x] * x[c];
+    }
+    __syncthreads();
+    const bool failed_elim = fail_sh != 0;
+    // back substitution, one column at a time
+    if (!failed_elim) {
+        for (int c = h - 1; c >= 0; --c) {
+            if (threadIdx.x == 0) x[c] = x[c] / A[c][c];
+            __syncthreads();
+            if (threadIdx.x < c) x[threadIdx.x] -= A[threadIdx.x][c] * x[c];
+            __syncthreads();
         }
     }
+    if (threadIdx.x != 0) return;
+    bool failed = failed_elim;
     float sum = 0.0f;
     if (!failed) {
-        for (int c = h - 1; c >= 0; --c) {
-            float t = x[c];
-            for (int q = c + 1; q < h; ++q) t -= A[c][q] * x[q];
-            x[c] = t / A[c][c];
-        }
         for (int c = 0; c < h; ++c) sum += x[c];
         failed = !(fabsf(sum) <= FLT_MAX);
     }

@@ -26,7 +26,7 @@ struct MethodLayout {
     size_t zero_bytes;            // from `slots` through `v`
     float *ut[2], *un[2], *vt[2], *vn[2];  // per iteration, by parity
     float *part_t, *part_n, *cost_partial;
-    float *hxu, *hxv, *hfu, *hfv, *gram, *alpha, *denom;
+    float *hxu, *hxv, *hfu, *hfv, *dots, *gram, *alpha, *denom;
     int rows, nstrips;
     size_t bytes;
 };
@@ -63,7 +63,8 @@ MethodLayout method_layout(void* ws, int B, int M, int N, int T, int method, int
     L.hfu = c.take<float>(kk * BM);
     L.hfv = c.take<float>(kk * BN);
     const size_t nchunk = (size_t(M) + N + mth::kGramChunk - 1) / mth::kGramChunk;
-    L.gram = c.take<float>(kk ? size_t(B) * nchunk * kMaxHistory * kMaxHistory : 0);
+    L.dots = c.take<float>(kk ? size_t(B) * nchunk * kMaxHistory : 0);
+    L.gram = c.take<float>(kk ? size_t(B) * kMaxHistory * kMaxHistory : 0);
     L.alpha = c.take<float>(kk ? size_t(B) * kMaxHistory : 0);
     L.denom = c.take<float>(kk ? size_t(B) : 0);
     L.bytes = c.used();
@@ -367,6 +368,7 @@ extern "C" int dot_sinkhorn_forward_method(const dot_sinkhorn_method_args* m, do
             aa.h = ring_size;
             for (int c = 0; c < ring_size; ++c) aa.order[c] = (ring_head + c) % k;
             aa.mixing_beta = m->mixing_beta;
+            aa.dots = L.dots;
             aa.gram = L.gram;
             aa.nchunk = (M + N + mth::kGramChunk - 1) / mth::kGramChunk;
             aa.alpha = L.alpha;
@@ -375,11 +377,8 @@ extern "C" int dot_sinkhorn_forward_method(const dot_sinkhorn_method_args* m, do
             aa.slots = cur;
             aa.tol = a->tol;
             ProfScope prof("mth_anderson", stream);
-            hipLaunchKernelGGL(mth::aa_push, vector_grid(BM + BN), dim3(kBlock), 0, stream, aa);
-            if (ring_size >= 2) {
-                hipLaunchKernelGGL(mth::aa_gram, dim3(ring_size, B, aa.nchunk), dim3(kBlock), 0, stream, aa);
-                hipLaunchKernelGGL(mth::aa_solve, dim3(B), dim3(kWave), 0, stream, aa);
-            }
+            hipLaunchKernelGGL(mth::aa_push, dim3(aa.nchunk, B), dim3(kBlock), 0, stream, aa);
+            hipLaunchKernelGGL(mth::aa_solve, dim3(B), dim3(kBlock), 0, stream, aa);
             hipLaunchKernelGGL(mth::aa_update, vector_grid(BM + BN), dim3(kBlock), 0, stream, aa);
         };
 
