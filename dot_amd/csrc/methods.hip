@@ -4,6 +4,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <string>
 #include <type_traits>
 #include <vector>
@@ -31,10 +32,24 @@ struct MethodLayout {
     size_t bytes;
 };
 
+// Rows per sweep workgroup: 32, halved (down to 4) while the grid has fewer
+// than 512 workgroups.  A solver sweep carries two column sums and adds its
+// flag maxima with atomics, so its per-workgroup cost is higher than the
+// vanilla sweep's: measured per momentum iteration, C4 (16 x 1024 x 2048)
+// 43 µs at 16 rows, 36 at 32, 39 at 64; C3 (64 x 512 x 512) 24.7 at 32, 27.7
+// at 64.  DOT_AMD_ROWS overrides it (tuning only).
+int solver_strip_rows(int B, int M) {
+    if (const char* s = std::getenv("DOT_AMD_ROWS"))
+        if (std::atoi(s) >= 1) return std::atoi(s);
+    int r = 32;
+    while (r > 4 && int64_t(B) * ((M + r - 1) / r) < 512) r /= 2;
+    return r;
+}
+
 MethodLayout method_layout(void* ws, int B, int M, int N, int T, int method, int k) {
     Carver c(ws);
     MethodLayout L{};
-    L.rows = tuned_strip_rows(B, M);
+    L.rows = solver_strip_rows(B, M);
     L.nstrips = M > 0 ? (M + L.rows - 1) / L.rows : 0;
     const size_t BM = size_t(B) * M, BN = size_t(B) * N;
     const bool adam = method == DOT_SK_ADAM, anderson = method == DOT_SK_ANDERSON;
