@@ -26,9 +26,10 @@ reference's: the implicit adjoint of the vanilla plan recomputed at
 ``n_iters_used`` iterations.
 
 On CPU tensors the reference's CPU path is followed through the
-``torch.ops.dot`` CPU operators.  The reference's pure-PyTorch solvers (its
-CPU and ``dual=False`` paths for momentum, Anderson, Adam, Newton, Muon and the
-schedules) are not implemented: asking for one raises ``NotImplementedError``.
+``torch.ops.dot`` CPU operators.  The reference's PyTorch-level solvers (its
+CPU and ``dual=False`` paths for momentum, Anderson, Adam and the schedules,
+and Newton and Muon everywhere) run as in the reference, from
+``dot_amd.solvers``, with the implicit backward at ``n_iters_used``.
 """
 
 from __future__ import annotations
@@ -40,7 +41,7 @@ from typing import Literal, Optional
 import torch
 import torch.nn as nn
 
-from . import _ops
+from . import _ops, solvers
 
 SCORES_LOG_ALPHA = 1
 SCORES_COST = -1
@@ -350,6 +351,31 @@ def _effective_method(method, schedule, reg_start, omega, tau_value, lr, beta1, 
 _METHODS = ("vanilla", "momentum", "anderson", "adam", "newton", "muon", "auto")
 
 
+def _solver(method, log_alpha, tau_value, log_a, log_b, omega, anderson_k, mixing_beta, lr, beta1, beta2,
+            eps_adam, bias_correction, reg_start, schedule):
+    """The reference's PyTorch solver for ``method`` (sinkhorn.py:1531-1693) and
+    its options: momentum estimates omega when none is given; plain Sinkhorn
+    with a schedule starts from reg_start or 10 * reg."""
+    if method == "momentum":
+        if omega is None:
+            omega = solvers.estimate_omega(log_alpha.detach(), tau_value,
+                                           log_a.detach() if log_a is not None else None,
+                                           log_b.detach() if log_b is not None else None)
+        return solvers.momentum_forward, dict(omega=float(omega), reg_start=reg_start, schedule=schedule)
+    if method == "anderson":
+        return solvers.anderson_forward, dict(anderson_k=anderson_k, mixing_beta=mixing_beta,
+                                              reg_start=reg_start, schedule=schedule)
+    if method == "adam":
+        return solvers.adam_forward, dict(lr=lr, beta1=beta1, beta2=beta2, eps_adam=eps_adam,
+                                          bias_correction=bias_correction, reg_start=reg_start, schedule=schedule)
+    if method == "muon":
+        return solvers.muon_forward, dict(lr=lr, reg_start=reg_start, schedule=schedule)
+    if method == "newton":
+        return solvers.newton_forward, dict(reg_start=reg_start, schedule=schedule)
+    start = float(reg_start) if reg_start is not None else 10.0 * tau_value
+    return solvers.scheduled_forward, dict(reg_start=start, schedule=schedule)
+
+
 def sinkhorn(
     cost_matrix: torch.Tensor,
     reg: float | torch.Tensor = 1.0,
@@ -382,12 +408,16 @@ def sinkhorn(
         backward_mode: 'implicit' (adjoint, default) or 'unrolled'
         backward_iters: Adjoint sweeps of the implicit backward (default: n_iters)
         a, b: Optional source/target marginals, shape (B, n)/(n,) and (B, m)/(m,)
-        method: Solver: 'vanilla', or on HIP tensors with dual=True and the
-            implicit backward 'momentum' (omega), 'anderson' (anderson_k,
-            mixing_beta) or 'adam' (lr, beta1, beta2, eps_adam,
-            bias_correction); 'auto' picks 'newton' up to 100x100
+        method: Solver: 'vanilla', 'momentum' (omega; estimated from a pilot
+            run off the device path when None), 'anderson' (anderson_k,
+            mixing_beta), 'adam' (lr, beta1, beta2, eps_adam,
+            bias_correction), 'newton' (n, m <= 100), 'muon' (lr); 'auto'
+            picks 'newton' up to 100x100.  Every method but 'vanilla' needs
+            the implicit backward.  On HIP tensors with dual=True, momentum,
+            anderson and adam run fused on the device (with the reference's
+            fall-backs to vanilla, sinkhorn.py:1373-1390)
         schedule: 'linear', 'exponential' or 'cosine' annealing of reg from
-            reg_start (default 10 * reg) over the iterations (HIP dual path)
+            reg_start (default 10 * reg) over the iterations
         tol: Stop after the first iteration with max|u_t - u_{t-1}| < tol over
             the whole batch (HIP tensors); 0 forces all iterations
         dual: Prefer the dual-state device path (HIP tensors)
@@ -439,9 +469,17 @@ def sinkhorn(
             raise ValueError(f"method='{method}' only supports implicit backward")
         if method == "vanilla" and backward_mode == "unrolled" and schedule is not None:
             raise ValueError("schedule is only supported with implicit backward")
-        raise NotImplementedError(
-            f"method={effective!r} (schedule={eff_schedule!r}) outside the HIP dual path (CUDA/HIP tensors, "
-            "dual=True, backward_mode='implicit') is not implemented by dot_amd")
+        log_alpha = -cost_matrix
+        runner, options = _solver(method, log_alpha, tau_value, log_a, log_b, omega, anderson_k, mixing_beta,
+                                  lr, beta1, beta2, eps_adam, bias_correction, reg_start, schedule)
+        P, used_t = solvers.ImplicitSolverFunction.apply(log_alpha, reg, n_iters, backward_iters, log_a, log_b,
+                                                         runner, options)
+        used = int(used_t)
+        converged = True if tol == 0 else used < n_iters
+        cost = (P * cost_matrix).sum(dim=(-2, -1))
+        if unbatched:
+            P, cost = P.squeeze(0), cost.squeeze(0)
+        return SinkhornResult(transport_plan=P, cost=cost, converged=converged, n_iters_used=used)
 
     mode = _MODE_UNROLLED if backward_mode == "unrolled" else _MODE_IMPLICIT
     if cuda_dual and not plain:

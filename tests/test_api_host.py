@@ -87,10 +87,8 @@ def test_validation_errors_before_any_kernel():
         dot.sinkhorn(C, backward_mode="sideways")
     with pytest.raises(ValueError, match="Unsupported method"):
         dot.sinkhorn(C, method="lbfgs")
-    with pytest.raises(NotImplementedError, match="momentum"):
-        dot.sinkhorn(C, method="momentum", omega=1.5)
-    with pytest.raises(NotImplementedError, match="schedule"):
-        dot.sinkhorn(C, schedule="linear")
+    with pytest.raises(ValueError, match="only supports n, m <= 100"):
+        dot.sinkhorn(torch.rand(1, 101, 3), method="newton")
     # the reference's solver branches reject the unrolled backward (sinkhorn.py:1533-1690)
     with pytest.raises(ValueError, match="only supports implicit backward"):
         dot.sinkhorn(C, method="anderson", backward_mode="unrolled")

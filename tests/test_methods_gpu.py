@@ -17,6 +17,7 @@ import pytest
 import torch
 
 import dot_amd
+from dot_amd import solvers
 from dot_amd import _ops
 from conftest import rel_err, sum_err
 from oracle import sinkhorn as osk
@@ -316,8 +317,10 @@ def test_api_dispatch_rules():
         dot_amd.sinkhorn(cost, reg=0.1, n_iters=5, method="momentum", omega=1.5, backward_mode="unrolled")
     with pytest.raises(ValueError, match="schedule is only supported"):
         dot_amd.sinkhorn(cost, reg=0.1, n_iters=5, schedule="linear", backward_mode="unrolled")
-    with pytest.raises(NotImplementedError):
-        dot_amd.sinkhorn(cost, reg=0.1, n_iters=5, method="momentum", omega=1.5, dual=False)
+    # dual=False runs the reference's PyTorch momentum solver (sinkhorn.py:1531-1556)
+    r = dot_amd.sinkhorn(cost, reg=0.1, n_iters=5, method="momentum", omega=1.5, dual=False)
+    P, used = solvers.momentum_forward(-cost, 0.1, 5, None, None, 1.5)
+    assert torch.equal(r.transport_plan, P) and r.n_iters_used == used
 
 
 # ---------------------------------------------------------------------------

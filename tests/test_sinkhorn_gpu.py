@@ -302,10 +302,10 @@ def test_api_errors():
         dot_amd.sinkhorn(C, a=torch.full((6,), 0.5, device=DEV))
     with pytest.raises(ValueError, match="n_iters must be an int"):
         dot_amd.sinkhorn(C, n_iters="many")
-    with pytest.raises(NotImplementedError):
-        dot_amd.sinkhorn(C, reg=0.02, method="newton")
-    with pytest.raises(NotImplementedError):
-        dot_amd.sinkhorn(C, reg=0.02, method="adam", lr=0.5, dual=False)
+    with pytest.raises(ValueError, match="only supports n, m <= 100"):
+        dot_amd.sinkhorn(torch.rand(1, 101, 4, device=DEV), reg=0.02, method="newton")
+    with pytest.raises(ValueError, match="only supports implicit"):
+        dot_amd.sinkhorn(C, reg=0.02, method="adam", lr=0.5, dual=False, backward_mode="unrolled")
     with pytest.raises(ValueError):
         dot_amd.sinkhorn(C, backward_mode="sideways")
 
