@@ -19,7 +19,9 @@ and T_b = adjoint sweeps executed.  The same line carries
 
 * ``roofline`` — the dominant kernel's algorithmic bytes per launch (one fp32
   read of the [B,M,N] matrix per sweep) over its average duration, measured
-  with HIP events on the launch stream during the timed steps;
+  with HIP events on the launch stream over a second pass of the same K steps
+  run right after the timed ones (the events would otherwise add their own
+  cost to ``value``);
 * ``cpu_baseline`` — the reference's own CPU kernels (oracle/_ref, compiled
   from the reference sources) timed on a bounded sample of the same input on
   one host core, or the numpy oracle when oracle/_ref is absent;
@@ -196,6 +198,22 @@ def bidi_cpu_baseline(sim_cpu, G_cpu, lengths_np, tau, target_s):
 
 
 # ---------------------------------------------------------------------------
+def profiled_pass(profiler, names, step, steps, torch):
+    """Per-kernel durations for the roofline: the same ``steps`` steps run again
+    right after the timed ones, with every launch of ``names`` bracketed by HIP
+    events on its own stream.  The events are kept out of the timed steps: on
+    the short bidirectional-softmax kernels they add ~25 us to a 200 us step."""
+    profiler.reset()
+    profiler.enable(True, kernels=names)
+    torch.cuda.synchronize()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    profiler.enable(False)
+    profiler.collect()
+    return kernel_stats(profiler, names)
+
+
 def bench_sinkhorn(args, torch, dot_amd, profiler):
     cfg = WORKLOADS[args.workload]
     dev = torch.device("cuda", 0)
@@ -223,18 +241,13 @@ def bench_sinkhorn(args, torch, dot_amd, profiler):
     torch.cuda.synchronize()
     sweeps = ["sk_fwd_sweep", "sk_imp_sweep", "sk_fwd_resident", "sk_imp_resident", "sk_fwd_persistent",
               "sk_imp_persistent", "mth_sweep", "mth_vfinish"]
-    profiler.reset()
-    profiler.enable(True, kernels=sweeps)
-    torch.cuda.synchronize()
     t0 = time.perf_counter()
     used = []
     for _ in range(args.steps):
         used.append(step())
     torch.cuda.synchronize()
     t1 = time.perf_counter()
-    profiler.enable(False)
-    profiler.collect()
-    stats = kernel_stats(profiler, sweeps)
+    stats = profiled_pass(profiler, sweeps, step, args.steps, torch)
 
     T_f = sum(used) / len(used)
     T_b = n_iters  # backward_iters defaults to n_iters; the adjoint runs exactly that many sweeps
@@ -295,8 +308,6 @@ def bench_bidi(args, torch, dot_amd, profiler):
     for _ in range(args.warmup):
         step()
     names = ["bidi_fwd_stats", "bidi_fwd_write", "bidi_bwd_dots", "bidi_bwd_write"]
-    profiler.reset()
-    profiler.enable(True, kernels=names)
     torch.cuda.synchronize()
     steps = max(args.steps, 10)
     t0 = time.perf_counter()
@@ -304,9 +315,7 @@ def bench_bidi(args, torch, dot_amd, profiler):
         step()
     torch.cuda.synchronize()
     t1 = time.perf_counter()
-    profiler.enable(False)
-    profiler.collect()
-    stats = kernel_stats(profiler, names)
+    stats = profiled_pass(profiler, names, step, steps, torch)
     E = B * L1 * L2
     sec = (t1 - t0) / steps
     # algorithmic bytes per launch of each kernel (reads + writes of [B,L1,L2] fp32 arrays)
