@@ -11,7 +11,8 @@ On HIP tensors the forward and backward run as fused dot_amd operators:
 
 * the forward iterates on the device, decides the stopping test on the
   device, and writes the plan and the transport cost ``sum(P * C)`` in one
-  pass (one host sync at the end, for ``n_iters_used``);
+  pass, with no host wait: ``n_iters_used`` and ``converged`` are copied to
+  the host behind it and read when the result's fields are first accessed;
 * the backward takes the plan saved by the forward (the reference recomputes
   the whole forward, torch_cuda.cpp:842-853, which yields the same plan) and
   runs the implicit adjoint (exactly ``backward_iters`` sweeps) or the
@@ -34,6 +35,7 @@ and Newton and Muon everywhere) run as in the reference, from
 
 from __future__ import annotations
 
+import collections
 import math
 from dataclasses import dataclass
 from typing import Literal, Optional
@@ -62,12 +64,95 @@ class SinkhornResult:
         cost: Transport cost sum(P * C) of shape (B,)
         converged: Whether the stopping test fired (True when tol == 0)
         n_iters_used: Forward iterations executed
+
+    On HIP tensors ``converged`` and ``n_iters_used`` come from the device:
+    the forward queues their copy to host memory without waiting, and the
+    first read of either field waits for that copy (for the forward only, not
+    for work queued after it, such as a backward).  A caller that reads them
+    only after queuing its backward keeps the device busy throughout; the
+    values are the same plain ``bool`` and ``int`` either way.
     """
 
     transport_plan: torch.Tensor
     cost: Optional[torch.Tensor] = None
     converged: bool = True
     n_iters_used: Optional[int] = None
+
+    def __getattribute__(self, name):
+        if name == "converged" or name == "n_iters_used":
+            d = object.__getattribute__(self, "__dict__")
+            resolve = d.get("_resolve")
+            if resolve is not None:
+                d["n_iters_used"], d["converged"] = resolve()
+                d["_resolve"] = None
+        return object.__getattribute__(self, name)
+
+    def __setattr__(self, name, value):
+        if name == "converged" or name == "n_iters_used":
+            getattr(self, name)  # settle a deferred pair before one half is replaced
+        object.__setattr__(self, name, value)
+
+    def __getstate__(self):
+        getattr(self, "n_iters_used")
+        state = dict(self.__dict__)
+        state.pop("_resolve", None)
+        return state
+
+    @classmethod
+    def _deferred(cls, transport_plan, cost, resolve):
+        """A result whose (n_iters_used, converged) come from ``resolve()`` on first read."""
+        r = cls(transport_plan=transport_plan, cost=cost)
+        r.__dict__["_resolve"] = resolve
+        return r
+
+
+_TIMEOUT_MESSAGE = "dot_sinkhorn_forward: a cross-workgroup exchange timed out (outputs are NaN)"
+
+
+class _DeviceCounts:
+    """A device forward's int32 ``[iters_used, converged]``, copied to pinned
+    host memory behind the forward on its stream; ``get()`` waits for that copy
+    only.  A negative count means a cross-workgroup exchange of the forward
+    timed out (the kernels bound every wait); ``get()`` raises for it."""
+
+    __slots__ = ("_host", "_event", "_value")
+
+    def __init__(self, counts: torch.Tensor):
+        self._host = torch.empty(2, dtype=torch.int32, pin_memory=True)
+        self._host.copy_(counts, non_blocking=True)
+        self._event = torch.cuda.Event()
+        self._event.record()
+        self._value = None
+
+    def ready(self) -> bool:
+        return self._value is not None or self._event.query()
+
+    def get(self):
+        if self._value is None:
+            self._event.synchronize()
+            used, conv = (int(x) for x in self._host.tolist())
+            if used < 0:
+                raise RuntimeError(_TIMEOUT_MESSAGE)
+            self._value = (used, bool(conv))
+        return self._value
+
+
+# Forwards whose counts nobody has read yet: each new device forward checks the
+# finished ones, so a timed-out exchange raises by the next call at the latest.
+_unchecked = collections.deque()
+_MAX_UNCHECKED = 64
+
+
+def _check_finished_forwards():
+    while _unchecked and (_unchecked[0].ready() or len(_unchecked) > _MAX_UNCHECKED):
+        _unchecked.popleft().get()
+
+
+def _track(counts: torch.Tensor) -> _DeviceCounts:
+    _check_finished_forwards()
+    dc = _DeviceCounts(counts)
+    _unchecked.append(dc)
+    return dc
 
 
 def _tau_value(tau) -> float:
@@ -154,10 +239,7 @@ def _run_fused(scores, reg, scores_kind, n_iters, backward_iters, log_a, log_b, 
         scores, tau_arg, scores_kind, int(n_iters), int(backward_iters), log_a, log_b, float(tol),
         mode, want_cost
     )
-    used, conv = (int(x) for x in counts.tolist())
-    if used < 0:
-        raise RuntimeError("dot_sinkhorn_forward: a cross-workgroup exchange timed out (outputs are NaN)")
-    return P, cost, used, bool(conv)
+    return P, cost, _track(counts)
 
 
 _METHOD_CODES = {"vanilla": 0, "momentum": 1, "anderson": 2, "adam": 3}
@@ -235,8 +317,7 @@ def _run_method(scores, reg, scores_kind, n_iters, backward_iters, log_a, log_b,
     P, cost, counts = _SinkhornMethodFunction.apply(
         scores, tau_arg, scores_kind, int(n_iters), int(backward_iters), log_a, log_b, float(tol), params,
         want_cost)
-    used, conv = (int(x) for x in counts.tolist())
-    return P, cost, used, bool(conv)
+    return P, cost, _track(counts)
 
 
 # ---------------------------------------------------------------------------
@@ -487,21 +568,16 @@ def sinkhorn(
                   float(mixing_beta), float(lr), float(beta1), float(beta2), float(eps_adam),
                   bool(bias_correction), -1.0 if eff_reg_start is None else float(eff_reg_start),
                   _SCHEDULE_CODES[eff_schedule])
-        P, cost, used, conv = _run_method(cost_matrix, reg, SCORES_COST, n_iters, backward_iters, log_a, log_b,
-                                          tol, params, True)
-        converged = conv if tol > 0 else True
-        cost = cost.to(torch.result_type(P, cost_matrix))
+        P, cost, counts = _run_method(cost_matrix, reg, SCORES_COST, n_iters, backward_iters, log_a, log_b,
+                                      tol, params, True)
+        rule = _dual_converged(tol)
     elif on_gpu:
         # dual=False is the reference's full-matrix path: it ignores tol and
         # always runs n_iters (sinkhorn.py:1693 with torch_cuda.cpp:599-656).
         run_tol = tol if dual else 0.0
-        P, cost, used, conv = _run_fused(cost_matrix, reg, SCORES_COST, n_iters, backward_iters,
-                                         log_a, log_b, run_tol, mode, True)
-        if dual:
-            converged = conv if tol > 0 else True
-        else:
-            converged = True if tol == 0 else used < n_iters
-        cost = cost.to(torch.result_type(P, cost_matrix))
+        P, cost, counts = _run_fused(cost_matrix, reg, SCORES_COST, n_iters, backward_iters,
+                                     log_a, log_b, run_tol, mode, True)
+        rule = _dual_converged(tol) if dual else _count_converged(tol, n_iters)
     else:
         log_alpha = -cost_matrix
         if mode == _MODE_UNROLLED:
@@ -512,10 +588,27 @@ def sinkhorn(
         converged = True if tol == 0 else used < n_iters
         cost = (P * cost_matrix).sum(dim=(-2, -1))
 
+    if on_gpu:
+        cost = cost.to(torch.result_type(P, cost_matrix))
     if unbatched:
         P = P.squeeze(0)
         cost = cost.squeeze(0)
+    if on_gpu:
+        def resolve():
+            used, conv = counts.get()
+            return used, rule(used, conv)
+        return SinkhornResult._deferred(P, cost, resolve)
     return SinkhornResult(transport_plan=P, cost=cost, converged=converged, n_iters_used=used)
+
+
+def _dual_converged(tol):
+    """The dual path's flag (sinkhorn.py:1530): the device's stop flag when tol > 0."""
+    return lambda used, conv: conv if tol > 0 else True
+
+
+def _count_converged(tol, n_iters):
+    """The other paths' rule (sinkhorn.py:1698-1699): stopped before n_iters."""
+    return lambda used, conv: True if tol == 0 else used < n_iters
 
 
 def sinkhorn_from_scores(
@@ -560,7 +653,7 @@ def sinkhorn_from_scores(
                                                       True)
         else:
             mode = _MODE_UNROLLED if backward_mode == "unrolled" else _MODE_IMPLICIT
-            result, _, _, _ = _run_fused(log_alpha, tau, SCORES_LOG_ALPHA, n_iters, backward_iters,
+            result, _, _ = _run_fused(log_alpha, tau, SCORES_LOG_ALPHA, n_iters, backward_iters,
                                          log_a, log_b, tol, mode, False)
     elif return_log:
         result = _ops.sinkhorn_log(log_alpha, tau_value, n_iters, log_a, log_b)

@@ -96,3 +96,34 @@ def test_validation_errors_before_any_kernel():
         dot.sinkhorn(C, schedule="cosine", backward_mode="unrolled")
     with pytest.raises(ValueError, match="spectral_preflight requires tol > 0"):
         dot.spectral_preflight(-C, 0.1, tol=0)
+
+
+def test_sinkhorn_result_deferred_counts():
+    """HIP results fill converged / n_iters_used on first read; the dataclass
+    behaves as one with plain fields (repr, asdict, equality, copy, pickle)."""
+    import copy
+    import dataclasses
+    import pickle
+
+    calls = []
+
+    def resolve():
+        calls.append(1)
+        return 7, True
+
+    P = torch.rand(2, 3, 4)
+    r = dot.SinkhornResult._deferred(P, P.sum((-2, -1)), resolve)
+    assert calls == []
+    assert r.n_iters_used == 7 and isinstance(r.n_iters_used, int)
+    assert r.converged is True and calls == [1]
+    assert dataclasses.asdict(r)["n_iters_used"] == 7
+    assert "n_iters_used=7" in repr(r)
+    r2 = pickle.loads(pickle.dumps(r))
+    assert r2.n_iters_used == 7 and r2.converged is True and calls == [1]
+    assert copy.copy(r).n_iters_used == 7
+    # assigning one field settles the pair first, so the other keeps its value
+    r3 = dot.SinkhornResult._deferred(P, None, lambda: (3, False))
+    r3.converged = True
+    assert r3.converged is True and r3.n_iters_used == 3
+    r4 = dot.SinkhornResult._deferred(P, None, lambda: (5, True))
+    assert pickle.loads(pickle.dumps(r4)).n_iters_used == 5

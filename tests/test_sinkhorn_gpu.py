@@ -667,3 +667,29 @@ def test_persistent_exact_column_fallback(monkeypatch):
         assert int(used) == T
         assert torch.isfinite(P).all(), name
         assert rel_err(P, Po) < FWD_TOL, name
+
+
+def test_counts_are_read_lazily_and_match():
+    """n_iters_used / converged are copied to the host behind the forward and
+    read on first access, after the backward has been queued."""
+    import importlib
+
+    sk = importlib.import_module("dot_amd.sinkhorn")
+    torch.manual_seed(5)
+    C = torch.rand(4, 64, 48, device=DEV, requires_grad=True)
+    r = dot_amd.sinkhorn(C, reg=0.1, n_iters=300, tol=1e-5)
+    assert r.__dict__.get("_resolve") is not None  # nothing read yet
+    r.cost.sum().backward()
+    used = r.n_iters_used
+    assert isinstance(used, int) and 1 <= used <= 300 and isinstance(r.converged, bool)
+    if used < 300:
+        assert r.converged
+    r2 = dot_amd.sinkhorn(C.detach(), reg=0.1, n_iters=300, tol=1e-5)
+    assert r2.n_iters_used == used and r2.converged == r.converged
+    assert dot_amd.sinkhorn(C.detach(), reg=0.1, n_iters=7, tol=0.0).n_iters_used == 7
+    for _ in range(100):
+        dot_amd.sinkhorn_from_scores(-C.detach(), 0.1, 5)
+    assert len(sk._unchecked) <= sk._MAX_UNCHECKED + 1
+    torch.cuda.synchronize()
+    sk._check_finished_forwards()
+    assert len(sk._unchecked) == 0
