@@ -38,4 +38,14 @@ bool launch_cooperative(K kernel, A& args, int G, int threads, size_t lds, hipSt
                                       static_cast<unsigned>(lds), stream) == hipSuccess;
 }
 
+// Launch of a resident-tier kernel: cooperative when its workgroups wait on
+// each other, so that all of them are resident even while other streams run;
+// a plain launch when none waits on another (one workgroup per batch element
+// and no batch-global test) — a cooperative launch costs ~17 us more.
+inline hipError_t launch_grid(const void* kernel, int G, int threads, void** params, size_t lds,
+                              hipStream_t stream, bool independent) {
+    if (independent) return hipLaunchKernel(kernel, dim3(G), dim3(threads), params, lds, stream);
+    return hipLaunchCooperativeKernel(kernel, dim3(G), dim3(threads), params, static_cast<unsigned>(lds), stream);
+}
+
 }  // namespace dot_amd

@@ -342,7 +342,7 @@ bool launch_stream_forward(const dot_sinkhorn_fwd_args* a, const FwdLayout& L, c
     return true;
 }
 
-// Cooperative launch of the register-resident forward; false when this shape or
+// Launch of the register-resident forward; false when this shape or
 // device cannot host it (the caller then runs the streaming sweeps).
 bool launch_resident_forward(const dot_sinkhorn_fwd_args* a, const FwdLayout& L, const ResidentCfg& rc,
                              float kscale, const float* ks_dev, float log_a_default, float log_b_default,
@@ -395,9 +395,11 @@ bool launch_resident_forward(const dot_sinkhorn_fwd_args* a, const FwdLayout& L,
         launch_fill_zero(L.xchg, L.res_words, stream);
         void* params[] = {&r};
         ProfScope prof("sk_fwd_resident", stream);
-        ok = hipLaunchCooperativeKernel(reinterpret_cast<const void*>(kernel), dim3(groups),
-                                        dim3(res::kThreads), params, static_cast<unsigned>(lds),
-                                        stream) == hipSuccess;
+        // one workgroup per element exchanges only with itself; the stop test
+        // (tol > 0) couples all workgroups of the batch
+        const bool independent = rc.W == 1 && (!(a->tol > 0.0f) || groups == 1);
+        ok = launch_grid(reinterpret_cast<const void*>(kernel), groups, res::kThreads, params, lds, stream,
+                         independent) == hipSuccess;
     });
     if (!ok) return false;
     if (a->cost) {
@@ -612,7 +614,7 @@ int bwd_degenerate(const dot_sinkhorn_bwd_args* a, hipStream_t stream, const cha
 
 namespace {
 
-// Cooperative launch of the register-resident adjoint; false when this shape or
+// Launch of the register-resident adjoint; false when this shape or
 // device cannot host it (the caller then runs the streaming sweeps).
 bool launch_resident_adjoint(const dot_sinkhorn_bwd_args* a, const ImpLayout& L, const ResidentCfg& rc,
                              float inv_tau, hipStream_t stream) {
@@ -650,9 +652,9 @@ bool launch_resident_adjoint(const dot_sinkhorn_bwd_args* a, const ImpLayout& L,
         launch_fill_zero(L.xchg, L.xchg_words, stream);
         void* params[] = {&r};
         ProfScope prof("sk_imp_resident", stream);
-        ok = hipLaunchCooperativeKernel(reinterpret_cast<const void*>(kernel), dim3(groups),
-                                        dim3(res::kThreads), params, static_cast<unsigned>(lds),
-                                        stream) == hipSuccess;
+        // the adjoint's exchanges stay within a batch element's W workgroups
+        ok = launch_grid(reinterpret_cast<const void*>(kernel), groups, res::kThreads, params, lds, stream,
+                         rc.W == 1) == hipSuccess;
     });
     if (!ok) return false;
     ProfScope prof("sk_batch_sum", stream);
