@@ -118,10 +118,12 @@ class _DeviceCounts:
     __slots__ = ("_host", "_event", "_value")
 
     def __init__(self, counts: torch.Tensor):
+        stream = torch.cuda.current_stream(counts.device)  # the stream the forward ran on
         self._host = torch.empty(2, dtype=torch.int32, pin_memory=True)
-        self._host.copy_(counts, non_blocking=True)
+        with torch.cuda.stream(stream):
+            self._host.copy_(counts, non_blocking=True)
         self._event = torch.cuda.Event()
-        self._event.record()
+        self._event.record(stream)
         self._value = None
 
     def ready(self) -> bool:
