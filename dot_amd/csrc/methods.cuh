@@ -255,9 +255,8 @@ __global__ __launch_bounds__(kBlock) void sweep(SweepArgs a) {
     for (int e = 0; e < R::PL; ++e) acc_t[e] = acc_n[e] = 0.0f;
     float gap0 = 0.0f, gap1 = 0.0f, move = 0.0f;
 
-    for (int i = r0 + wave; i < r1; i += kWavesPerBlock) {
-        float x[R::PL];
-        R::load(a.X + (bM + i) * a.N, lane, a.N, x, 0.0f);
+    auto row = [&](int i, RowBuf<R>& buf) {
+        float(&x)[R::PL] = buf.v;
         float mloc = -FLT_MAX;
 #pragma unroll
         for (int e = 0; e < R::PL; ++e) {
@@ -307,6 +306,18 @@ __global__ __launch_bounds__(kBlock) void sweep(SweepArgs a) {
                 a.ut[bM + i] = ut;
                 a.un[bM + i] = un;
             }
+        }
+    };
+    auto load = [&](int i, RowBuf<R>& buf) { R::load_clamped(a.X + (bM + i) * a.N, lane, a.N, buf.v, 0.0f); };
+    if constexpr (R::PL <= 16) {
+        // short rows: each row's load is issued one row ahead (rows of 32
+        // floats per lane would need the second buffer's registers)
+        pipelined_rows<RowBuf<R>>(r0 + wave, r1, kWavesPerBlock, load, row);
+    } else {
+        for (int i = r0 + wave; i < r1; i += kWavesPerBlock) {
+            RowBuf<R> buf;
+            load(i, buf);
+            row(i, buf);
         }
     }
 
