@@ -141,3 +141,21 @@ def test_op_argument_errors():
         _ops.bidirectional_softmax(sim, 1.0, torch.ones(2, 3, dtype=torch.int32, device=DEV))
     with pytest.raises(RuntimeError, match="tau must be > 0"):
         _ops.bidirectional_softmax(sim, 0.0, torch.ones(2, 2, dtype=torch.int32, device=DEV))
+
+
+@pytest.mark.gpu
+def test_reference_cpu_cuda_consistency():
+    """test_bidirectional_softmax.py's test_cpu_cuda_consistency, plus the
+    backward: the CPU operators and the HIP kernels agree."""
+    torch.manual_seed(3)
+    for B, L1, L2 in ((2, 8, 10), (3, 33, 70)):
+        sim_cpu = torch.randn(B, L1, L2)
+        G = torch.randn(B, L1, L2)
+        outs = []
+        for dev in ("cpu", DEV):
+            s = sim_cpu.detach().to(dev).clone().requires_grad_(True)
+            P = dot_amd.bidirectional_softmax(s, tau=1.0)
+            P.backward(G.to(dev))
+            outs.append((P.detach().cpu(), s.grad.cpu()))
+        assert torch.allclose(outs[0][0], outs[1][0], atol=1e-5)
+        assert rel_err(outs[1][1], outs[0][1]) < 1e-4

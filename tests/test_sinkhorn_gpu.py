@@ -693,3 +693,47 @@ def test_counts_are_read_lazily_and_match():
     torch.cuda.synchronize()
     sk._check_finished_forwards()
     assert len(sk._unchecked) == 0
+
+
+def test_reference_explicit_uniform_rectangular_cpu_and_composed_gradient():
+    """The reference's test_explicit_uniform_matches_default,
+    test_rectangular_cuda_matches_cpu, test_composed_gradient_through_points_and_reg
+    and test_sinkhorn_cuda_dual_matches_full_matrix_fixed_iterations
+    (test_sinkhorn.py:186-199, 359-371, 419-432, 792-804) on HIP tensors."""
+    torch.manual_seed(0)
+    B, n, m = 2, 8, 16
+    cost = torch.rand(B, n, m, device=DEV)
+    a = torch.full((B, n), 1.0 / n, device=DEV)
+    b = torch.full((B, m), 1.0 / m, device=DEV)
+    default = dot_amd.sinkhorn(cost, reg=1.0, n_iters=50)
+    explicit = dot_amd.sinkhorn(cost, reg=1.0, n_iters=50, a=a, b=b)
+    assert torch.allclose(default.transport_plan, explicit.transport_plan, atol=1e-4)
+    assert torch.allclose(default.cost, explicit.cost, atol=1e-4)
+
+    cost_cpu = torch.rand(B, n, m)
+    a_cpu = torch.softmax(torch.randn(B, n), dim=-1)
+    b_cpu = torch.softmax(torch.randn(B, m), dim=-1)
+    r_cpu = dot_amd.sinkhorn(cost_cpu, reg=1.0, a=a_cpu, b=b_cpu)
+    r_dev = dot_amd.sinkhorn(cost_cpu.to(DEV), reg=1.0, a=a_cpu.to(DEV), b=b_cpu.to(DEV))
+    assert torch.allclose(r_cpu.transport_plan, r_dev.transport_plan.cpu(), atol=1e-3)
+
+    source = torch.randn(5, 3, device=DEV, requires_grad=True)
+    target = torch.randn(5, 3, device=DEV)
+    eps = torch.tensor(0.1, device=DEV, requires_grad=True)
+    r = dot_amd.sinkhorn(torch.cdist(source, target).unsqueeze(0), reg=eps, n_iters=50)
+    r.cost.sum().backward()
+    assert source.grad is not None and torch.isfinite(source.grad).all()
+    assert eps.grad is not None and torch.isfinite(eps.grad).all()
+    # the same composition on the CPU gives the same gradients
+    s_cpu = source.detach().cpu().requires_grad_(True)
+    e_cpu = torch.tensor(0.1, requires_grad=True)
+    rc = dot_amd.sinkhorn(torch.cdist(s_cpu, target.cpu()).unsqueeze(0), reg=e_cpu, n_iters=50)
+    rc.cost.sum().backward()
+    assert rel_err(source.grad.cpu(), s_cpu.grad) < 1e-4
+    assert float(eps.grad) == pytest.approx(float(e_cpu.grad), rel=1e-4, abs=1e-6)
+
+    cost = torch.rand(1, 96, 128, device=DEV)
+    dual = dot_amd.sinkhorn(cost, reg=0.1, n_iters=50, tol=0, dual=True)
+    full = dot_amd.sinkhorn(cost, reg=0.1, n_iters=50, tol=0, dual=False)
+    assert dual.n_iters_used == 50 and full.n_iters_used == 50
+    assert torch.allclose(dual.transport_plan, full.transport_plan, atol=1e-5)
