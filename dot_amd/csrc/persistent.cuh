@@ -345,11 +345,14 @@ __global__ __launch_bounds__(kThreads) void forward(FwdArgs a) {
 #pragma unroll
         for (int e = 0; e < PL; ++e) acc[e] = 0.0f;
         float dmax = 0.0f;
-        for (int l = wave; row0 + l < rend; l += kWaves) {
+        // rows of up to 32 floats per lane: each row's load is issued one row ahead
+        auto load_row = [&](int l, RowBuf<R>& buf) {
+            R::load_clamped(a.X + (bM + row0 + l) * a.N, opaque_lane(), a.N, buf.v, 0.0f);
+        };
+        auto row = [&](int l, RowBuf<R>& buf) {
             const int i = row0 + l;
             const int ln = opaque_lane();
-            float y[PL];
-            R::load(a.X + (bM + i) * a.N, ln, a.N, y, 0.0f);
+            float(&y)[PL] = buf.v;
             float ml = -FLT_MAX;
 #pragma unroll
             for (int k = 0; k < CH; ++k) {
@@ -383,6 +386,15 @@ __global__ __launch_bounds__(kThreads) void forward(FwdArgs a) {
                 lds_u[cur * a.R + l] = u;
                 publish(a.uslot + size_t(cur) * a.B * a.M + bM + i, u, unsigned(t));
                 if (a.u_hist) a.u_hist[(size_t(t - 1) * a.B + b) * a.M + i] = u;
+            }
+        };
+        if constexpr (PL <= 32) {
+            pipelined_rows<RowBuf<R>>(wave, rend - row0, kWaves, load_row, row);
+        } else {  // 64-float rows: a second buffer would spill
+            for (int l = wave; l < rend - row0; l += kWaves) {
+                RowBuf<R> buf;
+                load_row(l, buf);
+                row(l, buf);
             }
         }
         if (lane == 0) scratch[1 + wave] = dmax;
