@@ -737,3 +737,20 @@ def test_reference_explicit_uniform_rectangular_cpu_and_composed_gradient():
     full = dot_amd.sinkhorn(cost, reg=0.1, n_iters=50, tol=0, dual=False)
     assert dual.n_iters_used == 50 and full.n_iters_used == 50
     assert torch.allclose(dual.transport_plan, full.transport_plan, atol=1e-5)
+
+
+def test_counts_on_a_side_stream():
+    """A forward queued on a non-default stream: its counts are copied and
+    awaited on that stream, so reading them after leaving the stream context
+    gives the same values as a run on the default stream."""
+    torch.manual_seed(6)
+    C = torch.rand(3, 40, 56, device=DEV)
+    ref = dot_amd.sinkhorn(C, reg=0.05, n_iters=400, tol=1e-5)
+    used_ref, conv_ref = ref.n_iters_used, ref.converged
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        r = dot_amd.sinkhorn(C, reg=0.05, n_iters=400, tol=1e-5)
+    assert r.n_iters_used == used_ref and r.converged == conv_ref
+    torch.cuda.current_stream().wait_stream(side)
+    assert torch.equal(r.transport_plan, ref.transport_plan)
