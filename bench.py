@@ -17,16 +17,29 @@ Printed: one JSON line.  ``value`` is Sinkhorn element-iterations per second,
 E * (T_f + T_b) per step with E = B*M*N, T_f = forward iterations executed
 and T_b = adjoint sweeps executed.  The same line carries
 
-* ``roofline`` — the dominant kernel's algorithmic bytes per launch (one fp32
-  read of the [B,M,N] matrix per sweep) over its average duration, measured
-  with HIP events on the launch stream over a second pass of the same K steps
-  run right after the timed ones (the events would otherwise add their own
-  cost to ``value``);
+* ``roofline`` — the dominant kernel against the roof that bounds it, with its
+  average launch duration measured with HIP events on the launch stream over a
+  second pass of the same K steps run right after the timed ones (the events
+  would otherwise add their own cost to ``value``):
+  - streaming tiers (the matrix is re-read from HBM / the Infinity Cache every
+    sweep): ``bound`` "hbm", 4 bytes per element-sweep over the duration
+    against 8 TB/s;
+  - the register-resident tier (the matrix stays in VGPRs for all sweeps):
+    ``bound`` "valu", the kernel's arithmetic — 4 flops per element-sweep in
+    the adjoint (two FMAs: the row dot and the column sum), 8 per
+    element-iteration in the forward (FMA, max, subtract, exp2, add, FMA) —
+    against the 157.3 TFLOP/s fp32 vector peak, beside the HBM traffic the
+    counters measured and the HBM-equivalent bytes the same sweeps would
+    stream;
 * ``cpu_baseline`` — the reference's own CPU kernels (oracle/_ref, compiled
-  from the reference sources) timed on a bounded sample of the same input on
-  one host core, or the numpy oracle when oracle/_ref is absent;
+  from the reference sources) timed on a bounded sample of the same input,
+  pinned to one host core with one torch thread, or the numpy oracle when
+  oracle/_ref is absent;
 * ``bidirectional_softmax`` — config C2 (B=32, 1024x1024, fwd+bwd) in GB/s of
-  algorithmic traffic (20 bytes per element), with its own roofline.
+  algorithmic traffic (20 bytes per element over the whole step), with the four
+  sweeps' own traffic beside it;
+* ``other_configs`` — C1, C4 and C5 measured the same way (``--headline-only``
+  skips them).
 
 ``--method`` / ``--schedule`` (with ``--omega``, ``--lr``, ``--anderson-k``,
 ``--reg-start``) time the accelerated solvers instead, on the same workload and
@@ -47,6 +60,10 @@ import sys
 import time
 
 HBM_PEAK_GBPS = 8000.0  # MI355X HBM3E, 8 TB/s
+FP32_PEAK_TFLOPS = 157.3  # MI355X fp32 vector peak (packed dual-issue)
+FP32_NONPACKED_TFLOPS = 78.6  # the same without packed fp32 instructions (this build disables them)
+# Algorithmic flops per element-sweep of the register-resident kernels.
+RESIDENT_FLOPS = {"sk_imp_resident": 4.0, "sk_fwd_resident": 8.0}
 ROOT = os.path.dirname(os.path.abspath(__file__))
 
 WORKLOADS = {
@@ -112,6 +129,33 @@ def kernel_stats(profiler, names):
 # ---------------------------------------------------------------------------
 # CPU baselines (bounded samples)
 # ---------------------------------------------------------------------------
+class one_core:
+    """Pins this process to one host CPU and torch to one thread for the
+    duration (the reference's CPU kernels are single-threaded); restores both."""
+
+    def __enter__(self):
+        import torch
+
+        self.threads = torch.get_num_threads()
+        self.mask = os.sched_getaffinity(0) if hasattr(os, "sched_getaffinity") else None
+        self.core = min(self.mask) if self.mask else None
+        if self.core is not None:
+            os.sched_setaffinity(0, {self.core})
+        torch.set_num_threads(1)
+        return self
+
+    def __exit__(self, *exc):
+        import torch
+
+        torch.set_num_threads(self.threads)
+        if self.mask is not None:
+            os.sched_setaffinity(0, self.mask)
+        return False
+
+    def label(self):
+        return f"pinned to CPU {self.core}, 1 torch thread" if self.core is not None else "1 torch thread"
+
+
 def sinkhorn_cpu_baseline(C_cpu, reg, a, b, target_s):
     """Reference CPU path, as torch_cpu.cpp runs it: forward T, then backward =
     recomputed forward T + adjoint T (here with tol 0 so the adjoint runs all T
@@ -146,12 +190,13 @@ def sinkhorn_cpu_baseline(C_cpu, reg, a, b, target_s):
             osk.implicit_backward(x, f2.P, -x, reg, T, None, dtype=np.float32)
         return time.perf_counter() - t0
 
-    t1 = run(1)
-    nb = max(1, min(Bt, int(target_s / max(t1, 1e-6))))
-    t = run(nb) if nb > 1 else t1
-    reps = _repeats(t, target_s)
-    if reps > 1:
-        t = sum(run(nb) for _ in range(reps))
+    with one_core() as pin:
+        t1 = run(1)
+        nb = max(1, min(Bt, int(target_s / max(t1, 1e-6))))
+        t = run(nb) if nb > 1 else t1
+        reps = _repeats(t, target_s)
+        if reps > 1:
+            t = sum(run(nb) for _ in range(reps))
     elem_iters = reps * nb * M * N * (T + T)  # the metric counts forward + adjoint, not the recompute
     return {
         "value": elem_iters / t,
@@ -160,7 +205,7 @@ def sinkhorn_cpu_baseline(C_cpu, reg, a, b, target_s):
         "kind": kind,
         "sample": f"{nb} of {Bt} batch elements of this workload ({M}x{N}), {T} forward + "
                   f"{T} recomputed forward + {T} adjoint iterations"
-                  + (f", {reps} times" if reps > 1 else "") + ", single-threaded "
+                  + (f", {reps} times" if reps > 1 else "") + f", single-threaded, {pin.label()} "
                   f"({t:.1f} s on {_cpu_model()}, host has {os.cpu_count()} logical CPUs)",
     }
 
@@ -196,19 +241,20 @@ def bidi_cpu_baseline(sim_cpu, G_cpu, lengths_np, tau, target_s):
             obs.backward(s[:nb], out, g[:nb], r, c, tau, lengths_np[:nb], dtype=np.float32)
         return time.perf_counter() - t0
 
-    t1 = run(1)
-    nb = max(1, min(B, int(target_s / max(t1, 1e-6))))
-    t = run(nb) if nb > 1 else t1
-    reps = _repeats(t, target_s)
-    if reps > 1:
-        t = sum(run(nb) for _ in range(reps))
+    with one_core() as pin:
+        t1 = run(1)
+        nb = max(1, min(B, int(target_s / max(t1, 1e-6))))
+        t = run(nb) if nb > 1 else t1
+        reps = _repeats(t, target_s)
+        if reps > 1:
+            t = sum(run(nb) for _ in range(reps))
     return {
         "value": 20.0 * reps * nb * L1 * L2 / t / 1e9,
         "unit": "GB/s",
         "cores": 1,
         "kind": kind,
         "sample": f"{nb} of {B} batch elements ({L1}x{L2}) forward + backward"
-                  + (f", {reps} times" if reps > 1 else "") + ", single-threaded "
+                  + (f", {reps} times" if reps > 1 else "") + f", single-threaded, {pin.label()} "
                   f"({t:.1f} s on {_cpu_model()})",
     }
 
@@ -230,16 +276,50 @@ def profiled_pass(profiler, names, step, steps, torch):
     return kernel_stats(profiler, names)
 
 
-def bench_sinkhorn(args, torch, dot_amd, profiler):
-    cfg = WORKLOADS[args.workload]
+def sinkhorn_roofline(dominant, stats, E, T_f, T_b, workload):
+    """Roofline object of the dominant Sinkhorn kernel (see the module docstring)."""
+    sweeps = {"sk_imp_resident": T_b, "sk_fwd_resident": T_f, "sk_imp_persistent": T_b,
+              "sk_fwd_persistent": T_f}.get(dominant, 1)
+    avg_s = stats[dominant]["avg_us"] * 1e-6
+    hbm_equiv = 4.0 * E * sweeps  # one fp32 read of the [B,M,N] matrix per sweep
+    traffic = _pmc_traffic(dominant, workload)
+    measured = None if traffic is None else {
+        "GBps": round(traffic / avg_s / 1e9, 1), "frac": round(traffic / avg_s / 1e9 / HBM_PEAK_GBPS, 4)}
+    if dominant in RESIDENT_FLOPS:
+        flops = RESIDENT_FLOPS[dominant] * E * sweeps
+        achieved = flops / avg_s / 1e12
+        return {"bound": "valu", "kernel": dominant, "achieved": round(achieved, 2),
+                "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / FP32_PEAK_TFLOPS, 4),
+                "frac_of_nonpacked_peak": round(achieved / FP32_NONPACKED_TFLOPS, 4),
+                "flops_per_launch": flops, "flops_per_elem_sweep": RESIDENT_FLOPS[dominant],
+                "sweeps_per_launch": sweeps, "traffic": traffic, "hbm_measured": measured,
+                "hbm_equivalent": {"bytes_per_launch": hbm_equiv,
+                                   "GBps": round(hbm_equiv / avg_s / 1e9, 1),
+                                   "note": "bytes the same sweeps would stream; the matrix stays in VGPRs"},
+                "tier": "register-resident (one launch, the matrix held in VGPRs; bound by VALU issue "
+                        "and the per-sweep cross-workgroup column exchange)"}
+    achieved = hbm_equiv / avg_s / 1e9
+    return {"bound": "hbm", "kernel": dominant, "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
+            "traffic": traffic, "hbm_measured": measured, "bytes_per_launch": hbm_equiv,
+            "sweeps_per_launch": sweeps,
+            "tier": "persistent streaming (one launch; the matrix is re-read every sweep)"
+            if "persistent" in dominant else "streaming sweeps (one launch per sweep)"}
+
+
+SINKHORN_KERNELS = ["sk_fwd_sweep", "sk_imp_sweep", "sk_fwd_resident", "sk_imp_resident",
+                    "sk_fwd_persistent", "sk_imp_persistent", "mth_sweep", "mth_vfinish",
+                    "sk_fwd_wide_rows", "sk_fwd_wide_cols", "sk_imp_wide_rows", "sk_imp_wide_cols"]
+
+
+def bench_sinkhorn(args, workload, steps, warmup, torch, dot_amd, profiler, solver=None):
+    cfg = WORKLOADS[workload]
     dev = torch.device("cuda", 0)
-    C, a, b = make_inputs(args.workload, torch, dev)
+    C, a, b = make_inputs(workload, torch, dev)
     B, M, N = C.shape
     E = B * M * N
     reg, n_iters, tol = cfg["reg"], cfg["n_iters"], cfg["tol"]
-
-    solver = dict(method=args.method, schedule=args.schedule, omega=args.omega, lr=args.lr,
-                  anderson_k=args.anderson_k, reg_start=args.reg_start)
+    solver = solver or {}
 
     def step():
         leaf = C.detach().requires_grad_(True)
@@ -249,52 +329,37 @@ def bench_sinkhorn(args, torch, dot_amd, profiler):
 
     from dot_amd.sinkhorn import _effective_method
     _, effective, eff_schedule, _ = _effective_method(
-        args.method, args.schedule, args.reg_start, args.omega, reg, args.lr, 0.9, 0.999, 1e-8, True,
+        solver.get("method", "vanilla"), solver.get("schedule"), solver.get("reg_start"),
+        solver.get("omega"), reg, solver.get("lr", 1.0), 0.9, 0.999, 1e-8, True,
         "implicit", True, True, (M, N))
 
-    for _ in range(args.warmup):
+    for _ in range(warmup):
         step()
     torch.cuda.synchronize()
-    sweeps = ["sk_fwd_sweep", "sk_imp_sweep", "sk_fwd_resident", "sk_imp_resident", "sk_fwd_persistent",
-              "sk_imp_persistent", "mth_sweep", "mth_vfinish"]
     t0 = time.perf_counter()
     used = []
-    for _ in range(args.steps):
+    for _ in range(steps):
         used.append(step())
     torch.cuda.synchronize()
     t1 = time.perf_counter()
-    stats = profiled_pass(profiler, sweeps, step, args.steps, torch)
+    stats = profiled_pass(profiler, SINKHORN_KERNELS, step, steps, torch)
 
     T_f = sum(used) / len(used)
     T_b = n_iters  # backward_iters defaults to n_iters; the adjoint runs exactly that many sweeps
-    sec_per_step = (t1 - t0) / args.steps
+    sec_per_step = (t1 - t0) / steps
     value = E * (T_f + T_b) / sec_per_step
 
     dominant = max(stats, key=lambda k: stats[k]["total_ms"]) if stats else None
-    roofline = None
-    if dominant:
-        # One fp32 read of the [B,M,N] matrix per sweep.  The resident kernels run all
-        # their sweeps in one launch with the matrix held in registers, so their bytes
-        # are HBM-equivalent: what the same sweeps would stream.
-        sweeps_per_launch = {"sk_imp_resident": T_b, "sk_fwd_resident": T_f, "sk_imp_persistent": T_b,
-                             "sk_fwd_persistent": T_f}.get(dominant, 1)
-        bytes_per_launch = 4.0 * E * sweeps_per_launch
-        achieved = bytes_per_launch / (stats[dominant]["avg_us"] * 1e-6) / 1e9
-        roofline = {"bound": "hbm", "kernel": dominant, "achieved": round(achieved, 1),
-                    "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
-                    "traffic": _pmc_traffic(dominant, args.workload),
-                    "bytes_per_launch": bytes_per_launch,
-                    "tier": ("register-resident (HBM-equivalent bytes)" if "resident" in dominant else
-                             "persistent streaming (one launch; the matrix is re-read every sweep)"
-                             if "persistent" in dominant else "streaming sweeps")}
+    roofline = sinkhorn_roofline(dominant, stats, E, T_f, T_b, workload) if dominant else None
     algo_bytes = 4.0 * E * (T_f + T_b) + 20.0 * E
     return {
         "value": value,
+        "unit": "elem-iters/s",
         "ms_per_step": 1000.0 * sec_per_step,
         "E": E,
         "T_f": T_f,
         "T_b": T_b,
-        "config": {"workload": f"{args.workload}: sinkhorn fwd+bwd B={B} M={M} N={N} reg={reg} "
+        "config": {"workload": f"{workload}: sinkhorn fwd+bwd B={B} M={M} N={N} reg={reg} "
                                f"n_iters={n_iters} tol={tol}"
                                + ("" if effective == "vanilla" and eff_schedule is None else
                                   f" method={effective} schedule={eff_schedule}"),
@@ -302,10 +367,14 @@ def bench_sinkhorn(args, torch, dot_amd, profiler):
                    "B": B, "M": M, "N": N, "reg": reg, "n_iters": n_iters, "tol": tol,
                    "n_iters_used": used[-1], "backward_iters": T_b},
         "algorithmic_GBps": algo_bytes / sec_per_step / 1e9,
+        "frac_of_hbm_peak": algo_bytes / sec_per_step / 1e9 / HBM_PEAK_GBPS,
         "kernels": stats,
         "roofline": roofline,
         "C_cpu": C.cpu(), "a": a, "b": b, "reg": reg,
     }
+
+
+BIDI_KERNEL_BYTES = {"bidi_fwd_stats": 4.0, "bidi_fwd_write": 8.0, "bidi_bwd_dots": 8.0, "bidi_bwd_write": 12.0}
 
 
 def bench_bidi(args, torch, dot_amd, profiler):
@@ -323,7 +392,7 @@ def bench_bidi(args, torch, dot_amd, profiler):
 
     for _ in range(args.warmup):
         step()
-    names = ["bidi_fwd_stats", "bidi_fwd_write", "bidi_bwd_dots", "bidi_bwd_write"]
+    names = sorted(BIDI_KERNEL_BYTES) + ["bidi_fwd_fused", "bidi_bwd_fused"]
     torch.cuda.synchronize()
     steps = max(args.steps, 10)
     t0 = time.perf_counter()
@@ -334,24 +403,32 @@ def bench_bidi(args, torch, dot_amd, profiler):
     stats = profiled_pass(profiler, names, step, steps, torch)
     E = B * L1 * L2
     sec = (t1 - t0) / steps
-    # algorithmic bytes per launch of each kernel (reads + writes of [B,L1,L2] fp32 arrays)
-    kernel_bytes = {"bidi_fwd_stats": 4.0 * E, "bidi_fwd_write": 8.0 * E,
-                    "bidi_bwd_dots": 8.0 * E, "bidi_bwd_write": 12.0 * E}
-    dominant = max(stats, key=lambda k: stats[k]["total_ms"]) if stats else None
-    roofline = None
-    if dominant:
-        achieved = kernel_bytes[dominant] / (stats[dominant]["avg_us"] * 1e-6) / 1e9
-        roofline = {"bound": "hbm", "kernel": dominant, "achieved": round(achieved, 1),
-                    "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
-                    "traffic": _pmc_traffic(dominant, "c2"), "bytes_per_launch": kernel_bytes[dominant]}
+    algo = 20.0 * E / sec / 1e9  # read sim, write P; read sim and grad, write grad: 20 B/elem per step
+    # each sweep's own traffic (its reads and writes of [B,L1,L2] fp32 arrays) over its duration
+    own = {}
+    for k, st in stats.items():
+        per_elem = BIDI_KERNEL_BYTES.get(k)
+        if per_elem:
+            bw = per_elem * E / (st["avg_us"] * 1e-6) / 1e9
+            own[k] = {"bytes_per_launch": per_elem * E, "GBps": round(bw, 1),
+                      "frac": round(bw / HBM_PEAK_GBPS, 4), "traffic": _pmc_traffic(k, "c2")}
+    traffic = [v["traffic"] for v in own.values()]
+    roofline = {"bound": "hbm", "kernel": "fwd+bwd step (" + ", ".join(sorted(stats)) + ")",
+                "achieved": round(algo, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                "frac": round(algo / HBM_PEAK_GBPS, 4),
+                "traffic": sum(traffic) if traffic and None not in traffic else None,
+                "bytes_per_step": 20.0 * E,
+                "note": "20 B/elem algorithmic over ms_per_step; kernels_own_traffic gives each "
+                        "sweep's own bytes over its event-timed duration"}
     return {
         "metric": "bidirectional softmax fwd+bwd algorithmic GB/s (20 B/elem)",
-        "value": 20.0 * E / sec / 1e9,
+        "value": algo,
         "unit": "GB/s",
         "ms_per_step": 1000.0 * sec,
-        "frac_of_hbm_peak": 20.0 * E / sec / 1e9 / HBM_PEAK_GBPS,
+        "frac_of_hbm_peak": algo / HBM_PEAK_GBPS,
         "config": {"workload": "c2: bidirectional_softmax fwd+bwd B=32 L1=L2=1024 tau=1.0"},
         "kernels": stats,
+        "kernels_own_traffic": own,
         "roofline": roofline,
         "_cpu": (sim, G, lengths.cpu().numpy()),
     }
@@ -368,6 +445,10 @@ def _pmc_traffic(kernel, workload):
         return None
 
 
+def _public(d):
+    return {k: v for k, v in d.items() if k not in ("C_cpu", "a", "b", "reg", "E")}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -381,9 +462,12 @@ def main():
     ap.add_argument("--anderson-k", type=int, default=5)
     ap.add_argument("--reg-start", type=float, default=None)
     ap.add_argument("--no-bidi", action="store_true", help="skip the bidirectional-softmax leg")
+    ap.add_argument("--headline-only", action="store_true",
+                    help="skip the other Sinkhorn configurations (C1, C4, C5 besides the headline)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
-                    help="approximate CPU time of each CPU-baseline sample")
+                    help="approximate CPU time of each CPU-baseline sample (half of it for the "
+                         "other configurations)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run 20 device copies of MIB MiB each (calibrates rocprofv3 "
                          "FETCH_SIZE / WRITE_SIZE against a known byte count) and exit")
@@ -414,8 +498,15 @@ def main():
     import dot_amd
     from dot_amd import profiler
 
-    sk = bench_sinkhorn(args, torch, dot_amd, profiler)
+    solver = dict(method=args.method, schedule=args.schedule, omega=args.omega, lr=args.lr,
+                  anderson_k=args.anderson_k, reg_start=args.reg_start)
+    sk = bench_sinkhorn(args, args.workload, args.steps, args.warmup, torch, dot_amd, profiler, solver)
     bidi = None if args.no_bidi else bench_bidi(args, torch, dot_amd, profiler)
+    others = {}
+    if not args.headline_only and args.method == "vanilla" and args.schedule is None:
+        for w in ("c1", "c3", "c4", "c5"):
+            if w != args.workload:
+                others[w] = bench_sinkhorn(args, w, args.steps, min(args.warmup, 2), torch, dot_amd, profiler)
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -424,6 +515,11 @@ def main():
             sim, G, ln = bidi["_cpu"]
             bidi["cpu_baseline"] = bidi_cpu_baseline(sim, G, ln, 1.0, args.cpu_seconds)
             bidi["speedup_vs_cpu"] = bidi["value"] / bidi["cpu_baseline"]["value"]
+        for w, o in others.items():
+            o["cpu_baseline"] = sinkhorn_cpu_baseline(o["C_cpu"], o["reg"], o["a"], o["b"],
+                                                      0.5 * args.cpu_seconds)
+            o["speedup_vs_cpu"] = o["value"] / o["cpu_baseline"]["value"]
+    profiler.shutdown()
 
     line = {
         "metric": "Sinkhorn fwd+bwd elem-iters/s and % HBM peak; bidir-softmax GB/s, 1 GPU",
@@ -442,7 +538,7 @@ def main():
         "n_iters_used": sk["T_f"],
         "backward_iters": sk["T_b"],
         "algorithmic_GBps": sk["algorithmic_GBps"],
-        "frac_of_hbm_peak": sk["algorithmic_GBps"] / HBM_PEAK_GBPS,
+        "frac_of_hbm_peak": sk["frac_of_hbm_peak"],
         "roofline": sk["roofline"],
         "kernels": sk["kernels"],
         "cpu_baseline": cpu,
@@ -451,6 +547,8 @@ def main():
     if bidi is not None:
         bidi.pop("_cpu", None)
         line["bidirectional_softmax"] = bidi
+    if others:
+        line["other_configs"] = {w: _public(o) for w, o in others.items()}
     print(json.dumps(line), flush=True)
 
 

@@ -48,16 +48,29 @@ def _run(cmd):
         raise RuntimeError(f"command failed ({res.returncode}): {cmd[0]} ... {cmd[-1]}")
 
 
-def _hip_object(src):
+def _stale(src, obj):
+    """True when obj is missing or older than src or any header of csrc/
+    (used by --changed; a plain build compiles everything)."""
+    if not os.path.exists(obj):
+        return True
+    t = os.path.getmtime(obj)
+    deps = [src] + [os.path.join(CSRC, h) for h in os.listdir(CSRC) if h.endswith((".cuh", ".hpp", ".h"))]
+    deps.append(os.path.join(ROOT, "include", "dot_amd.h"))
+    return any(os.path.getmtime(d) > t for d in deps if os.path.exists(d))
+
+
+def _hip_object(src, changed_only=False):
     obj = os.path.join(OBJ, os.path.splitext(src)[0] + ".o")
+    if changed_only and not _stale(os.path.join(CSRC, src), obj):
+        return obj
     _run([HIPCC, *HIP_FLAGS, "-c", os.path.join(CSRC, src), "-o", obj])
     return obj
 
 
-def build_capi():
+def build_capi(changed_only=False):
     os.makedirs(OBJ, exist_ok=True)
     with ThreadPoolExecutor(max_workers=min(len(HIP_SOURCES), os.cpu_count() or 1)) as ex:
-        objs = list(ex.map(_hip_object, HIP_SOURCES))
+        objs = list(ex.map(lambda s: _hip_object(s, changed_only), HIP_SOURCES))
     out = os.path.join(PKG, "libdot_amd.so")
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", out, *objs,
           "-Wl,-soname,libdot_amd.so"])
@@ -93,11 +106,13 @@ def build_torch_ops():
     return out
 
 
-def build():
-    build_capi()
+def build(changed_only=False):
+    """Compile both libraries.  ``changed_only`` (``--changed`` on the command
+    line) skips HIP objects newer than their source and every header."""
+    build_capi(changed_only)
     build_torch_ops()
 
 
 if __name__ == "__main__":
-    build()
+    build(changed_only="--changed" in sys.argv)
     sys.exit(0)

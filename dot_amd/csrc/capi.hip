@@ -146,3 +146,29 @@ extern "C" void dot_profile_reset(void) {
     std::lock_guard<std::mutex> lock(p.mu);
     p.totals.clear();
 }
+
+// Events still alive when the process exits are torn down after the HIP
+// runtime (and any profiling tool attached to it) has shut down; a process
+// that had created them then faulted inside exit().  This destroys every event
+// the profiler owns while the runtime is still up.
+extern "C" int dot_profile_shutdown(void) {
+    Profiler& p = profiler();
+    std::vector<Pending> work;
+    std::vector<hipEvent_t> pool;
+    {
+        std::lock_guard<std::mutex> lock(p.mu);
+        p.enabled = false;
+        work.swap(p.pending);
+        pool.swap(p.pool);
+    }
+    int rc = DOT_OK;
+    for (const Pending& w : work) {
+        if (hipEventSynchronize(w.stop) != hipSuccess)
+            rc = fail(DOT_ERR_HIP, std::string("profiler: event wait failed for ") + w.name);
+        pool.push_back(w.start);
+        pool.push_back(w.stop);
+    }
+    for (hipEvent_t e : pool)
+        if (hipEventDestroy(e) != hipSuccess) rc = fail(DOT_ERR_HIP, "profiler: hipEventDestroy failed");
+    return rc == DOT_OK ? ok() : rc;
+}

@@ -5,11 +5,21 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <cstdlib>
 
 namespace dot_amd {
 
 // Polls of one exchange word before a cooperative kernel gives up (~1-2 s).
 constexpr int kSpinLimit = 1 << 20;
+
+// The poll limit passed to cooperative kernels: kSpinLimit, or the value of
+// DOT_AMD_SPIN_LIMIT when set.  A negative value makes every bounded wait
+// report a timeout at once (the kernels then finish with NaN outputs and an
+// error status); it exists to test the error path.
+inline int spin_limit() {
+    const char* s = std::getenv("DOT_AMD_SPIN_LIMIT");
+    return s && *s ? std::atoi(s) : kSpinLimit;
+}
 
 inline int device_cus() {
     int dev = 0, cus = 0;

@@ -53,6 +53,7 @@ template <class Idx>
 __device__ __forceinline__ bool poll_many(const unsigned long long* base, int n, Idx idx, unsigned t,
                                           int spin_limit, int* status, bool& dead,
                                           float (&out)[kLoadsPerThread]) {
+    res::forced_timeout(spin_limit, status, dead);
     if (dead) {
 #pragma unroll
         for (int r = 0; r < kLoadsPerThread; ++r) out[r] = __builtin_nanf("");

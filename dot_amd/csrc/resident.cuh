@@ -49,8 +49,18 @@ __device__ __forceinline__ void publish(unsigned long long* p, float v, unsigned
 // `spin_limit` polls, or as soon as any workgroup has reported a timeout in
 // `status` (checked every 256 polls); `dead` then short-circuits every later
 // call of this lane, so a failure costs one bounded wait, not one per value.
+__device__ __forceinline__ void forced_timeout(int spin_limit, int* status, bool& dead) {
+    // A negative limit (set by the host only to test the error path) makes
+    // every bounded wait give up at once, without polling.
+    if (spin_limit < 0 && !dead) {
+        atomicOr(status, 1);
+        dead = true;
+    }
+}
+
 __device__ __forceinline__ float collect(unsigned long long* p, unsigned t, int spin_limit,
                                          int* status, bool& dead) {
+    forced_timeout(spin_limit, status, dead);
     if (dead) return __builtin_nanf("");
     for (int spins = 0;; ++spins) {
         const unsigned long long x = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -76,6 +86,7 @@ __device__ __forceinline__ void collect_row(unsigned long long* row, unsigned t,
                                             int* status, bool& dead, float (&out)[VEC * CH]) {
     using R = Row<VEC, CH>;
     const int lane = threadIdx.x % kWave;
+    forced_timeout(spin_limit, status, dead);
     if (dead) {
 #pragma unroll
         for (int e = 0; e < R::PL; ++e) out[e] = __builtin_nanf("");
@@ -257,6 +268,7 @@ __device__ __forceinline__ void exchange_columns(const float* part, unsigned lon
         }
     }
     unsigned long long* base = slot + size_t(b) * W * N;
+    forced_timeout(spin_limit, status, dead);
 #pragma unroll 1
     for (int q = 0; q < kColsPerThread; ++q) {
         const int j = threadIdx.x + q * kThreads;

@@ -154,6 +154,10 @@ __global__ void set_counts(int32_t* iters_used, int32_t* converged, int used, in
     }
 }
 
+__global__ void set_status(int32_t* status, int value) {
+    if (blockIdx.x == 0 && threadIdx.x == 0) *status = value;
+}
+
 __global__ void fill_value(float* p, size_t n, float value) {
     for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
          i += size_t(gridDim.x) * blockDim.x)
@@ -318,7 +322,7 @@ bool launch_stream_forward(const dot_sinkhorn_fwd_args* a, const FwdLayout& L, c
     r.N = N;
     r.W = sc.W;
     r.R = sc.R;
-    r.spin_limit = kSpinLimit;
+    r.spin_limit = spin_limit();
     const size_t words = size_t(reinterpret_cast<unsigned long long*>(r.status) - L.pst) + 1;
     bool ok = false;
     dispatch_row(N, vec4, [&](auto vc, auto cc) {
@@ -379,7 +383,7 @@ bool launch_resident_forward(const dot_sinkhorn_fwd_args* a, const FwdLayout& L,
     r.N = a->N;
     r.W = rc.W;
     r.R = rc.R;
-    r.spin_limit = kSpinLimit;
+    r.spin_limit = spin_limit();
     bool ok = false;
     dispatch_resident<true>(rc, [&](auto vc, auto cc, auto rr) {
         constexpr int V = decltype(vc)::value;
@@ -607,6 +611,7 @@ sk::GradSource grad_source(const dot_sinkhorn_bwd_args* a) {
 int bwd_degenerate(const dot_sinkhorn_bwd_args* a, hipStream_t stream, const char* what) {
     if (a->B > 0)
         hipLaunchKernelGGL(fill_value, dim3(1), dim3(kBlock), 0, stream, a->grad_tau, size_t(a->B), 0.0f);
+    if (a->status) hipLaunchKernelGGL(set_status, dim3(1), dim3(1), 0, stream, a->status, 0);
     return check_launch(what);
 }
 
@@ -637,7 +642,7 @@ bool launch_resident_adjoint(const dot_sinkhorn_bwd_args* a, const ImpLayout& L,
     r.W = rc.W;
     r.R = rc.R;
     r.iters = a->iters;
-    r.spin_limit = kSpinLimit;
+    r.spin_limit = spin_limit();
     bool ok = false;
     dispatch_resident<false>(rc, [&](auto vc, auto cc, auto rr) {
         constexpr int V = decltype(vc)::value;
@@ -659,7 +664,7 @@ bool launch_resident_adjoint(const dot_sinkhorn_bwd_args* a, const ImpLayout& L,
     if (!ok) return false;
     ProfScope prof("sk_batch_sum", stream);
     hipLaunchKernelGGL(sk::batch_sum, dim3(a->B), dim3(kWave), 0, stream, L.tau_partial, rc.W,
-                       -inv_tau, a->grad_tau);
+                       -inv_tau, a->grad_tau, L.status, a->status);
     return true;
 }
 
@@ -686,7 +691,7 @@ bool launch_stream_adjoint(const dot_sinkhorn_bwd_args* a, const ImpLayout& L, c
     r.W = sc.W;
     r.R = sc.R;
     r.iters = a->iters;
-    r.spin_limit = kSpinLimit;
+    r.spin_limit = spin_limit();
     const size_t words = size_t(reinterpret_cast<unsigned long long*>(r.status) - L.pst) + 1;
     const size_t S = (size_t(N) + sc.W - 1) / sc.W;
     bool ok = false;
@@ -703,7 +708,7 @@ bool launch_stream_adjoint(const dot_sinkhorn_bwd_args* a, const ImpLayout& L, c
     if (!ok) return false;
     ProfScope prof("sk_batch_sum", stream);
     hipLaunchKernelGGL(sk::batch_sum, dim3(B), dim3(kWave), 0, stream, L.tau_partial, sc.W, -inv_tau,
-                       a->grad_tau);
+                       a->grad_tau, static_cast<const int*>(r.status), a->status);
     return true;
 }
 
@@ -780,7 +785,7 @@ extern "C" int dot_sinkhorn_backward_implicit(const dot_sinkhorn_bwd_args* a, do
         {
             ProfScope prof("sk_batch_sum", stream);
             hipLaunchKernelGGL(sk::batch_sum, dim3(B), dim3(kWave), 0, stream, L.tau_partial,
-                               L.nstrips, -inv_tau, a->grad_tau);
+                               L.nstrips, -inv_tau, a->grad_tau, nullptr, a->status);
         }
     });
     if (!launched) return fail(DOT_ERR_UNSUPPORTED, "row length outside the supported range");
@@ -848,7 +853,7 @@ extern "C" int dot_sinkhorn_backward_unrolled(const dot_sinkhorn_bwd_args* a, do
         {
             ProfScope prof("sk_batch_sum", stream);
             hipLaunchKernelGGL(sk::batch_sum, dim3(B), dim3(kWave), 0, stream, L.tau_partial,
-                               L.nstrips, neg_inv_tau2, a->grad_tau);
+                               L.nstrips, neg_inv_tau2, a->grad_tau, nullptr, a->status);
         }
     });
     if (!launched) return fail(DOT_ERR_UNSUPPORTED, "row length outside the supported range");

@@ -236,12 +236,17 @@ __global__ __launch_bounds__(kBlock) void materialize(MaterializeArgs a) {
 }
 
 // out[b] = scale * sum_k partial[b, k] in a fixed order; one wave per batch element.
-static __global__ void batch_sum(const float* partial, int nblk, float scale, float* out) {
+// When status_out is given, block 0 also writes the preceding cooperative
+// kernel's status word there (0 when status_in is null): it runs after that
+// kernel on the stream, so the word is final.
+static __global__ void batch_sum(const float* partial, int nblk, float scale, float* out,
+                                 const int* status_in = nullptr, int32_t* status_out = nullptr) {
     const int b = blockIdx.x;
     float s = 0.0f;
     for (int k = threadIdx.x; k < nblk; k += kWave) s += partial[size_t(b) * nblk + k];
     s = wave_sum(s);
     if (threadIdx.x == 0) out[b] = s * scale;
+    if (status_out && b == 0 && threadIdx.x == 0) *status_out = status_in ? (*status_in != 0) : 0;
 }
 
 static __global__ void fill_zero(uint32_t* p, size_t n) {

@@ -280,6 +280,7 @@ std::vector<Tensor> run_backward(bool implicit, const Tensor& scores_f, int kind
     auto opts = scores_f.options().dtype(at::kFloat);
     Tensor grad = at::empty({B, M, N}, opts);
     Tensor grad_tau = at::empty({B}, opts);
+    Tensor status = at::empty({1}, scores_f.options().dtype(at::kInt));
     const size_t ws_bytes = implicit ? dot_sinkhorn_backward_implicit_workspace_bytes(int(B), int(M), int(N))
                                      : dot_sinkhorn_backward_unrolled_workspace_bytes(int(B), int(M), int(N));
     Tensor ws = workspace(ws_bytes, scores_f);
@@ -301,10 +302,21 @@ std::vector<Tensor> run_backward(bool implicit, const Tensor& scores_f, int kind
     a.grad_tau = grad_tau.data_ptr<float>();
     a.workspace = ws.data_ptr();
     a.workspace_bytes = ws_bytes;
+    a.status = status.data_ptr<int32_t>();
     const dot_stream_t s = current_stream(scores_f);
     if (implicit) check_rc(dot_sinkhorn_backward_implicit(&a, s), "dot_sinkhorn_backward_implicit");
     else check_rc(dot_sinkhorn_backward_unrolled(&a, s), "dot_sinkhorn_backward_unrolled");
-    return {grad, grad_tau};
+    return {grad, grad_tau, status};
+}
+
+// The reference's with_grads ops synchronise the device (cudaMalloc/cudaFree,
+// torch_cuda.cpp:803-871), so these ops check here, with one copy, that no
+// cross-workgroup exchange of the forward or the backward timed out.
+void check_fwd_bwd_status(const Tensor& counts, const Tensor& status) {
+    Tensor c = at::cat({counts.narrow(0, 0, 1), status}).to(at::kCPU);
+    const int32_t* p = c.data_ptr<int32_t>();
+    TORCH_CHECK(p[0] >= 0, "dot_sinkhorn_forward: a cross-workgroup exchange timed out (outputs are NaN)");
+    TORCH_CHECK(p[1] == 0, "dot_sinkhorn_backward: a cross-workgroup exchange timed out (gradients are NaN)");
 }
 
 void check_grad_shape(const Tensor& log_alpha, const Tensor& grad_P) {
@@ -326,6 +338,7 @@ std::vector<Tensor> sinkhorn_with_grads_unrolled_op(Tensor log_alpha, Tensor gra
                                f32c_opt(log_b), false, true, false, true);
     std::vector<Tensor> g = run_backward(false, la, DOT_SCORES_LOG_ALPHA, o.plan, f32c(grad_P),
                                          c10::nullopt, tau, n_iters, o.u_hist, o.v_hist);
+    check_fwd_bwd_status(o.counts, g[2]);
     return {o.plan, g[0], g[1]};
 }
 
@@ -344,6 +357,7 @@ std::vector<Tensor> sinkhorn_with_grads_implicit_op(Tensor log_alpha, Tensor gra
                                f32c_opt(log_b), false, true, false, false);
     std::vector<Tensor> g = run_backward(true, la, DOT_SCORES_LOG_ALPHA, o.plan, f32c(grad_P),
                                          c10::nullopt, tau, backward_iters, Tensor(), Tensor());
+    check_fwd_bwd_status(o.counts, g[2]);
     return {o.plan, g[0], g[1]};
 }
 
@@ -475,7 +489,9 @@ std::vector<Tensor> fused_forward_method_op(Tensor scores, int64_t scores_kind, 
     return {o.plan, cost, o.counts};
 }
 
-// -> [grad_scores, grad_tau (B,)]; mode 0 implicit (iters = adjoint sweeps), 1 unrolled (iters = T).
+// -> [grad_scores, grad_tau (B,), status (int32 [1] on the device: 1 when a
+// cross-workgroup exchange timed out)]; mode 0 implicit (iters = adjoint
+// sweeps), 1 unrolled (iters = T).
 std::vector<Tensor> fused_backward_op(Tensor scores, int64_t scores_kind, Tensor plan,
                                       optional<Tensor> grad_plan, optional<Tensor> grad_cost,
                                       double tau, int64_t mode, int64_t iters,

@@ -5,6 +5,7 @@ the stream it runs on; :func:`collect` waits for them and accumulates
 durations by kernel name.  Used by ``bench.py`` for the roofline figures.
 """
 
+import atexit
 import ctypes
 import os
 
@@ -22,6 +23,8 @@ _lib.dot_profile_query.argtypes = [ctypes.c_char_p, ctypes.POINTER(ctypes.c_int6
 _lib.dot_profile_query.restype = ctypes.c_int
 _lib.dot_profile_reset.argtypes = []
 _lib.dot_profile_reset.restype = None
+_lib.dot_profile_shutdown.argtypes = []
+_lib.dot_profile_shutdown.restype = ctypes.c_int
 _lib.dot_last_error.restype = ctypes.c_char_p
 
 
@@ -48,3 +51,14 @@ def query(kernel: str):
 
 def reset() -> None:
     _lib.dot_profile_reset()
+
+
+def shutdown() -> None:
+    """Disable the profiler and destroy its HIP events (idempotent)."""
+    if _lib.dot_profile_shutdown() != 0:
+        raise RuntimeError(_lib.dot_last_error().decode())
+
+
+# Events left to process teardown outlive the HIP runtime; release them while
+# it is still up (Python's exit hooks run before the C library's).
+atexit.register(_lib.dot_profile_shutdown)

@@ -35,6 +35,7 @@ and Newton and Muon everywhere) run as in the reference, from
 
 from __future__ import annotations
 
+import atexit
 import collections
 import math
 from dataclasses import dataclass
@@ -100,13 +101,20 @@ class SinkhornResult:
 
     @classmethod
     def _deferred(cls, transport_plan, cost, resolve):
-        """A result whose (n_iters_used, converged) come from ``resolve()`` on first read."""
+        """A result whose (n_iters_used, converged) come from ``resolve()`` on first read.
+
+        Until then the two fields are absent from the instance ``__dict__`` (so
+        ``vars(result)`` never shows placeholder values); every attribute read,
+        ``dataclasses.asdict``, ``repr``, ``==`` and pickling resolve them first."""
         r = cls(transport_plan=transport_plan, cost=cost)
-        r.__dict__["_resolve"] = resolve
+        d = r.__dict__
+        del d["n_iters_used"], d["converged"]
+        d["_resolve"] = resolve
         return r
 
 
 _TIMEOUT_MESSAGE = "dot_sinkhorn_forward: a cross-workgroup exchange timed out (outputs are NaN)"
+_BWD_TIMEOUT_MESSAGE = "dot_sinkhorn_backward: a cross-workgroup exchange timed out (gradients are NaN)"
 
 
 class _DeviceCounts:
@@ -117,11 +125,11 @@ class _DeviceCounts:
 
     __slots__ = ("_host", "_event", "_value")
 
-    def __init__(self, counts: torch.Tensor):
-        stream = torch.cuda.current_stream(counts.device)  # the stream the forward ran on
-        self._host = torch.empty(2, dtype=torch.int32, pin_memory=True)
+    def __init__(self, words: torch.Tensor):
+        stream = torch.cuda.current_stream(words.device)  # the stream the kernels ran on
+        self._host = torch.empty(words.numel(), dtype=torch.int32, pin_memory=True)
         with torch.cuda.stream(stream):
-            self._host.copy_(counts, non_blocking=True)
+            self._host.copy_(words, non_blocking=True)
         self._event = torch.cuda.Event()
         self._event.record(stream)
         self._value = None
@@ -129,24 +137,63 @@ class _DeviceCounts:
     def ready(self) -> bool:
         return self._value is not None or self._event.query()
 
+    def _decode(self, words):
+        used, conv = words
+        if used < 0:
+            raise RuntimeError(_TIMEOUT_MESSAGE)
+        return used, bool(conv)
+
     def get(self):
         if self._value is None:
             self._event.synchronize()
-            used, conv = (int(x) for x in self._host.tolist())
-            if used < 0:
-                raise RuntimeError(_TIMEOUT_MESSAGE)
-            self._value = (used, bool(conv))
+            self._value = self._decode([int(x) for x in self._host.tolist()])
         return self._value
 
 
-# Forwards whose counts nobody has read yet: each new device forward checks the
-# finished ones, so a timed-out exchange raises by the next call at the latest.
+class _DeviceStatus(_DeviceCounts):
+    """A device backward's int32 status word (1 when a cross-workgroup exchange
+    of the adjoint timed out); ``get()`` raises for it."""
+
+    __slots__ = ()
+
+    def _decode(self, words):
+        if words[0] != 0:
+            raise RuntimeError(_BWD_TIMEOUT_MESSAGE)
+        return True
+
+
+# Device calls whose status nobody has read yet: each new device forward or
+# backward checks the finished ones, so a timed-out exchange raises by the
+# next call at the latest.
 _unchecked = collections.deque()
 _MAX_UNCHECKED = 64
 
 
+def _release_unchecked():
+    """Wait for the pending status copies and drop their pinned buffers and
+    events while the HIP runtime is up (registered with atexit: objects left to
+    interpreter teardown are released after it)."""
+    while _unchecked:
+        dc = _unchecked.popleft()
+        try:
+            dc._event.synchronize()
+        except Exception:  # a failed device leaves nothing to wait for
+            pass
+
+
+atexit.register(_release_unchecked)
+
+
 def _check_finished_forwards():
     while _unchecked and (_unchecked[0].ready() or len(_unchecked) > _MAX_UNCHECKED):
+        _unchecked.popleft().get()
+
+
+def check_device_errors() -> None:
+    """Wait for every HIP Sinkhorn forward and backward issued so far and
+    raise RuntimeError if a cross-workgroup exchange of one of them timed out
+    (its outputs are then NaN).  Later calls check finished ones by themselves."""
+    while _unchecked:
         _unchecked.popleft().get()
 
 
@@ -155,6 +202,11 @@ def _track(counts: torch.Tensor) -> _DeviceCounts:
     dc = _DeviceCounts(counts)
     _unchecked.append(dc)
     return dc
+
+
+def _track_status(status: torch.Tensor) -> None:
+    _check_finished_forwards()
+    _unchecked.append(_DeviceStatus(status))
 
 
 def _tau_value(tau) -> float:
@@ -215,7 +267,7 @@ class _SinkhornFusedFunction(torch.autograd.Function):
         else:
             iters = ctx.backward_iters
             uh = vh = None
-        grad_scores, grad_tau = _ops.fused.sinkhorn_backward(
+        grad_scores, grad_tau, status = _ops.fused.sinkhorn_backward(
             scores,
             ctx.scores_kind,
             P,
@@ -227,6 +279,7 @@ class _SinkhornFusedFunction(torch.autograd.Function):
             uh,
             vh,
         )
+        _track_status(status)
         tau_grad = None
         if ctx.tau_is_tensor and ctx.needs_input_grad[1]:
             tau_grad = grad_tau.sum()
@@ -296,11 +349,12 @@ class _SinkhornMethodFunction(torch.autograd.Function):
         used = int(counts[0].item())
         P_vanilla = _ops.fused.sinkhorn_forward(scores, ctx.scores_kind, ctx.tau, used, 0.0, log_a, log_b,
                                                 False, False)[0]
-        grad_scores, grad_tau = _ops.fused.sinkhorn_backward(
+        grad_scores, grad_tau, status = _ops.fused.sinkhorn_backward(
             scores, ctx.scores_kind, P_vanilla,
             grad_P.contiguous() if grad_P is not None else None,
             grad_cost.contiguous() if grad_cost is not None else None,
             ctx.tau, _MODE_IMPLICIT, ctx.backward_iters, None, None)
+        _track_status(status)
         if grad_cost is not None:
             # the fused backward's direct cost term used P_vanilla; the cost was
             # computed from this forward's plan (d sum(P C)/dC = P, C = -log_alpha)

@@ -156,6 +156,9 @@ typedef struct {
     float* grad_tau;          /* [B] out (per batch element) */
     void* workspace;
     size_t workspace_bytes;
+    int32_t* status;          /* device int32 out, or NULL: 0 when the call's kernels finish
+                                 normally, 1 when a cross-workgroup exchange timed out (the
+                                 gradients are then NaN) */
 } dot_sinkhorn_bwd_args;
 
 /* Implicit-function adjoint: exactly `iters` Gauss-Seidel sweeps
@@ -271,6 +274,10 @@ void dot_profile_select(const char* names);
 int dot_profile_collect(void);
 int dot_profile_query(const char* kernel, int64_t* launches, double* total_ms);
 void dot_profile_reset(void);
+/* Disable the profiler, wait for its recorded events and destroy every event
+ * it holds.  Call before the process exits if the profiler was ever enabled:
+ * events left to process teardown outlive the HIP runtime. */
+int dot_profile_shutdown(void);
 
 #ifdef __cplusplus
 }

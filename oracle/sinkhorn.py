@@ -17,12 +17,17 @@ and exercised by ``tests/test_oracle.py``:
   kernels converge in one iteration to ``a b^T``); exact column marginals
   after every iteration; row/column shift invariance.  The batch-global
   ``max|u_t - u_{t-1}| < tol`` stopping rule (GPU only, torch_cuda.cpp:199-238)
-  is restated from the source; it is checked against the reference tests'
-  behavioural property (early stop before ``n_iters`` with the plan within
-  2e-3 of the fixed-count plan, test_sinkhorn.py:827-839) and by a mutation
-  check (a u-and-v criterion or a per-batch criterion gives a different count
-  on a designed input).  The exact crossing iteration is therefore only
-  partially pinned.
+  is restated from the source.  Pins: the reference tests' behavioural
+  property (early stop before ``n_iters`` with the plan within 2e-3 of the
+  fixed-count plan, test_sinkhorn.py:827-839); the count convention, by a
+  rank-one kernel, which is exact after iteration 1, so the test must fire at
+  iteration 2 (``n_iters_used == 2``: a count off by one fails); the
+  batch-global reduction, by an input where a per-element test stops earlier.
+  A criterion over u *and* v cannot be told apart from the u-only one: the
+  column update is 1-Lipschitz in the max norm, so ``max|v_t - v_{t-1}| <=
+  max|u_t - u_{t-1}|`` at every iteration (checked on random inputs).  The
+  iteration at which a general input crosses tol is property-pinned only
+  (float32 and float64 can cross one iteration apart).
 * ``implicit_backward`` — golden vectors of the reference's compiled
   ``sinkhorn_backward_implicit_cpu`` with ``tol=0`` (which runs exactly the
   GPU's fixed sweep count); at convergence, a dense float64 solve of the

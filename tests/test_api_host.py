@@ -127,3 +127,10 @@ def test_sinkhorn_result_deferred_counts():
     assert r3.converged is True and r3.n_iters_used == 3
     r4 = dot.SinkhornResult._deferred(P, None, lambda: (5, True))
     assert pickle.loads(pickle.dumps(r4)).n_iters_used == 5
+    # vars() never shows placeholder values: the fields are absent until resolved
+    r5 = dot.SinkhornResult._deferred(P, None, lambda: (9, False))
+    assert "n_iters_used" not in vars(r5) and "converged" not in vars(r5)
+    assert r5.converged is False
+    assert vars(r5)["n_iters_used"] == 9 and vars(r5)["converged"] is False
+    r6 = dot.SinkhornResult._deferred(P, None, lambda: (4, True))
+    assert copy.copy(r6).n_iters_used == 4 and r6 == dot.SinkhornResult(P, None, True, 4)

@@ -239,6 +239,46 @@ def test_early_stop_property_of_reference_tests():
     assert (early.deltas[: early.n_iters_used - 1] >= 1e-6).all()
 
 
+def test_early_stop_count_convention_rank_one():
+    # K_ij = x_i + y_j is exact after one iteration (u_2 = u_1 up to the float32
+    # rounding of the inputs, ~1e-7 here), so the
+    # u-change test fires at iteration 2: used_iters = iter + 1 at the break
+    # (torch_cuda.cpp:223-236).  A count off by one in either direction fails.
+    rng = np.random.default_rng(11)
+    for B, n, m in ((1, 5, 7), (3, 16, 9), (2, 33, 64)):
+        x = rng.standard_normal((B, n, 1))
+        y = rng.standard_normal((B, 1, m))
+        la = (x + y).astype(np.float32)
+        a = rng.random((B, n)) + 0.1
+        b = rng.random((B, m)) + 0.1
+        lga = np.log(a / a.sum(-1, keepdims=True)).astype(np.float32)
+        lgb = np.log(b / b.sum(-1, keepdims=True)).astype(np.float32)
+        f = osk.dual_forward(la, 0.7, 50, tol=1e-5, log_a=lga, log_b=lgb)
+        assert f.converged and f.n_iters_used == 2, f.deltas
+        assert f.deltas[0] > 1e-3
+
+
+def test_u_and_v_stop_criteria_coincide():
+    # The column update v = log b - LSE_i(K + u) is 1-Lipschitz in the max
+    # norm, so max|dv_t| <= max|du_t| at every t: a u-and-v criterion stops at
+    # the same iteration as the reference's u-only one on every input.
+    rng = np.random.default_rng(12)
+    for trial in range(12):
+        B, n, m = 2, int(rng.integers(3, 40)), int(rng.integers(3, 40))
+        la = -rng.random((B, n, m)).astype(np.float32) * float(rng.choice([0.5, 2.0, 8.0]))
+        lga = lgb = None
+        if trial % 2:
+            ea = -np.log(rng.random((B, n)))
+            eb = -np.log(rng.random((B, m)))
+            lga = np.log(ea / ea.sum(-1, keepdims=True)).astype(np.float32)
+            lgb = np.log(eb / eb.sum(-1, keepdims=True)).astype(np.float32)
+        f = osk.dual_forward(la, float(rng.choice([0.05, 0.2, 1.0])), 60, log_a=lga, log_b=lgb,
+                             keep_history=True)
+        du = np.abs(np.diff(f.u_hist, axis=0, prepend=0.0)).max(axis=(1, 2))
+        dv = np.abs(np.diff(f.v_hist, axis=0)).max(axis=(1, 2))
+        assert (dv <= du[1:] * (1 + 1e-9) + 1e-12).all()
+
+
 def test_early_stop_criterion_is_batch_global():
     # One slow batch element keeps the whole batch iterating (torch_cuda.cpp:226-233).
     rng = np.random.default_rng(7)

@@ -158,6 +158,24 @@ def test_early_stop_matches_oracle(seed, shape, tau):
     assert rel_err(P, matched.P) < FWD_TOL
 
 
+@pytest.mark.parametrize("B,M,N", [(3, 64, 96), (2, 200, 1500), (5, 33, 17)])
+def test_early_stop_count_convention_rank_one(B, M, N, monkeypatch):
+    """A rank-one kernel is exact after iteration 1, so the u-change test fires
+    at iteration 2 (used_iters = iter + 1 at the break, torch_cuda.cpp:223-236)
+    on every tier: register-resident, persistent and per-iteration sweeps."""
+    rng = np.random.default_rng(B * M + N)
+    la = (rng.standard_normal((B, M, 1)) + rng.standard_normal((B, 1, N))).astype(np.float32)
+    lga = np.log(_dirichlet(rng, B, M))
+    lgb = np.log(_dirichlet(rng, B, N))
+    Po = osk.dual_forward(la, 0.7, 2, log_a=lga, log_b=lgb).P
+    runs = {"default": _ops.sinkhorn_dual_forward(_t(la), 0.7, 50, 1e-3, _t(lga), _t(lgb))}
+    runs.update(_three_paths(monkeypatch, lambda: _ops.sinkhorn_dual_forward(
+        _t(la), 0.7, 50, 1e-3, _t(lga), _t(lgb))))
+    for name, (P, used, conv) in runs.items():
+        assert int(used) == 2 and int(conv) == 1, (name, int(used))
+        assert rel_err(P, Po) < FWD_TOL, name
+
+
 def test_zero_iterations_and_degenerate_shapes():
     C = np.random.default_rng(0).random((2, 5, 6)).astype(np.float32)
     P, used, conv = _ops.sinkhorn_dual_forward(_t(-C), 0.5, 0, 1e-6)
@@ -462,7 +480,37 @@ def test_config_c3_full_size():
     assert torch.equal(res2.transport_plan, res.transport_plan) and torch.equal(leaf2.grad, leaf.grad)
 
 
-def test_config_c4_full_size():
+def _column_sum_invariant(P, grad_C, tol=1e-3):
+    """dL/dlog_alpha = P - dL/dC for L = cost.sum(); after the adjoint's final
+    mu update its column sums vanish in exact arithmetic:
+    sum_i P (G - lambda - mu) = c - P^T lambda - mu * colsum(P) = 0."""
+    grad_la = P - grad_C
+    scale = grad_la.abs().sum(-2).amax()
+    return float(grad_la.sum(-2).abs().amax() / scale) < tol
+
+
+def _tier_grad_parity(C1, a1, b1, tau, T, monkeypatch):
+    """One batch element at its real shape, reg and marginals: plan, cost and
+    cost gradient after exactly T forward iterations and T adjoint sweeps on the
+    persistent tier and on the per-iteration sweeps, against the float64 oracle."""
+    Po, costo, dCo, _, _ = _oracle_cost_grads(C1, tau, T, T, a1, b1)
+    lt = lambda x: None if x is None else _t(x)
+
+    def run():
+        leaf = _t(C1).requires_grad_(True)
+        res = dot_amd.sinkhorn(leaf, reg=tau, n_iters=T, tol=0, a=lt(a1), b=lt(b1))
+        res.cost.sum().backward()
+        assert res.n_iters_used == T
+        return res.transport_plan.detach(), res.cost.detach(), leaf.grad
+
+    for name, (P, cost, g) in _three_paths(monkeypatch, run).items():
+        assert rel_err(P, Po) < FWD_TOL, name
+        assert rel_err(cost, costo) < FWD_TOL, name
+        assert rel_err(g, dCo) < GRAD_TOL, (name, rel_err(g, dCo))
+        assert _column_sum_invariant(P, g), name
+
+
+def test_config_c4_full_size(monkeypatch):
     g = torch.Generator().manual_seed(4)
     C = torch.rand(16, 1024, 2048, generator=g)
     ea, eb = -torch.log(torch.rand(16, 1024, generator=g)), -torch.log(torch.rand(16, 2048, generator=g))
@@ -475,16 +523,13 @@ def test_config_c4_full_size():
     assert torch.allclose(P.sum(-2), b.to(DEV), rtol=1e-4, atol=1e-9)
     if res.converged:
         assert torch.allclose(P.sum(-1), a.to(DEV), rtol=1e-3, atol=1e-8)
-    # parity at the real shape with a short fixed count (float64 oracle on one element)
-    Cn = C[:1].numpy()
-    r20 = dot_amd.sinkhorn(C[:1].to(DEV).requires_grad_(True), reg=0.05, n_iters=20, tol=0,
-                           a=a[:1].to(DEV), b=b[:1].to(DEV))
-    Po, costo, _, _, _ = _oracle_cost_grads(Cn, 0.05, 20, 1, a[:1].numpy(), b[:1].numpy())
-    assert rel_err(r20.transport_plan, Po) < FWD_TOL
-    assert rel_err(r20.cost, costo) < FWD_TOL
+    # the 500-sweep adjoint at reg 0.05 on the whole batch: exact column-sum invariant
+    assert _column_sum_invariant(P, leaf.grad)
+    # parity at the real shape, reg and Dirichlet marginals, 100 + 100 sweeps, both tiers
+    _tier_grad_parity(C[:1].numpy(), a[:1].numpy(), b[:1].numpy(), 0.05, 100, monkeypatch)
 
 
-def test_config_c5_full_size():
+def test_config_c5_full_size(monkeypatch):
     g = torch.Generator().manual_seed(5)
     x, y = torch.randn(4, 4096, 128, generator=g), torch.randn(4, 4096, 128, generator=g)
     C = torch.cdist(x.to(DEV), y.to(DEV))
@@ -496,10 +541,10 @@ def test_config_c5_full_size():
     assert torch.isfinite(P).all() and torch.isfinite(leaf.grad).all()
     assert torch.allclose(P.sum(-2), torch.full_like(P.sum(-2), 1 / 4096), rtol=1e-4, atol=0)
     assert torch.allclose(P.sum((-2, -1)), torch.ones(4, device=DEV), rtol=1e-4)
-    # parity at the real shape, 5 iterations, one element, float64 oracle
-    r5 = dot_amd.sinkhorn(C[:1], reg=0.02, n_iters=5, tol=0)
-    Po = osk.dual_forward(-C[:1].cpu().numpy(), 0.02, 5).P
-    assert rel_err(r5.transport_plan, Po) < FWD_TOL
+    # the 1000-sweep adjoint at reg 0.02 on the whole batch: exact column-sum invariant
+    assert _column_sum_invariant(P, leaf.grad)
+    # parity at the real shape and reg, 30 + 30 sweeps, one element, both tiers
+    _tier_grad_parity(C[:1].cpu().numpy(), None, None, 0.02, 30, monkeypatch)
 
 
 @pytest.mark.parametrize("B,M,N,tau,T", [(8, 64, 64, 1.0, 100), (4, 512, 512, 0.1, 150),
@@ -754,3 +799,59 @@ def test_counts_on_a_side_stream():
     assert r.n_iters_used == used_ref and r.converged == conv_ref
     torch.cuda.current_stream().wait_stream(side)
     assert torch.equal(r.transport_plan, ref.transport_plan)
+
+
+def _drain_errors():
+    """Empty the queue of unread device statuses, collecting the errors raised."""
+    from dot_amd.sinkhorn import check_device_errors
+
+    errors = []
+    while True:
+        try:
+            check_device_errors()
+            return errors
+        except RuntimeError as e:
+            errors.append(str(e))
+
+
+@pytest.mark.parametrize("shape,env", [((4, 512, 512), {}),
+                                       ((2, 300, 2048), {"DOT_AMD_RESIDENT": "0"})],
+                         ids=["resident", "persistent"])
+def test_exchange_timeout_is_raised(shape, env, monkeypatch):
+    """DOT_AMD_SPIN_LIMIT=-1 makes every bounded wait of the cooperative kernels
+    give up at once (the kernels then finish with NaN outputs): the forward's
+    count read, the schema ops and the lazily checked backward status raise,
+    and the next normal call is unaffected."""
+    for k, v in env.items():
+        monkeypatch.setenv(k, v)
+    _drain_errors()
+    rng = np.random.default_rng(sum(shape))
+    C = _t(rng.random(shape).astype(np.float32))
+    print(f"[timeout] shape={shape} env={env}", flush=True)
+    # forward timed out: reading the count raises
+    monkeypatch.setenv("DOT_AMD_SPIN_LIMIT", "-1")
+    res = dot_amd.sinkhorn(C, reg=0.1, n_iters=20, tol=1e-6)
+    with pytest.raises(RuntimeError, match="forward: a cross-workgroup exchange timed out"):
+        res.n_iters_used
+    assert torch.isnan(res.transport_plan).all()
+    # the reference-schema op checks both statuses itself
+    with pytest.raises(RuntimeError, match="timed out"):
+        _ops.sinkhorn_with_grads_implicit(-C, torch.ones_like(C), 0.1, 10, 10)
+    monkeypatch.delenv("DOT_AMD_SPIN_LIMIT")
+    _drain_errors()
+    # backward timed out after a normal forward: raised by the next check
+    leaf = C.clone().requires_grad_(True)
+    res = dot_amd.sinkhorn(leaf, reg=0.1, n_iters=20, tol=0)
+    assert res.n_iters_used == 20
+    monkeypatch.setenv("DOT_AMD_SPIN_LIMIT", "-1")
+    res.cost.sum().backward()
+    monkeypatch.delenv("DOT_AMD_SPIN_LIMIT")
+    errors = _drain_errors()
+    assert any("backward: a cross-workgroup exchange timed out" in e for e in errors), errors
+    assert torch.isnan(leaf.grad).all()
+    # the library state is clean afterwards
+    leaf = C.clone().requires_grad_(True)
+    res = dot_amd.sinkhorn(leaf, reg=0.1, n_iters=20, tol=0)
+    res.cost.sum().backward()
+    assert res.n_iters_used == 20 and torch.isfinite(leaf.grad).all()
+    assert _drain_errors() == []
