@@ -6,19 +6,24 @@
 #include <string>
 
 #include "bidi_kernels.cuh"
+#include "bidi_wide.cuh"
 #include "host.hpp"
 
 namespace dot_amd {
 namespace {
 
-int strip_rows_bidi(int B, int L1) {
+// Column chunks of a row: 1 when a row fits a wave's registers, else rows
+// are swept in wide::kChunk-column tiles (bidi_wide.cuh).
+int row_chunks(int L2) { return L2 > kMaxRowLen ? wide::num_chunks(L2) : 1; }
+
+int strip_rows_bidi(int B, int L1, int nchunks) {
     static const int forced = [] {
         const char* s = std::getenv("DOT_AMD_ROWS");
         return s ? std::atoi(s) : 0;
     }();
     if (forced >= 1) return forced;
     int r = 64;
-    while (r > 4 && int64_t(B) * ((L1 + r - 1) / r) < 1024) r /= 2;
+    while (r > 4 && int64_t(B) * nchunks * ((L1 + r - 1) / r) < 1024) r /= 2;
     return r;
 }
 
@@ -26,17 +31,20 @@ size_t lds_bytes(int N) { return (size_t(2) * N + 8) * sizeof(float); }
 
 struct FwdLayout {
     float *part_m, *part_s, *row_stats, *col_stats;
-    int rows, nstrips;
+    float2* rpart;  // rows longer than kMaxRowLen: [B, nchunks, L1] row partials
+    int rows, nstrips, nchunks;
     size_t bytes;
 };
 
 FwdLayout fwd_layout(void* ws, int B, int L1, int L2, bool own_stats) {
     Carver c(ws);
     FwdLayout L{};
-    L.rows = strip_rows_bidi(B, L1);
+    L.nchunks = row_chunks(L2);
+    L.rows = strip_rows_bidi(B, L1, L.nchunks);
     L.nstrips = (L1 + L.rows - 1) / L.rows;
     L.part_m = c.take<float>(size_t(B) * L.nstrips * L2);
     L.part_s = c.take<float>(size_t(B) * L.nstrips * L2);
+    L.rpart = c.take<float2>(L.nchunks > 1 ? size_t(B) * L.nchunks * L1 : 0);
     if (own_stats) {
         L.row_stats = c.take<float>(size_t(B) * 2 * L1);
         L.col_stats = c.take<float>(size_t(B) * 2 * L2);
@@ -47,19 +55,22 @@ FwdLayout fwd_layout(void* ws, int B, int L1, int L2, bool own_stats) {
 
 struct BwdLayout {
     float *dot_r, *dot_c, *partial, *tau_partial;
-    int rows, nstrips;
+    float* dpart;  // rows longer than kMaxRowLen: [B, nchunks, L1] row-dot partials
+    int rows, nstrips, nchunks;
     size_t bytes;
 };
 
 BwdLayout bwd_layout(void* ws, int B, int L1, int L2) {
     Carver c(ws);
     BwdLayout L{};
-    L.rows = strip_rows_bidi(B, L1);
+    L.nchunks = row_chunks(L2);
+    L.rows = strip_rows_bidi(B, L1, L.nchunks);
     L.nstrips = (L1 + L.rows - 1) / L.rows;
     L.dot_r = c.take<float>(size_t(B) * L1);
     L.dot_c = c.take<float>(size_t(B) * L2);
     L.partial = c.take<float>(size_t(B) * L.nstrips * L2);
-    L.tau_partial = c.take<float>(size_t(B) * L.nstrips);
+    L.tau_partial = c.take<float>(size_t(B) * L.nstrips * L.nchunks);
+    L.dpart = c.take<float>(L.nchunks > 1 ? size_t(B) * L.nchunks * L1 : 0);
     L.bytes = c.used();
     return L;
 }
@@ -81,11 +92,6 @@ __global__ void fill_value(float* p, size_t n, float value) {
 
 int check_common(int B, int L1, int L2, float tau, const void* lengths) {
     if (B < 0 || L1 < 0 || L2 < 0) return fail(DOT_ERR_INVALID_ARG, "B, L1 and L2 must be >= 0");
-    if (B > 65535) return fail(DOT_ERR_UNSUPPORTED, "batch size above 65535 is not supported");
-    if (L2 > kMaxRowLen)
-        return fail(DOT_ERR_UNSUPPORTED,
-                    "rows longer than 4096 columns are not supported by this build (L2=" +
-                        std::to_string(L2) + ")");
     if (!(std::isfinite(tau) && tau > 0.0f)) return fail(DOT_ERR_INVALID_ARG, "tau must be > 0");
     if (B > 0 && !lengths) return fail(DOT_ERR_INVALID_ARG, "lengths is NULL");
     return DOT_OK;
@@ -116,6 +122,7 @@ extern "C" int dot_bidisoftmax_forward(const dot_bidisoftmax_fwd_args* a, dot_st
     x.sim = a->sim;
     x.lengths = a->lengths;
     x.inv_T = 1.0f / a->tau;  // kernels.cu:426
+    x.B = B;
     x.L1 = L1;
     x.L2 = L2;
     x.rows = L.rows;
@@ -129,7 +136,37 @@ extern "C" int dot_bidisoftmax_forward(const dot_bidisoftmax_fwd_args* a, dot_st
     x.col_sm = a->col_sm;
     const bool vec4 = (L2 % 4 == 0) && aligned16(a->sim) && aligned16(a->out) &&
                       (!a->row_sm || aligned16(a->row_sm)) && (!a->col_sm || aligned16(a->col_sm));
-    const dim3 strips(L.nstrips, B);
+    const dim3 strips = batch_grid(unsigned(L.nstrips), B);
+    const dim3 fold_grid = batch_grid(unsigned((L2 + bidi::kFoldCols - 1) / bidi::kFoldCols), B);
+    if (L.nchunks > 1) {
+        bidi::wide_rows::Args w{};
+        w.f = x;
+        w.rpart = L.rpart;
+        w.B = B;
+        w.nchunks = L.nchunks;
+        const dim3 tiles = batch_grid(unsigned(L.nstrips) * unsigned(L.nchunks), B);
+        const unsigned row_blocks = unsigned((size_t(B) * L1 + kWavesPerBlock - 1) / kWavesPerBlock);
+        wide::dispatch_chunk(vec4, [&](auto vc, auto cc) {
+            constexpr int V = decltype(vc)::value;
+            constexpr int C = decltype(cc)::value;
+            {
+                ProfScope prof("bidi_fwd_stats", stream);
+                hipLaunchKernelGGL((bidi::wide_rows::fwd_stats<V, C>), tiles, dim3(kBlock),
+                                   lds_bytes(wide::kChunk), stream, w);
+            }
+            {
+                ProfScope prof("bidi_fwd_col_combine", stream);
+                hipLaunchKernelGGL(bidi::wide_rows::fwd_row_stats, dim3(row_blocks), dim3(kBlock), 0, stream, w);
+                hipLaunchKernelGGL(bidi::fwd_col_combine, fold_grid, dim3(kBlock), 0, stream, x);
+            }
+            {
+                ProfScope prof("bidi_fwd_write", stream);
+                hipLaunchKernelGGL((bidi::wide_rows::fwd_write<V, C>), tiles, dim3(kBlock),
+                                   2 * size_t(wide::kChunk) * sizeof(float), stream, w);
+            }
+        });
+        return check_launch("dot_bidisoftmax_forward");
+    }
     bool launched = dispatch_row(L2, vec4, [&](auto vc, auto cc) {
         constexpr int V = decltype(vc)::value;
         constexpr int C = decltype(cc)::value;
@@ -139,8 +176,7 @@ extern "C" int dot_bidisoftmax_forward(const dot_bidisoftmax_fwd_args* a, dot_st
         }
         {
             ProfScope prof("bidi_fwd_col_combine", stream);
-            hipLaunchKernelGGL(bidi::fwd_col_combine, dim3((L2 + bidi::kFoldCols - 1) / bidi::kFoldCols, B),
-                               dim3(kBlock), 0, stream, x);
+            hipLaunchKernelGGL(bidi::fwd_col_combine, fold_grid, dim3(kBlock), 0, stream, x);
         }
         {
             ProfScope prof("bidi_fwd_write", stream);
@@ -180,6 +216,7 @@ extern "C" int dot_bidisoftmax_backward(const dot_bidisoftmax_bwd_args* a, dot_s
     x.sim = a->sim;
     x.lengths = a->lengths;
     x.inv_T = 1.0f / a->tau;
+    x.B = B;
     x.L1 = L1;
     x.L2 = L2;
     x.rows = L.rows;
@@ -197,7 +234,47 @@ extern "C" int dot_bidisoftmax_backward(const dot_bidisoftmax_bwd_args* a, dot_s
     x.tau_partial = L.tau_partial;
     bool vec4 = (L2 % 4 == 0) && aligned16(a->sim) && aligned16(a->grad_out) && aligned16(a->grad_sim);
     if (buffers) vec4 = vec4 && aligned16(a->out) && aligned16(a->row_sm) && aligned16(a->col_sm);
-    const dim3 strips(L.nstrips, B);
+    const dim3 strips = batch_grid(unsigned(L.nstrips), B);
+    const dim3 fold_grid = batch_grid(unsigned((L2 + bidi::kFoldCols - 1) / bidi::kFoldCols), B);
+    if (L.nchunks > 1) {
+        bidi::wide_rows::Args w{};
+        w.g = x;
+        w.dpart = L.dpart;
+        w.B = B;
+        w.nchunks = L.nchunks;
+        const dim3 tiles = batch_grid(unsigned(L.nstrips) * unsigned(L.nchunks), B);
+        const unsigned row_blocks = unsigned((size_t(B) * L1 + kWavesPerBlock - 1) / kWavesPerBlock);
+        wide::dispatch_chunk(vec4, [&](auto vc, auto cc) {
+            constexpr int V = decltype(vc)::value;
+            constexpr int C = decltype(cc)::value;
+            auto run = [&](auto recompute) {
+                constexpr bool RC = decltype(recompute)::value;
+                {
+                    ProfScope prof("bidi_bwd_dots", stream);
+                    hipLaunchKernelGGL((bidi::wide_rows::bwd_dots<V, C, RC>), tiles, dim3(kBlock),
+                                       2 * size_t(wide::kChunk) * sizeof(float) + lds_bytes(wide::kChunk),
+                                       stream, w);
+                }
+                {
+                    ProfScope prof("bidi_bwd_fold", stream);
+                    hipLaunchKernelGGL(bidi::wide_rows::bwd_row_dots, dim3(row_blocks), dim3(kBlock), 0, stream, w);
+                    hipLaunchKernelGGL(bidi::column_fold, fold_grid, dim3(kBlock), 0, stream, L.partial, L.nstrips,
+                                       B, L2, L.dot_c);
+                }
+                {
+                    ProfScope prof("bidi_bwd_write", stream);
+                    hipLaunchKernelGGL((bidi::wide_rows::bwd_write<V, C, RC>), tiles, dim3(kBlock),
+                                       3 * size_t(wide::kChunk) * sizeof(float), stream, w);
+                }
+            };
+            if (buffers) run(std::false_type{});
+            else run(std::true_type{});
+        });
+        ProfScope prof("bidi_batch_sum", stream);
+        hipLaunchKernelGGL(batch_sum, dim3(B), dim3(kWave), 0, stream, L.tau_partial, int(tiles.x), -x.inv_T,
+                           a->grad_tau);
+        return check_launch("dot_bidisoftmax_backward");
+    }
     bool launched = dispatch_row(L2, vec4, [&](auto vc, auto cc) {
         constexpr int V = decltype(vc)::value;
         constexpr int C = decltype(cc)::value;
@@ -210,9 +287,8 @@ extern "C" int dot_bidisoftmax_backward(const dot_bidisoftmax_bwd_args* a, dot_s
             }
             {
                 ProfScope prof("bidi_bwd_fold", stream);
-                hipLaunchKernelGGL(bidi::column_fold, dim3((L2 + bidi::kFoldCols - 1) / bidi::kFoldCols, B),
-                                   dim3(kBlock), 0,
-                                   stream, L.partial, L.nstrips, L2, L.dot_c);
+                hipLaunchKernelGGL(bidi::column_fold, fold_grid, dim3(kBlock), 0, stream, L.partial, L.nstrips, B,
+                                   L2, L.dot_c);
             }
             {
                 ProfScope prof("bidi_bwd_write", stream);

@@ -70,7 +70,7 @@ struct FwdArgs {
     const float* sim;
     const int32_t* lengths;
     float inv_T;
-    int L1, L2, rows, nstrips;
+    int B, L1, L2, rows, nstrips;
     float* row_stats;    // [B,2,L1]
     float* col_stats;    // [B,2,L2]
     float* part_m;       // [B,nstrips,L2]
@@ -101,7 +101,8 @@ __global__ __launch_bounds__(kBlock) void fwd_stats(FwdArgs a) {
     const int lane = threadIdx.x % kWave;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);  // wave-uniform: scalar row loads
     const int st = blockIdx.x;
-    const int b = blockIdx.y;
+    const int b = batch_of_block();
+    if (b >= a.B) return;
     int l1, l2;
     valid_extent(a.lengths, b, a.L1, a.L2, l1, l2);
     const bool full = l2 == kWave * R::PL;
@@ -162,7 +163,8 @@ constexpr int kFoldLanes = kBlock / kFoldCols;  // 16
 
 static __global__ __launch_bounds__(kBlock) void fwd_col_combine(FwdArgs a) {
     __shared__ float sm_m[kFoldLanes][kFoldCols], sm_s[kFoldLanes][kFoldCols];
-    const int b = blockIdx.y;
+    const int b = batch_of_block();
+    if (b >= a.B) return;
     const int jj = threadIdx.x % kFoldCols;
     const int sl = threadIdx.x / kFoldCols;
     const int j = blockIdx.x * kFoldCols + jj;
@@ -192,9 +194,11 @@ static __global__ __launch_bounds__(kBlock) void fwd_col_combine(FwdArgs a) {
 
 // Column sums of the strips' partial rows, in the same fixed order as
 // fwd_col_combine.
-static __global__ __launch_bounds__(kBlock) void column_fold(const float* partial, int nstrips, int N, float* out) {
+static __global__ __launch_bounds__(kBlock) void column_fold(const float* partial, int nstrips, int B, int N,
+                                                             float* out) {
     __shared__ float sm[kFoldLanes][kFoldCols];
-    const int b = blockIdx.y;
+    const int b = batch_of_block();
+    if (b >= B) return;
     const int jj = threadIdx.x % kFoldCols;
     const int sl = threadIdx.x / kFoldCols;
     const int j = blockIdx.x * kFoldCols + jj;
@@ -218,12 +222,17 @@ static __global__ __launch_bounds__(kBlock) void column_fold(const float* partia
 // Column max and reciprocal column sum of one batch element into LDS, shared
 // by the block's waves (registers would hold them for the whole kernel and cost
 // occupancy).  The caller places the barrier before the first read.
-__device__ __forceinline__ void load_col_stats(const float* cstat, int L2, float* lcm, float* lics) {
-    for (int j = threadIdx.x; j < L2; j += kBlock) {
+__device__ __forceinline__ void load_col_stats(const float* cstat, int L2, int n, float* lcm, float* lics) {
+    // n columns from cstat (a column max plane, its sum plane L2 floats later)
+    for (int j = threadIdx.x; j < n; j += kBlock) {
         lcm[j] = cstat[j];
         const float cs = cstat[L2 + j];
         lics[j] = cs > 0.0f ? 1.0f / cs : 0.0f;
     }
+}
+
+__device__ __forceinline__ void load_col_stats(const float* cstat, int L2, float* lcm, float* lics) {
+    load_col_stats(cstat, L2, L2, lcm, lics);
 }
 
 // Row max and reciprocal row sum of the strip's valid rows [r0, r1) into LDS
@@ -247,7 +256,8 @@ __global__ __launch_bounds__(kBlock) void fwd_write(FwdArgs a) {
     extern __shared__ __align__(16) float lds[];
     const int lane = threadIdx.x % kWave;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-    const int b = blockIdx.y;
+    const int b = batch_of_block();
+    if (b >= a.B) return;
     int l1, l2;
     valid_extent(a.lengths, b, a.L1, a.L2, l1, l2);
     const bool full = l2 == kWave * R::PL;
@@ -304,7 +314,7 @@ struct BwdArgs {
     const float* sim;
     const int32_t* lengths;
     float inv_T;
-    int L1, L2, rows, nstrips;
+    int B, L1, L2, rows, nstrips;
     const float* grad_out;
     const float* out;      // buffer mode
     const float* row_sm;
@@ -431,7 +441,8 @@ __global__ __launch_bounds__(kBlock) void bwd_dots(BwdArgs a) {
     const int lane = threadIdx.x % kWave;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const int st = blockIdx.x;
-    const int b = blockIdx.y;
+    const int b = batch_of_block();
+    if (b >= a.B) return;
     int l1, l2;
     valid_extent(a.lengths, b, a.L1, a.L2, l1, l2);
     const bool full = l2 == kWave * R::PL;
@@ -471,7 +482,8 @@ __global__ __launch_bounds__(kBlock) void bwd_write(BwdArgs a) {
     extern __shared__ __align__(16) float lds[];
     const int lane = threadIdx.x % kWave;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-    const int b = blockIdx.y;
+    const int b = batch_of_block();
+    if (b >= a.B) return;
     int l1, l2;
     valid_extent(a.lengths, b, a.L1, a.L2, l1, l2);
     const bool full = l2 == kWave * R::PL;

@@ -188,7 +188,7 @@ __device__ __forceinline__ void block_flag_max(unsigned* s, int k0, float x0, in
 struct SweepArgs {
     const float* X;
     float kscale;               // K = X * kscale at this iteration's tau
-    int M, N, rows, nstrips;
+    int B, M, N, rows, nstrips;
     const float* log_a;         // [B,M] or null
     float log_a_default;
     const float* u_prev[2];     // [B,M] u* and u' of the previous iteration (null: zeros)
@@ -220,7 +220,8 @@ __global__ __launch_bounds__(kBlock) void sweep(SweepArgs a) {
     const int lane = threadIdx.x % kWave;
     const int wave = threadIdx.x / kWave;
     const int s = blockIdx.x;
-    const int b = blockIdx.y;
+    const int b = batch_of_block();
+    if (b >= a.B) return;
     // the previous iteration's flags and both of its v candidates, loaded
     // together before anything waits on them
     const Words words = load_words(a.prev);
@@ -233,7 +234,7 @@ __global__ __launch_bounds__(kBlock) void sweep(SweepArgs a) {
         for (int e = 0; e < R::PL; ++e) v[e] = v_alt[e] = 0.0f;
     }
     const Prev pv = previous_from(words, a.prev != nullptr, a.method, a.tol);
-    const bool first_block = blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0;
+    const bool first_block = blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0 && threadIdx.x == 0;
     if (pv.stop) {
         if (first_block) *a.converged = 1;
         return;
@@ -346,7 +347,7 @@ __global__ __launch_bounds__(kBlock) void sweep(SweepArgs a) {
 struct VfinishArgs {
     const float* X;
     float kscale;
-    int M, N, nstrips;
+    int B, M, N, nstrips;
     const float* log_b;         // [B,N] or null
     float log_b_default;
     const float* v_prev[2];     // as SweepArgs
@@ -373,7 +374,8 @@ __global__ __launch_bounds__(kBlock) void vfinish(VfinishArgs a) {
 #pragma clang fp contract(off)
     __shared__ float fold[kFoldLanes][kFoldCols];
     __shared__ float red[3 * kWavesPerBlock];
-    const int b = blockIdx.y;
+    const int b = batch_of_block();
+    if (b >= a.B) return;
     const int jj = threadIdx.x % kFoldCols;
     const int sl = threadIdx.x / kFoldCols;
     const int j = blockIdx.x * kFoldCols + jj;
@@ -541,7 +543,8 @@ static __global__ __launch_bounds__(kBlock) void aa_push(AaArgs a) {
     __shared__ float red[3 * kWavesPerBlock];
     __shared__ float dred[kWavesPerBlock][kMaxHistory];
     if (previous(a.prev, kAnderson, a.tol).stop) return;
-    const int ch = blockIdx.x, b = blockIdx.y, h = a.h;
+    const int ch = blockIdx.x, b = batch_of_block(), h = a.h;
+    if (b >= a.B) return;
     const size_t nu = size_t(a.B) * a.M, nv = size_t(a.B) * a.N;
     const int i1 = min((ch + 1) * kGramChunk, a.M + a.N);
     float acc[kMaxHistory];
@@ -716,7 +719,7 @@ static __global__ __launch_bounds__(kBlock) void aa_update(AaArgs a) {
 struct PlanArgs {
     const float* X;
     float kscale, csign;
-    int M, N, rows, return_log;
+    int B, M, N, rows, return_log;
     int safe;             // safe_exp (the vanilla materialisation) rather than exp
     const float* u;
     const float* v;
@@ -730,7 +733,8 @@ __global__ __launch_bounds__(kBlock) void plan(PlanArgs a) {
     __shared__ float scratch[kWavesPerBlock];
     const int lane = threadIdx.x % kWave;
     const int wave = threadIdx.x / kWave;
-    const int b = blockIdx.y;
+    const int b = batch_of_block();
+    if (b >= a.B) return;
     const int r0 = blockIdx.x * a.rows;
     const int r1 = min(r0 + a.rows, a.M);
     float v[R::PL];

@@ -176,10 +176,11 @@ extern "C" int dot_sinkhorn_forward_method(const dot_sinkhorn_method_args* m, do
     const dot_sinkhorn_fwd_args* a = &m->base;
     const int B = a->B, M = a->M, N = a->N, T = a->max_iter;
     if (B < 0 || M < 0 || N < 0) return fail(DOT_ERR_INVALID_ARG, "B, M and N must be >= 0");
-    if (B > 65535) return fail(DOT_ERR_UNSUPPORTED, "batch size above 65535 is not supported");
-    if (N > kMaxRowLen)
-        return fail(DOT_ERR_UNSUPPORTED, "rows longer than 4096 columns are not supported by this build (N=" +
-                                             std::to_string(N) + ")");
+    // the plain method (with or without a schedule) runs on dot_sinkhorn_forward's
+    // tiers, which take any row length; the accelerated sweeps hold whole rows
+    if (N > kMaxRowLen && m->method != DOT_SK_VANILLA)
+        return fail(DOT_ERR_UNSUPPORTED, "momentum, Anderson and Adam are not supported for rows longer than "
+                                         "4096 columns by this build (N=" + std::to_string(N) + ")");
     if (!(std::isfinite(a->tau) && a->tau > 0.0f)) return fail(DOT_ERR_INVALID_ARG, "tau must be > 0");
     if (T < 0) return fail(DOT_ERR_INVALID_ARG, "max_iter must be >= 0");
     if (a->scores_kind != DOT_SCORES_LOG_ALPHA && a->scores_kind != DOT_SCORES_COST)
@@ -266,8 +267,8 @@ extern "C" int dot_sinkhorn_forward_method(const dot_sinkhorn_method_args* m, do
     const bool launched = dispatch_row(N, vec4, [&](auto vc, auto cc) {
         constexpr int V = decltype(vc)::value;
         constexpr int C = decltype(cc)::value;
-        const dim3 strips(L.nstrips, B);
-        const dim3 cols((N + mth::kFoldCols - 1) / mth::kFoldCols, B);
+        const dim3 strips = batch_grid(unsigned(L.nstrips), B);
+        const dim3 cols = batch_grid(unsigned((N + mth::kFoldCols - 1) / mth::kFoldCols), B);
         const size_t sweep_lds = (size_t(2) * N + 16) * sizeof(float);  // columns + flag reduction
         int ring_head = 0, ring_size = 0;  // Anderson ring: logical position -> physical slot
 
@@ -284,6 +285,7 @@ extern "C" int dot_sinkhorn_forward_method(const dot_sinkhorn_method_args* m, do
             mth::SweepArgs sa{};
             sa.X = a->scores;
             sa.kscale = ks;
+            sa.B = B;
             sa.M = M;
             sa.N = N;
             sa.rows = L.rows;
@@ -327,6 +329,7 @@ extern "C" int dot_sinkhorn_forward_method(const dot_sinkhorn_method_args* m, do
             mth::VfinishArgs fa{};
             fa.X = a->scores;
             fa.kscale = ks;
+            fa.B = B;
             fa.M = M;
             fa.N = N;
             fa.nstrips = L.nstrips;
@@ -392,7 +395,7 @@ extern "C" int dot_sinkhorn_forward_method(const dot_sinkhorn_method_args* m, do
             aa.slots = cur;
             aa.tol = a->tol;
             ProfScope prof("mth_anderson", stream);
-            hipLaunchKernelGGL(mth::aa_push, dim3(aa.nchunk, B), dim3(kBlock), 0, stream, aa);
+            hipLaunchKernelGGL(mth::aa_push, batch_grid(unsigned(aa.nchunk), B), dim3(kBlock), 0, stream, aa);
             hipLaunchKernelGGL(mth::aa_solve, dim3(B), dim3(kBlock), 0, stream, aa);
             hipLaunchKernelGGL(mth::aa_update, vector_grid(BM + BN), dim3(kBlock), 0, stream, aa);
         };
@@ -447,6 +450,7 @@ extern "C" int dot_sinkhorn_forward_method(const dot_sinkhorn_method_args* m, do
             pa.X = a->scores;
             pa.kscale = kscale_at(tau);
             pa.csign = -sign;  // C = -log_alpha
+            pa.B = B;
             pa.M = M;
             pa.N = N;
             pa.rows = L.rows;

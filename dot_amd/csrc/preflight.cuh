@@ -33,7 +33,7 @@ constexpr int kColsPerThread = (kMaxRowLen + kBlock - 1) / kBlock;  // 16
 struct Args {
     const float* X;  // log_alpha [B,M,N]
     float inv_tau;
-    int M, N, rows, nstrips;
+    int B, M, N, rows, nstrips;
     float* lse;      // [B,M]
     float* u;        // [B,M]
     float* upart;    // [B,nstrips] strip sums of u
@@ -71,7 +71,8 @@ __global__ __launch_bounds__(kBlock) void spf_lse(Args a) {
     using R = Row<VEC, CH>;
     const int lane = threadIdx.x % kWave;
     const int wave = threadIdx.x / kWave;
-    const int b = blockIdx.y;
+    const int b = batch_of_block();
+    if (b >= a.B) return;
     const int r0 = blockIdx.x * a.rows;
     const int r1 = min(r0 + a.rows, a.M);
     for (int i = r0 + wave; i < r1; i += kWavesPerBlock) {
@@ -125,7 +126,8 @@ __global__ __launch_bounds__(kBlock) void spf_rowdot(Args a) {
     const int lane = threadIdx.x % kWave;
     const int wave = threadIdx.x / kWave;
     const int st = blockIdx.x;
-    const int b = blockIdx.y;
+    const int b = batch_of_block();
+    if (b >= a.B) return;
     const int r0 = st * a.rows;
     const int r1 = min(r0 + a.rows, a.M);
     float v[R::PL];
@@ -164,7 +166,8 @@ __global__ __launch_bounds__(kBlock) void spf_coldot(Args a) {
     const int lane = threadIdx.x % kWave;
     const int wave = threadIdx.x / kWave;
     const int st = blockIdx.x;
-    const int b = blockIdx.y;
+    const int b = batch_of_block();
+    if (b >= a.B) return;
     const int r0 = st * a.rows;
     const int r1 = min(r0 + a.rows, a.M);
     const float mean = u_mean(a, b);

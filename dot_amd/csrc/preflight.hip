@@ -45,7 +45,6 @@ extern "C" int dot_sinkhorn_spectral_preflight(const dot_spectral_preflight_args
     if (!a) return fail(DOT_ERR_INVALID_ARG, "args is NULL");
     const int B = a->B, M = a->M, N = a->N;
     if (B < 0 || M < 0 || N < 0) return fail(DOT_ERR_INVALID_ARG, "B, M and N must be >= 0");
-    if (B > 65535) return fail(DOT_ERR_UNSUPPORTED, "batch size above 65535 is not supported");
     if (N > kMaxRowLen)
         return fail(DOT_ERR_UNSUPPORTED, "rows longer than 4096 columns are not supported by this build (N=" +
                                              std::to_string(N) + ")");
@@ -61,6 +60,7 @@ extern "C" int dot_sinkhorn_spectral_preflight(const dot_spectral_preflight_args
     spf::Args x{};
     x.X = a->log_alpha;
     x.inv_tau = 1.0f / a->tau;  // kernels.cu:1527
+    x.B = B;
     x.M = M;
     x.N = N;
     x.rows = L.rows;
@@ -72,7 +72,7 @@ extern "C" int dot_sinkhorn_spectral_preflight(const dot_spectral_preflight_args
     x.vpart = L.vpart;
     x.tau_est = a->tau_est;
     const bool vec4 = (N % 4 == 0) && aligned16(a->log_alpha);
-    const dim3 strips(L.nstrips, B);
+    const dim3 strips = batch_grid(unsigned(L.nstrips), B);
     const size_t comb_lds = (size_t(2) * N + 8) * sizeof(float);
     bool launched = dispatch_row(N, vec4, [&](auto vc, auto cc) {
         constexpr int V = decltype(vc)::value;

@@ -20,6 +20,20 @@ constexpr int kBlock = 256;                 // threads per workgroup (4 waves)
 constexpr int kWavesPerBlock = kBlock / kWave;
 constexpr int kMaxRowLen = 4096;            // longest row held in registers
 
+// Batch-indexed grids: grid y holds at most 65535 batch elements, so larger
+// batches spill into grid z.  batch_grid(x, B) launches x workgroups per
+// element; a kernel takes its element from batch_of_block() and returns when
+// it is >= B (the last z slab may be partly empty).
+inline dim3 batch_grid(unsigned x, int B) {
+    const int z = (B + 65534) / 65535;
+    const int y = (B + z - 1) / z;
+    return dim3(x, unsigned(y > 0 ? y : 1), unsigned(z > 0 ? z : 1));
+}
+
+__device__ __forceinline__ int batch_of_block() {
+    return int(blockIdx.z) * int(gridDim.y) + int(blockIdx.y);
+}
+
 template <int VEC, int CH>
 struct Row {
     static constexpr int PL = VEC * CH;  // floats per lane

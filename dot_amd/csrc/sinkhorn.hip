@@ -11,6 +11,7 @@
 #include "persistent.cuh"
 #include "resident.cuh"
 #include "sinkhorn_kernels.cuh"
+#include "wide.cuh"
 
 namespace dot_amd {
 namespace {
@@ -21,7 +22,7 @@ int strip_rows(int B, int M) { return tuned_strip_rows(B, M); }
 
 size_t lds_bytes(int N) { return (size_t(2) * N + 8) * sizeof(float); }
 
-dim3 column_grid(int N, int B) { return dim3((N + kBlock - 1) / kBlock, B); }
+dim3 column_grid(int N, int B) { return batch_grid(unsigned((N + kBlock - 1) / kBlock), B); }
 
 // Upper bound on the workgroups of a resident launch: at most kMaxGroup per
 // batch element, at least 16 rows each, and at most 1024 in all.
@@ -44,6 +45,7 @@ struct FwdLayout {
     float* vbuf;
     size_t zero_words;
     float* partial;
+    float2* rpart;              // rows longer than kMaxRowLen: [B, nchunks, M] row partials
     float* cost_partial;
     // resident path: tagged exchange slots, cleared before each resident launch
     unsigned long long* xchg;   // [2, G, N]
@@ -54,9 +56,17 @@ struct FwdLayout {
     size_t res_words;           // 32-bit words from xchg through status
     unsigned long long* pst;    // persistent streaming path: tagged slots, laid out per launch
     size_t pst_groups;
-    int rows, nstrips;
+    int rows, nstrips, nchunks;
     size_t bytes;
 };
+
+// Column chunks of a row in the streaming sweeps: 1 when the row fits a
+// wave's registers, else rows are swept in wide::kChunk-column tiles.
+int row_chunks(int N) { return N > kMaxRowLen ? wide::num_chunks(N) : 1; }
+
+int sweep_rows(int B, int M, int nchunks) {
+    return nchunks > 1 ? wide::strip_rows(B, M, nchunks) : strip_rows(B, M);
+}
 
 FwdLayout fwd_layout(void* ws, int B, int M, int N, int max_iter) {
     Carver c(ws);
@@ -65,11 +75,14 @@ FwdLayout fwd_layout(void* ws, int B, int M, int N, int max_iter) {
     L.ubuf = c.take<float>(size_t(2) * B * M);
     L.vbuf = c.take<float>(size_t(2) * B * N);
     L.zero_words = c.used() / sizeof(uint32_t);
-    L.rows = strip_rows(B, M);
+    L.nchunks = row_chunks(N);
+    L.rows = sweep_rows(B, M, L.nchunks);
     L.nstrips = (M + L.rows - 1) / L.rows;
     L.partial = c.take<float>(size_t(B) * L.nstrips * N);
+    L.rpart = c.take<float2>(L.nchunks > 1 ? size_t(B) * L.nchunks * M : 0);
     L.pst_groups = pst_groups_max(B, M, N);
-    L.cost_partial = c.take<float>(std::max(size_t(B) * std::max(L.nstrips, res::kMaxGroup), L.pst_groups));
+    L.cost_partial = c.take<float>(
+        std::max(size_t(B) * std::max(size_t(L.nstrips) * L.nchunks, size_t(res::kMaxGroup)), L.pst_groups));
     L.groups = resident_groups_max(B, M, N);
     const size_t gn = L.groups * size_t(N);
     const size_t words = 6 * gn + res::kDeltaSlots * L.groups + 1;
@@ -90,20 +103,23 @@ FwdLayout fwd_layout(void* ws, int B, int M, int N, int max_iter) {
 
 struct ImpLayout {
     float *r, *rs, *lam, *c, *cs, *mu, *partA, *partB, *tau_partial;
+    float2* rpart;             // rows longer than kMaxRowLen: [B, nchunks, M] prologue row partials
+    float* dpart;              // ... and [B, nchunks, M] row partials of each sweep
     unsigned long long* xchg;  // resident path: tagged exchange slots, then status
     int* status;
     size_t groups;             // workgroups the slots are laid out for
     size_t xchg_words;         // 32-bit words to clear (slots and status)
     unsigned long long* pst;   // persistent streaming path: tagged slots, laid out per launch
     size_t pst_groups;
-    int rows, nstrips;
+    int rows, nstrips, nchunks;
     size_t bytes;
 };
 
 ImpLayout imp_layout(void* ws, int B, int M, int N) {
     Carver c(ws);
     ImpLayout L{};
-    L.rows = strip_rows(B, M);
+    L.nchunks = row_chunks(N);
+    L.rows = sweep_rows(B, M, L.nchunks);
     L.nstrips = (M + L.rows - 1) / L.rows;
     L.r = c.take<float>(size_t(B) * M);
     L.rs = c.take<float>(size_t(B) * M);
@@ -113,7 +129,9 @@ ImpLayout imp_layout(void* ws, int B, int M, int N) {
     L.mu = c.take<float>(size_t(B) * N);
     L.partA = c.take<float>(size_t(B) * L.nstrips * N);
     L.partB = c.take<float>(size_t(B) * L.nstrips * N);
-    L.tau_partial = c.take<float>(size_t(B) * std::max(L.nstrips, pst::kMaxGroups));
+    L.tau_partial = c.take<float>(size_t(B) * std::max(size_t(L.nstrips) * L.nchunks, size_t(pst::kMaxGroups)));
+    L.rpart = c.take<float2>(L.nchunks > 1 ? size_t(B) * L.nchunks * M : 0);
+    L.dpart = c.take<float>(L.nchunks > 1 ? size_t(B) * L.nchunks * M : 0);
     // The resident path runs at most one workgroup per CU and only for N <= 1024.
     const size_t groups = resident_groups_max(B, M, N);
     // [2, G, N] sweep slots, [2, G, N] prologue slots, then the status word
@@ -130,19 +148,22 @@ ImpLayout imp_layout(void* ws, int B, int M, int N) {
 
 struct UnrLayout {
     float *gamma, *partial, *colsum, *tau_partial;
-    int rows, nstrips;
+    float* tpart;  // rows longer than kMaxRowLen: [B, nchunks, M] row partials of each step
+    int rows, nstrips, nchunks;
     size_t bytes;
 };
 
 UnrLayout unr_layout(void* ws, int B, int M, int N) {
     Carver c(ws);
     UnrLayout L{};
-    L.rows = strip_rows(B, M);
+    L.nchunks = row_chunks(N);
+    L.rows = sweep_rows(B, M, L.nchunks);
     L.nstrips = (M + L.rows - 1) / L.rows;
     L.gamma = c.take<float>(size_t(B) * M * N);
     L.partial = c.take<float>(size_t(B) * L.nstrips * N);
     L.colsum = c.take<float>(size_t(B) * N);
-    L.tau_partial = c.take<float>(size_t(B) * L.nstrips);
+    L.tau_partial = c.take<float>(size_t(B) * L.nstrips * L.nchunks);
+    L.tpart = c.take<float>(L.nchunks > 1 ? size_t(B) * L.nchunks * M : 0);
     L.bytes = c.used();
     return L;
 }
@@ -174,11 +195,6 @@ void launch_fill_zero(void* p, size_t words, hipStream_t stream) {
 
 int check_shape(int B, int M, int N) {
     if (B < 0 || M < 0 || N < 0) return fail(DOT_ERR_INVALID_ARG, "B, M and N must be >= 0");
-    if (B > 65535) return fail(DOT_ERR_UNSUPPORTED, "batch size above 65535 is not supported");
-    if (N > kMaxRowLen)
-        return fail(DOT_ERR_UNSUPPORTED,
-                    "rows longer than 4096 columns are not supported by this build (N=" +
-                        std::to_string(N) + ")");
     return DOT_OK;
 }
 
@@ -414,6 +430,107 @@ bool launch_resident_forward(const dot_sinkhorn_fwd_args* a, const FwdLayout& L,
     return true;
 }
 
+// Rows longer than kMaxRowLen: per iteration a rows pass (chunk partials of
+// the row log-sum-exp), a columns pass (u and the column sums) and the column
+// combine; then the plan in chunk tiles.  The workspace's delta and potential
+// buffers are already cleared.
+void launch_wide_forward(const dot_sinkhorn_fwd_args* a, const FwdLayout& L, const float* ks_host,
+                         float kscale, float log_a_default, float log_b_default, bool keep, bool ret_log,
+                         bool vec4, hipStream_t stream) {
+    const int B = a->B, M = a->M, N = a->N, T = a->max_iter;
+    const dim3 tiles = batch_grid(unsigned(L.nstrips) * unsigned(L.nchunks), B);
+    const size_t lds = (size_t(2) * wide::kChunk + 8) * sizeof(float);
+    wide::dispatch_chunk(vec4, [&](auto vc, auto cc) {
+        constexpr int V = decltype(vc)::value;
+        constexpr int C = decltype(cc)::value;
+        for (int t = 1; t <= T; ++t) {
+            const int cur = t & 1, prev = (t - 1) & 1;
+            const float ks = ks_host ? ks_host[t - 1] : kscale;
+            wide::FwdArgs w{};
+            w.X = a->scores;
+            w.kscale = ks;
+            w.log_a = a->log_a;
+            w.log_a_default = log_a_default;
+            w.v_old = L.vbuf + size_t(prev) * B * N;
+            w.u_old = L.ubuf + size_t(prev) * B * M;
+            w.u_new = L.ubuf + size_t(cur) * B * M;
+            w.u_hist = keep ? a->u_hist + size_t(t - 1) * B * M : nullptr;
+            w.rpart = L.rpart;
+            w.partial = L.partial;
+            w.delta_bits = L.delta;
+            w.B = B;
+            w.M = M;
+            w.N = N;
+            w.rows = L.rows;
+            w.nstrips = L.nstrips;
+            w.nchunks = L.nchunks;
+            w.t = t;
+            w.tol = a->tol;
+            {
+                ProfScope prof("sk_fwd_wide_rows", stream);
+                hipLaunchKernelGGL((wide::fwd_rows<V, C>), tiles, dim3(kBlock), 0, stream, w);
+            }
+            {
+                ProfScope prof("sk_fwd_wide_cols", stream);
+                hipLaunchKernelGGL((wide::fwd_cols<V, C>), tiles, dim3(kBlock), lds, stream, w);
+            }
+            sk::FwdCombineArgs cb{};
+            cb.partial = L.partial;
+            cb.nstrips = L.nstrips;
+            cb.X = a->scores;
+            cb.kscale = ks;
+            cb.u_new = w.u_new;
+            cb.log_b = a->log_b;
+            cb.log_b_default = log_b_default;
+            cb.v_old = w.v_old;
+            cb.v_new = L.vbuf + size_t(cur) * B * N;
+            cb.v_hist = keep ? a->v_hist + size_t(t - 1) * B * N : nullptr;
+            cb.delta_bits = L.delta;
+            cb.tol = a->tol;
+            cb.t = t;
+            cb.B = B;
+            cb.M = M;
+            cb.N = N;
+            {
+                ProfScope prof("sk_fwd_combine", stream);
+                hipLaunchKernelGGL(sk::fwd_combine, column_grid(N, B), dim3(kBlock), 0, stream, cb);
+            }
+        }
+        {
+            ProfScope prof("sk_fwd_finalize", stream);
+            hipLaunchKernelGGL(sk::fwd_finalize, dim3(1), dim3(kWave), 0, stream, L.delta, T, a->tol,
+                               a->iters_used, a->converged);
+        }
+        if (a->plan || a->cost || a->u_out || a->v_out) {
+            sk::MaterializeArgs m{};
+            m.X = a->scores;
+            m.kscale = kscale;
+            m.scores_kind = a->scores_kind;
+            m.ubuf = L.ubuf;
+            m.vbuf = L.vbuf;
+            m.iters_used = a->iters_used;
+            m.plan = a->plan;
+            m.return_log = ret_log ? 1 : 0;
+            m.cost_partial = a->cost ? L.cost_partial : nullptr;
+            m.u_out = a->u_out;
+            m.v_out = a->v_out;
+            m.B = B;
+            m.M = M;
+            m.N = N;
+            m.rows = L.rows;
+            {
+                ProfScope prof("sk_materialize", stream);
+                hipLaunchKernelGGL((wide::materialize<V, C>), tiles, dim3(kBlock), 0, stream, m, L.nchunks);
+            }
+            if (a->cost) {
+                ProfScope prof("sk_batch_sum", stream);
+                hipLaunchKernelGGL(sk::batch_sum, dim3(B), dim3(kWave), 0, stream, L.cost_partial,
+                                   int(tiles.x), 1.0f, a->cost);
+            }
+        }
+    });
+}
+
 }  // namespace
 }  // namespace dot_amd
 
@@ -486,6 +603,10 @@ int dot_amd::sinkhorn_forward_scheduled(const dot_sinkhorn_fwd_args* a, const fl
     (void)hipGetLastError();
 
     launch_fill_zero(a->workspace, L.zero_words, stream);
+    if (L.nchunks > 1) {
+        launch_wide_forward(a, L, ks_host, kscale, log_a_default, log_b_default, keep, ret_log, vec4, stream);
+        return check_launch("dot_sinkhorn_forward");
+    }
 
     bool launched = dispatch_row(N, vec4, [&](auto vc, auto cc) {
         constexpr int V = decltype(vc)::value;
@@ -504,6 +625,7 @@ int dot_amd::sinkhorn_forward_scheduled(const dot_sinkhorn_fwd_args* a, const fl
             s.u_hist = keep ? a->u_hist + size_t(t - 1) * B * M : nullptr;
             s.partial = L.partial;
             s.delta_bits = L.delta;
+            s.B = B;
             s.M = M;
             s.N = N;
             s.rows = L.rows;
@@ -512,7 +634,7 @@ int dot_amd::sinkhorn_forward_scheduled(const dot_sinkhorn_fwd_args* a, const fl
             s.tol = a->tol;
             {
                 ProfScope prof("sk_fwd_sweep", stream);
-                hipLaunchKernelGGL((sk::fwd_sweep<V, C>), dim3(L.nstrips, B), dim3(kBlock), lds,
+                hipLaunchKernelGGL((sk::fwd_sweep<V, C>), batch_grid(unsigned(L.nstrips), B), dim3(kBlock), lds,
                                    stream, s);
             }
             sk::FwdCombineArgs cb{};
@@ -529,6 +651,7 @@ int dot_amd::sinkhorn_forward_scheduled(const dot_sinkhorn_fwd_args* a, const fl
             cb.delta_bits = L.delta;
             cb.tol = a->tol;
             cb.t = t;
+            cb.B = B;
             cb.M = M;
             cb.N = N;
             {
@@ -560,7 +683,7 @@ int dot_amd::sinkhorn_forward_scheduled(const dot_sinkhorn_fwd_args* a, const fl
             m.rows = L.rows;
             {
                 ProfScope prof("sk_materialize", stream);
-                hipLaunchKernelGGL((sk::materialize<V, C>), dim3(L.nstrips, B), dim3(kBlock), 0,
+                hipLaunchKernelGGL((sk::materialize<V, C>), batch_grid(unsigned(L.nstrips), B), dim3(kBlock), 0,
                                    stream, m);
             }
             if (a->cost) {
@@ -712,6 +835,108 @@ bool launch_stream_adjoint(const dot_sinkhorn_bwd_args* a, const ImpLayout& L, c
     return true;
 }
 
+// Rows longer than kMaxRowLen: the prologue in chunk tiles with a row-total
+// fold, then per sweep a rows pass (chunk partials of P mu), a columns pass
+// (lambda and the column partials of P lambda) and the mu combine, then the
+// gradient in chunk tiles.
+void launch_wide_implicit(const dot_sinkhorn_bwd_args* a, const ImpLayout& L, const sk::ImpArgs& x,
+                          float inv_tau, hipStream_t stream) {
+    const int B = a->B, M = a->M, N = a->N;
+    wide::ImpArgs w{};
+    w.s = x;
+    w.rpart = L.rpart;
+    w.dpart = L.dpart;
+    w.B = B;
+    w.nchunks = L.nchunks;
+    const dim3 tiles = batch_grid(unsigned(L.nstrips) * unsigned(L.nchunks), B);
+    const size_t lds = (size_t(2) * wide::kChunk + 8) * sizeof(float);
+    const unsigned row_blocks = unsigned((size_t(B) * M + kWavesPerBlock - 1) / kWavesPerBlock);
+    wide::dispatch_chunk(bwd_vec4(a), [&](auto vc, auto cc) {
+        constexpr int V = decltype(vc)::value;
+        constexpr int C = decltype(cc)::value;
+        {
+            ProfScope prof("sk_imp_prep", stream);
+            hipLaunchKernelGGL((wide::imp_prep<V, C>), tiles, dim3(kBlock), lds, stream, w);
+        }
+        {
+            ProfScope prof("sk_imp_prep_combine", stream);
+            hipLaunchKernelGGL(wide::imp_row_totals, dim3(row_blocks), dim3(kBlock), 0, stream, w);
+            hipLaunchKernelGGL(sk::imp_prep_combine, column_grid(N, B), dim3(kBlock), 0, stream, x);
+        }
+        for (int it = 0; it < a->iters; ++it) {
+            {
+                ProfScope prof("sk_imp_wide_rows", stream);
+                hipLaunchKernelGGL((wide::imp_rows<V, C>), tiles, dim3(kBlock), 0, stream, w);
+            }
+            {
+                ProfScope prof("sk_imp_wide_cols", stream);
+                hipLaunchKernelGGL((wide::imp_cols<V, C>), tiles, dim3(kBlock), lds, stream, w);
+            }
+            {
+                ProfScope prof("sk_imp_combine", stream);
+                hipLaunchKernelGGL(sk::imp_mu_combine, column_grid(N, B), dim3(kBlock), 0, stream, x);
+            }
+        }
+        {
+            ProfScope prof("sk_imp_final", stream);
+            hipLaunchKernelGGL((wide::imp_final<V, C>), tiles, dim3(kBlock), 0, stream, w);
+        }
+        {
+            ProfScope prof("sk_batch_sum", stream);
+            hipLaunchKernelGGL(sk::batch_sum, dim3(B), dim3(kWave), 0, stream, L.tau_partial, int(tiles.x),
+                               -inv_tau, a->grad_tau, nullptr, a->status);
+        }
+    });
+}
+
+// Rows longer than kMaxRowLen: Gamma = G P in chunk tiles, then per recorded
+// step the column fold, a rows pass (chunk partials of rowsum(Gamma_Y)) and a
+// columns pass (Gamma, or the gradient on the last step).
+void launch_wide_unrolled(const dot_sinkhorn_bwd_args* a, const UnrLayout& L, const sk::UnrArgs& x0,
+                          float neg_inv_tau2, hipStream_t stream) {
+    const int B = a->B, M = a->M, N = a->N, T = a->iters;
+    wide::UnrArgs w{};
+    w.s = x0;
+    w.tpart = L.tpart;
+    w.B = B;
+    w.nchunks = L.nchunks;
+    const dim3 tiles = batch_grid(unsigned(L.nstrips) * unsigned(L.nchunks), B);
+    const size_t lds = (size_t(2) * wide::kChunk + 8) * sizeof(float);
+    wide::dispatch_chunk(bwd_vec4(a), [&](auto vc, auto cc) {
+        constexpr int V = decltype(vc)::value;
+        constexpr int C = decltype(cc)::value;
+        w.s.final_step = T == 0;
+        {
+            ProfScope prof("sk_unr_init", stream);
+            hipLaunchKernelGGL((wide::unr_init<V, C>), tiles, dim3(kBlock), lds, stream, w);
+        }
+        for (int t = T - 1; t >= 0; --t) {
+            {
+                ProfScope prof("sk_unr_fold", stream);
+                hipLaunchKernelGGL(sk::column_fold, column_grid(N, B), dim3(kBlock), 0, stream, L.partial,
+                                   L.nstrips, B, N, L.colsum);
+            }
+            w.s.u_t = a->u_hist + size_t(t) * B * M;
+            w.s.v_t = a->v_hist + size_t(t) * B * N;
+            w.s.v_tm1 = t > 0 ? a->v_hist + size_t(t - 1) * B * N : nullptr;
+            w.s.final_step = t == 0;
+            {
+                ProfScope prof("sk_unr_wide_rows", stream);
+                hipLaunchKernelGGL((wide::unr_rows<V, C>), tiles, dim3(kBlock), 0, stream, w);
+            }
+            {
+                ProfScope prof("sk_unr_step", stream);
+                hipLaunchKernelGGL((wide::unr_cols<V, C>), tiles, dim3(kBlock), lds, stream, w);
+            }
+        }
+        {
+            ProfScope prof("sk_batch_sum", stream);
+            hipLaunchKernelGGL(sk::batch_sum, dim3(B), dim3(kWave), 0, stream, L.tau_partial, int(tiles.x),
+                               neg_inv_tau2, a->grad_tau, nullptr, a->status);
+        }
+    });
+}
+
 }  // namespace
 
 extern "C" size_t dot_sinkhorn_backward_implicit_workspace_bytes(int B, int M, int N) {
@@ -744,11 +969,12 @@ extern "C" int dot_sinkhorn_backward_implicit(const dot_sinkhorn_bwd_args* a, do
     x.grad = a->grad_scores;
     x.tau_partial = L.tau_partial;
     x.inv_tau = inv_tau;
+    x.B = B;
     x.M = M;
     x.N = N;
     x.rows = L.rows;
     const size_t lds = lds_bytes(N);
-    const dim3 strips(L.nstrips, B);
+    const dim3 strips = batch_grid(unsigned(L.nstrips), B);
     const ResidentCfg rc = resident_config<false>(B, M, N, bwd_vec4(a));
     if (rc.ok && launch_resident_adjoint(a, L, rc, inv_tau, stream))
         return check_launch("dot_sinkhorn_backward_implicit");
@@ -757,6 +983,10 @@ extern "C" int dot_sinkhorn_backward_implicit(const dot_sinkhorn_bwd_args* a, do
     if (sc.ok && launch_stream_adjoint(a, L, sc, inv_tau, bwd_vec4(a), stream))
         return check_launch("dot_sinkhorn_backward_implicit");
     (void)hipGetLastError();
+    if (L.nchunks > 1) {
+        launch_wide_implicit(a, L, x, inv_tau, stream);
+        return check_launch("dot_sinkhorn_backward_implicit");
+    }
     bool launched = dispatch_row(N, bwd_vec4(a), [&](auto vc, auto cc) {
         constexpr int V = decltype(vc)::value;
         constexpr int C = decltype(cc)::value;
@@ -822,11 +1052,16 @@ extern "C" int dot_sinkhorn_backward_unrolled(const dot_sinkhorn_bwd_args* a, do
     x.grad = a->grad_scores;
     x.tau_partial = L.tau_partial;
     x.inv_tau = inv_tau;
+    x.B = B;
     x.M = M;
     x.N = N;
     x.rows = L.rows;
     const size_t lds = lds_bytes(N);
-    const dim3 strips(L.nstrips, B);
+    const dim3 strips = batch_grid(unsigned(L.nstrips), B);
+    if (L.nchunks > 1) {
+        launch_wide_unrolled(a, L, x, neg_inv_tau2, stream);
+        return check_launch("dot_sinkhorn_backward_unrolled");
+    }
     bool launched = dispatch_row(N, bwd_vec4(a), [&](auto vc, auto cc) {
         constexpr int V = decltype(vc)::value;
         constexpr int C = decltype(cc)::value;
@@ -839,7 +1074,7 @@ extern "C" int dot_sinkhorn_backward_unrolled(const dot_sinkhorn_bwd_args* a, do
             {
                 ProfScope prof("sk_unr_fold", stream);
                 hipLaunchKernelGGL(sk::column_fold, column_grid(N, B), dim3(kBlock), 0, stream,
-                                   L.partial, L.nstrips, N, L.colsum);
+                                   L.partial, L.nstrips, B, N, L.colsum);
             }
             x.u_t = a->u_hist + size_t(t) * B * M;
             x.v_t = a->v_hist + size_t(t) * B * N;

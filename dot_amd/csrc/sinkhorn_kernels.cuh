@@ -46,7 +46,7 @@ struct FwdSweepArgs {
     float* u_hist;         // [B,M] slice of the history for this iteration, or null
     float* partial;        // [B,nstrips,N]
     unsigned* delta_bits;  // [max_iter+1]
-    int M, N, rows, nstrips, t;
+    int B, M, N, rows, nstrips, t;
     float tol;
 };
 
@@ -65,7 +65,8 @@ __global__ __launch_bounds__(kBlock) void fwd_sweep(FwdSweepArgs a) {
     const int lane = threadIdx.x % kWave;
     const int wave = threadIdx.x / kWave;
     const int s = blockIdx.x;
-    const int b = blockIdx.y;
+    const int b = batch_of_block();
+    if (b >= a.B) return;
     const int r0 = s * a.rows;
     const int r1 = min(r0 + a.rows, a.M);
     const size_t bM = size_t(b) * a.M;
@@ -128,7 +129,7 @@ struct FwdCombineArgs {
     float* v_hist;         // [B,N] slice or null
     const unsigned* delta_bits;
     float tol;
-    int t, M, N;
+    int t, B, M, N;
 };
 
 // Column update v_j = log b_j + v_j - log colsum_j (kernels.cu:629-671 in
@@ -136,7 +137,8 @@ struct FwdCombineArgs {
 // finite) take the reference's exact max-shifted LSE over the column.
 static __global__ __launch_bounds__(kBlock) void fwd_combine(FwdCombineArgs a) {
     if (stopped_before(a.delta_bits, a.t, a.tol)) return;
-    const int b = blockIdx.y;
+    const int b = batch_of_block();
+    if (b >= a.B) return;
     const int j = blockIdx.x * kBlock + threadIdx.x;
     if (j >= a.N) return;
     const float* p = a.partial + size_t(b) * a.nstrips * a.N + j;
@@ -203,7 +205,8 @@ __global__ __launch_bounds__(kBlock) void materialize(MaterializeArgs a) {
     __shared__ float scratch[kWavesPerBlock];
     const int lane = threadIdx.x % kWave;
     const int wave = threadIdx.x / kWave;
-    const int b = blockIdx.y;
+    const int b = batch_of_block();
+    if (b >= a.B) return;
     const int par = (*a.iters_used) & 1;
     const float* u = a.ubuf + (size_t(par) * a.B + b) * a.M;
     const float* vsrc = a.vbuf + (size_t(par) * a.B + b) * a.N;
@@ -302,7 +305,7 @@ struct ImpArgs {
     float* grad;     // [B,M,N]
     float* tau_partial;  // [B, gridDim.x]
     float inv_tau;
-    int M, N, rows;
+    int B, M, N, rows;
 };
 
 // Row sums of P*G and P, plus their column partials, once per backward: the
@@ -315,7 +318,8 @@ __global__ __launch_bounds__(kBlock) void imp_prep(ImpArgs a) {
     const int lane = threadIdx.x % kWave;
     const int wave = threadIdx.x / kWave;
     const int s = blockIdx.x;
-    const int b = blockIdx.y;
+    const int b = batch_of_block();
+    if (b >= a.B) return;
     const int r0 = s * a.rows;
     const int r1 = min(r0 + a.rows, a.M);
     const size_t bM = size_t(b) * a.M;
@@ -351,7 +355,8 @@ __global__ __launch_bounds__(kBlock) void imp_prep(ImpArgs a) {
 }
 
 static __global__ __launch_bounds__(kBlock) void imp_prep_combine(ImpArgs a) {
-    const int b = blockIdx.y;
+    const int b = batch_of_block();
+    if (b >= a.B) return;
     const int j = blockIdx.x * kBlock + threadIdx.x;
     if (j >= a.N) return;
     const size_t base = size_t(b) * a.nstrips * a.N + j;
@@ -375,7 +380,8 @@ __global__ __launch_bounds__(kBlock) void imp_lambda_sweep(ImpArgs a) {
     const int lane = threadIdx.x % kWave;
     const int wave = threadIdx.x / kWave;
     const int s = blockIdx.x;
-    const int b = blockIdx.y;
+    const int b = batch_of_block();
+    if (b >= a.B) return;
     const int r0 = s * a.rows;
     const int r1 = min(r0 + a.rows, a.M);
     const size_t bM = size_t(b) * a.M;
@@ -402,7 +408,8 @@ __global__ __launch_bounds__(kBlock) void imp_lambda_sweep(ImpArgs a) {
 
 // mu_k = (sum_i P G - sum_i P lambda_i) / max(sum_i P, 1e-12)   (kernels.cu:1007-1047)
 static __global__ __launch_bounds__(kBlock) void imp_mu_combine(ImpArgs a) {
-    const int b = blockIdx.y;
+    const int b = batch_of_block();
+    if (b >= a.B) return;
     const int j = blockIdx.x * kBlock + threadIdx.x;
     if (j >= a.N) return;
     const size_t base = size_t(b) * a.nstrips * a.N + j;
@@ -420,7 +427,8 @@ __global__ __launch_bounds__(kBlock) void imp_final(ImpArgs a) {
     __shared__ float scratch[kWavesPerBlock];
     const int lane = threadIdx.x % kWave;
     const int wave = threadIdx.x / kWave;
-    const int b = blockIdx.y;
+    const int b = batch_of_block();
+    if (b >= a.B) return;
     const int r0 = blockIdx.x * a.rows;
     const int r1 = min(r0 + a.rows, a.M);
     const size_t bM = size_t(b) * a.M;
@@ -466,7 +474,7 @@ struct UnrArgs {
     float* grad;           // [B,M,N] written on the final step
     float* tau_partial;    // [B, gridDim.x]
     float inv_tau;
-    int M, N, rows;
+    int B, M, N, rows;
     int final_step;
 };
 
@@ -497,7 +505,8 @@ __global__ __launch_bounds__(kBlock) void unr_init(UnrArgs a) {
     const int lane = threadIdx.x % kWave;
     const int wave = threadIdx.x / kWave;
     const int s = blockIdx.x;
-    const int b = blockIdx.y;
+    const int b = batch_of_block();
+    if (b >= a.B) return;
     const int r0 = s * a.rows;
     const int r1 = min(r0 + a.rows, a.M);
     const size_t bM = size_t(b) * a.M;
@@ -529,9 +538,10 @@ __global__ __launch_bounds__(kBlock) void unr_init(UnrArgs a) {
 }
 
 // colsum[b, j] = sum over strips of partial (plain sum, fixed order).
-static __global__ __launch_bounds__(kBlock) void column_fold(const float* partial, int nstrips, int N,
+static __global__ __launch_bounds__(kBlock) void column_fold(const float* partial, int nstrips, int B, int N,
                                                      float* out) {
-    const int b = blockIdx.y;
+    const int b = batch_of_block();
+    if (b >= B) return;
     const int j = blockIdx.x * kBlock + threadIdx.x;
     if (j >= N) return;
     const size_t base = size_t(b) * nstrips * N + j;
@@ -550,7 +560,8 @@ __global__ __launch_bounds__(kBlock) void unr_step(UnrArgs a) {
     const int lane = threadIdx.x % kWave;
     const int wave = threadIdx.x / kWave;
     const int s = blockIdx.x;
-    const int b = blockIdx.y;
+    const int b = batch_of_block();
+    if (b >= a.B) return;
     const int r0 = s * a.rows;
     const int r1 = min(r0 + a.rows, a.M);
     const size_t bM = size_t(b) * a.M;

@@ -49,6 +49,11 @@ SHAPES = [
     (1, 512, 4096, 1.0, None),
     (1, 300, 4093, 0.8, [[250, 4000]]),
     (4, 1500, 64, 1.0, [[1500, 64], [1, 1], [700, 10], [1499, 63]]),
+    # rows longer than 4096 columns (strips x chunks tiles); L2 % 4 != 0: scalar loads
+    (2, 40, 4097, 1.0, [[40, 4097], [17, 3000]]),
+    (1, 64, 6000, 0.7, None),
+    (2, 33, 8192, 1.3, [[33, 8192], [20, 6001]]),
+    (1, 16, 5001, 1.0, [[16, 4500]]),
 ]
 
 
@@ -159,3 +164,34 @@ def test_reference_cpu_cuda_consistency():
             outs.append((P.detach().cpu(), s.grad.cpu()))
         assert torch.allclose(outs[0][0], outs[1][0], atol=1e-5)
         assert rel_err(outs[1][1], outs[0][1]) < 1e-4
+
+
+def test_batch_above_65535():
+    """Batch elements spill from grid y into grid z beyond 65535: forward and
+    backward at B = 70001 against the oracle, ragged lengths included."""
+    rng = np.random.default_rng(65536)
+    B, L1, L2, tau = 70001, 3, 5, 0.9
+    s = rng.standard_normal((B, L1, L2)).astype(np.float32)
+    g = rng.standard_normal((B, L1, L2)).astype(np.float32)
+    ln = np.stack([rng.integers(0, L1 + 1, B), rng.integers(0, L2 + 1, B)], 1).astype(np.int32)
+    ln[-1] = [L1, L2]
+    out_o, r_o, c_o = obs.forward(s, tau, ln)
+    gs_o, gt_o = obs.backward(s, out_o, g, r_o, c_o, tau, ln)
+    out, r, c = _ops.bidirectional_softmax(_t(s), tau, _t(ln))
+    assert rel_err(out, out_o) < FWD_TOL and rel_err(c, c_o) < FWD_TOL
+    gs, gt = _ops.bidirectional_softmax_backward(_t(s), out, _t(g), r, c, tau, _t(ln))
+    assert rel_err(gs, gs_o) < GRAD_TOL
+    # grad_tau of 70001 tiny elements: where one valid row meets a few valid
+    # columns its terms nearly cancel, and float32 itself lands up to ~4e-4 of
+    # sum|terms| from float64 (the oracle's float32 run shows the same figure),
+    # so each element is held to max(1e-4, 2x the float32 spread)
+    o32, r32, c32 = obs.forward(s, tau, ln, dtype=np.float32)
+    _, gt32 = obs.backward(s, o32, g, r32, c32, tau, ln, dtype=np.float32)
+    terms = gs_o * s / tau
+    spread = sum_err(gt32, gt_o, terms)
+    assert sum_err(gt, gt_o, terms) < max(GRAD_TOL, 2 * spread), spread
+    x = _t(s).requires_grad_(True)
+    P = dot_amd.bidirectional_softmax(x, tau, _t(ln))
+    P.backward(_t(g))
+    assert rel_err(P, out_o) < FWD_TOL and rel_err(x.grad, gs_o) < GRAD_TOL
+    assert rel_err(x.grad[-1:], gs_o[-1:]) < GRAD_TOL

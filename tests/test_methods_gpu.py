@@ -108,6 +108,21 @@ def test_scheduled_plain_iteration_on_every_tier(tier, shape, monkeypatch):
     assert rel_err(P, ref.P) < FWD_TOL
 
 
+def test_scheduled_plain_iteration_on_long_rows():
+    """The plain method with a schedule on rows longer than 4096 columns (the
+    forward's strips x chunks tiles with a per-iteration K scale); the
+    accelerated methods refuse such rows with a clear error."""
+    B, M, N = 1, 24, 4500
+    la, lga, lgb = _case(4500, B, M, N, marginals=True)
+    for schedule, T in ((LIN, 3), (EXP, 12)):
+        P, used, conv = _gpu(la, 0.1, T, 0.0, lga, lgb, schedule=schedule, reg_start=0.4)
+        ref = _oracle(la, 0.1, T, 0.0, lga, lgb, schedule=schedule, reg_start=0.4)
+        assert used == T and conv == 0
+        assert rel_err(P, ref.P) < FWD_TOL, (schedule, T)
+    with pytest.raises(RuntimeError, match="longer than 4096"):
+        _gpu(la, 0.1, 5, 0.0, lga, lgb, method=1, omega=1.3)
+
+
 def test_schedule_with_start_equal_to_target_is_the_plain_iteration():
     la, _, _ = _case(3, 2, 48, 40)
     P_plain, _, _ = _gpu(la, 0.1, 30)

@@ -201,8 +201,8 @@ def test_op_argument_errors():
         _ops.sinkhorn_with_grads_implicit(x, torch.zeros(2, 4, 5, device=DEV), 1.0, 5, 5)
     with pytest.raises(RuntimeError, match="anderson_k"):
         _ops.sinkhorn_dual_forward(x, 1.0, 5, 0.0, None, None, False, 2, 1.5, 0)
-    with pytest.raises(RuntimeError, match="4096"):
-        _ops.sinkhorn(torch.rand(1, 2, 4097, device=DEV), 1.0, 1)
+    with pytest.raises(RuntimeError, match="method"):
+        _ops.sinkhorn_dual_forward(x, 1.0, 5, 0.0, None, None, False, 7)
 
 
 # ---------------------------------------------------------------------------
@@ -855,3 +855,105 @@ def test_exchange_timeout_is_raised(shape, env, monkeypatch):
     res.cost.sum().backward()
     assert res.n_iters_used == 20 and torch.isfinite(leaf.grad).all()
     assert _drain_errors() == []
+
+
+# ---------------------------------------------------------------------------
+# Rows longer than 4096 columns (strips x chunks tiles) and batches above 65535
+# ---------------------------------------------------------------------------
+WIDE = [
+    # (B, M, N, tau, T, tol, nonuniform); N % 4 != 0 takes the scalar-load tiles
+    (1, 64, 4097, 0.3, 20, 0.0, False),
+    (2, 40, 6000, 0.1, 30, 1e-6, True),
+    (1, 33, 8192, 0.5, 15, 0.0, True),
+    (2, 17, 5001, 1.0, 10, 0.0, False),
+]
+
+
+@pytest.mark.parametrize("B,M,N,tau,T,tol,nonuni", WIDE)
+def test_wide_rows_match_oracle(B, M, N, tau, T, tol, nonuni):
+    """Forward (with and without the stop test), implicit and unrolled adjoints,
+    and the public API's cost gradient, for rows longer than a wave holds in
+    registers (the reference chunks any row length: kernels.cuh:36-44,
+    kernels.cu:547-627)."""
+    rng = np.random.default_rng(B * 31 + M + N)
+    C = rng.random((B, M, N)).astype(np.float32)
+    G = rng.standard_normal((B, M, N)).astype(np.float32)
+    lga = lgb = None
+    if nonuni:
+        lga, lgb = np.log(_dirichlet(rng, B, M)), np.log(_dirichlet(rng, B, N))
+    lt = lambda x: None if x is None else _t(x)
+    print(f"[wide] B={B} M={M} N={N} tau={tau} T={T} tol={tol}", flush=True)
+    P, used, conv = _ops.sinkhorn_dual_forward(_t(-C), tau, T, tol, lt(lga), lt(lgb))
+    used = int(used)
+    if tol > 0:
+        o = osk.dual_forward(-C, tau, T, tol=tol, log_a=lga, log_b=lgb)
+        assert abs(used - o.n_iters_used) <= 1, (used, o.n_iters_used)
+    else:
+        assert used == T and int(conv) == 0
+    assert rel_err(P, osk.dual_forward(-C, tau, used, log_a=lga, log_b=lgb).P) < FWD_TOL
+    P, gi, gti = _ops.sinkhorn_with_grads_implicit(_t(-C), _t(G), tau, T, T, lt(lga), lt(lgb))
+    Po, go, gto = osk.with_grads_implicit(-C, G, tau, T, T, lga, lgb)
+    assert rel_err(P, Po) < FWD_TOL
+    assert rel_err(gi, go) < GRAD_TOL
+    assert sum_err(gti, gto, go * -C / tau) < GRAD_TOL
+    Tu = min(T, 12)
+    P, gu, gtu = _ops.sinkhorn_with_grads_unrolled(_t(-C), _t(G), tau, Tu, lt(lga), lt(lgb))
+    Po, go, gto = osk.with_grads_unrolled(-C, G, tau, Tu, lga, lgb)
+    assert rel_err(P, Po) < FWD_TOL
+    assert rel_err(gu, go) < GRAD_TOL
+    assert sum_err(gtu, gto, go * -C / tau) < GRAD_TOL
+    # public API: plan, cost and cost gradient, return_log
+    leaf = _t(C).requires_grad_(True)
+    a = None if lga is None else _t(np.exp(lga))
+    b = None if lgb is None else _t(np.exp(lgb))
+    res = dot_amd.sinkhorn(leaf, reg=tau, n_iters=T, tol=0, a=a, b=b)
+    res.cost.sum().backward()
+    Pc, costc, dC, _, _ = _oracle_cost_grads(C, tau, T, T, None if a is None else np.exp(lga),
+                                             None if b is None else np.exp(lgb))
+    assert rel_err(res.transport_plan, Pc) < FWD_TOL
+    assert rel_err(res.cost, costc) < FWD_TOL
+    assert rel_err(leaf.grad, dC) < GRAD_TOL
+    logP = _ops.sinkhorn_log(_t(-C), tau, T, lt(lga), lt(lgb))
+    assert rel_err(logP.exp(), Pc) < FWD_TOL
+
+
+def test_wide_rows_exact_column_fallback():
+    """Columns whose sum underflows take the exact column log-sum-exp on the
+    tiled path too."""
+    rng = np.random.default_rng(91)
+    B, M, N, tau, T = 1, 24, 4500, 0.01, 8
+    C = (0.1 * rng.random((B, M, N))).astype(np.float32)
+    C[:, :, 7] = 0.7
+    C[:, :, 4400] = 0.8
+    P, used, _ = _ops.sinkhorn_dual_forward(_t(-C), tau, T, 0.0)
+    assert int(used) == T and torch.isfinite(P).all()
+    assert rel_err(P, osk.dual_forward(-C, tau, T).P) < FWD_TOL
+
+
+def test_batch_above_65535():
+    """Grids put batch elements on y and z (at most 65535 per dimension):
+    forward, both adjoints and the cost gradient at B = 70001 against the
+    oracle, on small matrices of the streaming tier."""
+    rng = np.random.default_rng(70001)
+    B, M, N, tau, T = 70001, 3, 6, 0.5, 12
+    C = rng.random((B, M, N)).astype(np.float32)
+    G = rng.standard_normal((B, M, N)).astype(np.float32)
+    print(f"[batch] B={B} M={M} N={N}", flush=True)
+    P, used, conv = _ops.sinkhorn_dual_forward(_t(-C), tau, 200, 1e-6)
+    o = osk.dual_forward(-C, tau, 200, tol=1e-6)
+    assert abs(int(used) - o.n_iters_used) <= 1
+    assert rel_err(P, osk.dual_forward(-C, tau, int(used)).P) < FWD_TOL
+    P, gi, gti = _ops.sinkhorn_with_grads_implicit(_t(-C), _t(G), tau, T, T)
+    Po, go, gto = osk.with_grads_implicit(-C, G, tau, T, T)
+    assert rel_err(P, Po) < FWD_TOL and rel_err(gi, go) < GRAD_TOL
+    assert sum_err(gti, gto, go * -C / tau) < GRAD_TOL
+    P, gu, gtu = _ops.sinkhorn_with_grads_unrolled(_t(-C), _t(G), tau, T)
+    Po, go, gto = osk.with_grads_unrolled(-C, G, tau, T)
+    assert rel_err(P, Po) < FWD_TOL and rel_err(gu, go) < GRAD_TOL
+    # the last batch element is computed (not dropped by the z slab's tail)
+    assert rel_err(gu[-1:], go[-1:]) < GRAD_TOL
+    leaf = _t(C).requires_grad_(True)
+    res = dot_amd.sinkhorn(leaf, reg=tau, n_iters=T, tol=0)
+    res.cost.sum().backward()
+    Pc, costc, dC, _, _ = _oracle_cost_grads(C, tau, T, T)
+    assert rel_err(res.cost, costc) < FWD_TOL and rel_err(leaf.grad, dC) < GRAD_TOL
