@@ -84,6 +84,23 @@ typedef struct {
 size_t dot_sinkhorn_forward_workspace_bytes(int B, int M, int N, int max_iter, int flags);
 int dot_sinkhorn_forward(const dot_sinkhorn_fwd_args* args, dot_stream_t stream);
 
+/* Bytes of the static device scratch behind dot_sinkhorn_forward_noalloc. */
+#define DOT_STATIC_SCRATCH_BYTES (64u << 20)
+
+/* dot_sinkhorn_forward without a workspace argument and without any
+ * allocation: args->workspace and args->workspace_bytes are ignored and the
+ * scratch is a file-scope device array of DOT_STATIC_SCRATCH_BYTES per GPU,
+ * held from the first call on that GPU until the process ends.  Shapes whose
+ * dot_sinkhorn_forward_workspace_bytes() exceeds DOT_STATIC_SCRATCH_BYTES
+ * return DOT_ERR_UNSUPPORTED.  Results are those of dot_sinkhorn_forward.
+ * All calls on one GPU share its array (each call clears what must start at
+ * zero), so calls that overlap on one GPU — on different streams, or from
+ * different threads — race and must be serialised by the caller.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). */
+int dot_sinkhorn_forward_noalloc(const dot_sinkhorn_fwd_args* args, dot_stream_t stream);
+
 /* Solver of dot_sinkhorn_method_args.method (the reference's method codes). */
 #define DOT_SK_VANILLA 0
 #define DOT_SK_MOMENTUM 1

@@ -150,6 +150,21 @@ def test_method_forward_rejects_bad_arguments_on_the_host(lib):
     assert f(ctypes.byref(m), None) == DOT_ERR_WORKSPACE
 
 
+def test_noalloc_forward_rejects_on_the_host(lib):
+    """The allocation-free forward checks the shape against its static scratch
+    (DOT_STATIC_SCRATCH_BYTES) before touching a device."""
+    f = lib.dot_sinkhorn_forward_noalloc
+    f.argtypes = [ctypes.POINTER(FwdArgs), ctypes.c_void_p]
+    q = lib.dot_sinkhorn_forward_workspace_bytes
+    q.restype = ctypes.c_size_t
+    assert f(None, None) == DOT_ERR_INVALID_ARG
+    assert q(256, 2048, 2048, 100, 0) > 64 << 20
+    a = FwdArgs(B=256, M=2048, N=2048, scores_kind=1, tau=1.0, max_iter=100)
+    assert f(ctypes.byref(a), None) == DOT_ERR_UNSUPPORTED
+    assert "static scratch holds 67108864" in _last_error(lib)
+    assert "#define DOT_STATIC_SCRATCH_BYTES (64u << 20)" in open(HEADER).read()
+
+
 def test_long_rows_and_large_batches_have_workspace(lib):
     """Rows longer than 4096 columns and batches above 65535 are accepted: the
     workspace queries size their chunk and strip partials."""
