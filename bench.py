@@ -279,9 +279,12 @@ def profiled_pass(profiler, names, step, steps, torch):
 def sinkhorn_roofline(dominant, stats, E, T_f, T_b, workload):
     """Roofline object of the dominant Sinkhorn kernel (see the module docstring)."""
     sweeps = {"sk_imp_resident": T_b, "sk_fwd_resident": T_f, "sk_imp_persistent": T_b,
-              "sk_fwd_persistent": T_f}.get(dominant, 1)
+              "sk_fwd_persistent": T_f, "sk_unr_persistent": T_b}.get(dominant, 1)
     avg_s = stats[dominant]["avg_us"] * 1e-6
     hbm_equiv = 4.0 * E * sweeps  # one fp32 read of the [B,M,N] matrix per sweep
+    if dominant in ("sk_unr_step", "sk_unr_persistent"):
+        # a reverse step of the unrolled backward reads Gamma and C and writes Gamma
+        hbm_equiv = 12.0 * E * sweeps
     traffic = _pmc_traffic(dominant, workload)
     measured = None if traffic is None else {
         "GBps": round(traffic / avg_s / 1e9, 1), "frac": round(traffic / avg_s / 1e9 / HBM_PEAK_GBPS, 4)}
@@ -304,12 +307,14 @@ def sinkhorn_roofline(dominant, stats, E, T_f, T_b, workload):
             "traffic": traffic, "hbm_measured": measured, "bytes_per_launch": hbm_equiv,
             "sweeps_per_launch": sweeps,
             "tier": "persistent streaming (one launch; the matrix is re-read every sweep)"
-            if "persistent" in dominant else "streaming sweeps (one launch per sweep)"}
+            if "persistent" in dominant else "streaming sweeps (one launch per sweep)",
+            "bytes_per_elem_sweep": 12.0 if "unr" in dominant else 4.0}
 
 
 SINKHORN_KERNELS = ["sk_fwd_sweep", "sk_imp_sweep", "sk_fwd_resident", "sk_imp_resident",
                     "sk_fwd_persistent", "sk_imp_persistent", "mth_sweep", "mth_vfinish",
-                    "sk_fwd_wide_rows", "sk_fwd_wide_cols", "sk_imp_wide_rows", "sk_imp_wide_cols"]
+                    "sk_fwd_wide_rows", "sk_fwd_wide_cols", "sk_imp_wide_rows", "sk_imp_wide_cols",
+                    "sk_unr_step", "sk_unr_init", "sk_unr_fold", "sk_unr_resident", "sk_unr_persistent"]
 
 
 def bench_sinkhorn(args, workload, steps, warmup, torch, dot_amd, profiler, solver=None):
@@ -345,7 +350,9 @@ def bench_sinkhorn(args, workload, steps, warmup, torch, dot_amd, profiler, solv
     stats = profiled_pass(profiler, SINKHORN_KERNELS, step, steps, torch)
 
     T_f = sum(used) / len(used)
-    T_b = n_iters  # backward_iters defaults to n_iters; the adjoint runs exactly that many sweeps
+    # implicit: backward_iters defaults to n_iters and the adjoint runs exactly that many
+    # sweeps; unrolled: one reverse step per recorded forward iteration
+    T_b = T_f if solver.get("backward_mode") == "unrolled" else n_iters
     sec_per_step = (t1 - t0) / steps
     value = E * (T_f + T_b) / sec_per_step
 
@@ -365,7 +372,8 @@ def bench_sinkhorn(args, workload, steps, warmup, torch, dot_amd, profiler, solv
                                   f" method={effective} schedule={eff_schedule}"),
                    "method": effective, "schedule": eff_schedule,
                    "B": B, "M": M, "N": N, "reg": reg, "n_iters": n_iters, "tol": tol,
-                   "n_iters_used": used[-1], "backward_iters": T_b},
+                   "n_iters_used": used[-1], "backward_iters": T_b,
+                   "backward_mode": solver.get("backward_mode", "implicit")},
         "algorithmic_GBps": algo_bytes / sec_per_step / 1e9,
         "frac_of_hbm_peak": algo_bytes / sec_per_step / 1e9 / HBM_PEAK_GBPS,
         "kernels": stats,
@@ -461,6 +469,9 @@ def main():
     ap.add_argument("--lr", type=float, default=1.0)
     ap.add_argument("--anderson-k", type=int, default=5)
     ap.add_argument("--reg-start", type=float, default=None)
+    ap.add_argument("--backward-mode", default="implicit", choices=["implicit", "unrolled"],
+                    help="the backward the step runs (unrolled: the reverse pass through the "
+                         "n_iters_used recorded iterations)")
     ap.add_argument("--no-bidi", action="store_true", help="skip the bidirectional-softmax leg")
     ap.add_argument("--headline-only", action="store_true",
                     help="skip the other Sinkhorn configurations (C1, C4, C5 besides the headline)")
@@ -500,10 +511,13 @@ def main():
 
     solver = dict(method=args.method, schedule=args.schedule, omega=args.omega, lr=args.lr,
                   anderson_k=args.anderson_k, reg_start=args.reg_start)
+    if args.backward_mode != "implicit":
+        solver["backward_mode"] = args.backward_mode
     sk = bench_sinkhorn(args, args.workload, args.steps, args.warmup, torch, dot_amd, profiler, solver)
     bidi = None if args.no_bidi else bench_bidi(args, torch, dot_amd, profiler)
     others = {}
-    if not args.headline_only and args.method == "vanilla" and args.schedule is None:
+    if (not args.headline_only and args.method == "vanilla" and args.schedule is None
+            and args.backward_mode == "implicit"):
         for w in ("c1", "c3", "c4", "c5"):
             if w != args.workload:
                 others[w] = bench_sinkhorn(args, w, args.steps, min(args.warmup, 2), torch, dot_amd, profiler)

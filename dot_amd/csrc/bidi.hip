@@ -203,8 +203,8 @@ extern "C" int dot_bidisoftmax_backward(const dot_bidisoftmax_bwd_args* a, dot_s
             hipLaunchKernelGGL(fill_value, dim3(1), dim3(kBlock), 0, stream, a->grad_tau, size_t(B), 0.0f);
         return check_launch("dot_bidisoftmax_backward");
     }
-    if (!a->sim || !a->grad_out || !a->grad_sim || !a->grad_tau)
-        return fail(DOT_ERR_INVALID_ARG, "sim, grad_out, grad_sim and grad_tau must be non-NULL");
+    if (!a->sim || !a->grad_out || !a->grad_sim)
+        return fail(DOT_ERR_INVALID_ARG, "sim, grad_out and grad_sim must be non-NULL");
     const bool buffers = a->out && a->row_sm && a->col_sm;
     if (!buffers && !(a->row_stats && a->col_stats))
         return fail(DOT_ERR_INVALID_ARG,
@@ -231,7 +231,7 @@ extern "C" int dot_bidisoftmax_backward(const dot_bidisoftmax_bwd_args* a, dot_s
     x.dot_c = L.dot_c;
     x.partial = L.partial;
     x.grad_sim = a->grad_sim;
-    x.tau_partial = L.tau_partial;
+    x.tau_partial = a->grad_tau ? L.tau_partial : nullptr;
     bool vec4 = (L2 % 4 == 0) && aligned16(a->sim) && aligned16(a->grad_out) && aligned16(a->grad_sim);
     if (buffers) vec4 = vec4 && aligned16(a->out) && aligned16(a->row_sm) && aligned16(a->col_sm);
     const dim3 strips = batch_grid(unsigned(L.nstrips), B);
@@ -270,9 +270,11 @@ extern "C" int dot_bidisoftmax_backward(const dot_bidisoftmax_bwd_args* a, dot_s
             if (buffers) run(std::false_type{});
             else run(std::true_type{});
         });
-        ProfScope prof("bidi_batch_sum", stream);
-        hipLaunchKernelGGL(batch_sum, dim3(B), dim3(kWave), 0, stream, L.tau_partial, int(tiles.x), -x.inv_T,
-                           a->grad_tau);
+        if (a->grad_tau) {
+            ProfScope prof("bidi_batch_sum", stream);
+            hipLaunchKernelGGL(batch_sum, dim3(B), dim3(kWave), 0, stream, L.tau_partial, int(tiles.x), -x.inv_T,
+                               a->grad_tau);
+        }
         return check_launch("dot_bidisoftmax_backward");
     }
     bool launched = dispatch_row(L2, vec4, [&](auto vc, auto cc) {
@@ -298,7 +300,7 @@ extern "C" int dot_bidisoftmax_backward(const dot_bidisoftmax_bwd_args* a, dot_s
         };
         if (buffers) run(std::false_type{});
         else run(std::true_type{});
-        {
+        if (a->grad_tau) {
             ProfScope prof("bidi_batch_sum", stream);
             hipLaunchKernelGGL(batch_sum, dim3(B), dim3(kWave), 0, stream, L.tau_partial, L.nstrips,
                                -x.inv_T, a->grad_tau);

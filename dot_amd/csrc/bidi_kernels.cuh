@@ -325,7 +325,7 @@ struct BwdArgs {
     float* dot_c;          // [B,L2]
     float* partial;        // [B,nstrips,L2]
     float* grad_sim;
-    float* tau_partial;    // [B,gridDim.x]
+    float* tau_partial;    // [B,gridDim.x], or null when grad_tau is not requested
 };
 
 // For one row: r, c and d = g / (2 out) (kernels.cu:249-274), from the
@@ -498,6 +498,7 @@ __global__ __launch_bounds__(kBlock) void bwd_write(BwdArgs a) {
     src.init(a, b, lds, r0, rv);
     __syncthreads();
     float tacc = 0.0f;
+    const bool want_tau = a.tau_partial != nullptr;  // null: grad_tau not requested
     auto store = [&](int i, const float(&gs)[R::PL]) {
         R::store_stream(a.grad_sim + (size_t(b) * a.L1 + i) * a.L2, lane, a.L2, gs);
     };
@@ -515,7 +516,7 @@ __global__ __launch_bounds__(kBlock) void bwd_write(BwdArgs a) {
                 const bool valid = full || R::valid(lane, e, l2);
                 const float tt = (d[e] * c[e] - dr) * r[e] + (d[e] * r[e] - dc[q]) * c[e];
                 gs[e] = valid ? tt * a.inv_T : 0.0f;
-                tacc = valid ? fmaf(gs[e], t.y[e], tacc) : tacc;
+                if (want_tau) tacc = valid ? fmaf(gs[e], t.y[e], tacc) : tacc;
             }
         }
         store(i, gs);
@@ -525,8 +526,10 @@ __global__ __launch_bounds__(kBlock) void bwd_write(BwdArgs a) {
     for (int e = 0; e < R::PL; ++e) z[e] = 0.0f;
     for (int i = r0 + wave; i < r1; i += kWavesPerBlock)
         if (i >= l1) store(i, z);
-    const float tsum = block_reduce<kWavesPerBlock>(wave_sum(tacc), scratch, OpSum{});
-    if (threadIdx.x == 0) a.tau_partial[size_t(b) * gridDim.x + blockIdx.x] = tsum;
+    if (want_tau) {
+        const float tsum = block_reduce<kWavesPerBlock>(wave_sum(tacc), scratch, OpSum{});
+        if (threadIdx.x == 0) a.tau_partial[size_t(b) * gridDim.x + blockIdx.x] = tsum;
+    }
 }
 
 }  // namespace bidi

@@ -327,7 +327,7 @@ __global__ __launch_bounds__(kBlock) void bwd_write(Args w) {
                     const bool valid = R::valid(lane, e, nv);
                     const float tt = (d[e] * c[e] - dr) * r[e] + (d[e] * r[e] - dc[q]) * c[e];
                     gs[e] = valid ? tt * a.inv_T : 0.0f;
-                    tacc = valid ? fmaf(gs[e], y[e], tacc) : tacc;
+                    if (a.tau_partial) tacc = valid ? fmaf(gs[e], y[e], tacc) : tacc;
                 }
             }
         } else {
@@ -336,8 +336,10 @@ __global__ __launch_bounds__(kBlock) void bwd_write(Args w) {
         }
         R::store_stream(a.grad_sim + off, lane, tl.nc, gs);
     }
-    const float tsum = block_reduce<kWavesPerBlock>(wave_sum(tacc), scratch, OpSum{});
-    if (threadIdx.x == 0) a.tau_partial[size_t(b) * gridDim.x + blockIdx.x] = tsum;
+    if (a.tau_partial) {
+        const float tsum = block_reduce<kWavesPerBlock>(wave_sum(tacc), scratch, OpSum{});
+        if (threadIdx.x == 0) a.tau_partial[size_t(b) * gridDim.x + blockIdx.x] = tsum;
+    }
 }
 
 }  // namespace wide_rows

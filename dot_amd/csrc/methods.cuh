@@ -34,7 +34,7 @@ namespace mth {
 
 constexpr float kSumFloor = 1.0e-12f;     // log(max(sum, 1e-12)), kernels.cu:523-538, :649-664
 constexpr float kColSumFloor = 1.0e-20f;  // smaller column sums take the exact column LSE
-constexpr int kMaxHistory = 16;           // longest Anderson history (anderson_k) supported
+constexpr int kMaxHistory = 64;           // longest Anderson ring held (pairs)
 
 // Solver codes (the reference's method codes); Anderson runs the plain sweep.
 constexpr int kPlain = 0, kMomentum = 1, kAnderson = 2, kAdam = 3;
@@ -617,9 +617,8 @@ static __global__ void aa_solve(AaArgs a) {
     if (threadIdx.x < h) x[threadIdx.x] = 1.0f;
     __shared__ float fr[kMaxHistory];
     __shared__ int piv_sh, fail_sh;
-    const int tr = threadIdx.x / kMaxHistory, tq = threadIdx.x % kMaxHistory;  // (row, column) of this thread
     // forward elimination: per column, the pivot by one thread, then the row
-    // swap and the updates of the rows below by one thread per entry
+    // swap and the updates of the rows below, the entries spread over the threads
     for (int c = 0; c < h; ++c) {
         __syncthreads();
         if (threadIdx.x == 0) {
@@ -647,7 +646,11 @@ static __global__ void aa_solve(AaArgs a) {
         }
         if (threadIdx.x > c && threadIdx.x < h) fr[threadIdx.x] = A[threadIdx.x][c] / A[c][c];
         __syncthreads();
-        if (tr > c && tr < h && tq >= c && tq < h) A[tr][tq] -= fr[tr] * A[c][tq];
+        const int rows = h - c - 1, cols = h - c;  // rows c+1 .. h-1, columns c .. h-1
+        for (int e = threadIdx.x; e < rows * cols; e += blockDim.x) {
+            const int tr = c + 1 + e / cols, tq = c + e % cols;
+            A[tr][tq] -= fr[tr] * A[c][tq];
+        }
         if (threadIdx.x > c && threadIdx.x < h) x[threadIdx.x] -= fr[threadIdx.x] * x[c];
     }
     __syncthreads();

@@ -145,15 +145,22 @@ __global__ void fill_table(float* dst, TableChunk c, int n) {
 // then dot_sinkhorn_forward's workspace.
 size_t vanilla_table_bytes(int T) { return (size_t(T) * sizeof(float) + 255) & ~size_t(255); }
 
+// Pairs the Anderson ring holds: the reference keeps the last anderson_k
+// (torch_cuda.cpp:395-420), and a run of max_iter iterations pushes at most
+// max_iter, so a ring of min(anderson_k, max_iter) never drops one the
+// reference would keep.
+int ring_pairs(int anderson_k, int max_iter) { return std::max(1, std::min(anderson_k, max_iter)); }
+
 int check_method_args(const dot_sinkhorn_method_args* m) {
     if (m->method < DOT_SK_VANILLA || m->method > DOT_SK_ADAM)
         return fail(DOT_ERR_INVALID_ARG, "method must be 0 (vanilla), 1 (momentum), 2 (anderson) or 3 (adam)");
     if (m->schedule < DOT_SK_SCHEDULE_NONE || m->schedule > DOT_SK_SCHEDULE_COSINE)
         return fail(DOT_ERR_INVALID_ARG, "schedule must be 0 (none), 1 (linear), 2 (exponential) or 3 (cosine)");
     if (m->anderson_k < 1) return fail(DOT_ERR_INVALID_ARG, "anderson_k must be >= 1");
-    if (m->method == DOT_SK_ANDERSON && m->anderson_k > kMaxHistory)
-        return fail(DOT_ERR_UNSUPPORTED, "anderson_k above " + std::to_string(kMaxHistory) +
-                                              " is not supported by this build");
+    if (m->method == DOT_SK_ANDERSON && ring_pairs(m->anderson_k, m->base.max_iter) > kMaxHistory)
+        return fail(DOT_ERR_UNSUPPORTED, "Anderson histories longer than " + std::to_string(kMaxHistory) +
+                                              " pairs (anderson_k and max_iter both above it) are not "
+                                              "supported by this build");
     return DOT_OK;
 }
 
@@ -167,7 +174,8 @@ extern "C" size_t dot_sinkhorn_forward_method_workspace_bytes(int B, int M, int 
     if (B < 0 || M < 0 || N < 0 || max_iter < 0 || anderson_k < 0) return 0;
     if (method == DOT_SK_VANILLA)
         return vanilla_table_bytes(max_iter) + dot_sinkhorn_forward_workspace_bytes(B, M, N, max_iter, 0);
-    return method_layout(nullptr, B, M, N, max_iter, method, std::min(anderson_k, kMaxHistory)).bytes;
+    return method_layout(nullptr, B, M, N, max_iter, method, std::min(ring_pairs(anderson_k, max_iter), kMaxHistory))
+        .bytes;
 }
 
 extern "C" int dot_sinkhorn_forward_method(const dot_sinkhorn_method_args* m, dot_stream_t stream_) {
@@ -240,7 +248,7 @@ extern "C" int dot_sinkhorn_forward_method(const dot_sinkhorn_method_args* m, do
         return sinkhorn_forward_scheduled(&f, ks.data(), table, stream);
     }
 
-    const int k = std::min(m->anderson_k, kMaxHistory);
+    const int k = ring_pairs(m->anderson_k, T);  // <= kMaxHistory (checked)
     const MethodLayout L = method_layout(a->workspace, B, M, N, T, method, k);
     if (!a->workspace || a->workspace_bytes < L.bytes)
         return fail(DOT_ERR_WORKSPACE, "workspace smaller than dot_sinkhorn_forward_method_workspace_bytes()");

@@ -696,5 +696,165 @@ __global__ __launch_bounds__(kThreads) void implicit_adjoint(ImpArgs a) {
     if (threadIdx.x == 0) a.tau_partial[gid] = failed ? __builtin_nanf("") : tsum;
 }
 
+// ---------------------------------------------------------------------------
+// Unrolled backward
+// ---------------------------------------------------------------------------
+struct UnrArgs {
+    const float* X;        // scores [B,M,N]
+    int scores_kind;
+    float kscale;          // K = X * kscale
+    const float* gP;       // [B,M,N] or null
+    const float* gC;       // [B] or null
+    const float* P;        // [B,M,N]
+    const float* u_hist;   // [T,B,M]
+    const float* v_hist;   // [T,B,N]
+    float* gamma;          // [B,M,N] Gamma between steps
+    unsigned long long* part;  // [2, G, N] tagged workgroup column sums
+    unsigned long long* res;   // [2, B, N] tagged column sums of the element
+    float* grad;
+    float* tau_partial;    // [G] by logical workgroup: sum(Gamma * log_alpha)
+    int* status;
+    float inv_tau;
+    int B, M, N, W, R, T, spin_limit;
+};
+
+// The unrolled backward (kernels.cu:1622-1680) streaming Gamma and the scores
+// once per reverse step: Gamma = G P; then for t = T-1 .. 0
+//   Gamma_Y = Gamma - safe_exp(K + u_t + v_t) colsum(Gamma)
+//   Gamma   = Gamma_Y - safe_exp(K + u_t + v_{t-1}) rowsum(Gamma_Y)
+// with colsum(Gamma) from the reduce-scatter / all-gather of the previous
+// step; the last step writes grad = Gamma / tau (log-alpha kind: that -
+// grad_cost P; cost kind: grad_cost P - that) instead of Gamma.
+template <int VEC, int CH>
+__global__ __launch_bounds__(kThreads) void unrolled(UnrArgs a) {
+    using R = Row<VEC, CH>;
+    constexpr int PL = R::PL;
+    // LDS: fold (kFoldRows) N | colsum N | v_t N | v_{t-1} N | red N + W | scratch 16
+    extern __shared__ float lds[];
+    const int lane = threadIdx.x % kWave;
+    const int wave = threadIdx.x / kWave;
+    const int G = gridDim.x;
+    const int gid = res::logical_group(a.W);
+    const int b = gid / a.W;
+    const int w = gid % a.W;
+    const int row0 = w * a.R;
+    const int rend = min(row0 + a.R, a.M);
+    const int c0 = slice_begin(w, a.W, a.N), c1 = slice_begin(w + 1, a.W, a.N);
+    float* tree = lds;
+    float* lds_cs = tree + kFoldRows<VEC, CH> * a.N;
+    float* lds_v = lds_cs + a.N;
+    float* lds_vm = lds_v + a.N;
+    float* red = lds_vm + a.N;
+    float* scratch = red + a.N + a.W;
+    const size_t bM = size_t(b) * a.M;
+    const bool cost_kind = a.scores_kind < 0;
+    const float gc = a.gC ? a.gC[b] : 0.0f;
+    const float csign = cost_kind ? 1.0f : -1.0f;  // C = csign * scores
+    bool dead = false;
+    float tacc = 0.0f;
+
+    // The gradient of a row from its final Gamma (kernels.cu:926-963).
+    auto epilogue = [&](size_t off, int ln, float (&gam)[PL], const float (&x)[PL]) {
+        float p[PL];
+        R::load(a.P + off, ln, a.N, p, 0.0f);
+#pragma unroll
+        for (int e = 0; e < PL; ++e) {
+            const float gl = gam[e] * a.inv_tau;
+            const float la = cost_kind ? -x[e] : x[e];
+            if (R::valid(ln, e, a.N)) tacc = fmaf(gam[e], la, tacc);
+            gam[e] = cost_kind ? gc * p[e] - gl : gl - gc * p[e];
+        }
+        R::store_stream(a.grad + off, ln, a.N, gam);
+    };
+    // Column sums of the workgroup's Gamma rows -> every workgroup's lds_cs.
+    auto exchange = [&](float (&acc)[PL], unsigned tag) {
+        const int cur = tag & 1;
+        publish_row<VEC, CH>(acc, tree, a.N, a.part + (size_t(cur) * G + gid) * a.N, tag);
+        unsigned long long* res_row = a.res + (size_t(cur) * a.B + b) * a.N;
+        reduce_slice(a.part + size_t(cur) * G * a.N + size_t(b) * a.W * a.N, a.N, a.W, c0, c1, tag, red,
+                     a.spin_limit, a.status, dead, [&](int j, float tot) { publish(res_row + j, tot, tag); });
+        gather(res_row, a.N, tag, lds_cs, a.spin_limit, a.status, dead);
+        __syncthreads();
+    };
+
+    // Gamma = G * P (kernels.cu:844-854).
+    float acc[PL];
+#pragma unroll
+    for (int e = 0; e < PL; ++e) acc[e] = 0.0f;
+    for (int l = wave; row0 + l < rend; l += kWaves) {
+        const size_t off = (bM + row0 + l) * a.N;
+        const int ln = opaque_lane();
+        float gam[PL], x[PL];
+        R::load(a.P + off, ln, a.N, gam, 0.0f);
+        R::load(a.X + off, ln, a.N, x, 0.0f);
+        if (a.gP) {
+            float g[PL];
+            R::load(a.gP + off, ln, a.N, g, 0.0f);
+#pragma unroll
+            for (int e = 0; e < PL; ++e) gam[e] *= g[e] + (a.gC ? gc * (csign * x[e]) : 0.0f);
+        } else {
+#pragma unroll
+            for (int e = 0; e < PL; ++e) gam[e] *= a.gC ? gc * (csign * x[e]) : 0.0f;
+        }
+#pragma unroll
+        for (int e = 0; e < PL; ++e) acc[e] += gam[e];
+        if (a.T == 0) epilogue(off, ln, gam, x);
+        else R::store(a.gamma + off, ln, a.N, gam);
+    }
+    unsigned tag = 1;
+    if (a.T > 0) exchange(acc, tag);
+
+    for (int t = a.T - 1; t >= 0; --t) {
+        const float* vt = a.v_hist + (size_t(t) * a.B + b) * a.N;
+        const float* vm = t > 0 ? a.v_hist + (size_t(t - 1) * a.B + b) * a.N : nullptr;
+        for (int j = threadIdx.x; j < a.N; j += kThreads) {
+            lds_v[j] = vt[j];
+            lds_vm[j] = vm ? vm[j] : 0.0f;
+        }
+        __syncthreads();
+        const float* ut = a.u_hist + size_t(t) * a.B * a.M + bM;
+#pragma unroll
+        for (int e = 0; e < PL; ++e) acc[e] = 0.0f;
+        for (int l = wave; row0 + l < rend; l += kWaves) {
+            const size_t off = (bM + row0 + l) * a.N;
+            const int ln = opaque_lane();
+            const float ui = ut[row0 + l];
+            float gam[PL], x[PL];
+            R::load(a.gamma + off, ln, a.N, gam, 0.0f);
+            R::load(a.X + off, ln, a.N, x, 0.0f);
+            float tl = 0.0f;
+#pragma unroll
+            for (int k = 0; k < CH; ++k) {
+                float cs[VEC], vv[VEC];
+                R::chunk(lds_cs, ln, k, a.N, cs);
+                R::chunk(lds_v, ln, k, a.N, vv);
+#pragma unroll
+                for (int q = 0; q < VEC; ++q) {
+                    const int e = k * VEC + q;
+                    gam[e] = gam[e] - safe_fast_exp((x[e] * a.kscale + ui) + vv[q]) * cs[q];
+                    if (R::valid(ln, e, a.N)) tl += gam[e];
+                }
+            }
+            const float ti = wave_sum(tl);
+#pragma unroll
+            for (int k = 0; k < CH; ++k) {
+                float vv[VEC];
+                R::chunk(lds_vm, ln, k, a.N, vv);
+#pragma unroll
+                for (int q = 0; q < VEC; ++q) {
+                    const int e = k * VEC + q;
+                    gam[e] = gam[e] - safe_fast_exp((x[e] * a.kscale + ui) + vv[q]) * ti;
+                    acc[e] += gam[e];
+                }
+            }
+            if (t == 0) epilogue(off, ln, gam, x);
+            else R::store(a.gamma + off, ln, a.N, gam);
+        }
+        if (t > 0) exchange(acc, ++tag);
+    }
+    const float tsum = block_reduce<kWaves>(wave_sum(tacc), scratch, OpSum{});
+    if (threadIdx.x == 0) a.tau_partial[gid] = dead ? __builtin_nanf("") : tsum;
+}
+
 }  // namespace pst
 }  // namespace dot_amd

@@ -23,7 +23,6 @@ int strip_rows(int B, int M) { return tuned_strip_rows(B, M); }
 
 size_t lds_bytes(int N) { return (size_t(2) * N + 8) * sizeof(float); }
 
-dim3 column_grid(int N, int B) { return batch_grid(unsigned((N + kBlock - 1) / kBlock), B); }
 
 // Upper bound on the workgroups of a resident launch: at most kMaxGroup per
 // batch element, at least 16 rows each, and at most 1024 in all.
@@ -150,6 +149,8 @@ ImpLayout imp_layout(void* ws, int B, int M, int N) {
 struct UnrLayout {
     float *gamma, *partial, *colsum, *tau_partial;
     float* tpart;  // rows longer than kMaxRowLen: [B, nchunks, M] row partials of each step
+    unsigned long long* pst;  // persistent streaming path: [2, G, N] rows | [2, B, N] sums | status
+    size_t pst_groups;
     int rows, nstrips, nchunks;
     size_t bytes;
 };
@@ -163,8 +164,10 @@ UnrLayout unr_layout(void* ws, int B, int M, int N) {
     L.gamma = c.take<float>(size_t(B) * M * N);
     L.partial = c.take<float>(size_t(B) * L.nstrips * N);
     L.colsum = c.take<float>(size_t(B) * N);
-    L.tau_partial = c.take<float>(size_t(B) * L.nstrips * L.nchunks);
+    L.pst_groups = pst_groups_max(B, M, N);
+    L.tau_partial = c.take<float>(std::max(size_t(B) * L.nstrips * L.nchunks, L.pst_groups));
     L.tpart = c.take<float>(L.nchunks > 1 ? size_t(B) * L.nchunks * M : 0);
+    L.pst = c.take<unsigned long long>(L.pst_groups ? 2 * L.pst_groups * size_t(N) + 2 * size_t(B) * N + 1 : 0);
     L.bytes = c.used();
     return L;
 }
@@ -494,7 +497,7 @@ void launch_wide_forward(const dot_sinkhorn_fwd_args* a, const FwdLayout& L, con
             cb.N = N;
             {
                 ProfScope prof("sk_fwd_combine", stream);
-                hipLaunchKernelGGL(sk::fwd_combine, column_grid(N, B), dim3(kBlock), 0, stream, cb);
+                hipLaunchKernelGGL(sk::fwd_combine, sk::fold_grid(N, B), dim3(kBlock), 0, stream, cb);
             }
         }
         {
@@ -657,7 +660,7 @@ int dot_amd::sinkhorn_forward_scheduled(const dot_sinkhorn_fwd_args* a, const fl
             cb.N = N;
             {
                 ProfScope prof("sk_fwd_combine", stream);
-                hipLaunchKernelGGL(sk::fwd_combine, column_grid(N, B), dim3(kBlock), 0, stream, cb);
+                hipLaunchKernelGGL(sk::fwd_combine, sk::fold_grid(N, B), dim3(kBlock), 0, stream, cb);
             }
         }
         {
@@ -862,7 +865,7 @@ void launch_wide_implicit(const dot_sinkhorn_bwd_args* a, const ImpLayout& L, co
         {
             ProfScope prof("sk_imp_prep_combine", stream);
             hipLaunchKernelGGL(wide::imp_row_totals, dim3(row_blocks), dim3(kBlock), 0, stream, w);
-            hipLaunchKernelGGL(sk::imp_prep_combine, column_grid(N, B), dim3(kBlock), 0, stream, x);
+            hipLaunchKernelGGL(sk::imp_prep_combine, sk::fold_grid(N, B), dim3(kBlock), 0, stream, x);
         }
         for (int it = 0; it < a->iters; ++it) {
             {
@@ -875,7 +878,7 @@ void launch_wide_implicit(const dot_sinkhorn_bwd_args* a, const ImpLayout& L, co
             }
             {
                 ProfScope prof("sk_imp_combine", stream);
-                hipLaunchKernelGGL(sk::imp_mu_combine, column_grid(N, B), dim3(kBlock), 0, stream, x);
+                hipLaunchKernelGGL(sk::imp_mu_combine, sk::fold_grid(N, B), dim3(kBlock), 0, stream, x);
             }
         }
         {
@@ -888,6 +891,57 @@ void launch_wide_implicit(const dot_sinkhorn_bwd_args* a, const ImpLayout& L, co
                                -inv_tau, a->grad_tau, nullptr, a->status);
         }
     });
+}
+
+// The whole reverse pass as one cooperative launch when every batch element
+// can have W workgroups (the persistent streaming tier): Gamma and the scores
+// are streamed once per step and the column sums of Gamma go through the
+// tagged reduce-scatter / all-gather instead of a fold launch per step.
+bool launch_stream_unrolled(const dot_sinkhorn_bwd_args* a, const UnrLayout& L, const StreamCfg& sc,
+                            float inv_tau, float neg_inv_tau2, bool vec4, hipStream_t stream) {
+    const int B = a->B, N = a->N, G = B * sc.W;
+    if (!L.pst || size_t(G) > L.pst_groups) return false;
+    pst::UnrArgs r{};
+    r.X = a->scores;
+    r.scores_kind = a->scores_kind;
+    r.kscale = float(a->scores_kind) * inv_tau;
+    r.gP = a->grad_plan;
+    r.gC = a->grad_cost;
+    r.P = a->plan;
+    r.u_hist = a->u_hist;
+    r.v_hist = a->v_hist;
+    r.gamma = L.gamma;
+    r.part = L.pst;
+    r.res = r.part + 2 * size_t(G) * N;
+    r.status = reinterpret_cast<int*>(r.res + 2 * size_t(B) * N);
+    r.grad = a->grad_scores;
+    r.tau_partial = L.tau_partial;
+    r.inv_tau = inv_tau;
+    r.B = B;
+    r.M = a->M;
+    r.N = N;
+    r.W = sc.W;
+    r.R = sc.R;
+    r.T = a->iters;
+    r.spin_limit = spin_limit();
+    const size_t words = size_t(reinterpret_cast<unsigned long long*>(r.status) - L.pst) + 1;
+    bool ok = false;
+    dispatch_row(N, vec4, [&](auto vc, auto cc) {
+        constexpr int V = decltype(vc)::value;
+        constexpr int C = decltype(cc)::value;
+        if constexpr (V * C <= 32) {  // longer rows would spill: Gamma, the scores and the sums per lane
+            // fold rows | colsum | v_t | v_{t-1} N each | red N + W | scratch
+            const size_t lds = (size_t(pst::kFoldRows<V, C> + 4) * N + sc.W + 16) * sizeof(float);
+            launch_fill_zero(L.pst, 2 * words, stream);
+            ProfScope prof("sk_unr_persistent", stream);
+            ok = launch_cooperative(pst::unrolled<V, C>, r, G, res::kThreads, lds, stream);
+        }
+    });
+    if (!ok) return false;
+    ProfScope prof("sk_batch_sum", stream);
+    hipLaunchKernelGGL(sk::batch_sum, dim3(B), dim3(kWave), 0, stream, L.tau_partial, sc.W, neg_inv_tau2,
+                       a->grad_tau, static_cast<const int*>(r.status), a->status);
+    return true;
 }
 
 // Rows longer than kMaxRowLen: Gamma = G P in chunk tiles, then per recorded
@@ -914,7 +968,7 @@ void launch_wide_unrolled(const dot_sinkhorn_bwd_args* a, const UnrLayout& L, co
         for (int t = T - 1; t >= 0; --t) {
             {
                 ProfScope prof("sk_unr_fold", stream);
-                hipLaunchKernelGGL(sk::column_fold, column_grid(N, B), dim3(kBlock), 0, stream, L.partial,
+                hipLaunchKernelGGL(sk::column_fold, sk::fold_grid(N, B), dim3(kBlock), 0, stream, L.partial,
                                    L.nstrips, B, N, L.colsum);
             }
             w.s.u_t = a->u_hist + size_t(t) * B * M;
@@ -997,7 +1051,7 @@ extern "C" int dot_sinkhorn_backward_implicit(const dot_sinkhorn_bwd_args* a, do
         }
         {
             ProfScope prof("sk_imp_prep_combine", stream);
-            hipLaunchKernelGGL(sk::imp_prep_combine, column_grid(N, B), dim3(kBlock), 0, stream, x);
+            hipLaunchKernelGGL(sk::imp_prep_combine, sk::fold_grid(N, B), dim3(kBlock), 0, stream, x);
         }
         for (int it = 0; it < a->iters; ++it) {
             {
@@ -1006,7 +1060,7 @@ extern "C" int dot_sinkhorn_backward_implicit(const dot_sinkhorn_bwd_args* a, do
             }
             {
                 ProfScope prof("sk_imp_combine", stream);
-                hipLaunchKernelGGL(sk::imp_mu_combine, column_grid(N, B), dim3(kBlock), 0, stream, x);
+                hipLaunchKernelGGL(sk::imp_mu_combine, sk::fold_grid(N, B), dim3(kBlock), 0, stream, x);
             }
         }
         {
@@ -1059,6 +1113,10 @@ extern "C" int dot_sinkhorn_backward_unrolled(const dot_sinkhorn_bwd_args* a, do
     x.rows = L.rows;
     const size_t lds = lds_bytes(N);
     const dim3 strips = batch_grid(unsigned(L.nstrips), B);
+    const StreamCfg sc = stream_config(B, M, N);
+    if (sc.ok && launch_stream_unrolled(a, L, sc, inv_tau, neg_inv_tau2, bwd_vec4(a), stream))
+        return check_launch("dot_sinkhorn_backward_unrolled");
+    (void)hipGetLastError();  // a refused cooperative launch falls back to the per-step sweeps
     if (L.nchunks > 1) {
         launch_wide_unrolled(a, L, x, neg_inv_tau2, stream);
         return check_launch("dot_sinkhorn_backward_unrolled");
@@ -1074,7 +1132,7 @@ extern "C" int dot_sinkhorn_backward_unrolled(const dot_sinkhorn_bwd_args* a, do
         for (int t = T - 1; t >= 0; --t) {
             {
                 ProfScope prof("sk_unr_fold", stream);
-                hipLaunchKernelGGL(sk::column_fold, column_grid(N, B), dim3(kBlock), 0, stream,
+                hipLaunchKernelGGL(sk::column_fold, sk::fold_grid(N, B), dim3(kBlock), 0, stream,
                                    L.partial, L.nstrips, B, N, L.colsum);
             }
             x.u_t = a->u_hist + size_t(t) * B * M;

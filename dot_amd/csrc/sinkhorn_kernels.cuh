@@ -24,6 +24,49 @@ namespace sk {
 constexpr float kColSumFloor = 1.0e-20f;
 constexpr float kSumFloor = 1.0e-12f;  // log(max(sum, 1e-12)), kernels.cu:538
 
+// Folds of per-strip column partials ([B, nstrips, N]) run kFoldCols columns
+// per workgroup with kFoldLanes lanes per column: lane l adds strips l,
+// l + kFoldLanes, ... in order, then a fixed halving tree adds the lanes, so
+// every column is summed in the same order on every run (one thread per column
+// looping over the strips left most of the chip idle).
+constexpr int kFoldCols = 16;
+constexpr int kFoldLanes = kBlock / kFoldCols;  // 16
+
+inline dim3 fold_grid(int N, int B) { return batch_grid(unsigned((N + kFoldCols - 1) / kFoldCols), B); }
+
+// Column j's sums of NS partial planes; valid in the threads with fold_lane() == 0.
+// Every thread of the workgroup must call it (barriers).
+__device__ __forceinline__ int fold_lane() { return int(threadIdx.x) / kFoldCols; }
+__device__ __forceinline__ int fold_col() { return int(blockIdx.x) * kFoldCols + int(threadIdx.x) % kFoldCols; }
+
+template <int NS>
+__device__ __forceinline__ void fold_strips(const float* const (&planes)[NS], int nstrips, int N, int b,
+                                            float (&out)[NS]) {
+    __shared__ float sm[NS][kFoldLanes][kFoldCols];
+    const int jj = int(threadIdx.x) % kFoldCols, sl = fold_lane(), j = fold_col();
+#pragma unroll
+    for (int q = 0; q < NS; ++q) out[q] = 0.0f;
+    if (j < N) {
+        const size_t base = size_t(b) * nstrips * N + j;
+        for (int k = sl; k < nstrips; k += kFoldLanes)
+#pragma unroll
+            for (int q = 0; q < NS; ++q) out[q] += planes[q][base + size_t(k) * N];
+    }
+#pragma unroll
+    for (int q = 0; q < NS; ++q) sm[q][sl][jj] = out[q];
+#pragma unroll
+    for (int half = kFoldLanes / 2; half >= 1; half /= 2) {
+        __syncthreads();
+        if (sl < half) {
+#pragma unroll
+            for (int q = 0; q < NS; ++q) {
+                out[q] += sm[q][sl + half][jj];
+                sm[q][sl][jj] = out[q];
+            }
+        }
+    }
+}
+
 // True when the stopping test fired at or before iteration t-1, so iteration
 // t must not run.  delta[t] holds the batch-global max|u_t - u_{t-1}| as float
 // bits (atomicMax of non-negative floats); iterations that never ran leave 0,
@@ -139,11 +182,12 @@ static __global__ __launch_bounds__(kBlock) void fwd_combine(FwdCombineArgs a) {
     if (stopped_before(a.delta_bits, a.t, a.tol)) return;
     const int b = batch_of_block();
     if (b >= a.B) return;
-    const int j = blockIdx.x * kBlock + threadIdx.x;
-    if (j >= a.N) return;
-    const float* p = a.partial + size_t(b) * a.nstrips * a.N + j;
-    float cs = 0.0f;
-    for (int s = 0; s < a.nstrips; ++s) cs += p[size_t(s) * a.N];
+    const float* planes[1] = {a.partial};
+    float sum[1];
+    fold_strips<1>(planes, a.nstrips, a.N, b, sum);
+    const int j = fold_col();
+    if (fold_lane() != 0 || j >= a.N) return;
+    const float cs = sum[0];
     const size_t bj = size_t(b) * a.N + j;
     const float lgb = a.log_b ? a.log_b[bj] : a.log_b_default;
     float vn;
@@ -357,17 +401,14 @@ __global__ __launch_bounds__(kBlock) void imp_prep(ImpArgs a) {
 static __global__ __launch_bounds__(kBlock) void imp_prep_combine(ImpArgs a) {
     const int b = batch_of_block();
     if (b >= a.B) return;
-    const int j = blockIdx.x * kBlock + threadIdx.x;
-    if (j >= a.N) return;
-    const size_t base = size_t(b) * a.nstrips * a.N + j;
-    float sa = 0.0f, sb = 0.0f;
-    for (int s = 0; s < a.nstrips; ++s) {
-        sa += a.partA[base + size_t(s) * a.N];
-        sb += a.partB[base + size_t(s) * a.N];
-    }
+    const float* planes[2] = {a.partA, a.partB};
+    float sum[2];
+    fold_strips<2>(planes, a.nstrips, a.N, b, sum);
+    const int j = fold_col();
+    if (fold_lane() != 0 || j >= a.N) return;
     const size_t bj = size_t(b) * a.N + j;
-    a.c[bj] = sa;
-    a.cs[bj] = sb;
+    a.c[bj] = sum[0];
+    a.cs[bj] = sum[1];
     a.mu[bj] = 0.0f;
 }
 
@@ -410,13 +451,13 @@ __global__ __launch_bounds__(kBlock) void imp_lambda_sweep(ImpArgs a) {
 static __global__ __launch_bounds__(kBlock) void imp_mu_combine(ImpArgs a) {
     const int b = batch_of_block();
     if (b >= a.B) return;
-    const int j = blockIdx.x * kBlock + threadIdx.x;
-    if (j >= a.N) return;
-    const size_t base = size_t(b) * a.nstrips * a.N + j;
-    float sl = 0.0f;
-    for (int s = 0; s < a.nstrips; ++s) sl += a.partA[base + size_t(s) * a.N];
+    const float* planes[1] = {a.partA};
+    float sum[1];
+    fold_strips<1>(planes, a.nstrips, a.N, b, sum);
+    const int j = fold_col();
+    if (fold_lane() != 0 || j >= a.N) return;
     const size_t bj = size_t(b) * a.N + j;
-    a.mu[bj] = (a.c[bj] - sl) / fmaxf(a.cs[bj], kSumFloor);
+    a.mu[bj] = (a.c[bj] - sum[0]) / fmaxf(a.cs[bj], kSumFloor);
 }
 
 // grad = P (G - lambda_i - mu_k) / tau (kernels.cu:1049-1071) with the
@@ -542,17 +583,18 @@ static __global__ __launch_bounds__(kBlock) void column_fold(const float* partia
                                                      float* out) {
     const int b = batch_of_block();
     if (b >= B) return;
-    const int j = blockIdx.x * kBlock + threadIdx.x;
-    if (j >= N) return;
-    const size_t base = size_t(b) * nstrips * N + j;
-    float s = 0.0f;
-    for (int k = 0; k < nstrips; ++k) s += partial[base + size_t(k) * N];
-    out[size_t(b) * N + j] = s;
+    const float* planes[1] = {partial};
+    float sum[1];
+    fold_strips<1>(planes, nstrips, N, b, sum);
+    const int j = fold_col();
+    if (fold_lane() != 0 || j >= N) return;
+    out[size_t(b) * N + j] = sum[0];
 }
 
 // One reverse step (kernels.cu:1660-1670):
 //   Gamma_Y = Gamma - safe_exp(K + u_t + v_t) * colsum(Gamma)
 //   Gamma   = Gamma_Y - safe_exp(K + u_t + v_{t-1}) * rowsum(Gamma_Y)
+// (safe_exp's clamps on the hardware exponential, safe_fast_exp)
 template <int VEC, int CH>
 __global__ __launch_bounds__(kBlock) void unr_step(UnrArgs a) {
     using R = Row<VEC, CH>;
@@ -583,7 +625,7 @@ __global__ __launch_bounds__(kBlock) void unr_step(UnrArgs a) {
 #pragma unroll
         for (int e = 0; e < R::PL; ++e) {
             const float ku = x[e] * a.kscale + ui;
-            const float q = safe_exp(ku + vec[e]);
+            const float q = safe_fast_exp(ku + vec[e]);
             gam[e] = gam[e] - q * cs[e];
             if (R::valid(lane, e, a.N)) tl += gam[e];
         }
@@ -593,7 +635,7 @@ __global__ __launch_bounds__(kBlock) void unr_step(UnrArgs a) {
 #pragma unroll
         for (int e = 0; e < R::PL; ++e) {
             const float ku = x[e] * a.kscale + ui;
-            const float pe = safe_exp(ku + (a.v_tm1 ? vec[e] : 0.0f));
+            const float pe = safe_fast_exp(ku + (a.v_tm1 ? vec[e] : 0.0f));
             gam[e] = gam[e] - pe * ti;
             acc[e] += gam[e];
         }

@@ -181,7 +181,7 @@ ForwardOut run_forward_method(const Tensor& scores_f, int kind, double tau, int6
     o.plan = at::empty({B, M, N}, opts);
     if (want_cost) o.cost = at::empty({B}, opts);
     o.counts = at::empty({2}, scores_f.options().dtype(at::kInt));
-    const int k = int(std::min<int64_t>(mp.anderson_k, DOT_SK_MAX_ANDERSON));
+    const int k = int(std::min<int64_t>(mp.anderson_k, INT32_MAX));
     const size_t ws_bytes = dot_sinkhorn_forward_method_workspace_bytes(int(B), int(M), int(N), int(n_iters),
                                                                         int(mp.method), k);
     Tensor ws = workspace(ws_bytes, scores_f);
@@ -403,11 +403,11 @@ std::vector<Tensor> bidirectional_softmax_op(Tensor sim, double tau, Tensor leng
 std::vector<Tensor> bidi_backward_common(const Tensor& sim, const Tensor& grad_output, double tau,
                                          const Tensor& lengths, const Tensor& out, const Tensor& r,
                                          const Tensor& c, const Tensor& row_stats,
-                                         const Tensor& col_stats) {
+                                         const Tensor& col_stats, bool want_tau = true) {
     const int64_t B = sim.size(0), L1 = sim.size(1), L2 = sim.size(2);
     auto opts = sim.options();
     Tensor grad = at::empty({B, L1, L2}, opts);
-    Tensor grad_tau = at::empty({B}, opts);
+    Tensor grad_tau = at::empty({want_tau ? B : 0}, opts);
     const size_t ws_bytes = dot_bidisoftmax_backward_workspace_bytes(int(B), int(L1), int(L2));
     Tensor ws = workspace(ws_bytes, sim);
     dot_bidisoftmax_bwd_args a{};
@@ -424,7 +424,7 @@ std::vector<Tensor> bidi_backward_common(const Tensor& sim, const Tensor& grad_o
     a.row_stats = row_stats.defined() ? row_stats.data_ptr<float>() : nullptr;
     a.col_stats = col_stats.defined() ? col_stats.data_ptr<float>() : nullptr;
     a.grad_sim = grad.data_ptr<float>();
-    a.grad_tau = grad_tau.data_ptr<float>();
+    a.grad_tau = want_tau ? grad_tau.data_ptr<float>() : nullptr;
     a.workspace = ws.data_ptr();
     a.workspace_bytes = ws_bytes;
     check_rc(dot_bidisoftmax_backward(&a, current_stream(sim)), "dot_bidisoftmax_backward");
@@ -553,8 +553,9 @@ std::vector<Tensor> bidi_backward_op(Tensor sim, Tensor grad_output, Tensor row_
     check_lengths(lengths, sim.size(0));
     TORCH_CHECK(tau > 0.0, "tau must be > 0");
     c10::OptionalDeviceGuard guard(sim.device());
+    // the autograd path has no tau gradient (the reference drops it): grad_tau is skipped
     return bidi_backward_common(f32c(sim), f32c(grad_output), tau, lengths.contiguous(), Tensor(),
-                                Tensor(), Tensor(), f32c(row_stats), f32c(col_stats));
+                                Tensor(), Tensor(), f32c(row_stats), f32c(col_stats), false);
 }
 
 }  // namespace

@@ -434,7 +434,7 @@ __device__ __forceinline__ void unr_column_part(const sk::UnrArgs& a, size_t off
     R::load(a.colsum + bN + c0, lane, nc, cs, 0.0f);
 #pragma unroll
     for (int e = 0; e < R::PL; ++e) {
-        const float q = safe_exp((x[e] * a.kscale + ui) + vec[e]);
+        const float q = safe_fast_exp((x[e] * a.kscale + ui) + vec[e]);
         gam[e] = gam[e] - q * cs[e];
     }
 }
@@ -498,7 +498,7 @@ __global__ __launch_bounds__(kBlock) void unr_cols(UnrArgs w) {
         if (a.v_tm1) R::load(a.v_tm1 + bN + tl.c0, lane, tl.nc, vec, 0.0f);
 #pragma unroll
         for (int e = 0; e < R::PL; ++e) {
-            const float pe = safe_exp((x[e] * a.kscale + ui) + (a.v_tm1 ? vec[e] : 0.0f));
+            const float pe = safe_fast_exp((x[e] * a.kscale + ui) + (a.v_tm1 ? vec[e] : 0.0f));
             gam[e] = gam[e] - pe * ti;
             acc[e] += gam[e];
         }

@@ -135,9 +135,12 @@ def test_method_forward_rejects_bad_arguments_on_the_host(lib):
         assert f(ctypes.byref(m), None) == code
         assert text in _last_error(lib)
         setattr(m, field, good)
-    m.method, m.anderson_k = 2, 17
+    # the ring holds min(anderson_k, max_iter) pairs, at most DOT_SK_MAX_ANDERSON = 64
+    m.method, m.anderson_k, m.base.max_iter = 2, 65, 65
     assert f(ctypes.byref(m), None) == DOT_ERR_UNSUPPORTED
-    assert "anderson_k" in _last_error(lib)
+    assert "anderson_k and max_iter" in _last_error(lib)
+    assert q(2, 64, 64, 40, 2, 1000) == q(2, 64, 64, 40, 2, 40)  # a ring of max_iter pairs
+    assert "#define DOT_SK_MAX_ANDERSON 64" in open(HEADER).read()
     m.anderson_k = 5
     m.base.flags = 0x2  # history is not kept by the accelerated solvers
     assert f(ctypes.byref(m), None) == DOT_ERR_INVALID_ARG

@@ -216,6 +216,23 @@ def test_anderson_reaches_the_vanilla_fixed_point(B):
     assert rel_err(P, ref.P) < 1e-4
 
 
+@pytest.mark.parametrize("k,T", [(20, 24), (40, 43), (100, 30)])
+def test_anderson_long_histories(k, T):
+    """Histories above 16 pairs (the reference takes any anderson_k >= 1,
+    torch_cuda.cpp:290, :395-446): rings of 20 and 40 pairs that wrap, and
+    anderson_k = 100 over 30 iterations (a ring of 30 pairs never wraps)."""
+    la, _, _ = _case(61 + k, 1, 28, 33)
+    print(f"anderson k={k} T={T}", flush=True)
+    P, used, _ = _gpu(la, 0.5, T, method=AND, anderson_k=k)
+    ref, tol = _fp32_spread(la, 0.5, T, None, None, method=AND, anderson_k=k)
+    assert used == T and rel_err(P, ref.P) < tol, (k, T, tol)
+    # through the public API, with the implicit backward
+    C = torch.from_numpy(-la).to(DEV).requires_grad_(True)
+    res = dot_amd.sinkhorn(C, reg=0.5, n_iters=T, tol=0, method="anderson", anderson_k=k)
+    res.cost.sum().backward()
+    assert rel_err(res.transport_plan, ref.P) < tol and torch.isfinite(C.grad).all()
+
+
 def test_anderson_ring_beyond_its_length():
     # more iterations than the history holds: the ring wraps, oldest pairs drop
     la, _, _ = _case(53, 1, 30, 30)
@@ -283,8 +300,8 @@ def test_argument_errors():
     la = torch.rand(1, 4, 4, device=DEV)
     with pytest.raises(RuntimeError, match="anderson_k"):
         _ops.sinkhorn_dual_forward(la, 0.1, 5, 0.0, None, None, False, 2, 1.5, 0)
-    with pytest.raises(RuntimeError, match="anderson_k"):
-        _ops.sinkhorn_dual_forward(la, 0.1, 5, 0.0, None, None, False, 2, 1.5, 17)
+    with pytest.raises(RuntimeError, match="anderson_k and max_iter"):
+        _ops.sinkhorn_dual_forward(la, 0.1, 65, 0.0, None, None, False, 2, 1.5, 65)
     with pytest.raises(RuntimeError, match="method"):
         _ops.sinkhorn_dual_forward(la, 0.1, 5, 0.0, None, None, False, 9)
     with pytest.raises(RuntimeError, match="schedule"):

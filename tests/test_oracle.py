@@ -436,3 +436,15 @@ def test_methods_reach_the_vanilla_fixed_point(method, kw):
     van = osk.dual_forward(la, 0.1, 400, 0.0)
     r = osk.dual_forward_method(la, 0.1, 400, 0.0, method=method, **kw)
     np.testing.assert_allclose(r.P, van.P, rtol=0, atol=1e-7)
+
+
+def test_anderson_ring_longer_than_the_run_never_wraps():
+    # A ring of anderson_k pairs over T < anderson_k iterations holds every
+    # push (torch_cuda.cpp:395-420), so it equals a ring of T pairs: the build
+    # holds min(anderson_k, max_iter) pairs and accepts any anderson_k.
+    la = -np.random.default_rng(5).random((2, 9, 11)).astype(np.float32)
+    a = osk.dual_forward_method(la, 0.3, 12, method=osk.METHOD_ANDERSON, anderson_k=100)
+    b = osk.dual_forward_method(la, 0.3, 12, method=osk.METHOD_ANDERSON, anderson_k=12)
+    c = osk.dual_forward_method(la, 0.3, 12, method=osk.METHOD_ANDERSON, anderson_k=11)
+    assert np.array_equal(a.P, b.P)
+    assert not np.array_equal(a.P, c.P)  # a ring one pair shorter does wrap

@@ -957,3 +957,42 @@ def test_batch_above_65535():
     res.cost.sum().backward()
     Pc, costc, dC, _, _ = _oracle_cost_grads(C, tau, T, T)
     assert rel_err(res.cost, costc) < FWD_TOL and rel_err(leaf.grad, dC) < GRAD_TOL
+
+
+@pytest.mark.parametrize("B,M,N,tau,T,nonuni", [
+    (2, 300, 2048, 0.3, 12, True),
+    (3, 64, 96, 0.5, 20, False),
+    (1, 7, 3, 0.7, 6, True),
+    (4, 257, 1000, 0.2, 0, False),
+])
+def test_unrolled_persistent_and_sweeps_agree_with_oracle(B, M, N, tau, T, nonuni, monkeypatch):
+    """The unrolled backward as one cooperative launch (Gamma streamed each
+    step, column sums through the tagged exchange) and as per-step sweeps,
+    each against the oracle's restatement of kernels.cu:1622-1680; plus the
+    public API's cost gradient in unrolled mode on both tiers."""
+    rng = np.random.default_rng(3 * B + M + N + T)
+    C = rng.random((B, M, N)).astype(np.float32)
+    G = rng.standard_normal((B, M, N)).astype(np.float32)
+    lga = np.log(_dirichlet(rng, B, M)) if nonuni else None
+    lgb = np.log(_dirichlet(rng, B, N)) if nonuni else None
+    lt = lambda x: None if x is None else _t(x)
+    print(f"[unrolled tiers] B={B} M={M} N={N} T={T}", flush=True)
+    runs = _three_paths(monkeypatch, lambda: _ops.sinkhorn_with_grads_unrolled(
+        _t(-C), _t(G), tau, T, lt(lga), lt(lgb)))
+    Po, go, gto = osk.with_grads_unrolled(-C, G, tau, T, lga, lgb)
+    for name, (P, g, gt) in runs.items():
+        assert rel_err(P, Po) < FWD_TOL, name
+        assert rel_err(g, go) < GRAD_TOL, (name, rel_err(g, go))
+        assert sum_err(gt, gto, go * -C / tau) < GRAD_TOL, name
+    a = None if lga is None else np.exp(lga)
+    b = None if lgb is None else np.exp(lgb)
+    _, _, dC, _, _ = _oracle_cost_grads(C, tau, T, T, a, b, mode="unrolled")
+
+    def api():
+        leaf = _t(C).requires_grad_(True)
+        res = dot_amd.sinkhorn(leaf, reg=tau, n_iters=T, tol=0, a=lt(a), b=lt(b), backward_mode="unrolled")
+        res.cost.sum().backward()
+        return leaf.grad
+
+    for name, g in _three_paths(monkeypatch, api).items():
+        assert rel_err(g, dC) < GRAD_TOL, (name, rel_err(g, dC))
