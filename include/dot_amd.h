@@ -111,14 +111,15 @@ int dot_sinkhorn_forward_noalloc(const dot_sinkhorn_fwd_args* args, dot_stream_t
 #define DOT_SK_SCHEDULE_LINEAR 1
 #define DOT_SK_SCHEDULE_EXPONENTIAL 2
 #define DOT_SK_SCHEDULE_COSINE 3
-#define DOT_SK_MAX_ANDERSON 16  /* longest Anderson history this build supports */
+#define DOT_SK_MAX_ANDERSON 64  /* longest Anderson ring this build holds: anderson_k above it
+                                   is accepted while max_iter <= 64 (the ring never wraps) */
 
 typedef struct {
     dot_sinkhorn_fwd_args base;  /* as for dot_sinkhorn_forward; DOT_SK_KEEP_HISTORY is not
                                     accepted (u_hist, v_hist unused) */
     int method;                  /* DOT_SK_VANILLA .. DOT_SK_ADAM */
     float omega;                 /* momentum over-relaxation */
-    int anderson_k;              /* Anderson history, 1 .. DOT_SK_MAX_ANDERSON */
+    int anderson_k;              /* Anderson history >= 1; min(anderson_k, max_iter) <= DOT_SK_MAX_ANDERSON */
     float mixing_beta;           /* Anderson mixing */
     float lr, beta1, beta2, eps_adam;
     int bias_correction;         /* Adam: nonzero divides the moments by 1 - beta^t */
@@ -259,7 +260,8 @@ typedef struct {
     const float* row_stats;   /* [B,2,L1] as written by the forward */
     const float* col_stats;   /* [B,2,L2] */
     float* grad_sim;          /* [B,L1,L2] out (0 outside the valid region) */
-    float* grad_tau;          /* [B] out: -sum(grad_sim * sim) / tau over the valid region */
+    float* grad_tau;          /* [B] out: -sum(grad_sim * sim) / tau over the valid region,
+                                 or NULL to skip it (the autograd path has no tau gradient) */
     void* workspace;
     size_t workspace_bytes;
 } dot_bidisoftmax_bwd_args;
