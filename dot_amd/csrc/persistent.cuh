@@ -130,7 +130,7 @@ constexpr int kFoldRows = VEC * CH <= 32 ? kWaves : kWaves / 2;
 // holds 8 N floats.
 template <int VEC, int CH>
 __device__ __forceinline__ void publish_row_flat(const float (&acc)[VEC * CH], float* rows, int N,
-                                                 unsigned long long* slot_row, unsigned t) {
+                                                 unsigned long long* slot_row, unsigned t, bool local) {
     using R = Row<VEC, CH>;
     const int wave = threadIdx.x / kWave;
     __syncthreads();  // earlier readers of `rows` are done
@@ -142,7 +142,7 @@ __device__ __forceinline__ void publish_row_flat(const float (&acc)[VEC * CH], f
         float s = rows[j];
 #pragma unroll
         for (int v = 1; v < kWaves; ++v) s += rows[v * N + j];
-        publish(slot_row + j, s, t);
+        publish(slot_row + j, s, t, local);
     }
 }
 
@@ -152,7 +152,7 @@ __device__ __forceinline__ void publish_row_flat(const float (&acc)[VEC * CH], f
 // them.  Contains barriers; `rows` holds 4 N floats.
 template <int VEC, int CH>
 __device__ __forceinline__ void publish_row_pairs(float (&acc)[VEC * CH], float* rows, int N,
-                                                  unsigned long long* slot_row, unsigned t) {
+                                                  unsigned long long* slot_row, unsigned t, bool local) {
     using R = Row<VEC, CH>;
     const int wave = threadIdx.x / kWave;
     constexpr int H = kWaves / 2;
@@ -174,19 +174,20 @@ __device__ __forceinline__ void publish_row_pairs(float (&acc)[VEC * CH], float*
         float s = rows[j];
 #pragma unroll
         for (int v = 1; v < H; ++v) s += rows[v * N + j];
-        publish(slot_row + j, s, t);
+        publish(slot_row + j, s, t, local);
     }
 }
 
 // Step 1: fold the waves' per-lane column sums in a fixed order and publish
-// the workgroup's row with tag t at slot_row (every thread publishes).
+// the workgroup's row with tag t at slot_row (every thread publishes; `local`
+// as for res::publish).
 template <int VEC, int CH>
 __device__ __forceinline__ void publish_row(float (&acc)[VEC * CH], float* tree, int N,
-                                            unsigned long long* slot_row, unsigned t) {
+                                            unsigned long long* slot_row, unsigned t, bool local) {
     if constexpr (kFoldRows<VEC, CH> == kWaves)
-        publish_row_flat<VEC, CH>(acc, tree, N, slot_row, t);
+        publish_row_flat<VEC, CH>(acc, tree, N, slot_row, t, local);
     else
-        publish_row_pairs<VEC, CH>(acc, tree, N, slot_row, t);
+        publish_row_pairs<VEC, CH>(acc, tree, N, slot_row, t, local);
 }
 
 // Step 2: the owner's sums over the element's W rows for its slice [c0, c1),
@@ -305,6 +306,7 @@ __global__ __launch_bounds__(kThreads) void forward(FwdArgs a) {
     // scheduled runs: this iteration's scale, and the next one's already in flight
     float ks_it = a.kscale;
     float ks_next = (SCHED && a.max_iter > 0) ? a.kscale_t[0] : a.kscale;
+    res::announce_xcc(a.part, a.N, b, a.W, w);
 
     for (int l = threadIdx.x; l < a.R; l += kThreads) {
         const int i = row0 + l;
@@ -319,6 +321,7 @@ __global__ __launch_bounds__(kThreads) void forward(FwdArgs a) {
     }
     __syncthreads();
     bool dead = false;
+    const bool local = res::element_on_one_xcd(a.part, a.N, b, a.W, w, a.spin_limit, a.status, dead, scratch);
     int used = a.max_iter;
     int conv = 0;
 
@@ -385,7 +388,7 @@ __global__ __launch_bounds__(kThreads) void forward(FwdArgs a) {
             dmax = fmaxf(dmax, fabsf(u - lds_u[prev * a.R + l]));
             if (lane == 0) {
                 lds_u[cur * a.R + l] = u;
-                publish(a.uslot + size_t(cur) * a.B * a.M + bM + i, u, unsigned(t));
+                publish(a.uslot + size_t(cur) * a.B * a.M + bM + i, u, unsigned(t), local);
                 if (a.u_hist) a.u_hist[(size_t(t - 1) * a.B + b) * a.M + i] = u;
             }
         };
@@ -399,7 +402,7 @@ __global__ __launch_bounds__(kThreads) void forward(FwdArgs a) {
             }
         }
         if (lane == 0) scratch[1 + wave] = dmax;
-        publish_row<VEC, CH>(acc, tree, a.N, a.part + (size_t(cur) * G + gid) * a.N, unsigned(t));
+        publish_row<VEC, CH>(acc, tree, a.N, a.part + (size_t(cur) * G + gid) * a.N, unsigned(t), local);
         if (check && threadIdx.x == 0) {
             float d = scratch[1];
 #pragma unroll
@@ -431,7 +434,7 @@ __global__ __launch_bounds__(kThreads) void forward(FwdArgs a) {
                              }
                              vn = lds_lb[j] - (mx + logf(fmaxf(sm, sk::kSumFloor)));
                          }
-                         publish(res_row + j, vn, unsigned(t));
+                         publish(res_row + j, vn, unsigned(t), local);
                          if (a.v_hist) a.v_hist[(size_t(t - 1) * a.B + b) * a.N + j] = vn;
                      });
         __syncthreads();  // the owners have read lds_v (v_{t-1}); it now receives v_t
@@ -593,6 +596,7 @@ __global__ __launch_bounds__(kThreads) void implicit_adjoint(ImpArgs a) {
     const float gc = a.gC ? a.gC[b] : 0.0f;
     const float csign = cost_kind ? 1.0f : -1.0f;  // C = csign * scores
     bool dead = false;
+    res::announce_xcc(a.part, a.N, b, a.W, w);
 
     // Prologue: row sums of P G and P; column sums to the slice owners.
     float cg[PL], cp[PL];
@@ -620,8 +624,9 @@ __global__ __launch_bounds__(kThreads) void implicit_adjoint(ImpArgs a) {
             lds_lam[l] = 0.0f;
         }
     }
-    publish_row<VEC, CH>(cg, tree, a.N, a.pro + size_t(gid) * a.N, 1u);
-    publish_row<VEC, CH>(cp, tree, a.N, a.pro + (size_t(G) + gid) * a.N, 1u);
+    const bool local = res::element_on_one_xcd(a.part, a.N, b, a.W, w, a.spin_limit, a.status, dead, scratch);
+    publish_row<VEC, CH>(cg, tree, a.N, a.pro + size_t(gid) * a.N, 1u, local);
+    publish_row<VEC, CH>(cp, tree, a.N, a.pro + (size_t(G) + gid) * a.N, 1u, local);
     reduce_slice(a.pro + size_t(b) * a.W * a.N, a.N, a.W, c0, c1, 1u, red, a.spin_limit, a.status, dead,
                  [&](int j, float tot) { lds_c[j - c0] = tot; });
     __syncthreads();
@@ -655,11 +660,11 @@ __global__ __launch_bounds__(kThreads) void implicit_adjoint(ImpArgs a) {
             for (int e = 0; e < PL; ++e) acc[e] = fmaf(p[e], lam, acc[e]);
             if (lane == 0) lds_lam[l] = lam;
         }
-        publish_row<VEC, CH>(acc, tree, a.N, a.part + (size_t(cur) * G + gid) * a.N, unsigned(t));
+        publish_row<VEC, CH>(acc, tree, a.N, a.part + (size_t(cur) * G + gid) * a.N, unsigned(t), local);
         unsigned long long* res_row = a.res + (size_t(cur) * a.B + b) * a.N;
         reduce_slice(a.part + size_t(cur) * G * a.N + size_t(b) * a.W * a.N, a.N, a.W, c0, c1, unsigned(t),
                      red, a.spin_limit, a.status, dead, [&](int j, float tot) {
-                         publish(res_row + j, (lds_c[j - c0] - tot) / lds_cs[j - c0], unsigned(t));
+                         publish(res_row + j, (lds_c[j - c0] - tot) / lds_cs[j - c0], unsigned(t), local);
                      });
         gather(res_row, a.N, unsigned(t), lds_mu, a.spin_limit, a.status, dead);
         __syncthreads();
@@ -731,7 +736,6 @@ __global__ __launch_bounds__(kThreads) void unrolled(UnrArgs a) {
     constexpr int PL = R::PL;
     // LDS: fold (kFoldRows) N | colsum N | v_t N | v_{t-1} N | red N + W | scratch 16
     extern __shared__ float lds[];
-    const int lane = threadIdx.x % kWave;
     const int wave = threadIdx.x / kWave;
     const int G = gridDim.x;
     const int gid = res::logical_group(a.W);
@@ -752,6 +756,8 @@ __global__ __launch_bounds__(kThreads) void unrolled(UnrArgs a) {
     const float csign = cost_kind ? 1.0f : -1.0f;  // C = csign * scores
     bool dead = false;
     float tacc = 0.0f;
+    res::announce_xcc(a.part, a.N, b, a.W, w);
+    bool local = false;  // set by the XCD check before the first exchange
 
     // The gradient of a row from its final Gamma (kernels.cu:926-963).
     auto epilogue = [&](size_t off, int ln, float (&gam)[PL], const float (&x)[PL]) {
@@ -769,10 +775,10 @@ __global__ __launch_bounds__(kThreads) void unrolled(UnrArgs a) {
     // Column sums of the workgroup's Gamma rows -> every workgroup's lds_cs.
     auto exchange = [&](float (&acc)[PL], unsigned tag) {
         const int cur = tag & 1;
-        publish_row<VEC, CH>(acc, tree, a.N, a.part + (size_t(cur) * G + gid) * a.N, tag);
+        publish_row<VEC, CH>(acc, tree, a.N, a.part + (size_t(cur) * G + gid) * a.N, tag, local);
         unsigned long long* res_row = a.res + (size_t(cur) * a.B + b) * a.N;
         reduce_slice(a.part + size_t(cur) * G * a.N + size_t(b) * a.W * a.N, a.N, a.W, c0, c1, tag, red,
-                     a.spin_limit, a.status, dead, [&](int j, float tot) { publish(res_row + j, tot, tag); });
+                     a.spin_limit, a.status, dead, [&](int j, float tot) { publish(res_row + j, tot, tag, local); });
         gather(res_row, a.N, tag, lds_cs, a.spin_limit, a.status, dead);
         __syncthreads();
     };
@@ -801,6 +807,7 @@ __global__ __launch_bounds__(kThreads) void unrolled(UnrArgs a) {
         if (a.T == 0) epilogue(off, ln, gam, x);
         else R::store(a.gamma + off, ln, a.N, gam);
     }
+    local = res::element_on_one_xcd(a.part, a.N, b, a.W, w, a.spin_limit, a.status, dead, scratch);
     unsigned tag = 1;
     if (a.T > 0) exchange(acc, tag);
 

@@ -45,6 +45,28 @@ __device__ __forceinline__ void publish(unsigned long long* p, float v, unsigned
     __hip_atomic_store(p, tag_pack(v, t), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Exchange words read only by workgroups on the writer's XCD.  An agent-scope
+// store writes through to memory; a workgroup-scope store stops in the XCD's
+// L2 (the vector L1 is write-through), where the readers' agent-scope loads
+// find it: a tagged ping-pong between two workgroups of one XCD takes 0.53 us
+// per round trip this way against 1.09 us with agent-scope stores.  A word
+// stored this way is not visible to another XCD before its line leaves the
+// L2, so `local` must be true only when every reader runs on the writer's XCD
+// (element_on_one_xcd).
+__device__ __forceinline__ void publish(unsigned long long* p, float v, unsigned t, bool local) {
+    if (local)
+        __hip_atomic_store(p, tag_pack(v, t), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    else
+        __hip_atomic_store(p, tag_pack(v, t), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// The XCD (XCC) this workgroup runs on.
+__device__ __forceinline__ int xcc_id() {
+    unsigned x;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(x));
+    return int(x & 0xfu);
+}
+
 // Waits for slot `p` to carry tag `t` and returns its value.  Gives up after
 // `spin_limit` polls, or as soon as any workgroup has reported a timeout in
 // `status` (checked every 256 polls); `dead` then short-circuits every later
@@ -77,6 +99,43 @@ __device__ __forceinline__ float collect(unsigned long long* p, unsigned t, int 
         }
         __builtin_amdgcn_s_sleep(1);
     }
+}
+
+// Tag of the XCD-id words; exchange tags are iteration numbers (>= 1) or 0 in
+// a cleared slot, so this one never matches them.
+constexpr unsigned kXccTag = 0xfffffffeu;
+
+// XCD check of a batch element, in two steps so that the round trip hides
+// under other work.  announce_xcc: each workgroup publishes its XCC id (agent
+// scope) into word 0 of its row `rows + (b * W + w) * stride`.  The row must
+// be one that no workgroup of the element writes again before every
+// workgroup of the element has passed element_on_one_xcd (the sweep slot of
+// iteration parity 0 qualifies: iteration 2 is published only after every
+// workgroup has published iteration 1, which each does after the check).
+__device__ __forceinline__ void announce_xcc(unsigned long long* rows, size_t stride, int b, int W, int w) {
+    if (threadIdx.x == 0) publish(rows + (size_t(b) * W + w) * stride, __int_as_float(xcc_id()), kXccTag);
+}
+
+// True when the W workgroups of batch element b (this one is w) all run on
+// one XCD, so that their exchanges may use publish(..., local = true): wave 0
+// reads the element's W announced ids.  A timeout reads as "not one XCD" (and
+// sets `dead` as any poll does).  Contains barriers; every thread must call it.
+__device__ __forceinline__ bool element_on_one_xcd(unsigned long long* rows, size_t stride, int b, int W, int w,
+                                                   int spin_limit, int* status, bool& dead, float* scratch) {
+    const int me = xcc_id();
+    if (threadIdx.x < kWave) {
+        const int g = threadIdx.x;
+        int same = 1;
+        if (g < W && g != w)
+            same = __float_as_int(collect(rows + (size_t(b) * W + g) * stride, kXccTag, spin_limit, status,
+                                          dead)) == me;
+        const int all = __all(same);
+        if (g == 0) scratch[0] = all ? 1.0f : 0.0f;
+    }
+    __syncthreads();
+    const bool local = scratch[0] != 0.0f;
+    __syncthreads();
+    return local;
 }
 
 // Collects one published row (this lane's PL columns) with every load of a poll
@@ -249,10 +308,11 @@ __device__ __forceinline__ void put(float (&v)[N], int q, float x) {
 // workgroup order (every workgroup of the element gets the same bits).
 // Every lane polls its own values (a separate "ready" word would add a
 // second memory round trip).  f(j, total) consumes each total; totals are
-// NaN after a timeout.
+// NaN after a timeout.  `local`: every workgroup of the element runs on this
+// XCD (element_on_one_xcd).
 template <class F>
 __device__ __forceinline__ void exchange_columns(const float* part, unsigned long long* slot, int N,
-                                                 int b, int W, int w, unsigned t, int spin_limit,
+                                                 int b, int W, int w, unsigned t, bool local, int spin_limit,
                                                  int* status, bool& dead, F&& f) {
     float own[kColsPerThread];
 #pragma unroll
@@ -264,43 +324,57 @@ __device__ __forceinline__ void exchange_columns(const float* part, unsigned lon
 #pragma unroll
             for (int v = 0; v < kWaves; ++v) s += part[v * N + j];
             own[q] = s;
-            publish(slot + (size_t(b) * W + w) * N + j, s, t);
+            if (W > 1) publish(slot + (size_t(b) * W + w) * N + j, s, t, local);
         }
     }
     unsigned long long* base = slot + size_t(b) * W * N;
     forced_timeout(spin_limit, status, dead);
-#pragma unroll 1
+    // One poll round issues the loads of every (column, workgroup) pair first
+    // and only then looks at the tags, so the round costs one memory latency
+    // (a load whose tag is tested before the next load is issued makes the
+    // compiler wait for each in turn).  Pairs outside the element or the row,
+    // and this workgroup's own slot, are not loaded and count as ready.
+    float got[kColsPerThread][kMaxGroup] = {};
+    const int nq = N > kThreads ? 2 : 1;  // column rounds with any column < N (uniform)
+    for (int spins = 0; W > 1 && !dead; ++spins) {
+        unsigned long long x[kColsPerThread][kMaxGroup];
+#pragma unroll
+        for (int q = 0; q < kColsPerThread; ++q) {
+            const int j = threadIdx.x + q * kThreads;
+#pragma unroll
+            for (int g = 0; g < kMaxGroup; ++g) {
+                x[q][g] = tag_pack(0.0f, t);
+                if (q < nq && g < W && g != w && j < N)
+                    x[q][g] = __hip_atomic_load(base + size_t(g) * N + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+        bool ready = true;
+#pragma unroll
+        for (int q = 0; q < kColsPerThread; ++q)
+#pragma unroll
+            for (int g = 0; g < kMaxGroup; ++g) {
+                ready = ready && static_cast<unsigned>(x[q][g] >> 32) == t;
+                got[q][g] = __uint_as_float(static_cast<unsigned>(x[q][g]));
+            }
+        if (ready) break;
+        if (((spins & 255) == 255 &&
+             __hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) ||
+            spins >= spin_limit) {
+            if (spins >= spin_limit) atomicOr(status, 1);
+            dead = true;
+            break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+#pragma unroll
     for (int q = 0; q < kColsPerThread; ++q) {
         const int j = threadIdx.x + q * kThreads;
         if (j >= N) continue;
-        float got[kMaxGroup];
-        for (int spins = 0; !dead; ++spins) {
-            bool ready = true;
-#pragma unroll
-            for (int g = 0; g < kMaxGroup; ++g) {
-                got[g] = 0.0f;
-                if (g < W && g != w) {
-                    const unsigned long long x = __hip_atomic_load(base + size_t(g) * N + j, __ATOMIC_RELAXED,
-                                                                   __HIP_MEMORY_SCOPE_AGENT);
-                    ready = ready && static_cast<unsigned>(x >> 32) == t;
-                    got[g] = __uint_as_float(static_cast<unsigned>(x));
-                }
-            }
-            if (ready) break;
-            if (((spins & 255) == 255 &&
-                 __hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) ||
-                spins >= spin_limit) {
-                if (spins >= spin_limit) atomicOr(status, 1);
-                dead = true;
-                break;
-            }
-            __builtin_amdgcn_s_sleep(1);
-        }
-        const float mine = pick(own, q);
+        const float mine = own[q];
         float tot = 0.0f;
 #pragma unroll
         for (int g = 0; g < kMaxGroup; ++g)
-            if (g < W) tot += (g == w) ? mine : got[g];
+            if (g < W) tot += (g == w) ? mine : got[q][g];
         f(j, dead ? __builtin_nanf("") : tot);
     }
 }
@@ -369,6 +443,7 @@ __global__ __launch_bounds__(kThreads) void implicit_adjoint(ImpResArgs a) {
     const float gc = a.gC ? a.gC[b] : 0.0f;
     const float csign = cost_kind ? 1.0f : -1.0f;  // C = csign * scores
     bool dead = false;
+    announce_xcc(a.xchg, a.N, b, a.W, w);
 
     // Prologue, streamed (one row at a time, nothing kept): row sums r and rs
     // of this lane's row slot and the workgroup's column partials of P G and P.
@@ -413,14 +488,15 @@ __global__ __launch_bounds__(kThreads) void implicit_adjoint(ImpResArgs a) {
     }
     const float inv_rs = 1.0f / fmaxf(rs_l, sk::kSumFloor);
     float c_own[kColsPerThread], cs_own[kColsPerThread];
+    const bool local = element_on_one_xcd(a.xchg, a.N, b, a.W, w, a.spin_limit, a.status, dead, scratch);
     R::store(part + wave * a.N, lane, a.N, cg);
     __syncthreads();
-    exchange_columns(part, a.pro, a.N, b, a.W, w, 1u, a.spin_limit, a.status, dead,
+    exchange_columns(part, a.pro, a.N, b, a.W, w, 1u, local, a.spin_limit, a.status, dead,
                      [&](int j, float tot) { put(c_own, (j - threadIdx.x) / kThreads, tot); });
     __syncthreads();
     R::store(part + wave * a.N, lane, a.N, cp);
     __syncthreads();
-    exchange_columns(part, a.pro + size_t(G) * a.N, a.N, b, a.W, w, 1u, a.spin_limit, a.status, dead,
+    exchange_columns(part, a.pro + size_t(G) * a.N, a.N, b, a.W, w, 1u, local, a.spin_limit, a.status, dead,
                      [&](int j, float tot) { put(cs_own, (j - threadIdx.x) / kThreads, fmaxf(tot, sk::kSumFloor)); });
 
     // Sweeps.
@@ -446,10 +522,12 @@ __global__ __launch_bounds__(kThreads) void implicit_adjoint(ImpResArgs a) {
 #pragma unroll
             for (int e = 0; e < PL; ++e) acc[e] = fmaf(p[k][e], lk, acc[e]);
         }
-        __syncthreads();  // previous readers of part and lds_mu are done
+        // No barrier needed here: the last readers of part and lds_mu (the
+        // previous exchange and mu reload) are behind the barrier that ends
+        // the previous sweep.
         R::store(part + wave * a.N, lane, a.N, acc);
         __syncthreads();
-        exchange_columns(part, a.xchg + size_t(t & 1) * G * a.N, a.N, b, a.W, w, unsigned(t),
+        exchange_columns(part, a.xchg + size_t(t & 1) * G * a.N, a.N, b, a.W, w, unsigned(t), local,
                          a.spin_limit, a.status, dead, [&](int j, float tot) {
                              const int q = (j - threadIdx.x) / kThreads;
                              lds_mu[j] = (pick(c_own, q) - tot) / pick(cs_own, q);
@@ -590,6 +668,7 @@ __global__ __launch_bounds__(kThreads) void forward(FwdResArgs a) {
     const bool check = a.tol > 0.0f;
     // Padding (columns >= N, rows >= rend) holds the value whose K is -inf.
     const float pad = a.kscale > 0.0f ? -INFINITY : INFINITY;
+    announce_xcc(a.xchg, a.N, b, a.W, w);
 
     float x[RPW][PL];
 #pragma unroll
@@ -629,6 +708,7 @@ __global__ __launch_bounds__(kThreads) void forward(FwdResArgs a) {
     float ks_it = a.kscale;
     float ks_next = (SCHED && a.max_iter > 0) ? a.kscale_t[0] : a.kscale;
     bool dead = false;
+    const bool local = element_on_one_xcd(a.xchg, a.N, b, a.W, w, a.spin_limit, a.status, dead, scratch);
     int used = a.max_iter;
     int conv = 0;
 
@@ -717,7 +797,8 @@ __global__ __launch_bounds__(kThreads) void forward(FwdResArgs a) {
                 }
             }
         }
-        __syncthreads();  // previous readers of part are done
+        // The last readers of part (the previous exchange or exact fallback)
+        // are behind the barrier that ends the previous iteration's exchange.
         R::store(part + wave * a.N, lane, a.N, acc);
         if (lane == 0) scratch[1 + wave] = dmax;
         __syncthreads();
@@ -728,7 +809,7 @@ __global__ __launch_bounds__(kThreads) void forward(FwdResArgs a) {
             publish(a.dxchg + size_t(t % kDeltaSlots) * G + gid, d, unsigned(t));
         }
         int low = 0;
-        exchange_columns(part, a.xchg + size_t(cur) * G * a.N, a.N, b, a.W, w, unsigned(t), a.spin_limit,
+        exchange_columns(part, a.xchg + size_t(cur) * G * a.N, a.N, b, a.W, w, unsigned(t), local, a.spin_limit,
                          a.status, dead, [&](int j, float cs) {
                              if (cs >= sk::kColSumFloor && cs <= FLT_MAX) {
                                  lds_v[cur * a.N + j] = lds_lb[j] + lds_v[prev * a.N + j] - logf(cs);
@@ -777,7 +858,7 @@ __global__ __launch_bounds__(kThreads) void forward(FwdResArgs a) {
 #pragma unroll
                     for (int q = 0; q < VEC; ++q) {
                         const int col = R::col(lane, k) + q;
-                        if (col < a.N) publish(mine + col, cm[k * VEC + q], unsigned(t));
+                        if (col < a.N) publish(mine + col, cm[k * VEC + q], unsigned(t), local);
                     }
             }
             __syncthreads();
@@ -816,7 +897,7 @@ __global__ __launch_bounds__(kThreads) void forward(FwdResArgs a) {
 #pragma unroll
                     for (int q = 0; q < VEC; ++q) {
                         const int col = R::col(lane, k) + q;
-                        if (col < a.N) publish(mine + col, sm[k * VEC + q], unsigned(t));
+                        if (col < a.N) publish(mine + col, sm[k * VEC + q], unsigned(t), local);
                     }
             }
             __syncthreads();
