@@ -28,6 +28,7 @@
 #include <cstdint>
 
 #include "row.cuh"
+#include "tile.cuh"
 
 namespace dot_amd {
 namespace mth {
@@ -335,6 +336,203 @@ __global__ __launch_bounds__(kBlock) void sweep(SweepArgs a) {
         block_flag_max<3>(a.slots, kGapU, gap0, kGapU + 1, gap1, kMoveU, move, red);
     } else if (a.track) {
         block_flag_max<1>(a.slots, kGapU + 1, gap1, 0, 0.0f, 0, 0.0f, red);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// The sweep for rows longer than kMaxRowLen, in three launches over the
+// strips x chunks tiling of tile.cuh (workgroup (s, c) owns rows
+// [s*rows, (s+1)*rows) and columns [c*kChunk, (c+1)*kChunk)):
+//   wide_rows    per row and chunk, (max, sum) of exp over K_ij + v_j;
+//   wide_finish  per row, the chunk partials folded in chunk order into u*,
+//                the method's candidate u' (Adam's moments advanced once),
+//                the flag maxima, and the row's shift m_i and weights
+//                w_i = a_i / s_i, w2_i = w_i exp(u'_i - u*_i);
+//   wide_cols    per tile, the column sums sum_i exp(K_ij + v_j - m_i) w_i
+//                (and w2_i) of the chunk's columns, one partial row per strip
+//                in the [B, nstrips, N] layout vfinish reads.
+// The values are those of the fused sweep up to the rounding of the chunked
+// log-sum-exp.
+// ---------------------------------------------------------------------------
+struct WideArgs {
+    SweepArgs s;       // nstrips counts strips of the tiling; rows is its strip height
+    int nchunks;
+    float2* rpart;     // [B, nchunks, M] chunk (max, sum)
+    float* row_m;      // [B, M] the row's max of K + v
+    float* row_w;      // [B, M] a_i / s_i
+    float* row_w2;     // [B, M] (a_i / s_i) exp(u'_i - u*_i)
+};
+
+// The previous iteration's decision and the v this iteration sweeps with
+// (v* or v', chunk columns); false when the stop test fired before it.
+template <class R, int MODE>
+__device__ __forceinline__ bool wide_prologue(const SweepArgs& a, int b, int c0, int nc, Prev& pv,
+                                              float (&v)[R::PL]) {
+    const int lane = threadIdx.x % kWave;
+    const Words words = load_words(a.prev);
+    float v_alt[R::PL];
+    if (a.v_prev[0]) {
+        R::load(a.v_prev[0] + size_t(b) * a.N + c0, lane, nc, v, 0.0f);
+        if constexpr (MODE != kPlain) R::load(a.v_prev[1] + size_t(b) * a.N + c0, lane, nc, v_alt, 0.0f);
+    } else {
+#pragma unroll
+        for (int e = 0; e < R::PL; ++e) v[e] = v_alt[e] = 0.0f;
+    }
+    pv = previous_from(words, a.prev != nullptr, a.method, a.tol);
+    if (pv.stop) return false;
+    if constexpr (MODE != kPlain) {
+        if (pv.d.keep_v)
+#pragma unroll
+            for (int e = 0; e < R::PL; ++e) v[e] = v_alt[e];
+    }
+    return true;
+}
+
+template <int VEC, int CH, int MODE>
+__global__ __launch_bounds__(kBlock) void wide_rows(WideArgs w) {
+#pragma clang fp contract(off)
+    using R = Row<VEC, CH>;
+    const SweepArgs& a = w.s;
+    const int b = batch_of_block();
+    if (b >= a.B) return;
+    const wide::Tile tl = wide::tile_of_block(w.nchunks, a.N);
+    const int lane = threadIdx.x % kWave;
+    const int wave = threadIdx.x / kWave;
+    Prev pv;
+    float v[R::PL];
+    if (!wide_prologue<R, MODE>(a, b, tl.c0, tl.nc, pv, v)) return;
+    const int r0 = tl.s * a.rows;
+    const int r1 = min(r0 + a.rows, a.M);
+    const size_t bM = size_t(b) * a.M;
+    float2* part = w.rpart + (size_t(b) * w.nchunks + tl.c) * a.M;
+    for (int i = r0 + wave; i < r1; i += kWavesPerBlock) {
+        float x[R::PL];
+        R::load(a.X + (bM + i) * a.N + tl.c0, lane, tl.nc, x, 0.0f);
+        float mloc = -FLT_MAX;
+#pragma unroll
+        for (int e = 0; e < R::PL; ++e) {
+            x[e] = R::valid(lane, e, tl.nc) ? fmaf(x[e], a.kscale, v[e]) : -INFINITY;
+            mloc = fmaxf(mloc, x[e]);
+        }
+        const float m = wave_max(mloc);
+        float sloc = 0.0f;
+#pragma unroll
+        for (int e = 0; e < R::PL; ++e) sloc += fast_exp(x[e] - m);
+        const float s = wave_sum(sloc);
+        if (lane == 0) part[i] = make_float2(m, s);
+    }
+}
+
+constexpr int kFinishRowsPerWave = 8;
+
+template <int MODE>
+__global__ __launch_bounds__(kBlock) void wide_finish(WideArgs w) {
+#pragma clang fp contract(off)
+    const SweepArgs& a = w.s;
+    __shared__ float red[3 * kWavesPerBlock];
+    const int lane = threadIdx.x % kWave;
+    const int wave = threadIdx.x / kWave;
+    const int b = batch_of_block();
+    if (b >= a.B) return;
+    const Prev pv = previous(a.prev, a.method, a.tol);
+    const bool first_block = blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0 && threadIdx.x == 0;
+    if (pv.stop) {
+        if (first_block) *a.converged = 1;
+        return;
+    }
+    if (first_block) *a.used = a.t + 1;
+    const float* uc = MODE != kPlain && pv.d.keep_u ? a.u_prev[1] : a.u_prev[0];
+    const size_t bM = size_t(b) * a.M;
+    const float2* part = w.rpart + size_t(b) * w.nchunks * a.M;
+    const int i0 = (blockIdx.x * kWavesPerBlock + wave) * kFinishRowsPerWave;
+    const int i1 = min(i0 + kFinishRowsPerWave, a.M);
+    float gap0 = 0.0f, gap1 = 0.0f, move = 0.0f;
+    for (int i = i0; i < i1; ++i) {
+        float m, ssum;
+        wide::fold_lse(part + i, a.M, w.nchunks, m, ssum);
+        const float lga = a.log_a ? a.log_a[bM + i] : a.log_a_default;
+        const float ls = logf(fmaxf(ssum, kSumFloor));
+        const float ut = lga - (m + ls);
+        const float wt = fast_exp(lga - ls);
+        const float ucur = uc ? uc[bM + i] : 0.0f;
+        float un = ut;
+        if constexpr (MODE == kPlain) {
+            gap1 = fmaxf(gap1, fabsf(ucur - ut));
+        } else {
+            if constexpr (MODE == kMomentum) {
+                un = (1.0f - a.omega) * ucur + a.omega * ut;  // torch_cuda.cpp:470-474
+            } else {
+                // torch_cuda.cpp:475-484: the moments advance whether or not u' is kept
+                const float g = ut - ucur;
+                const float mm = a.beta1 * a.m1[bM + i] + (1.0f - a.beta1) * g;
+                const float vv = a.beta2 * a.m2[bM + i] + (1.0f - a.beta2) * (g * g);
+                if (lane == 0) {
+                    a.m1[bM + i] = mm;
+                    a.m2[bM + i] = vv;
+                }
+                un = ucur + a.lr * (mm / a.c1) / (sqrtf(vv / a.c2) + a.eps);
+            }
+            gap0 = fmaxf(gap0, fabsf(un - ut));
+            gap1 = fmaxf(gap1, fabsf(ucur - ut));
+            move = fmaxf(move, fabsf(un - ucur));
+        }
+        if (lane == 0) {
+            a.ut[bM + i] = ut;
+            if constexpr (MODE != kPlain) {
+                a.un[bM + i] = un;
+                w.row_w2[bM + i] = wt * fast_exp(un - ut);
+            }
+            w.row_m[bM + i] = m;
+            w.row_w[bM + i] = wt;
+        }
+    }
+    if constexpr (MODE != kPlain) {
+        block_flag_max<3>(a.slots, kGapU, gap0, kGapU + 1, gap1, kMoveU, move, red);
+    } else if (a.track) {
+        block_flag_max<1>(a.slots, kGapU + 1, gap1, 0, 0.0f, 0, 0.0f, red);
+    }
+}
+
+template <int VEC, int CH, int MODE>
+__global__ __launch_bounds__(kBlock) void wide_cols(WideArgs w) {
+#pragma clang fp contract(off)
+    using R = Row<VEC, CH>;
+    const SweepArgs& a = w.s;
+    extern __shared__ __align__(16) float lds[];  // 2 kChunk floats
+    const int b = batch_of_block();
+    if (b >= a.B) return;
+    const wide::Tile tl = wide::tile_of_block(w.nchunks, a.N);
+    const int lane = threadIdx.x % kWave;
+    const int wave = threadIdx.x / kWave;
+    Prev pv;
+    float v[R::PL];
+    if (!wide_prologue<R, MODE>(a, b, tl.c0, tl.nc, pv, v)) return;
+    const int r0 = tl.s * a.rows;
+    const int r1 = min(r0 + a.rows, a.M);
+    const size_t bM = size_t(b) * a.M;
+    float acc_t[R::PL], acc_n[R::PL];
+#pragma unroll
+    for (int e = 0; e < R::PL; ++e) acc_t[e] = acc_n[e] = 0.0f;
+    for (int i = r0 + wave; i < r1; i += kWavesPerBlock) {
+        float x[R::PL];
+        R::load(a.X + (bM + i) * a.N + tl.c0, lane, tl.nc, x, 0.0f);
+        const float m = w.row_m[bM + i];
+        const float wt = w.row_w[bM + i];
+        const float w2 = MODE != kPlain ? w.row_w2[bM + i] : 0.0f;
+#pragma unroll
+        for (int e = 0; e < R::PL; ++e) {
+            const float y = R::valid(lane, e, tl.nc) ? fmaf(x[e], a.kscale, v[e]) : -INFINITY;
+            const float ex = fast_exp(y - m);
+            acc_t[e] = fmaf(ex, wt, acc_t[e]);
+            if constexpr (MODE != kPlain) acc_n[e] = fmaf(ex, w2, acc_n[e]);
+        }
+    }
+    const size_t off = (size_t(b) * a.nstrips + tl.s) * a.N + tl.c0;
+    block_column_combine<VEC, CH>(acc_t, lds, tl.nc);
+    if (wave == 0) R::store(a.part_t + off, lane, tl.nc, acc_t);
+    if constexpr (MODE != kPlain) {
+        block_column_combine<VEC, CH>(acc_n, lds, tl.nc);
+        if (wave == 0) R::store(a.part_n + off, lane, tl.nc, acc_n);
     }
 }
 
@@ -723,13 +921,15 @@ struct PlanArgs {
     const float* X;
     float kscale, csign;
     int B, M, N, rows, return_log;
+    int nchunks;          // column chunks per row (1 unless N > kMaxRowLen)
     int safe;             // safe_exp (the vanilla materialisation) rather than exp
     const float* u;
     const float* v;
     float* plan;          // or null
-    float* cost_partial;  // [B,nstrips] or null
+    float* cost_partial;  // [B, nstrips * nchunks] or null
 };
 
+// One strip x chunk tile (tile.cuh) per workgroup; a whole row when nchunks is 1.
 template <int VEC, int CH>
 __global__ __launch_bounds__(kBlock) void plan(PlanArgs a) {
     using R = Row<VEC, CH>;
@@ -738,24 +938,25 @@ __global__ __launch_bounds__(kBlock) void plan(PlanArgs a) {
     const int wave = threadIdx.x / kWave;
     const int b = batch_of_block();
     if (b >= a.B) return;
-    const int r0 = blockIdx.x * a.rows;
+    const wide::Tile tl = wide::tile_of_block(a.nchunks, a.N);
+    const int r0 = tl.s * a.rows;
     const int r1 = min(r0 + a.rows, a.M);
     float v[R::PL];
-    R::load(a.v + size_t(b) * a.N, lane, a.N, v, 0.0f);
+    R::load(a.v + size_t(b) * a.N + tl.c0, lane, tl.nc, v, 0.0f);
     float cacc = 0.0f;
     for (int i = r0 + wave; i < r1; i += kWavesPerBlock) {
-        const size_t off = (size_t(b) * a.M + i) * a.N;
+        const size_t off = (size_t(b) * a.M + i) * a.N + tl.c0;
         float x[R::PL];
-        R::load(a.X + off, lane, a.N, x, 0.0f);
+        R::load(a.X + off, lane, tl.nc, x, 0.0f);
         const float ui = a.u[size_t(b) * a.M + i];
 #pragma unroll
         for (int e = 0; e < R::PL; ++e) {
             const float lp = x[e] * a.kscale + ui + v[e];
             const float p = a.return_log ? lp : (a.safe ? safe_exp(lp) : expf(lp));
-            if (a.cost_partial && R::valid(lane, e, a.N)) cacc = fmaf(p, a.csign * x[e], cacc);
+            if (a.cost_partial && R::valid(lane, e, tl.nc)) cacc = fmaf(p, a.csign * x[e], cacc);
             x[e] = p;
         }
-        if (a.plan) R::store(a.plan + off, lane, a.N, x);
+        if (a.plan) R::store(a.plan + off, lane, tl.nc, x);
     }
     if (a.cost_partial) {
         const float s = block_reduce<kWavesPerBlock>(wave_sum(cacc), scratch, OpSum{});

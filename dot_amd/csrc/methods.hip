@@ -28,7 +28,10 @@ struct MethodLayout {
     float *ut[2], *un[2], *vt[2], *vn[2];  // per iteration, by parity
     float *part_t, *part_n, *cost_partial;
     float *hxu, *hxv, *hfu, *hfv, *dots, *gram, *alpha, *denom;
-    int rows, nstrips;
+    // rows longer than kMaxRowLen (nchunks > 1): chunk partials and row terms
+    float2* rpart;                // [B, nchunks, M]
+    float *row_m, *row_w, *row_w2;  // [B, M]
+    int rows, nstrips, nchunks;
     size_t bytes;
 };
 
@@ -49,7 +52,9 @@ int solver_strip_rows(int B, int M) {
 MethodLayout method_layout(void* ws, int B, int M, int N, int T, int method, int k) {
     Carver c(ws);
     MethodLayout L{};
-    L.rows = solver_strip_rows(B, M);
+    // rows longer than a wave's registers run on the strips x chunks tiling
+    L.nchunks = N > kMaxRowLen ? wide::num_chunks(N) : 1;
+    L.rows = L.nchunks > 1 ? wide::strip_rows(B, M, L.nchunks) : solver_strip_rows(B, M);
     L.nstrips = M > 0 ? (M + L.rows - 1) / L.rows : 0;
     const size_t BM = size_t(B) * M, BN = size_t(B) * N;
     const bool adam = method == DOT_SK_ADAM, anderson = method == DOT_SK_ANDERSON;
@@ -71,7 +76,12 @@ MethodLayout method_layout(void* ws, int B, int M, int N, int T, int method, int
     }
     L.part_t = c.take<float>(size_t(B) * L.nstrips * N);
     L.part_n = cand ? c.take<float>(size_t(B) * L.nstrips * N) : L.part_t;
-    L.cost_partial = c.take<float>(size_t(B) * L.nstrips);
+    L.cost_partial = c.take<float>(size_t(B) * L.nstrips * L.nchunks);
+    const bool wide_rows = L.nchunks > 1;
+    L.rpart = c.take<float2>(wide_rows ? size_t(B) * L.nchunks * M : 0);
+    L.row_m = c.take<float>(wide_rows ? BM : 0);
+    L.row_w = c.take<float>(wide_rows ? BM : 0);
+    L.row_w2 = c.take<float>(wide_rows && cand ? BM : 0);
     const size_t kk = anderson ? size_t(k) : 0;
     L.hxu = c.take<float>(kk * BM);
     L.hxv = c.take<float>(kk * BN);
@@ -184,11 +194,6 @@ extern "C" int dot_sinkhorn_forward_method(const dot_sinkhorn_method_args* m, do
     const dot_sinkhorn_fwd_args* a = &m->base;
     const int B = a->B, M = a->M, N = a->N, T = a->max_iter;
     if (B < 0 || M < 0 || N < 0) return fail(DOT_ERR_INVALID_ARG, "B, M and N must be >= 0");
-    // the plain method (with or without a schedule) runs on dot_sinkhorn_forward's
-    // tiers, which take any row length; the accelerated sweeps hold whole rows
-    if (N > kMaxRowLen && m->method != DOT_SK_VANILLA)
-        return fail(DOT_ERR_UNSUPPORTED, "momentum, Anderson and Adam are not supported for rows longer than "
-                                         "4096 columns by this build (N=" + std::to_string(N) + ")");
     if (!(std::isfinite(a->tau) && a->tau > 0.0f)) return fail(DOT_ERR_INVALID_ARG, "tau must be > 0");
     if (T < 0) return fail(DOT_ERR_INVALID_ARG, "max_iter must be >= 0");
     if (a->scores_kind != DOT_SCORES_LOG_ALPHA && a->scores_kind != DOT_SCORES_COST)
@@ -272,12 +277,14 @@ extern "C" int dot_sinkhorn_forward_method(const dot_sinkhorn_method_args* m, do
     const bool anderson = method == DOT_SK_ANDERSON;
 
     int rc = DOT_OK;
-    const bool launched = dispatch_row(N, vec4, [&](auto vc, auto cc) {
+    // V, C: the row layout (a whole row, or one kChunk tile of it when WIDE)
+    auto body = [&](auto vc, auto cc, auto wide_c) {
         constexpr int V = decltype(vc)::value;
         constexpr int C = decltype(cc)::value;
-        const dim3 strips = batch_grid(unsigned(L.nstrips), B);
+        constexpr bool WIDE = decltype(wide_c)::value;
+        const dim3 strips = batch_grid(unsigned(L.nstrips * L.nchunks), B);  // strips x chunks tiles
         const dim3 cols = batch_grid(unsigned((N + mth::kFoldCols - 1) / mth::kFoldCols), B);
-        const size_t sweep_lds = (size_t(2) * N + 16) * sizeof(float);  // columns + flag reduction
+        const size_t sweep_lds = (size_t(2) * (WIDE ? wide::kChunk : N) + 16) * sizeof(float);  // columns + flags
         int ring_head = 0, ring_size = 0;  // Anderson ring: logical position -> physical slot
 
         auto iteration = [&](auto mode_c, int t, float ks) {
@@ -330,7 +337,21 @@ extern "C" int dot_sinkhorn_forward_method(const dot_sinkhorn_method_args* m, do
             sa.t = t;
             sa.used = a->iters_used;
             sa.converged = a->converged;
-            {
+            if constexpr (WIDE) {
+                mth::WideArgs wa{};
+                wa.s = sa;
+                wa.nchunks = L.nchunks;
+                wa.rpart = L.rpart;
+                wa.row_m = L.row_m;
+                wa.row_w = L.row_w;
+                wa.row_w2 = L.row_w2;
+                const int fin_rows = kWavesPerBlock * mth::kFinishRowsPerWave;
+                ProfScope prof("mth_sweep", stream);
+                hipLaunchKernelGGL((mth::wide_rows<V, C, MODE>), strips, dim3(kBlock), 0, stream, wa);
+                hipLaunchKernelGGL((mth::wide_finish<MODE>), batch_grid(unsigned((M + fin_rows - 1) / fin_rows), B),
+                                   dim3(kBlock), 0, stream, wa);
+                hipLaunchKernelGGL((mth::wide_cols<V, C, MODE>), strips, dim3(kBlock), sweep_lds, stream, wa);
+            } else {
                 ProfScope prof("mth_sweep", stream);
                 hipLaunchKernelGGL((mth::sweep<V, C, MODE>), strips, dim3(kBlock), sweep_lds, stream, sa);
             }
@@ -462,6 +483,7 @@ extern "C" int dot_sinkhorn_forward_method(const dot_sinkhorn_method_args* m, do
             pa.M = M;
             pa.N = N;
             pa.rows = L.rows;
+            pa.nchunks = L.nchunks;
             pa.return_log = ret_log ? 1 : 0;
             pa.safe = method == DOT_SK_VANILLA ? 1 : 0;
             pa.u = L.u;
@@ -471,10 +493,15 @@ extern "C" int dot_sinkhorn_forward_method(const dot_sinkhorn_method_args* m, do
             ProfScope prof("mth_plan", stream);
             hipLaunchKernelGGL((mth::plan<V, C>), strips, dim3(kBlock), 0, stream, pa);
             if (a->cost)
-                hipLaunchKernelGGL(batch_sum_m, dim3(B), dim3(kWave), 0, stream, L.cost_partial, L.nstrips,
-                                   a->cost);
+                hipLaunchKernelGGL(batch_sum_m, dim3(B), dim3(kWave), 0, stream, L.cost_partial,
+                                   L.nstrips * L.nchunks, a->cost);
         }
-    });
+    };
+    bool launched = true;
+    if (L.nchunks > 1)
+        wide::dispatch_chunk(vec4, [&](auto vc, auto cc) { body(vc, cc, std::true_type{}); });
+    else
+        launched = dispatch_row(N, vec4, [&](auto vc, auto cc) { body(vc, cc, std::false_type{}); });
     if (rc != DOT_OK) return rc;
     if (!launched) return fail(DOT_ERR_UNSUPPORTED, "row length outside the supported range");
     if (a->u_out && hipMemcpyAsync(a->u_out, L.u, BM * sizeof(float), hipMemcpyDeviceToDevice, stream) != hipSuccess)

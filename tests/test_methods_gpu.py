@@ -110,8 +110,7 @@ def test_scheduled_plain_iteration_on_every_tier(tier, shape, monkeypatch):
 
 def test_scheduled_plain_iteration_on_long_rows():
     """The plain method with a schedule on rows longer than 4096 columns (the
-    forward's strips x chunks tiles with a per-iteration K scale); the
-    accelerated methods refuse such rows with a clear error."""
+    forward's strips x chunks tiles with a per-iteration K scale)."""
     B, M, N = 1, 24, 4500
     la, lga, lgb = _case(4500, B, M, N, marginals=True)
     for schedule, T in ((LIN, 3), (EXP, 12)):
@@ -119,8 +118,43 @@ def test_scheduled_plain_iteration_on_long_rows():
         ref = _oracle(la, 0.1, T, 0.0, lga, lgb, schedule=schedule, reg_start=0.4)
         assert used == T and conv == 0
         assert rel_err(P, ref.P) < FWD_TOL, (schedule, T)
-    with pytest.raises(RuntimeError, match="longer than 4096"):
-        _gpu(la, 0.1, 5, 0.0, lga, lgb, method=1, omega=1.3)
+
+
+LONG_ROW_METHODS = [(MOM, {"omega": 1.3}), (ADAM, {"lr": 0.5}), (AND, {"anderson_k": 4})]
+
+
+@pytest.mark.parametrize("method,kw", LONG_ROW_METHODS)
+@pytest.mark.parametrize("shape", [(2, 20, 4500), (1, 9, 4097), (1, 70, 8192)])
+def test_methods_on_long_rows(method, kw, shape):
+    """Momentum, Adam and Anderson on rows longer than 4096 columns: the sweep
+    as a rows pass, a per-row finish and a columns pass over strips x chunks
+    tiles (N % 4 != 0 takes scalar loads).  Judged against the fp32 spread of
+    the oracle, as the short-row tests of these methods."""
+    B, M, N = shape
+    la, lga, lgb = _case(83 + N, B, M, N, marginals=(B == 2))
+    for T in (1, 4, 15):
+        print(f"long rows method={method} shape={shape} T={T}", flush=True)
+        P, used, conv = _gpu(la, 0.1, T, 0.0, lga, lgb, method=method, **kw)
+        ref, tol = _fp32_spread(la, 0.1, T, lga, lgb, method=method, **kw)
+        assert used == T and conv == 0
+        assert rel_err(P, ref.P) < tol, (T, tol)
+
+
+@pytest.mark.parametrize("method,kw", LONG_ROW_METHODS)
+def test_methods_on_long_rows_stop_test_and_cost(method, kw):
+    # the device stop test, and the cost through the public API (per-tile cost partials)
+    la, _, _ = _case(89, 2, 16, 5000)
+    P, used, conv = _gpu(la, 0.2, 120, 1e-4, method=method, **kw)
+    ref = _oracle(la, 0.2, 120, 1e-4, method=method, **kw)
+    assert ref.converged and conv == 1
+    assert abs(used - ref.n_iters_used) <= 1, (used, ref.n_iters_used)
+    # reg 0.03: the API keeps Adam (non-default lr) and Anderson below 0.05 (sinkhorn.py:1362-1390)
+    name = {MOM: "momentum", ADAM: "adam", AND: "anderson"}[method]
+    C = -la
+    res = dot_amd.sinkhorn(_t(C), reg=0.03, n_iters=12, tol=0.0, method=name, **kw)
+    at, tol_p = _fp32_spread(la, 0.03, 12, None, None, method=method, **kw)
+    assert rel_err(res.transport_plan, at.P) < tol_p
+    assert rel_err(res.cost, (at.P * C).sum((1, 2))) < tol_p
 
 
 def test_schedule_with_start_equal_to_target_is_the_plain_iteration():
