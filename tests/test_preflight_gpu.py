@@ -22,6 +22,10 @@ DEV = torch.device("cuda", 0)
     (1, 300, 4096, 0.2, 5, 0.3),
     (4, 512, 512, 0.05, 8, 0.02),
     (2, 1000, 257, 1.0, 3, 2.0),
+    # rows longer than 4096 columns: strips x chunks tiles; 4097 takes scalar loads
+    (2, 40, 4500, 0.2, 5, 0.3),
+    (1, 33, 4097, 0.5, 4, 1.0),
+    (1, 130, 8192, 0.1, 6, 0.1),
 ])
 def test_preflight_matches_oracle(B, M, N, tau, n_power, scale):
     rng = np.random.default_rng(B + M + N)
@@ -41,6 +45,19 @@ def test_preflight_is_deterministic_and_batch_independent():
     # element b of a batch sees the start vector of index b
     one = _ops.sinkhorn_spectral_preflight(X[:1].contiguous(), 0.1, 8)
     assert torch.equal(one, a[:1])
+
+
+def test_auto_iterations_on_long_rows():
+    # n_iters='auto' end to end on rows longer than 4096 columns: the count the
+    # preflight predicts, then the forward at that count
+    rng = np.random.default_rng(5)
+    C = torch.from_numpy((0.2 * rng.random((2, 24, 5000))).astype(np.float32)).to(DEV)
+    predicted = dot_amd.spectral_preflight(-C, 0.1, tol=1e-6)
+    tau_est = osk.spectral_preflight_tau(-C.cpu().numpy(), 0.1, 5)
+    assert predicted.shape == (2,) and (predicted >= 1).all()
+    res = dot_amd.sinkhorn(C, reg=0.1, n_iters="auto", tol=1e-6)
+    assert 1 <= res.n_iters_used <= int(predicted.max())
+    assert torch.isfinite(res.transport_plan).all() and np.all(tau_est < 1.0)
 
 
 def test_preflight_argument_errors():
