@@ -181,6 +181,14 @@ def test_long_rows_and_large_batches_have_workspace(lib):
     u = lib.dot_sinkhorn_backward_unrolled_workspace_bytes
     u.restype = ctypes.c_size_t
     assert u(B, M, N) >= B * M * N * 4 + B * 4 * M * 4  # Gamma and the row partials
+    # the accelerated methods and the preflight tile rows the same way
+    mq = lib.dot_sinkhorn_forward_method_workspace_bytes
+    mq.restype = ctypes.c_size_t
+    assert mq(B, M, N, 10, 1, 5) >= B * 4 * M * 8 + 3 * B * M * 4  # (max, sum) plane and row terms
+    assert mq(B, M, N, 10, 2, 5) > mq(B, M, 4096, 10, 2, 5)
+    pq = lib.dot_sinkhorn_spectral_preflight_workspace_bytes
+    pq.restype = ctypes.c_size_t
+    assert pq(B, M, N) >= B * 4 * M * (8 + 4)  # LSE and row-dot chunk planes
     for name in ("dot_sinkhorn_backward_implicit_workspace_bytes", "dot_bidisoftmax_forward_workspace_bytes",
                  "dot_bidisoftmax_backward_workspace_bytes"):
         f = getattr(lib, name)
