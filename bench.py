@@ -71,6 +71,9 @@ WORKLOADS = {
     "c3": dict(B=64, M=512, N=512, reg=0.1, n_iters=200, tol=1e-6, seed=3),
     "c4": dict(B=16, M=1024, N=2048, reg=0.05, n_iters=500, tol=1e-6, seed=4),
     "c5": dict(B=4, M=4096, N=4096, reg=0.02, n_iters=1000, tol=1e-6, seed=5),
+    # not a BASELINE configuration: rows of 16384 columns, the strips x chunks
+    # tiles of the streaming sweeps (``--workload wide``; never in other_configs)
+    "wide": dict(B=4, M=1024, N=16384, reg=0.05, n_iters=100, tol=0.0, seed=6),
 }
 
 
@@ -91,7 +94,7 @@ def make_inputs(name: str, torch, device):
     g = torch.Generator().manual_seed(cfg["seed"])
     B, M, N = cfg["B"], cfg["M"], cfg["N"]
     a = b = None
-    if name == "c1":
+    if name in ("c1", "wide"):
         C = torch.rand(B, M, N, generator=g)
     elif name == "c3":
         x = torch.randn(B, M, 64, generator=g)
