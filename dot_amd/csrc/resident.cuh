@@ -271,6 +271,11 @@ __device__ __forceinline__ int lane_of_slot(int k) {
 }
 
 constexpr int kColsPerThread = (1024 + kThreads - 1) / kThreads;  // N <= 1024
+
+// Column rounds of the per-column exchange for rows of PL floats per lane
+// (64 PL columns at most): thread t takes columns t, t + kThreads, ...
+template <int PL>
+constexpr int kColRounds = (kWave * PL + kThreads - 1) / kThreads;
 constexpr int kXcds = 8;  // MI355X dispatches consecutive workgroups round-robin over 8 XCDs
 
 // Logical index of this workgroup, b * W + w.  When the grid splits evenly,
@@ -309,14 +314,15 @@ __device__ __forceinline__ void put(float (&v)[N], int q, float x) {
 // Every lane polls its own values (a separate "ready" word would add a
 // second memory round trip).  f(j, total) consumes each total; totals are
 // NaN after a timeout.  `local`: every workgroup of the element runs on this
-// XCD (element_on_one_xcd).
-template <class F>
+// XCD (element_on_one_xcd).  NQ: column rounds (kColRounds of the row layout).
+template <int NQ, class F>
 __device__ __forceinline__ void exchange_columns(const float* part, unsigned long long* slot, int N,
                                                  int b, int W, int w, unsigned t, bool local, int spin_limit,
                                                  int* status, bool& dead, F&& f) {
-    float own[kColsPerThread];
+    static_assert(NQ >= 1 && NQ <= kColsPerThread, "rows of at most 1024 columns");
+    float own[NQ];
 #pragma unroll
-    for (int q = 0; q < kColsPerThread; ++q) {
+    for (int q = 0; q < NQ; ++q) {
         const int j = threadIdx.x + q * kThreads;
         own[q] = 0.0f;
         if (j < N) {
@@ -334,23 +340,22 @@ __device__ __forceinline__ void exchange_columns(const float* part, unsigned lon
     // (a load whose tag is tested before the next load is issued makes the
     // compiler wait for each in turn).  Pairs outside the element or the row,
     // and this workgroup's own slot, are not loaded and count as ready.
-    float got[kColsPerThread][kMaxGroup] = {};
-    const int nq = N > kThreads ? 2 : 1;  // column rounds with any column < N (uniform)
+    float got[NQ][kMaxGroup] = {};
     for (int spins = 0; W > 1 && !dead; ++spins) {
-        unsigned long long x[kColsPerThread][kMaxGroup];
+        unsigned long long x[NQ][kMaxGroup];
 #pragma unroll
-        for (int q = 0; q < kColsPerThread; ++q) {
+        for (int q = 0; q < NQ; ++q) {
             const int j = threadIdx.x + q * kThreads;
 #pragma unroll
             for (int g = 0; g < kMaxGroup; ++g) {
                 x[q][g] = tag_pack(0.0f, t);
-                if (q < nq && g < W && g != w && j < N)
+                if (g < W && g != w && j < N)
                     x[q][g] = __hip_atomic_load(base + size_t(g) * N + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
         }
         bool ready = true;
 #pragma unroll
-        for (int q = 0; q < kColsPerThread; ++q)
+        for (int q = 0; q < NQ; ++q)
 #pragma unroll
             for (int g = 0; g < kMaxGroup; ++g) {
                 ready = ready && static_cast<unsigned>(x[q][g] >> 32) == t;
@@ -367,7 +372,7 @@ __device__ __forceinline__ void exchange_columns(const float* part, unsigned lon
         __builtin_amdgcn_s_sleep(1);
     }
 #pragma unroll
-    for (int q = 0; q < kColsPerThread; ++q) {
+    for (int q = 0; q < NQ; ++q) {
         const int j = threadIdx.x + q * kThreads;
         if (j >= N) continue;
         const float mine = own[q];
@@ -487,17 +492,19 @@ __global__ __launch_bounds__(kThreads) void implicit_adjoint(ImpResArgs a) {
         }
     }
     const float inv_rs = 1.0f / fmaxf(rs_l, sk::kSumFloor);
-    float c_own[kColsPerThread], cs_own[kColsPerThread];
+    float c_own[kColRounds<PL>], cs_own[kColRounds<PL>];
     const bool local = element_on_one_xcd(a.xchg, a.N, b, a.W, w, a.spin_limit, a.status, dead, scratch);
     R::store(part + wave * a.N, lane, a.N, cg);
     __syncthreads();
-    exchange_columns(part, a.pro, a.N, b, a.W, w, 1u, local, a.spin_limit, a.status, dead,
-                     [&](int j, float tot) { put(c_own, (j - threadIdx.x) / kThreads, tot); });
+    exchange_columns<kColRounds<PL>>(part, a.pro, a.N, b, a.W, w, 1u, local, a.spin_limit, a.status, dead,
+                                     [&](int j, float tot) { put(c_own, (j - threadIdx.x) / kThreads, tot); });
     __syncthreads();
     R::store(part + wave * a.N, lane, a.N, cp);
     __syncthreads();
-    exchange_columns(part, a.pro + size_t(G) * a.N, a.N, b, a.W, w, 1u, local, a.spin_limit, a.status, dead,
-                     [&](int j, float tot) { put(cs_own, (j - threadIdx.x) / kThreads, fmaxf(tot, sk::kSumFloor)); });
+    exchange_columns<kColRounds<PL>>(part, a.pro + size_t(G) * a.N, a.N, b, a.W, w, 1u, local, a.spin_limit,
+                                     a.status, dead, [&](int j, float tot) {
+                                         put(cs_own, (j - threadIdx.x) / kThreads, fmaxf(tot, sk::kSumFloor));
+                                     });
 
     // Sweeps.
     float mu[PL];
@@ -527,11 +534,11 @@ __global__ __launch_bounds__(kThreads) void implicit_adjoint(ImpResArgs a) {
         // the previous sweep.
         R::store(part + wave * a.N, lane, a.N, acc);
         __syncthreads();
-        exchange_columns(part, a.xchg + size_t(t & 1) * G * a.N, a.N, b, a.W, w, unsigned(t), local,
-                         a.spin_limit, a.status, dead, [&](int j, float tot) {
-                             const int q = (j - threadIdx.x) / kThreads;
-                             lds_mu[j] = (pick(c_own, q) - tot) / pick(cs_own, q);
-                         });
+        exchange_columns<kColRounds<PL>>(part, a.xchg + size_t(t & 1) * G * a.N, a.N, b, a.W, w, unsigned(t),
+                                         local, a.spin_limit, a.status, dead, [&](int j, float tot) {
+                                             const int q = (j - threadIdx.x) / kThreads;
+                                             lds_mu[j] = (pick(c_own, q) - tot) / pick(cs_own, q);
+                                         });
         __syncthreads();
         R::load(lds_mu, lane, a.N, mu, 0.0f);
     }
@@ -809,15 +816,16 @@ __global__ __launch_bounds__(kThreads) void forward(FwdResArgs a) {
             publish(a.dxchg + size_t(t % kDeltaSlots) * G + gid, d, unsigned(t));
         }
         int low = 0;
-        exchange_columns(part, a.xchg + size_t(cur) * G * a.N, a.N, b, a.W, w, unsigned(t), local, a.spin_limit,
-                         a.status, dead, [&](int j, float cs) {
-                             if (cs >= sk::kColSumFloor && cs <= FLT_MAX) {
-                                 lds_v[cur * a.N + j] = lds_lb[j] + lds_v[prev * a.N + j] - logf(cs);
-                             } else {
-                                 lds_v[cur * a.N + j] = __builtin_nanf("");  // exact LSE below
-                                 low = 1;
-                             }
-                         });
+        exchange_columns<kColRounds<PL>>(
+            part, a.xchg + size_t(cur) * G * a.N, a.N, b, a.W, w, unsigned(t), local, a.spin_limit, a.status, dead,
+            [&](int j, float cs) {
+                if (cs >= sk::kColSumFloor && cs <= FLT_MAX) {
+                    lds_v[cur * a.N + j] = lds_lb[j] + lds_v[prev * a.N + j] - logf(cs);
+                } else {
+                    lds_v[cur * a.N + j] = __builtin_nanf("");  // exact LSE below
+                    low = 1;
+                }
+            });
         if (test && wave == 0) {
             float gmax = 0.0f;
 #pragma unroll
