@@ -335,6 +335,13 @@ __device__ __forceinline__ void exchange_columns(const float* part, unsigned lon
     }
     unsigned long long* base = slot + size_t(b) * W * N;
     forced_timeout(spin_limit, status, dead);
+    // The guards below depend only on the thread and the element; computed
+    // from these opaque copies they are rebuilt at each call instead of being
+    // hoisted out of the caller's iteration loop and held in scalar registers
+    // for the whole kernel (C3 adjoint: 70 -> 42 spilled SGPRs, 3 % faster).
+    int tid = threadIdx.x;
+    asm volatile("" : "+v"(tid));
+    asm volatile("" : "+s"(W), "+s"(w));
     // One poll round issues the loads of every (column, workgroup) pair first
     // and only then looks at the tags, so the round costs one memory latency
     // (a load whose tag is tested before the next load is issued makes the
@@ -345,7 +352,7 @@ __device__ __forceinline__ void exchange_columns(const float* part, unsigned lon
         unsigned long long x[NQ][kMaxGroup];
 #pragma unroll
         for (int q = 0; q < NQ; ++q) {
-            const int j = threadIdx.x + q * kThreads;
+            const int j = tid + q * kThreads;
 #pragma unroll
             for (int g = 0; g < kMaxGroup; ++g) {
                 x[q][g] = tag_pack(0.0f, t);
