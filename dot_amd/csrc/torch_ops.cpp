@@ -273,14 +273,18 @@ Tensor sinkhorn_spectral_preflight_op(Tensor log_alpha, double tau, int64_t n_po
     return tau_est;
 }
 
+// status_on_host: the status word is pinned host memory that the backward's
+// last kernel writes through, so reading it needs no device-to-host copy.
 std::vector<Tensor> run_backward(bool implicit, const Tensor& scores_f, int kind, const Tensor& plan,
                                  const optional<Tensor>& grad_plan, const optional<Tensor>& grad_cost,
-                                 double tau, int64_t iters, const Tensor& u_hist, const Tensor& v_hist) {
+                                 double tau, int64_t iters, const Tensor& u_hist, const Tensor& v_hist,
+                                 bool status_on_host = false) {
     const int64_t B = scores_f.size(0), M = scores_f.size(1), N = scores_f.size(2);
     auto opts = scores_f.options().dtype(at::kFloat);
     Tensor grad = at::empty({B, M, N}, opts);
     Tensor grad_tau = at::empty({B}, opts);
-    Tensor status = at::empty({1}, scores_f.options().dtype(at::kInt));
+    Tensor status = status_on_host ? at::empty({1}, at::TensorOptions().dtype(at::kInt).pinned_memory(true))
+                                   : at::empty({1}, scores_f.options().dtype(at::kInt));
     const size_t ws_bytes = implicit ? dot_sinkhorn_backward_implicit_workspace_bytes(int(B), int(M), int(N))
                                      : dot_sinkhorn_backward_unrolled_workspace_bytes(int(B), int(M), int(N));
     Tensor ws = workspace(ws_bytes, scores_f);
@@ -489,9 +493,10 @@ std::vector<Tensor> fused_forward_method_op(Tensor scores, int64_t scores_kind, 
     return {o.plan, cost, o.counts};
 }
 
-// -> [grad_scores, grad_tau (B,), status (int32 [1] on the device: 1 when a
-// cross-workgroup exchange timed out)]; mode 0 implicit (iters = adjoint
-// sweeps), 1 unrolled (iters = T).
+// -> [grad_scores, grad_tau (B,), status (int32 [1] in pinned host memory,
+// written by the backward's last kernel: 1 when a cross-workgroup exchange
+// timed out; read it after the stream has passed the call)]; mode 0 implicit
+// (iters = adjoint sweeps), 1 unrolled (iters = T).
 std::vector<Tensor> fused_backward_op(Tensor scores, int64_t scores_kind, Tensor plan,
                                       optional<Tensor> grad_plan, optional<Tensor> grad_cost,
                                       double tau, int64_t mode, int64_t iters,
@@ -511,7 +516,7 @@ std::vector<Tensor> fused_backward_op(Tensor scores, int64_t scores_kind, Tensor
         TORCH_CHECK(uh.defined() && vh.defined() && uh.size(0) >= iters && vh.size(0) >= iters,
                     "unrolled backward needs the u/v history of every iteration");
     return run_backward(mode == 0, f32c(scores), int(scores_kind), f32c(plan), f32c_opt(grad_plan),
-                        f32c_opt(grad_cost), tau, iters, uh, vh);
+                        f32c_opt(grad_cost), tau, iters, uh, vh, /*status_on_host=*/true);
 }
 
 // -> [out, row_stats (B,2,L1), col_stats (B,2,L2)]

@@ -120,16 +120,22 @@ _BWD_TIMEOUT_MESSAGE = "dot_sinkhorn_backward: a cross-workgroup exchange timed 
 class _DeviceCounts:
     """A device forward's int32 ``[iters_used, converged]``, copied to pinned
     host memory behind the forward on its stream; ``get()`` waits for that copy
-    only.  A negative count means a cross-workgroup exchange of the forward
-    timed out (the kernels bound every wait); ``get()`` raises for it."""
+    only.  Words already in pinned host memory (written there by the call's
+    last kernel) need no copy: ``get()`` waits for the call itself.  A negative
+    count means a cross-workgroup exchange of the forward timed out (the
+    kernels bound every wait); ``get()`` raises for it."""
 
     __slots__ = ("_host", "_event", "_value")
 
-    def __init__(self, words: torch.Tensor):
-        stream = torch.cuda.current_stream(words.device)  # the stream the kernels ran on
-        self._host = torch.empty(words.numel(), dtype=torch.int32, pin_memory=True)
-        with torch.cuda.stream(stream):
-            self._host.copy_(words, non_blocking=True)
+    def __init__(self, words: torch.Tensor, device: Optional[torch.device] = None):
+        if words.is_cuda:
+            stream = torch.cuda.current_stream(words.device)  # the stream the kernels ran on
+            self._host = torch.empty(words.numel(), dtype=torch.int32, pin_memory=True)
+            with torch.cuda.stream(stream):
+                self._host.copy_(words, non_blocking=True)
+        else:
+            stream = torch.cuda.current_stream(device)
+            self._host = words
         self._event = torch.cuda.Event()
         self._event.record(stream)
         self._value = None
@@ -204,9 +210,9 @@ def _track(counts: torch.Tensor) -> _DeviceCounts:
     return dc
 
 
-def _track_status(status: torch.Tensor) -> None:
+def _track_status(status: torch.Tensor, device: torch.device) -> None:
     _check_finished_forwards()
-    _unchecked.append(_DeviceStatus(status))
+    _unchecked.append(_DeviceStatus(status, device))
 
 
 def _tau_value(tau) -> float:
@@ -279,7 +285,7 @@ class _SinkhornFusedFunction(torch.autograd.Function):
             uh,
             vh,
         )
-        _track_status(status)
+        _track_status(status, scores.device)
         tau_grad = None
         if ctx.tau_is_tensor and ctx.needs_input_grad[1]:
             tau_grad = grad_tau.sum()
@@ -354,7 +360,7 @@ class _SinkhornMethodFunction(torch.autograd.Function):
             grad_P.contiguous() if grad_P is not None else None,
             grad_cost.contiguous() if grad_cost is not None else None,
             ctx.tau, _MODE_IMPLICIT, ctx.backward_iters, None, None)
-        _track_status(status)
+        _track_status(status, scores.device)
         if grad_cost is not None:
             # the fused backward's direct cost term used P_vanilla; the cost was
             # computed from this forward's plan (d sum(P C)/dC = P, C = -log_alpha)

@@ -174,9 +174,10 @@ typedef struct {
     float* grad_tau;          /* [B] out (per batch element) */
     void* workspace;
     size_t workspace_bytes;
-    int32_t* status;          /* device int32 out, or NULL: 0 when the call's kernels finish
-                                 normally, 1 when a cross-workgroup exchange timed out (the
-                                 gradients are then NaN) */
+    int32_t* status;          /* int32 out written by a kernel (device memory, or pinned host
+                                 memory the device can reach), or NULL: 0 when the call's
+                                 kernels finish normally, 1 when a cross-workgroup exchange
+                                 timed out (the gradients are then NaN) */
 } dot_sinkhorn_bwd_args;
 
 /* Implicit-function adjoint: exactly `iters` Gauss-Seidel sweeps
