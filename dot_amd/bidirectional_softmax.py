@@ -30,6 +30,7 @@ class _BidirectionalSoftmaxFusedFunction(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, sim_matrix, tau, lengths):
+        # lengths None: every element full (no lengths tensor to build per call)
         out, row_stats, col_stats = _ops.fused.bidirectional_softmax_forward(sim_matrix, float(tau),
                                                                              lengths)
         ctx.save_for_backward(sim_matrix, row_stats, col_stats, lengths)
@@ -90,11 +91,11 @@ def bidirectional_softmax(
     if unbatched:
         sim_matrix = sim_matrix.unsqueeze(0)
     B, L1, L2 = sim_matrix.size(0), sim_matrix.size(1), sim_matrix.size(2)
-    if lengths is None:
-        lengths = _make_lengths(B, L1, L2, sim_matrix.device)
     if sim_matrix.is_cuda:
         result = _BidirectionalSoftmaxFusedFunction.apply(sim_matrix, tau, lengths)
     else:
+        if lengths is None:
+            lengths = _make_lengths(B, L1, L2, sim_matrix.device)
         result = _BidirectionalSoftmaxFunction.apply(sim_matrix, tau, lengths)
     if unbatched:
         result = result.squeeze(0)

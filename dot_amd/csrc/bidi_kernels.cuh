@@ -27,6 +27,11 @@ constexpr float kEps = 1.0e-9f;  // kernels.cu:29
 
 __device__ __forceinline__ void valid_extent(const int32_t* lengths, int b, int L1, int L2, int& l1,
                                              int& l2) {
+    if (!lengths) {  // no lengths: every element is full
+        l1 = L1;
+        l2 = L2;
+        return;
+    }
     l1 = min(max(lengths[2 * b], 0), L1);
     l2 = min(max(lengths[2 * b + 1], 0), L2);
 }

@@ -17,7 +17,10 @@
 #include <torch/library.h>
 
 #include <cmath>
+#include <map>
+#include <mutex>
 #include <string>
+#include <utility>
 #include <vector>
 
 #include "../../include/dot_amd.h"
@@ -44,6 +47,34 @@ Tensor f32c(const Tensor& t) { return t.to(at::kFloat).contiguous(); }
 Tensor workspace(size_t bytes, const Tensor& like) {
     return at::empty({static_cast<int64_t>(std::max<size_t>(bytes, 1))},
                      like.options().dtype(at::kByte));
+}
+
+// Exchange words of the one-pass bidirectional-softmax kernels, one set per
+// (device, stream): calls on one stream run in order, so no two kernels use a
+// set at once, and the growing epoch keeps a call from reading words an
+// earlier call left.  Cleared once (and again when the epoch would pass its
+// limit); held until the process ends (the map is never destroyed, so no
+// device memory is freed during interpreter teardown).
+struct ExchangeSet {
+    Tensor words;
+    uint32_t epoch = 0;
+};
+
+std::pair<void*, uint32_t> bidi_exchange(const Tensor& like) {
+    static std::mutex mu;
+    static auto* sets = new std::map<std::pair<int, void*>, ExchangeSet>();
+    const int dev = like.device().index();
+    void* stream = c10::hip::getCurrentHIPStream(dev).stream();
+    std::lock_guard<std::mutex> lock(mu);
+    ExchangeSet& x = (*sets)[{dev, stream}];
+    if (!x.words.defined() || x.epoch >= DOT_BIDISOFTMAX_MAX_EPOCH) {
+        if (!x.words.defined())
+            x.words = at::empty({static_cast<int64_t>(dot_bidisoftmax_exchange_bytes())},
+                                like.options().dtype(at::kByte));
+        x.words.zero_();  // on the current stream, ahead of the kernel
+        x.epoch = 0;
+    }
+    return {x.words.data_ptr(), ++x.epoch};
 }
 
 const float* ptr_or_null(const optional<Tensor>& t) {
@@ -416,7 +447,7 @@ std::vector<Tensor> bidi_backward_common(const Tensor& sim, const Tensor& grad_o
     Tensor ws = workspace(ws_bytes, sim);
     dot_bidisoftmax_bwd_args a{};
     a.sim = sim.data_ptr<float>();
-    a.lengths = lengths.data_ptr<int32_t>();
+    a.lengths = lengths.defined() ? lengths.data_ptr<int32_t>() : nullptr;
     a.B = int(B);
     a.L1 = int(L1);
     a.L2 = int(L2);
@@ -431,6 +462,7 @@ std::vector<Tensor> bidi_backward_common(const Tensor& sim, const Tensor& grad_o
     a.grad_tau = want_tau ? grad_tau.data_ptr<float>() : nullptr;
     a.workspace = ws.data_ptr();
     a.workspace_bytes = ws_bytes;
+    std::tie(a.exchange, a.exchange_epoch) = bidi_exchange(sim);
     check_rc(dot_bidisoftmax_backward(&a, current_stream(sim)), "dot_bidisoftmax_backward");
     return {grad, grad_tau};
 }
@@ -519,15 +551,15 @@ std::vector<Tensor> fused_backward_op(Tensor scores, int64_t scores_kind, Tensor
                         f32c_opt(grad_cost), tau, iters, uh, vh, /*status_on_host=*/true);
 }
 
-// -> [out, row_stats (B,2,L1), col_stats (B,2,L2)]
-std::vector<Tensor> bidi_forward_op(Tensor sim, double tau, Tensor lengths) {
+// -> [out, row_stats (B,2,L1), col_stats (B,2,L2)]; no lengths: every element full
+std::vector<Tensor> bidi_forward_op(Tensor sim, double tau, optional<Tensor> lengths) {
     check_hip_input(sim, "sim_matrix");
     TORCH_CHECK(sim.dim() == 3, "sim_matrix must be 3D [B, L1, L2]");
-    check_lengths(lengths, sim.size(0));
+    if (lengths.has_value()) check_lengths(*lengths, sim.size(0));
     TORCH_CHECK(tau > 0.0, "tau must be > 0");
     c10::OptionalDeviceGuard guard(sim.device());
     Tensor s = f32c(sim);
-    Tensor ln = lengths.contiguous();
+    Tensor ln = lengths.has_value() ? lengths->contiguous() : Tensor();
     const int64_t B = s.size(0), L1 = s.size(1), L2 = s.size(2);
     auto opts = s.options();
     Tensor out = at::empty({B, L1, L2}, opts);
@@ -537,7 +569,7 @@ std::vector<Tensor> bidi_forward_op(Tensor sim, double tau, Tensor lengths) {
     Tensor ws = workspace(ws_bytes, s);
     dot_bidisoftmax_fwd_args a{};
     a.sim = s.data_ptr<float>();
-    a.lengths = ln.data_ptr<int32_t>();
+    a.lengths = ln.defined() ? ln.data_ptr<int32_t>() : nullptr;
     a.B = int(B);
     a.L1 = int(L1);
     a.L2 = int(L2);
@@ -547,20 +579,22 @@ std::vector<Tensor> bidi_forward_op(Tensor sim, double tau, Tensor lengths) {
     a.col_stats = cs.data_ptr<float>();
     a.workspace = ws.data_ptr();
     a.workspace_bytes = ws_bytes;
+    std::tie(a.exchange, a.exchange_epoch) = bidi_exchange(s);
     check_rc(dot_bidisoftmax_forward(&a, current_stream(s)), "dot_bidisoftmax_forward");
     return {out, rs, cs};
 }
 
 std::vector<Tensor> bidi_backward_op(Tensor sim, Tensor grad_output, Tensor row_stats,
-                                     Tensor col_stats, double tau, Tensor lengths) {
+                                     Tensor col_stats, double tau, optional<Tensor> lengths) {
     for (auto* t : {&sim, &grad_output, &row_stats, &col_stats}) check_hip_input(*t, "inputs");
     TORCH_CHECK(sim.dim() == 3 && grad_output.sizes() == sim.sizes(), "grad_output must match sim");
-    check_lengths(lengths, sim.size(0));
+    if (lengths.has_value()) check_lengths(*lengths, sim.size(0));
     TORCH_CHECK(tau > 0.0, "tau must be > 0");
     c10::OptionalDeviceGuard guard(sim.device());
     // the autograd path has no tau gradient (the reference drops it): grad_tau is skipped
-    return bidi_backward_common(f32c(sim), f32c(grad_output), tau, lengths.contiguous(), Tensor(),
-                                Tensor(), Tensor(), f32c(row_stats), f32c(col_stats), false);
+    return bidi_backward_common(f32c(sim), f32c(grad_output), tau,
+                                lengths.has_value() ? lengths->contiguous() : Tensor(), Tensor(), Tensor(), Tensor(),
+                                f32c(row_stats), f32c(col_stats), false);
 }
 
 }  // namespace
@@ -597,8 +631,8 @@ TORCH_LIBRARY(dot_amd, m) {
     m.def("sinkhorn_forward(Tensor scores, int scores_kind, float tau, int n_iters, float tol, Tensor? log_a, Tensor? log_b, bool want_cost, bool keep_history) -> Tensor[]");
     m.def("sinkhorn_forward_method(Tensor scores, int scores_kind, float tau, int n_iters, float tol, Tensor? log_a, Tensor? log_b, int method, float omega, int anderson_k, float mixing_beta, float lr, float beta1, float beta2, float eps_adam, bool bias_correction, float reg_start, int schedule, bool want_cost) -> Tensor[]");
     m.def("sinkhorn_backward(Tensor scores, int scores_kind, Tensor plan, Tensor? grad_plan, Tensor? grad_cost, float tau, int mode, int iters, Tensor? u_hist, Tensor? v_hist) -> Tensor[]");
-    m.def("bidirectional_softmax_forward(Tensor sim, float tau, Tensor lengths) -> Tensor[]");
-    m.def("bidirectional_softmax_backward(Tensor sim, Tensor grad_output, Tensor row_stats, Tensor col_stats, float tau, Tensor lengths) -> Tensor[]");
+    m.def("bidirectional_softmax_forward(Tensor sim, float tau, Tensor? lengths) -> Tensor[]");
+    m.def("bidirectional_softmax_backward(Tensor sim, Tensor grad_output, Tensor row_stats, Tensor col_stats, float tau, Tensor? lengths) -> Tensor[]");
 }
 
 TORCH_LIBRARY_IMPL(dot_amd, CUDA, m) {

@@ -225,7 +225,8 @@ int dot_sinkhorn_spectral_preflight(const dot_spectral_preflight_args* args, dot
 /* ---------------------------------------------------------------------- */
 typedef struct {
     const float* sim;         /* [B,L1,L2] */
-    const int32_t* lengths;   /* [B,2] valid (rows, cols) per batch element, device int32 */
+    const int32_t* lengths;   /* [B,2] valid (rows, cols) per batch element, device int32;
+                                 NULL: every element is full (L1, L2) */
     int B, L1, L2;
     float tau;
     float* out;               /* [B,L1,L2] sqrt(1e-9 + r*c) in the valid region, else 0 */
@@ -238,6 +239,17 @@ typedef struct {
     float* col_stats;         /* [B,2,L2] column max plane then column sum plane, or NULL */
     void* workspace;
     size_t workspace_bytes;
+    /* Optional exchange words of the one-pass kernels (both L1 and L2 in
+     * 513..1024, B at least the GPU's XCD count, row_sm and col_sm NULL; see
+     * dot_bidisoftmax_exchange_bytes): NULL, and the library takes them from
+     * the workspace and clears them with one more small kernel per call; or
+     * caller-owned device memory of dot_bidisoftmax_exchange_bytes() bytes,
+     * zeroed once, used by calls on one stream only, with exchange_epoch
+     * 1, 2, ... (at most DOT_BIDISOFTMAX_MAX_EPOCH) growing by one per call
+     * (forward and backward calls share one sequence); zero the words again
+     * before the sequence restarts at 1.  No counterpart in the reference. */
+    void* exchange;
+    uint32_t exchange_epoch;
 } dot_bidisoftmax_fwd_args;
 
 /* Replaces bidirectional_softmax_forward_cuda
@@ -265,6 +277,10 @@ typedef struct {
                                  or NULL to skip it (the autograd path has no tau gradient) */
     void* workspace;
     size_t workspace_bytes;
+    /* As in dot_bidisoftmax_fwd_args (the one-pass backward runs from the
+     * statistics, with grad_tau NULL). */
+    void* exchange;
+    uint32_t exchange_epoch;
 } dot_bidisoftmax_bwd_args;
 
 /* Replaces bidirectional_softmax_backward_cuda
@@ -273,6 +289,11 @@ typedef struct {
  * registry.cpp:34). */
 size_t dot_bidisoftmax_backward_workspace_bytes(int B, int L1, int L2);
 int dot_bidisoftmax_backward(const dot_bidisoftmax_bwd_args* args, dot_stream_t stream);
+
+/* Size of the caller-owned exchange words (the `exchange` fields above) and
+ * the largest call epoch they take.  No counterpart in the reference. */
+#define DOT_BIDISOFTMAX_MAX_EPOCH 1048575u
+size_t dot_bidisoftmax_exchange_bytes(void);
 
 /* ---------------------------------------------------------------------- */
 /* Diagnostics (no counterpart in the reference)                           */
