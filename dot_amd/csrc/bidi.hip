@@ -218,12 +218,14 @@ extern "C" int dot_bidisoftmax_forward(const dot_bidisoftmax_fwd_args* a, dot_st
         if (!onepass_exchange(a->exchange, a->exchange_epoch, L.exchange, stream, o.x)) return DOT_ERR_INVALID_ARG;
         const dim3 grid(unsigned(o.x.groups * op::kMembers));
         ProfScope prof("bidi_fwd_onepass", stream);
-        // rows of exactly 1024 or 768 columns: the column bounds are constants
-        if (L2 == 1024)
+        // full tiles (no lengths, 1024 rows of 1024 or 768 columns): the bounds
+        // are constants
+        const bool tile = !a->lengths && L1 == op::kMaxRows;
+        if (tile && L2 == 1024)
             hipLaunchKernelGGL((op::fwd_kernel<4, true>), grid, dim3(op::kThreads), 0, stream, o);
         else if (L2 > 768)
             hipLaunchKernelGGL((op::fwd_kernel<4, false>), grid, dim3(op::kThreads), 0, stream, o);
-        else if (L2 == 768)
+        else if (tile && L2 == 768)
             hipLaunchKernelGGL((op::fwd_kernel<3, true>), grid, dim3(op::kThreads), 0, stream, o);
         else
             hipLaunchKernelGGL((op::fwd_kernel<3, false>), grid, dim3(op::kThreads), 0, stream, o);
@@ -344,6 +346,7 @@ extern "C" int dot_bidisoftmax_backward(const dot_bidisoftmax_bwd_args* a, dot_s
         if (!onepass_exchange(a->exchange, a->exchange_epoch, L.exchange, stream, o.x)) return DOT_ERR_INVALID_ARG;
         const dim3 grid(unsigned(o.x.groups * op::kMembers));
         ProfScope prof("bidi_bwd_onepass", stream);
+        // rows of exactly 1024 or 768 columns: the column bounds are constants
         if (L2 == 1024)
             hipLaunchKernelGGL((op::bwd_kernel<4, true>), grid, dim3(op::kThreads), 0, stream, o);
         else if (L2 > 768)

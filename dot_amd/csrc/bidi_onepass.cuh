@@ -146,6 +146,18 @@ __device__ __forceinline__ void scalar_extent(const int32_t* lengths, int b, int
     l2 = min(max(q[1], 0), L2);
 }
 
+// Valid rows and columns of element b; a full tile (no lengths) has constant
+// ones.
+__device__ __forceinline__ void extent(const int32_t* lengths, int b, int L1, int L2, bool full_tile, int& l1,
+                                       int& l2) {
+    if (full_tile) {
+        l1 = L1;
+        l2 = L2;
+    } else {
+        scalar_extent(lengths, b, L1, L2, l1, l2);
+    }
+}
+
 // Online (max, sum) state of base-2 exponentials, one exponential per update:
 // after a sequence of updates s * 2^m is the sum of 2^y.  Starting state
 // (-FLT_MAX, 0); y = -inf adds nothing.
@@ -299,11 +311,14 @@ template <int CH, bool FW>
 __device__ void fwd_fallback(const FwdArgs1& a, int e, int l1, int l2, int g, int m, int p, unsigned tag, bool local,
                              bool own, float* lm, float* ls, float* clse) {
     using R = Row<4, CH>;
-    const int L2 = FW ? 4 * kWave * CH : a.L2;  // full-width rows: a constant
+    // FW (full tile): no lengths, 1024 rows of 256 * CH columns; the extents
+    // are then constants and every row and column check folds away
+    const int L2 = FW ? 4 * kWave * CH : a.L2;
+    const int L1 = FW ? kMaxRows : a.L1;
     const int lane = threadIdx.x % kWave;
     const int wave = threadIdx.x / kWave;
     const int t = threadIdx.x;
-    const auto rs = element_rsrc(a.sim, size_t(a.L1) * L2, e);
+    const auto rs = element_rsrc(a.sim, size_t(L1) * L2, e);
     float M0 = -FLT_MAX, S0 = 0.0f, M1 = -FLT_MAX, S1 = 0.0f;
     for (int mm = 0; mm < kMembers; ++mm) {
         float cm[R::PL], cs[R::PL];
@@ -320,7 +335,7 @@ __device__ void fwd_fallback(const FwdArgs1& a, int e, int l1, int l2, int g, in
             for (int j = 0; j < kRowsPerWave; ++j) {
                 const int i = mm * kRowsPerMember + wave * kRowsPerWave + j;
                 float v[R::PL];
-                load_row<CH>(rs, min(i, a.L1 - 1), L2, lane, v);
+                load_row<CH>(rs, min(i, L1 - 1), L2, lane, v);
                 scale_mask<R>(v, a.sc, i < l1, lane, l2, full_cols && i < l1);
                 if (pass == 0)
                     column_max(cm, v);
@@ -380,7 +395,10 @@ __device__ __forceinline__ bool group_on_one_xcd(const Exchange& x, int g, unsig
 template <int CH, bool FW>
 __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(FwdArgs1 a) {
     using R = Row<4, CH>;
-    const int L2 = FW ? 4 * kWave * CH : a.L2;  // full-width rows: a constant
+    // FW (full tile): no lengths, 1024 rows of 256 * CH columns; the extents
+    // are then constants and every row and column check folds away
+    const int L2 = FW ? 4 * kWave * CH : a.L2;
+    const int L1 = FW ? kMaxRows : a.L1;
     constexpr int PL = R::PL;
     __shared__ __align__(16) float lm[kWaves * kMaxCols];
     __shared__ __align__(16) float ls[kWaves * kMaxCols];
@@ -403,12 +421,12 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(FwdArgs1 a) {
     float X[kRowsPerWave][PL], Y[kRowsPerWave][PL];
     // rows of element k of this group (past the last element: row 0 of element
     // `kc`, a cache hit, so that every load is unconditional)
-    const size_t elem = size_t(a.L1) * L2;
+    const size_t elem = size_t(L1) * L2;
     auto load = [&](int k, int kc, float(&buf)[kRowsPerWave][PL]) {
         const bool real = k < n;
         const auto rs = element_rsrc(a.sim, elem, g + G * (real ? k : kc));
 #pragma unroll
-        for (int j = 0; j < kRowsPerWave; ++j) load_row<CH>(rs, real ? min(row0 + j, a.L1 - 1) : 0, L2, lane, buf[j]);
+        for (int j = 0; j < kRowsPerWave; ++j) load_row<CH>(rs, real ? min(row0 + j, L1 - 1) : 0, L2, lane, buf[j]);
     };
     load(0, 0, X);
     load(1, 0, Y);
@@ -426,7 +444,7 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(FwdArgs1 a) {
         const unsigned tag = tag0 | unsigned(k + 1);
         const int p = k & 1;
         int l1, l2;
-        scalar_extent(a.lengths, e, a.L1, L2, l1, l2);
+        extent(a.lengths, e, L1, L2, FW, l1, l2);
         // ---- row statistics and this wave's column states
         float rl[kRowsPerWave];
         float cm[PL], cs[PL];
@@ -435,7 +453,7 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(FwdArgs1 a) {
             cm[q] = -FLT_MAX;
             cs[q] = 0.0f;
         }
-        float* rst = a.row_stats + size_t(e) * 2 * a.L1;
+        float* rst = a.row_stats + size_t(e) * 2 * L1;
         const bool full_cols = l2 == 4 * kWave * CH;
 #pragma unroll
         for (int j = 0; j < kRowsPerWave; ++j) {
@@ -459,7 +477,7 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(FwdArgs1 a) {
             rl[j] = rm + __builtin_amdgcn_logf(rs);
             if (i < l1) {  // wave-uniform
                 rst[i] = rm;
-                rst[a.L1 + i] = rs;
+                rst[L1 + i] = rs;
             }
         }
         // ---- fold the waves, publish this member's column words
@@ -535,8 +553,8 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(FwdArgs1 a) {
 #pragma unroll
                 for (int ee = 0; ee < PL; ++ee) o[ee] = (i < l1 && R::valid(lane, ee, l2)) ? o[ee] : 0.0f;
             }
-            if (i < a.L1) store_row<CH>(ro, i, L2, lane, o);
-            load_row<CH>(rs, real ? min(i, a.L1 - 1) : 0, L2, lane, buf[j]);
+            if (i < L1) store_row<CH>(ro, i, L2, lane, o);
+            load_row<CH>(rs, real ? min(i, L1 - 1) : 0, L2, lane, buf[j]);
         }
     };
     for (int k = 0; k < n; k += 2) {

@@ -86,21 +86,38 @@ def test_onepass_agrees_with_two_sweeps(monkeypatch):
 
 
 @pytest.mark.parametrize("ticks", ["-1", "0"])
-def test_fallback_is_bitwise_the_exchange(monkeypatch, ticks):
+@pytest.mark.parametrize("tile", [False, True])
+def test_fallback_is_bitwise_the_exchange(monkeypatch, ticks, tile):
     """-1: every workgroup computes the column statistics itself; 0: a wait gives
     up at its first miss, so exchange and fallback mix.  Either way the results
-    are bitwise those of the exchange path (same arithmetic, same order)."""
-    print(f"fallback ticks={ticks}", flush=True)
+    are bitwise those of the exchange path (same arithmetic, same order).  `tile`:
+    no lengths and 1024 x 1024 elements (the kernels with constant extents)."""
+    print(f"fallback ticks={ticks} tile={tile}", flush=True)
     rng = np.random.default_rng(5)
-    B, L1, L2, tau = 10, 1000, 1024, 0.7
+    B, L1, L2, tau = (8, 1024, 1024, 0.7) if tile else (10, 1000, 1024, 0.7)
     s = _t((2.0 * rng.standard_normal((B, L1, L2))).astype(np.float32))
     g = _t(rng.standard_normal((B, L1, L2)).astype(np.float32))
-    ln = _t(_lengths(B, L1, L2, "ragged", rng))
+    ln = None if tile else _t(_lengths(B, L1, L2, "ragged", rng))
     P1, g1 = _fused(s, g, tau, ln)
     monkeypatch.setenv("DOT_AMD_BIDI_WAIT_TICKS", ticks)
     P2, g2 = _fused(s, g, tau, ln)
     assert torch.equal(P1, P2)
     assert torch.equal(g1, g2)
+
+
+def test_full_tile_matches_oracle():
+    """No lengths and 1024 x 1024 elements: the kernels whose extents are
+    constants, against the oracle."""
+    rng = np.random.default_rng(21)
+    B, L1, L2, tau = 8, 1024, 1024, 0.6
+    s = (2.0 * rng.standard_normal((B, L1, L2))).astype(np.float32)
+    g = rng.standard_normal((B, L1, L2)).astype(np.float32)
+    ln = np.array([[L1, L2]] * B, np.int32)
+    out_o, r_o, c_o = obs.forward(s, tau, ln)
+    gs_o, _ = obs.backward(s, out_o, g, r_o, c_o, tau, ln)
+    P, grad = _fused(_t(s), _t(g), tau, None)
+    assert rel_err(P, out_o) < FWD_TOL
+    assert rel_err(grad, gs_o) < GRAD_TOL
 
 
 def test_repeated_calls_are_deterministic():
