@@ -315,11 +315,14 @@ __device__ __forceinline__ void put(float (&v)[N], int q, float x) {
 // second memory round trip).  f(j, total) consumes each total; totals are
 // NaN after a timeout.  `local`: every workgroup of the element runs on this
 // XCD (element_on_one_xcd).  NQ: column rounds (kColRounds of the row layout).
-template <int NQ, class F>
+// MG >= W: the workgroups per element the poll registers are sized for (an
+// element of at most 4 workgroups polls from half the registers).
+template <int NQ, int MG = kMaxGroup, class F>
 __device__ __forceinline__ void exchange_columns(const float* part, unsigned long long* slot, int N,
                                                  int b, int W, int w, unsigned t, bool local, int spin_limit,
                                                  int* status, bool& dead, F&& f) {
     static_assert(NQ >= 1 && NQ <= kColsPerThread, "rows of at most 1024 columns");
+    static_assert(MG >= 1 && MG <= kMaxGroup, "at most kMaxGroup workgroups per element");
     float own[NQ];
 #pragma unroll
     for (int q = 0; q < NQ; ++q) {
@@ -347,14 +350,14 @@ __device__ __forceinline__ void exchange_columns(const float* part, unsigned lon
     // (a load whose tag is tested before the next load is issued makes the
     // compiler wait for each in turn).  Pairs outside the element or the row,
     // and this workgroup's own slot, are not loaded and count as ready.
-    float got[NQ][kMaxGroup] = {};
+    float got[NQ][MG] = {};
     for (int spins = 0; W > 1 && !dead; ++spins) {
-        unsigned long long x[NQ][kMaxGroup];
+        unsigned long long x[NQ][MG];
 #pragma unroll
         for (int q = 0; q < NQ; ++q) {
             const int j = tid + q * kThreads;
 #pragma unroll
-            for (int g = 0; g < kMaxGroup; ++g) {
+            for (int g = 0; g < MG; ++g) {
                 x[q][g] = tag_pack(0.0f, t);
                 if (g < W && g != w && j < N)
                     x[q][g] = __hip_atomic_load(base + size_t(g) * N + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -364,7 +367,7 @@ __device__ __forceinline__ void exchange_columns(const float* part, unsigned lon
 #pragma unroll
         for (int q = 0; q < NQ; ++q)
 #pragma unroll
-            for (int g = 0; g < kMaxGroup; ++g) {
+            for (int g = 0; g < MG; ++g) {
                 ready = ready && static_cast<unsigned>(x[q][g] >> 32) == t;
                 got[q][g] = __uint_as_float(static_cast<unsigned>(x[q][g]));
             }
@@ -376,7 +379,10 @@ __device__ __forceinline__ void exchange_columns(const float* part, unsigned lon
             dead = true;
             break;
         }
-        __builtin_amdgcn_s_sleep(1);
+        // Rounds go back to back: a round is one memory latency (~0.6 us under
+        // the sweep's load at C3), and a 64-clock sleep between rounds cost
+        // 0.05 us per sweep; issuing the next round before testing the last
+        // one (two in flight) cost 0.15 us.
     }
 #pragma unroll
     for (int q = 0; q < NQ; ++q) {
@@ -385,7 +391,7 @@ __device__ __forceinline__ void exchange_columns(const float* part, unsigned lon
         const float mine = own[q];
         float tot = 0.0f;
 #pragma unroll
-        for (int g = 0; g < kMaxGroup; ++g)
+        for (int g = 0; g < MG; ++g)
             if (g < W) tot += (g == w) ? mine : got[q][g];
         f(j, dead ? __builtin_nanf("") : tot);
     }
@@ -432,8 +438,8 @@ __device__ __forceinline__ void upstream_row(const ImpResArgs& a, size_t off, in
 //   mu_k = (c_k - sum_i P lambda_i) / max(cs_k, 1e-12)   (one exchange)
 // Final phase: grad = P (G - lambda - mu) / tau (cost kind: grad_cost P - that;
 // log-alpha kind: that - grad_cost P) and this workgroup's share of
-// sum(grad * log_alpha) for grad_tau.
-template <int VEC, int CH, int RPW>
+// sum(grad * log_alpha) for grad_tau.  MG >= W (exchange_columns).
+template <int VEC, int CH, int RPW, int MG = kMaxGroup>
 __global__ __launch_bounds__(kThreads) void implicit_adjoint(ImpResArgs a) {
     using R = Row<VEC, CH>;
     constexpr int PL = R::PL;
@@ -503,12 +509,12 @@ __global__ __launch_bounds__(kThreads) void implicit_adjoint(ImpResArgs a) {
     const bool local = element_on_one_xcd(a.xchg, a.N, b, a.W, w, a.spin_limit, a.status, dead, scratch);
     R::store(part + wave * a.N, lane, a.N, cg);
     __syncthreads();
-    exchange_columns<kColRounds<PL>>(part, a.pro, a.N, b, a.W, w, 1u, local, a.spin_limit, a.status, dead,
+    exchange_columns<kColRounds<PL>, MG>(part, a.pro, a.N, b, a.W, w, 1u, local, a.spin_limit, a.status, dead,
                                      [&](int j, float tot) { put(c_own, (j - threadIdx.x) / kThreads, tot); });
     __syncthreads();
     R::store(part + wave * a.N, lane, a.N, cp);
     __syncthreads();
-    exchange_columns<kColRounds<PL>>(part, a.pro + size_t(G) * a.N, a.N, b, a.W, w, 1u, local, a.spin_limit,
+    exchange_columns<kColRounds<PL>, MG>(part, a.pro + size_t(G) * a.N, a.N, b, a.W, w, 1u, local, a.spin_limit,
                                      a.status, dead, [&](int j, float tot) {
                                          put(cs_own, (j - threadIdx.x) / kThreads, fmaxf(tot, sk::kSumFloor));
                                      });
@@ -541,7 +547,7 @@ __global__ __launch_bounds__(kThreads) void implicit_adjoint(ImpResArgs a) {
         // the previous sweep.
         R::store(part + wave * a.N, lane, a.N, acc);
         __syncthreads();
-        exchange_columns<kColRounds<PL>>(part, a.xchg + size_t(t & 1) * G * a.N, a.N, b, a.W, w, unsigned(t),
+        exchange_columns<kColRounds<PL>, MG>(part, a.xchg + size_t(t & 1) * G * a.N, a.N, b, a.W, w, unsigned(t),
                                          local, a.spin_limit, a.status, dead, [&](int j, float tot) {
                                              const int q = (j - threadIdx.x) / kThreads;
                                              lds_mu[j] = (pick(c_own, q) - tot) / pick(cs_own, q);

@@ -776,7 +776,8 @@ bool launch_resident_adjoint(const dot_sinkhorn_bwd_args* a, const ImpLayout& L,
         constexpr int C = decltype(cc)::value;
         constexpr int RPW = decltype(rr)::value;
         const size_t lds = (size_t(res::kWaves + 1) * a->N + res::kWaves) * sizeof(float);
-        auto kernel = res::implicit_adjoint<V, C, RPW>;
+        // elements of at most 4 workgroups poll their exchange from fewer registers
+        auto kernel = rc.W <= 4 ? res::implicit_adjoint<V, C, RPW, 4> : res::implicit_adjoint<V, C, RPW>;
         int per_cu = 0;
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, res::kThreads, lds) != hipSuccess ||
             per_cu < 1 || int64_t(per_cu) * device_cus() < groups)

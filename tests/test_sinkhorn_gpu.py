@@ -652,6 +652,33 @@ def test_resident_forward_exact_column_fallback(monkeypatch):
         assert rel_err(P, Po) < FWD_TOL, mode
 
 
+@pytest.mark.parametrize("B,M,N,tau,T,tol,b_range", [
+    (4, 256, 384, 0.05, 60, 0.0, 30.0),
+    (4, 256, 384, 0.05, 60, 0.0, 60.0),
+    (3, 130, 70, 0.02, 40, 0.0, 60.0),
+    (2, 1000, 1024, 0.2, 20, 1e-5, 45.0),
+])
+def test_resident_forward_wide_column_marginals(B, M, N, tau, T, tol, b_range, monkeypatch):
+    """Column marginals b_j ~ exp(-b_range q_j) spread the dual potentials v
+    over tens of nats from the first iteration on (and push some column sums
+    under the exact-LSE floor); the resident forward against the oracle and
+    against the streaming sweeps."""
+    print(f"[sk_gpu] wide column marginals B={B} M={M} N={N} tau={tau} b_range={b_range}", flush=True)
+    rng = np.random.default_rng(M + N + int(1000 * tau))
+    C = rng.random((B, M, N)).astype(np.float32)
+    lb = -b_range * rng.random((B, N))
+    lgb = (lb - np.log(np.exp(lb).sum(1, keepdims=True))).astype(np.float32)
+    args = (_t(-C), tau, T, tol, None, _t(lgb))
+    res = _both_paths(monkeypatch, lambda: _ops.sinkhorn_dual_forward(*args))
+    for mode, (P, used, _) in res.items():
+        Po = osk.dual_forward(-C, tau, int(used), log_b=lgb).P
+        assert rel_err(P, Po) < FWD_TOL, mode
+    if int(res["1"][1]) == int(res["0"][1]):
+        assert rel_err(res["1"][0], res["0"][0].cpu().numpy()) < 1e-5
+    else:  # fp32 rounding at the stop threshold: one iteration apart at most
+        assert abs(int(res["1"][1]) - int(res["0"][1])) <= 1
+
+
 def _three_paths(monkeypatch, fn):
     """fn() on the persistent streaming kernels ("persistent", the register-
     resident tier switched off) and on the per-iteration sweeps ("sweeps")."""
