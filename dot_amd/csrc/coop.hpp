@@ -2,15 +2,18 @@
 // tagged words) kernels of both operators.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstdint>
 #include <cstdlib>
 
 namespace dot_amd {
 
-// Polls of one exchange word before a cooperative kernel gives up (~1-2 s).
-constexpr int kSpinLimit = 1 << 20;
+// Polls of one exchange word before a kernel of the exchange tiers gives up
+// (~2-4 s: long enough for work of other libraries that holds CUs to finish).
+constexpr int kSpinLimit = 1 << 22;
 
 // The poll limit passed to cooperative kernels: kSpinLimit, or the value of
 // DOT_AMD_SPIN_LIMIT when set.  A negative value makes every bounded wait
@@ -34,9 +37,83 @@ inline int pow2_ceil(int x) {
     return p;
 }
 
-// Launches `kernel` on G workgroups of `threads` threads only if all of them
-// can be resident at once (the exchange protocol spins on other workgroups);
-// false, with nothing launched, otherwise.
+// Launch of a resident-tier kernel.  Its workgroups wait on one another
+// (unless `independent`: one workgroup per batch element and no batch-global
+// test), so all G of them must be resident at once.  G never exceeds the
+// device's resident capacity for the kernel (the callers check occupancy), so
+// a plain launch has them all resident as soon as the CUs are free; a
+// cooperative launch adds a device-wide order among such launches and costs
+// ~18 us more per launch (two per Sinkhorn fwd+bwd step: 5 % of a C3 step).
+// The order that matters here -- two of this library's exchange kernels never
+// sharing the device, so neither holds CUs the other's missing workgroups
+// need -- is kept by resident_order: a launch on a stream other than the
+// previous launch's first waits for that launch.  Work of other libraries
+// that holds CUs (a communication kernel on a side stream) only delays the
+// missing workgroups; the waits are bounded (spin_limit) and a wait that gives
+// up is reported as an error, never as a result.  DOT_AMD_COOPERATIVE=1 asks
+// for cooperative launches instead (a device shared with long-running
+// kernels of other processes).
+inline bool cooperative_requested() {
+    const char* s = std::getenv("DOT_AMD_COOPERATIVE");
+    return s && s[0] == '1';
+}
+
+class ResidentOrder {
+  public:
+    // Plain launch of `kernel`, after the previous one of this device when that
+    // went to another stream.  The launch itself marks its completion on an
+    // event (hipExtLaunchKernel's stop event: no separate marker in the queue).
+    hipError_t launch(const void* kernel, int G, int threads, void** params, size_t lds, hipStream_t stream,
+                      bool cooperative = false) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+        while (flag_.test_and_set(std::memory_order_acquire)) {
+        }
+        Slot& s = slots_[dev];
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        // a capture cannot wait on (or record) work outside it
+        const bool capturing = hipStreamIsCapturing(stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone;
+        hipError_t e = hipSuccess;
+        if (!capturing && s.ev && s.last != stream) e = hipStreamWaitEvent(stream, s.ev, 0);
+        if (!capturing && !s.ev && hipEventCreateWithFlags(&s.ev, hipEventDefault) != hipSuccess) s.ev = nullptr;
+        if (e == hipSuccess && cooperative) {
+            e = hipLaunchCooperativeKernel(kernel, dim3(G), dim3(threads), params, static_cast<unsigned>(lds),
+                                           stream);
+            if (e == hipSuccess && !capturing && s.ev && hipEventRecord(s.ev, stream) == hipSuccess) s.last = stream;
+        } else if (e == hipSuccess) {
+            e = hipExtLaunchKernel(kernel, dim3(G), dim3(threads), params, lds, stream, nullptr,
+                                   capturing ? nullptr : s.ev, 0);
+            if (e == hipSuccess && !capturing && s.ev) s.last = stream;
+        }
+        flag_.clear(std::memory_order_release);
+        return e;
+    }
+
+  private:
+    static constexpr int kMaxDevices = 64;
+    struct Slot {
+        hipEvent_t ev = nullptr;  // completes with the device's last launch (never destroyed)
+        hipStream_t last = nullptr;
+    };
+    Slot slots_[kMaxDevices];
+    std::atomic_flag flag_ = ATOMIC_FLAG_INIT;
+};
+
+inline ResidentOrder& resident_order() {
+    static ResidentOrder* o = new ResidentOrder();  // never destroyed: its events outlive static teardown
+    return *o;
+}
+
+inline hipError_t launch_grid(const void* kernel, int G, int threads, void** params, size_t lds,
+                              hipStream_t stream, bool independent) {
+    if (independent) return hipLaunchKernel(kernel, dim3(G), dim3(threads), params, lds, stream);
+    return resident_order().launch(kernel, G, threads, params, lds, stream, cooperative_requested());
+}
+
+// Launch of a persistent-tier kernel (workgroups that wait on one another,
+// milliseconds long, so the ~18 us of a cooperative launch do not count):
+// only if all G workgroups can be resident at once (false, with nothing
+// launched, otherwise); cooperative, and ordered with the resident launches.
 template <class K, class A>
 bool launch_cooperative(K kernel, A& args, int G, int threads, size_t lds, hipStream_t stream) {
     int per_cu = 0;
@@ -44,18 +121,8 @@ bool launch_cooperative(K kernel, A& args, int G, int threads, size_t lds, hipSt
         per_cu < 1 || int64_t(per_cu) * device_cus() < G)
         return false;
     void* params[] = {&args};
-    return hipLaunchCooperativeKernel(reinterpret_cast<const void*>(kernel), dim3(G), dim3(threads), params,
-                                      static_cast<unsigned>(lds), stream) == hipSuccess;
-}
-
-// Launch of a resident-tier kernel: cooperative when its workgroups wait on
-// each other, so that all of them are resident even while other streams run;
-// a plain launch when none waits on another (one workgroup per batch element
-// and no batch-global test) — a cooperative launch costs ~17 us more.
-inline hipError_t launch_grid(const void* kernel, int G, int threads, void** params, size_t lds,
-                              hipStream_t stream, bool independent) {
-    if (independent) return hipLaunchKernel(kernel, dim3(G), dim3(threads), params, lds, stream);
-    return hipLaunchCooperativeKernel(kernel, dim3(G), dim3(threads), params, static_cast<unsigned>(lds), stream);
+    return resident_order().launch(reinterpret_cast<const void*>(kernel), G, threads, params, lds, stream,
+                                   true) == hipSuccess;
 }
 
 }  // namespace dot_amd

@@ -191,8 +191,14 @@ __global__ void fill_value(float* p, size_t n, float value) {
 
 void launch_fill_zero(void* p, size_t words, hipStream_t stream) {
     if (words == 0) return;
-    const unsigned blocks = unsigned(std::min<size_t>((words + kBlock - 1) / kBlock, 2048));
     ProfScope prof("dot_fill_zero", stream);
+    if (reinterpret_cast<uintptr_t>(p) % 16 == 0) {
+        const unsigned blocks = unsigned(std::min<size_t>((words / 4 + kBlock - 1) / kBlock + 1, 2048));
+        hipLaunchKernelGGL(sk::fill_zero16, dim3(blocks), dim3(kBlock), 0, stream, static_cast<uint32_t*>(p),
+                           words);
+        return;
+    }
+    const unsigned blocks = unsigned(std::min<size_t>((words + kBlock - 1) / kBlock, 2048));
     hipLaunchKernelGGL(sk::fill_zero, dim3(blocks), dim3(kBlock), 0, stream,
                        static_cast<uint32_t*>(p), words);
 }

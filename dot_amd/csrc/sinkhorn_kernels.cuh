@@ -302,6 +302,15 @@ static __global__ void fill_zero(uint32_t* p, size_t n) {
         p[i] = 0u;
 }
 
+// fill_zero for a 16-byte aligned p: 16-byte stores, then the last n % 4 words.
+static __global__ void fill_zero16(uint32_t* p, size_t n) {
+    const size_t stride = size_t(gridDim.x) * blockDim.x;
+    const size_t t = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    uint4* q = reinterpret_cast<uint4*>(p);
+    for (size_t i = t; i < n / 4; i += stride) q[i] = make_uint4(0u, 0u, 0u, 0u);
+    if (t < n % 4) p[n - n % 4 + t] = 0u;
+}
+
 // -------------------------------------------------------------------------
 // Upstream gradient of the plan: G = grad_plan + grad_cost[b] * C.
 // -------------------------------------------------------------------------
