@@ -71,29 +71,34 @@ __device__ __forceinline__ int xcc_id() {
 // `spin_limit` polls, or as soon as any workgroup has reported a timeout in
 // `status` (checked every 256 polls); `dead` then short-circuits every later
 // call of this lane, so a failure costs one bounded wait, not one per value.
-__device__ __forceinline__ void forced_timeout(int spin_limit, int* status, bool& dead) {
+//
+// `mark` is this call's failure mark: a wait that gives up raises the status
+// word to it (atomic max), and a status at or above it means this call has
+// failed.  A status word cleared for the call takes mark 1; one that persists
+// across calls takes marks that grow from call to call (the call epoch).
+__device__ __forceinline__ void forced_timeout(int spin_limit, int* status, bool& dead, int mark = 1) {
     // A negative limit (set by the host only to test the error path) makes
     // every bounded wait give up at once, without polling.
     if (spin_limit < 0 && !dead) {
-        atomicOr(status, 1);
+        atomicMax(status, mark);
         dead = true;
     }
 }
 
 __device__ __forceinline__ float collect(unsigned long long* p, unsigned t, int spin_limit,
-                                         int* status, bool& dead) {
-    forced_timeout(spin_limit, status, dead);
+                                         int* status, bool& dead, int mark = 1) {
+    forced_timeout(spin_limit, status, dead, mark);
     if (dead) return __builtin_nanf("");
     for (int spins = 0;; ++spins) {
         const unsigned long long x = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (static_cast<unsigned>(x >> 32) == t) return __uint_as_float(static_cast<unsigned>(x));
         if ((spins & 255) == 255 &&
-            __hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) {
+            __hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= mark) {
             dead = true;
             return __builtin_nanf("");
         }
         if (spins >= spin_limit) {
-            atomicOr(status, 1);
+            atomicMax(status, mark);
             dead = true;
             return __builtin_nanf("");
         }
@@ -101,8 +106,10 @@ __device__ __forceinline__ float collect(unsigned long long* p, unsigned t, int 
     }
 }
 
-// Tag of the XCD-id words; exchange tags are iteration numbers (>= 1) or 0 in
-// a cleared slot, so this one never matches them.
+// Tag of the XCD-id words in slots cleared for the call, whose exchange tags
+// are iteration numbers (>= 1), so this one never matches them.  Slots that
+// persist across calls carry (epoch << 16) | t, and (epoch << 16) | 0xffff for
+// the XCD ids (callers pass `tag`).
 constexpr unsigned kXccTag = 0xfffffffeu;
 
 // XCD check of a batch element, in two steps so that the round trip hides
@@ -112,8 +119,9 @@ constexpr unsigned kXccTag = 0xfffffffeu;
 // workgroup of the element has passed element_on_one_xcd (the sweep slot of
 // iteration parity 0 qualifies: iteration 2 is published only after every
 // workgroup has published iteration 1, which each does after the check).
-__device__ __forceinline__ void announce_xcc(unsigned long long* rows, size_t stride, int b, int W, int w) {
-    if (threadIdx.x == 0) publish(rows + (size_t(b) * W + w) * stride, __int_as_float(xcc_id()), kXccTag);
+__device__ __forceinline__ void announce_xcc(unsigned long long* rows, size_t stride, int b, int W, int w,
+                                             unsigned tag = kXccTag) {
+    if (threadIdx.x == 0) publish(rows + (size_t(b) * W + w) * stride, __int_as_float(xcc_id()), tag);
 }
 
 // True when the W workgroups of batch element b (this one is w) all run on
@@ -121,14 +129,15 @@ __device__ __forceinline__ void announce_xcc(unsigned long long* rows, size_t st
 // reads the element's W announced ids.  A timeout reads as "not one XCD" (and
 // sets `dead` as any poll does).  Contains barriers; every thread must call it.
 __device__ __forceinline__ bool element_on_one_xcd(unsigned long long* rows, size_t stride, int b, int W, int w,
-                                                   int spin_limit, int* status, bool& dead, float* scratch) {
+                                                   int spin_limit, int* status, bool& dead, float* scratch,
+                                                   unsigned tag = kXccTag, int mark = 1) {
     const int me = xcc_id();
     if (threadIdx.x < kWave) {
         const int g = threadIdx.x;
         int same = 1;
         if (g < W && g != w)
-            same = __float_as_int(collect(rows + (size_t(b) * W + g) * stride, kXccTag, spin_limit, status,
-                                          dead)) == me;
+            same = __float_as_int(collect(rows + (size_t(b) * W + g) * stride, tag, spin_limit, status,
+                                          dead, mark)) == me;
         const int all = __all(same);
         if (g == 0) scratch[0] = all ? 1.0f : 0.0f;
     }
@@ -142,10 +151,10 @@ __device__ __forceinline__ bool element_on_one_xcd(unsigned long long* rows, siz
 // round in flight at once; returns false after a timeout (values are then NaN).
 template <int VEC, int CH>
 __device__ __forceinline__ void collect_row(unsigned long long* row, unsigned t, int N, int spin_limit,
-                                            int* status, bool& dead, float (&out)[VEC * CH]) {
+                                            int* status, bool& dead, float (&out)[VEC * CH], int mark) {
     using R = Row<VEC, CH>;
     const int lane = threadIdx.x % kWave;
-    forced_timeout(spin_limit, status, dead);
+    forced_timeout(spin_limit, status, dead, mark);
     if (dead) {
 #pragma unroll
         for (int e = 0; e < R::PL; ++e) out[e] = __builtin_nanf("");
@@ -166,9 +175,9 @@ __device__ __forceinline__ void collect_row(unsigned long long* row, unsigned t,
         }
         if (ready) return;
         if (((spins & 255) == 255 &&
-             __hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) ||
+             __hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= mark) ||
             spins >= spin_limit) {
-            if (spins >= spin_limit) atomicOr(status, 1);
+            if (spins >= spin_limit) atomicMax(status, mark);
             dead = true;
 #pragma unroll
             for (int e = 0; e < R::PL; ++e) out[e] = __builtin_nanf("");
@@ -320,7 +329,7 @@ __device__ __forceinline__ void put(float (&v)[N], int q, float x) {
 template <int NQ, int MG = kMaxGroup, class F>
 __device__ __forceinline__ void exchange_columns(const float* part, unsigned long long* slot, int N,
                                                  int b, int W, int w, unsigned t, bool local, int spin_limit,
-                                                 int* status, bool& dead, F&& f) {
+                                                 int* status, bool& dead, int mark, F&& f) {
     static_assert(NQ >= 1 && NQ <= kColsPerThread, "rows of at most 1024 columns");
     static_assert(MG >= 1 && MG <= kMaxGroup, "at most kMaxGroup workgroups per element");
     float own[NQ];
@@ -337,7 +346,7 @@ __device__ __forceinline__ void exchange_columns(const float* part, unsigned lon
         }
     }
     unsigned long long* base = slot + size_t(b) * W * N;
-    forced_timeout(spin_limit, status, dead);
+    forced_timeout(spin_limit, status, dead, mark);
     // The guards below depend only on the thread and the element; computed
     // from these opaque copies they are rebuilt at each call instead of being
     // hoisted out of the caller's iteration loop and held in scalar registers
@@ -373,9 +382,9 @@ __device__ __forceinline__ void exchange_columns(const float* part, unsigned lon
             }
         if (ready) break;
         if (((spins & 255) == 255 &&
-             __hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) ||
+             __hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= mark) ||
             spins >= spin_limit) {
-            if (spins >= spin_limit) atomicOr(status, 1);
+            if (spins >= spin_limit) atomicMax(status, mark);
             dead = true;
             break;
         }
@@ -410,6 +419,9 @@ struct ImpResArgs {
     int* status;
     float inv_tau;
     int M, N, W, R, iters, spin_limit;
+    unsigned tag_base;         // exchange tags are tag_base | t (0: slots cleared for the call)
+    unsigned xcc_tag;          // tag of the XCD-id words
+    int mark;                  // failure mark in *status (forced_timeout)
 };
 
 // Upstream gradient of one row: G = grad_plan + grad_cost[b] * C, C = csign * scores.
@@ -461,7 +473,7 @@ __global__ __launch_bounds__(kThreads) void implicit_adjoint(ImpResArgs a) {
     const float gc = a.gC ? a.gC[b] : 0.0f;
     const float csign = cost_kind ? 1.0f : -1.0f;  // C = csign * scores
     bool dead = false;
-    announce_xcc(a.xchg, a.N, b, a.W, w);
+    announce_xcc(a.xchg, a.N, b, a.W, w, a.xcc_tag);
 
     // Prologue, streamed (one row at a time, nothing kept): row sums r and rs
     // of this lane's row slot and the workgroup's column partials of P G and P.
@@ -506,16 +518,18 @@ __global__ __launch_bounds__(kThreads) void implicit_adjoint(ImpResArgs a) {
     }
     const float inv_rs = 1.0f / fmaxf(rs_l, sk::kSumFloor);
     float c_own[kColRounds<PL>], cs_own[kColRounds<PL>];
-    const bool local = element_on_one_xcd(a.xchg, a.N, b, a.W, w, a.spin_limit, a.status, dead, scratch);
+    const bool local =
+        element_on_one_xcd(a.xchg, a.N, b, a.W, w, a.spin_limit, a.status, dead, scratch, a.xcc_tag, a.mark);
     R::store(part + wave * a.N, lane, a.N, cg);
     __syncthreads();
-    exchange_columns<kColRounds<PL>, MG>(part, a.pro, a.N, b, a.W, w, 1u, local, a.spin_limit, a.status, dead,
-                                     [&](int j, float tot) { put(c_own, (j - threadIdx.x) / kThreads, tot); });
+    exchange_columns<kColRounds<PL>, MG>(part, a.pro, a.N, b, a.W, w, a.tag_base | 1u, local, a.spin_limit,
+                                         a.status, dead, a.mark,
+                                         [&](int j, float tot) { put(c_own, (j - threadIdx.x) / kThreads, tot); });
     __syncthreads();
     R::store(part + wave * a.N, lane, a.N, cp);
     __syncthreads();
-    exchange_columns<kColRounds<PL>, MG>(part, a.pro + size_t(G) * a.N, a.N, b, a.W, w, 1u, local, a.spin_limit,
-                                     a.status, dead, [&](int j, float tot) {
+    exchange_columns<kColRounds<PL>, MG>(part, a.pro + size_t(G) * a.N, a.N, b, a.W, w, a.tag_base | 1u, local,
+                                         a.spin_limit, a.status, dead, a.mark, [&](int j, float tot) {
                                          put(cs_own, (j - threadIdx.x) / kThreads, fmaxf(tot, sk::kSumFloor));
                                      });
 
@@ -547,8 +561,9 @@ __global__ __launch_bounds__(kThreads) void implicit_adjoint(ImpResArgs a) {
         // the previous sweep.
         R::store(part + wave * a.N, lane, a.N, acc);
         __syncthreads();
-        exchange_columns<kColRounds<PL>, MG>(part, a.xchg + size_t(t & 1) * G * a.N, a.N, b, a.W, w, unsigned(t),
-                                         local, a.spin_limit, a.status, dead, [&](int j, float tot) {
+        exchange_columns<kColRounds<PL>, MG>(part, a.xchg + size_t(t & 1) * G * a.N, a.N, b, a.W, w,
+                                             a.tag_base | unsigned(t), local, a.spin_limit, a.status, dead,
+                                             a.mark, [&](int j, float tot) {
                                              const int q = (j - threadIdx.x) / kThreads;
                                              lds_mu[j] = (pick(c_own, q) - tot) / pick(cs_own, q);
                                          });
@@ -557,7 +572,7 @@ __global__ __launch_bounds__(kThreads) void implicit_adjoint(ImpResArgs a) {
     }
 
     // Final phase: stream G again and write this workgroup's gradient rows.
-    const bool failed = __hip_atomic_load(a.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
+    const bool failed = __hip_atomic_load(a.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= a.mark;
     float tacc = 0.0f;
 #pragma unroll
     for (int k = 0; k < RPW; ++k) {
@@ -617,8 +632,11 @@ struct FwdResArgs {
     unsigned long long* xchg;   // [2, G, N] tagged column partials
     unsigned long long* fxchg;  // [2, 2, G, N] tagged exact-fallback column max / sum
     unsigned long long* dxchg;  // [kDeltaSlots, G] tagged per-workgroup deltas
-    int* status;                // non-zero after a poll timeout
+    int* status;                // at least `mark` after a poll timeout of this call
     int B, M, N, W, R, spin_limit;
+    unsigned tag_base;          // exchange tags are tag_base | t (0: slots cleared for the call)
+    unsigned xcc_tag;           // tag of the XCD-id words
+    int mark;                   // failure mark in *status (forced_timeout)
 };
 
 // Waits for G tagged per-workgroup deltas of iteration t and returns their
@@ -632,7 +650,7 @@ __device__ __forceinline__ float global_delta(const FwdResArgs& a, int t, float*
         unsigned long long* ds = a.dxchg + size_t(t % kDeltaSlots) * G;
         float m = 0.0f;
         for (int g = lane; g < G; g += kWave) {
-            const float d = collect(ds + g, unsigned(t), a.spin_limit, a.status, dead);
+            const float d = collect(ds + g, a.tag_base | unsigned(t), a.spin_limit, a.status, dead, a.mark);
             m = (d != d) ? d : fmaxf(m, d);  // NaN (timeout) propagates
         }
         m = wave_reduce(m, OpMaxNan{});
@@ -688,7 +706,7 @@ __global__ __launch_bounds__(kThreads) void forward(FwdResArgs a) {
     const bool check = a.tol > 0.0f;
     // Padding (columns >= N, rows >= rend) holds the value whose K is -inf.
     const float pad = a.kscale > 0.0f ? -INFINITY : INFINITY;
-    announce_xcc(a.xchg, a.N, b, a.W, w);
+    announce_xcc(a.xchg, a.N, b, a.W, w, a.xcc_tag);
 
     float x[RPW][PL];
 #pragma unroll
@@ -728,7 +746,8 @@ __global__ __launch_bounds__(kThreads) void forward(FwdResArgs a) {
     float ks_it = a.kscale;
     float ks_next = (SCHED && a.max_iter > 0) ? a.kscale_t[0] : a.kscale;
     bool dead = false;
-    const bool local = element_on_one_xcd(a.xchg, a.N, b, a.W, w, a.spin_limit, a.status, dead, scratch);
+    const bool local =
+        element_on_one_xcd(a.xchg, a.N, b, a.W, w, a.spin_limit, a.status, dead, scratch, a.xcc_tag, a.mark);
     int used = a.max_iter;
     int conv = 0;
 
@@ -747,7 +766,7 @@ __global__ __launch_bounds__(kThreads) void forward(FwdResArgs a) {
             for (int q = 0; q < kDeltaPrefetch; ++q) {
                 const int g = lane + q * kWave;
                 dpre[q] = g < G ? __hip_atomic_load(ds + g, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                                : tag_pack(0.0f, unsigned(t - 1));
+                                : tag_pack(0.0f, a.tag_base | unsigned(t - 1));
             }
         }
         // Row update (kernels.cu:503-545) and the shared-exponential column sums,
@@ -826,11 +845,12 @@ __global__ __launch_bounds__(kThreads) void forward(FwdResArgs a) {
             float d = scratch[1];
 #pragma unroll
             for (int q = 1; q < kWaves; ++q) d = fmaxf(d, scratch[1 + q]);
-            publish(a.dxchg + size_t(t % kDeltaSlots) * G + gid, d, unsigned(t));
+            publish(a.dxchg + size_t(t % kDeltaSlots) * G + gid, d, a.tag_base | unsigned(t));
         }
         int low = 0;
         exchange_columns<kColRounds<PL>>(
-            part, a.xchg + size_t(cur) * G * a.N, a.N, b, a.W, w, unsigned(t), local, a.spin_limit, a.status, dead,
+            part, a.xchg + size_t(cur) * G * a.N, a.N, b, a.W, w, a.tag_base | unsigned(t), local, a.spin_limit,
+            a.status, dead, a.mark,
             [&](int j, float cs) {
                 if (cs >= sk::kColSumFloor && cs <= FLT_MAX) {
                     lds_v[cur * a.N + j] = lds_lb[j] + lds_v[prev * a.N + j] - logf(cs);
@@ -846,13 +866,14 @@ __global__ __launch_bounds__(kThreads) void forward(FwdResArgs a) {
                 const int g = lane + q * kWave;
                 if (g < G) {
                     float d = __uint_as_float(static_cast<unsigned>(dpre[q]));
-                    if (static_cast<unsigned>(dpre[q] >> 32) != unsigned(t - 1))
-                        d = collect(ds + g, unsigned(t - 1), a.spin_limit, a.status, dead);
+                    if (static_cast<unsigned>(dpre[q] >> 32) != (a.tag_base | unsigned(t - 1)))
+                        d = collect(ds + g, a.tag_base | unsigned(t - 1), a.spin_limit, a.status, dead, a.mark);
                     gmax = OpMaxNan{}(gmax, d);
                 }
             }
             for (int g = lane + kDeltaPrefetch * kWave; g < G; g += kWave)
-                gmax = OpMaxNan{}(gmax, collect(ds + g, unsigned(t - 1), a.spin_limit, a.status, dead));
+                gmax = OpMaxNan{}(gmax, collect(ds + g, a.tag_base | unsigned(t - 1), a.spin_limit, a.status,
+                                                dead, a.mark));
             gmax = wave_reduce(gmax, OpMaxNan{});
             if (lane == 0) scratch[0] = gmax;
         }
@@ -879,14 +900,14 @@ __global__ __launch_bounds__(kThreads) void forward(FwdResArgs a) {
 #pragma unroll
                     for (int q = 0; q < VEC; ++q) {
                         const int col = R::col(lane, k) + q;
-                        if (col < a.N) publish(mine + col, cm[k * VEC + q], unsigned(t), local);
+                        if (col < a.N) publish(mine + col, cm[k * VEC + q], a.tag_base | unsigned(t), local);
                     }
             }
             __syncthreads();
             for (int w2 = wave; w2 < a.W; w2 += kWaves) {
                 float got[PL];
-                collect_row<VEC, CH>(fslot + (size_t(b) * a.W + w2) * a.N, unsigned(t), a.N,
-                                     a.spin_limit, a.status, dead, got);
+                collect_row<VEC, CH>(fslot + (size_t(b) * a.W + w2) * a.N, a.tag_base | unsigned(t), a.N,
+                                     a.spin_limit, a.status, dead, got, a.mark);
                 R::store(part + w2 * a.N, lane, a.N, got);
             }
             __syncthreads();
@@ -918,14 +939,14 @@ __global__ __launch_bounds__(kThreads) void forward(FwdResArgs a) {
 #pragma unroll
                     for (int q = 0; q < VEC; ++q) {
                         const int col = R::col(lane, k) + q;
-                        if (col < a.N) publish(mine + col, sm[k * VEC + q], unsigned(t), local);
+                        if (col < a.N) publish(mine + col, sm[k * VEC + q], a.tag_base | unsigned(t), local);
                     }
             }
             __syncthreads();
             for (int w2 = wave; w2 < a.W; w2 += kWaves) {
                 float got[PL];
-                collect_row<VEC, CH>(sslot + (size_t(b) * a.W + w2) * a.N, unsigned(t), a.N,
-                                     a.spin_limit, a.status, dead, got);
+                collect_row<VEC, CH>(sslot + (size_t(b) * a.W + w2) * a.N, a.tag_base | unsigned(t), a.N,
+                                     a.spin_limit, a.status, dead, got, a.mark);
                 R::store(part + w2 * a.N, lane, a.N, got);
             }
             __syncthreads();
@@ -956,7 +977,7 @@ __global__ __launch_bounds__(kThreads) void forward(FwdResArgs a) {
     // P = safe_exp(K + u + v) (kernels.cu:755-775) and this workgroup's share of sum(P C).
     const int par = used & 1;
     __syncthreads();
-    const bool failed = __hip_atomic_load(a.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
+    const bool failed = __hip_atomic_load(a.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= a.mark;
     float vf[PL];
     R::load(lds_v + par * a.N, lane, a.N, vf, 0.0f);
     if (a.v_out && w == 0 && wave == 0) R::store(a.v_out + bN, lane, a.N, vf);

@@ -203,6 +203,39 @@ void launch_fill_zero(void* p, size_t words, hipStream_t stream) {
                        static_cast<uint32_t*>(p), words);
 }
 
+// Caller-owned exchange words of the register-resident kernels (the
+// `exchange` fields): word 0 is the status, whose failure mark is the call's
+// epoch; the tagged slots follow at kExchangeHead, tagged (epoch << 16) | t.
+// The slots of the forward ([2, G, N] column sums, [2, 2, G, N] exact-LSE
+// rows, [kDeltaSlots, G] deltas) are the larger set; the adjoint's ([2, G, N]
+// sweep sums, [2, G, N] prologue sums) fit in them.
+constexpr size_t kExchangeHead = 32;  // 256 bytes
+
+size_t exchange_groups_max() { return size_t(std::max(0, std::min(device_cus(), 1024))); }
+
+struct Tagging {
+    unsigned long long* slots;
+    int* status;
+    unsigned tag_base, xcc_tag;
+    int mark;
+    bool cleared_per_call;  // slots from the workspace: clear them before the launch
+};
+
+Tagging tagging(void* exchange, uint32_t epoch, int iters, unsigned long long* ws_slots, int* ws_status) {
+    if (exchange && iters <= DOT_SINKHORN_MAX_TAGGED_ITERS) {
+        const unsigned base = epoch << 16;
+        return {static_cast<unsigned long long*>(exchange) + kExchangeHead, static_cast<int*>(exchange), base,
+                base | 0xffffu, int(epoch), false};
+    }
+    return {ws_slots, ws_status, 0u, res::kXccTag, 1, true};
+}
+
+int check_exchange(const void* exchange, uint32_t epoch) {
+    if (exchange && (epoch == 0 || epoch > DOT_SINKHORN_MAX_EPOCH))
+        return fail(DOT_ERR_INVALID_ARG, "exchange_epoch must be in 1..DOT_SINKHORN_MAX_EPOCH");
+    return DOT_OK;
+}
+
 int check_shape(int B, int M, int N) {
     if (B < 0 || M < 0 || N < 0) return fail(DOT_ERR_INVALID_ARG, "B, M and N must be >= 0");
     return DOT_OK;
@@ -400,10 +433,14 @@ bool launch_resident_forward(const dot_sinkhorn_fwd_args* a, const FwdLayout& L,
     r.iters_used = a->iters_used;
     r.converged = a->converged;
     // The exchange regions are laid out for L.groups workgroups; index them by the real grid.
-    r.xchg = L.xchg;
-    r.fxchg = L.xchg + 2 * size_t(groups) * a->N;
+    const Tagging tg = tagging(a->exchange, a->exchange_epoch, a->max_iter, L.xchg, L.status);
+    r.xchg = tg.slots;
+    r.fxchg = tg.slots + 2 * size_t(groups) * a->N;
     r.dxchg = r.fxchg + 4 * size_t(groups) * a->N;
-    r.status = L.status;
+    r.status = tg.status;
+    r.tag_base = tg.tag_base;
+    r.xcc_tag = tg.xcc_tag;
+    r.mark = tg.mark;
     r.B = a->B;
     r.M = a->M;
     r.N = a->N;
@@ -422,7 +459,7 @@ bool launch_resident_forward(const dot_sinkhorn_fwd_args* a, const FwdLayout& L,
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, res::kThreads, lds) != hipSuccess ||
             per_cu < 1 || int64_t(per_cu) * device_cus() < groups)
             return;
-        launch_fill_zero(L.xchg, L.res_words, stream);
+        if (tg.cleared_per_call) launch_fill_zero(L.xchg, L.res_words, stream);
         void* params[] = {&r};
         ProfScope prof("sk_fwd_resident", stream);
         // one workgroup per element exchanges only with itself; the stop test
@@ -552,6 +589,11 @@ extern "C" size_t dot_sinkhorn_forward_workspace_bytes(int B, int M, int N, int 
     return fwd_layout(nullptr, B, M, N, max_iter).bytes;
 }
 
+extern "C" size_t dot_sinkhorn_exchange_bytes(void) {
+    const size_t G = exchange_groups_max();
+    return (kExchangeHead + 6 * G * 1024 + res::kDeltaSlots * G) * sizeof(unsigned long long);
+}
+
 extern "C" int dot_sinkhorn_forward(const dot_sinkhorn_fwd_args* a, dot_stream_t stream_) {
     return dot_amd::sinkhorn_forward_scheduled(a, nullptr, nullptr, reinterpret_cast<hipStream_t>(stream_));
 }
@@ -568,6 +610,7 @@ int dot_amd::sinkhorn_forward_scheduled(const dot_sinkhorn_fwd_args* a, const fl
         return fail(DOT_ERR_INVALID_ARG, "scores_kind must be DOT_SCORES_LOG_ALPHA or DOT_SCORES_COST");
     if (!a->iters_used || !a->converged)
         return fail(DOT_ERR_INVALID_ARG, "iters_used and converged must be device pointers");
+    if (int rc = check_exchange(a->exchange, a->exchange_epoch)) return rc;
     const bool keep = (a->flags & DOT_SK_KEEP_HISTORY) != 0;
     const bool ret_log = (a->flags & DOT_SK_RETURN_LOG) != 0;
     if (a->flags & ~(DOT_SK_KEEP_HISTORY | DOT_SK_RETURN_LOG))
@@ -723,7 +766,7 @@ int check_bwd(const dot_sinkhorn_bwd_args* a) {
     if (elems > 0 && (!a->scores || !a->plan || !a->grad_scores))
         return fail(DOT_ERR_INVALID_ARG, "scores, plan and grad_scores must be non-NULL");
     if (a->B > 0 && !a->grad_tau) return fail(DOT_ERR_INVALID_ARG, "grad_tau must be non-NULL");
-    return DOT_OK;
+    return check_exchange(a->exchange, a->exchange_epoch);
 }
 
 bool bwd_vec4(const dot_sinkhorn_bwd_args* a) {
@@ -764,11 +807,15 @@ bool launch_resident_adjoint(const dot_sinkhorn_bwd_args* a, const ImpLayout& L,
     r.gP = a->grad_plan;
     r.gC = a->grad_cost;
     r.P = a->plan;
-    r.xchg = L.xchg;
-    r.pro = L.xchg + 2 * size_t(groups) * a->N;
+    const Tagging tg = tagging(a->exchange, a->exchange_epoch, a->iters, L.xchg, L.status);
+    r.xchg = tg.slots;
+    r.pro = tg.slots + 2 * size_t(groups) * a->N;
     r.grad = a->grad_scores;
     r.tau_partial = L.tau_partial;
-    r.status = L.status;
+    r.status = tg.status;
+    r.tag_base = tg.tag_base;
+    r.xcc_tag = tg.xcc_tag;
+    r.mark = tg.mark;
     r.inv_tau = inv_tau;
     r.M = a->M;
     r.N = a->N;
@@ -788,7 +835,7 @@ bool launch_resident_adjoint(const dot_sinkhorn_bwd_args* a, const ImpLayout& L,
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, res::kThreads, lds) != hipSuccess ||
             per_cu < 1 || int64_t(per_cu) * device_cus() < groups)
             return;
-        launch_fill_zero(L.xchg, L.xchg_words, stream);
+        if (tg.cleared_per_call) launch_fill_zero(L.xchg, L.xchg_words, stream);
         void* params[] = {&r};
         ProfScope prof("sk_imp_resident", stream);
         // the adjoint's exchanges stay within a batch element's W workgroups
@@ -798,7 +845,7 @@ bool launch_resident_adjoint(const dot_sinkhorn_bwd_args* a, const ImpLayout& L,
     if (!ok) return false;
     ProfScope prof("sk_batch_sum", stream);
     hipLaunchKernelGGL(sk::batch_sum, dim3(a->B), dim3(kWave), 0, stream, L.tau_partial, rc.W,
-                       -inv_tau, a->grad_tau, L.status, a->status);
+                       -inv_tau, a->grad_tau, tg.status, a->status, tg.mark);
     return true;
 }
 

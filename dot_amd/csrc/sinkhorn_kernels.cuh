@@ -286,14 +286,16 @@ __global__ __launch_bounds__(kBlock) void materialize(MaterializeArgs a) {
 // When status_out is given, block 0 also writes the preceding cooperative
 // kernel's status word there (0 when status_in is null): it runs after that
 // kernel on the stream, so the word is final.
+// status_out (block 0): 1 when *status_in has reached `mark` (the call's
+// failure mark, 1 for a status word cleared for the call), else 0.
 static __global__ void batch_sum(const float* partial, int nblk, float scale, float* out,
-                                 const int* status_in = nullptr, int32_t* status_out = nullptr) {
+                                 const int* status_in = nullptr, int32_t* status_out = nullptr, int mark = 1) {
     const int b = blockIdx.x;
     float s = 0.0f;
     for (int k = threadIdx.x; k < nblk; k += kWave) s += partial[size_t(b) * nblk + k];
     s = wave_sum(s);
     if (threadIdx.x == 0) out[b] = s * scale;
-    if (status_out && b == 0 && threadIdx.x == 0) *status_out = status_in ? (*status_in != 0) : 0;
+    if (status_out && b == 0 && threadIdx.x == 0) *status_out = status_in ? (*status_in >= mark) : 0;
 }
 
 static __global__ void fill_zero(uint32_t* p, size_t n) {

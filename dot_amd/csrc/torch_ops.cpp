@@ -49,32 +49,41 @@ Tensor workspace(size_t bytes, const Tensor& like) {
                      like.options().dtype(at::kByte));
 }
 
-// Exchange words of the one-pass bidirectional-softmax kernels, one set per
-// (device, stream): calls on one stream run in order, so no two kernels use a
-// set at once, and the growing epoch keeps a call from reading words an
-// earlier call left.  Cleared once (and again when the epoch would pass its
-// limit); held until the process ends (the map is never destroyed, so no
-// device memory is freed during interpreter teardown).
+// Exchange words of the kernels whose workgroups exchange tagged words (the
+// one-pass bidirectional softmax, the register-resident Sinkhorn tier), one
+// set per operator and (device, stream): calls on one stream run in order, so
+// no two kernels use a set at once, and the growing epoch keeps a call from
+// reading words an earlier call left.  Cleared once (and again when the epoch
+// would pass its limit); held until the process ends (the map is never
+// destroyed, so no device memory is freed during interpreter teardown).
 struct ExchangeSet {
     Tensor words;
     uint32_t epoch = 0;
 };
 
-std::pair<void*, uint32_t> bidi_exchange(const Tensor& like) {
+template <size_t (*Bytes)(), uint32_t MaxEpoch>
+std::pair<void*, uint32_t> stream_exchange(const Tensor& like) {
     static std::mutex mu;
     static auto* sets = new std::map<std::pair<int, void*>, ExchangeSet>();
     const int dev = like.device().index();
     void* stream = c10::hip::getCurrentHIPStream(dev).stream();
     std::lock_guard<std::mutex> lock(mu);
     ExchangeSet& x = (*sets)[{dev, stream}];
-    if (!x.words.defined() || x.epoch >= DOT_BIDISOFTMAX_MAX_EPOCH) {
+    if (!x.words.defined() || x.epoch >= MaxEpoch) {
         if (!x.words.defined())
-            x.words = at::empty({static_cast<int64_t>(dot_bidisoftmax_exchange_bytes())},
-                                like.options().dtype(at::kByte));
+            x.words = at::empty({static_cast<int64_t>(Bytes())}, like.options().dtype(at::kByte));
         x.words.zero_();  // on the current stream, ahead of the kernel
         x.epoch = 0;
     }
     return {x.words.data_ptr(), ++x.epoch};
+}
+
+std::pair<void*, uint32_t> bidi_exchange(const Tensor& like) {
+    return stream_exchange<dot_bidisoftmax_exchange_bytes, DOT_BIDISOFTMAX_MAX_EPOCH>(like);
+}
+
+std::pair<void*, uint32_t> sinkhorn_exchange(const Tensor& like) {
+    return stream_exchange<dot_sinkhorn_exchange_bytes, DOT_SINKHORN_MAX_EPOCH>(like);
 }
 
 const float* ptr_or_null(const optional<Tensor>& t) {
@@ -138,6 +147,7 @@ ForwardOut run_forward(const Tensor& scores_f, int kind, double tau, int64_t n_i
     a.converged = o.counts.data_ptr<int32_t>() + 1;
     a.workspace = ws.data_ptr();
     a.workspace_bytes = ws_bytes;
+    std::tie(a.exchange, a.exchange_epoch) = sinkhorn_exchange(scores_f);
     check_rc(dot_sinkhorn_forward(&a, current_stream(scores_f)), "dot_sinkhorn_forward");
     return o;
 }
@@ -235,6 +245,7 @@ ForwardOut run_forward_method(const Tensor& scores_f, int kind, double tau, int6
     a.converged = o.counts.data_ptr<int32_t>() + 1;
     a.workspace = ws.data_ptr();
     a.workspace_bytes = ws_bytes;
+    std::tie(a.exchange, a.exchange_epoch) = sinkhorn_exchange(scores_f);
     m.method = int(mp.method);
     m.omega = static_cast<float>(mp.omega);
     m.anderson_k = int(std::min<int64_t>(mp.anderson_k, INT32_MAX));
@@ -338,6 +349,7 @@ std::vector<Tensor> run_backward(bool implicit, const Tensor& scores_f, int kind
     a.workspace = ws.data_ptr();
     a.workspace_bytes = ws_bytes;
     a.status = status.data_ptr<int32_t>();
+    std::tie(a.exchange, a.exchange_epoch) = sinkhorn_exchange(scores_f);
     const dot_stream_t s = current_stream(scores_f);
     if (implicit) check_rc(dot_sinkhorn_backward_implicit(&a, s), "dot_sinkhorn_backward_implicit");
     else check_rc(dot_sinkhorn_backward_unrolled(&a, s), "dot_sinkhorn_backward_unrolled");

@@ -68,6 +68,16 @@ typedef struct {
     int32_t* converged;    /* device int32 out: 1 if the tol test fired */
     void* workspace;
     size_t workspace_bytes;
+    /* Optional exchange words of the register-resident kernels (see
+     * dot_sinkhorn_exchange_bytes): NULL, and the library takes them from the
+     * workspace and clears them with one more small kernel per call; or
+     * caller-owned device memory of dot_sinkhorn_exchange_bytes() bytes,
+     * zeroed once, used by calls on one stream only, with exchange_epoch
+     * 1, 2, ... (at most DOT_SINKHORN_MAX_EPOCH) growing by one per call
+     * (forward and backward calls share one sequence); zero the words again
+     * before the sequence restarts at 1.  No counterpart in the reference. */
+    void* exchange;
+    uint32_t exchange_epoch;
 } dot_sinkhorn_fwd_args;
 
 /* Dual log-domain Sinkhorn: u_i = log a_i - LSE_j(K_ij + v_j), then
@@ -178,6 +188,8 @@ typedef struct {
                                  memory the device can reach), or NULL: 0 when the call's
                                  kernels finish normally, 1 when a cross-workgroup exchange
                                  timed out (the gradients are then NaN) */
+    void* exchange;           /* optional exchange words, as in dot_sinkhorn_fwd_args */
+    uint32_t exchange_epoch;
 } dot_sinkhorn_bwd_args;
 
 /* Implicit-function adjoint: exactly `iters` Gauss-Seidel sweeps
@@ -294,6 +306,15 @@ int dot_bidisoftmax_backward(const dot_bidisoftmax_bwd_args* args, dot_stream_t 
  * the largest call epoch they take.  No counterpart in the reference. */
 #define DOT_BIDISOFTMAX_MAX_EPOCH 1048575u
 size_t dot_bidisoftmax_exchange_bytes(void);
+
+/* Size of the caller-owned exchange words of the Sinkhorn calls (the
+ * `exchange` fields of dot_sinkhorn_fwd_args and dot_sinkhorn_bwd_args) for
+ * the current device, and the largest call epoch they take.  Calls whose
+ * iteration count (max_iter, iters) exceeds DOT_SINKHORN_MAX_TAGGED_ITERS use
+ * the workspace instead.  No counterpart in the reference. */
+#define DOT_SINKHORN_MAX_EPOCH 65534u
+#define DOT_SINKHORN_MAX_TAGGED_ITERS 65533
+size_t dot_sinkhorn_exchange_bytes(void);
 
 /* ---------------------------------------------------------------------- */
 /* Diagnostics (no counterpart in the reference)                           */

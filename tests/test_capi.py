@@ -36,7 +36,8 @@ class FwdArgs(ctypes.Structure):
                 ("plan", ctypes.c_void_p), ("cost", ctypes.c_void_p), ("u_out", ctypes.c_void_p),
                 ("v_out", ctypes.c_void_p), ("u_hist", ctypes.c_void_p), ("v_hist", ctypes.c_void_p),
                 ("iters_used", ctypes.c_void_p), ("converged", ctypes.c_void_p),
-                ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t)]
+                ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t),
+                ("exchange", ctypes.c_void_p), ("exchange_epoch", ctypes.c_uint32)]
 
 
 def test_header_declares_the_expected_entry_points():

@@ -8,13 +8,16 @@ n_iters_used with tol = 0: fp32 and float64 can cross the tolerance one
 iteration apart.
 """
 
+import ctypes
+import os
+
 import numpy as np
 import pytest
 import torch
 
 import dot_amd
 from dot_amd import _ops
-from conftest import load_golden, rel_err, sum_err
+from conftest import ROOT, load_golden, rel_err, sum_err
 from oracle import sinkhorn as osk
 
 pytestmark = pytest.mark.gpu
@@ -677,6 +680,83 @@ def test_resident_forward_wide_column_marginals(B, M, N, tau, T, tol, b_range, m
         assert rel_err(res["1"][0], res["0"][0].cpu().numpy()) < 1e-5
     else:  # fp32 rounding at the stop threshold: one iteration apart at most
         assert abs(int(res["1"][1]) - int(res["0"][1])) <= 1
+
+
+class SkFwdArgs(ctypes.Structure):
+    _fields_ = [("scores", ctypes.c_void_p), ("log_a", ctypes.c_void_p), ("log_b", ctypes.c_void_p),
+                ("B", ctypes.c_int), ("M", ctypes.c_int), ("N", ctypes.c_int),
+                ("scores_kind", ctypes.c_int), ("tau", ctypes.c_float), ("max_iter", ctypes.c_int),
+                ("tol", ctypes.c_float), ("flags", ctypes.c_int),
+                ("plan", ctypes.c_void_p), ("cost", ctypes.c_void_p), ("u_out", ctypes.c_void_p),
+                ("v_out", ctypes.c_void_p), ("u_hist", ctypes.c_void_p), ("v_hist", ctypes.c_void_p),
+                ("iters_used", ctypes.c_void_p), ("converged", ctypes.c_void_p),
+                ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t),
+                ("exchange", ctypes.c_void_p), ("exchange_epoch", ctypes.c_uint32)]
+
+
+class SkBwdArgs(ctypes.Structure):
+    _fields_ = [("scores", ctypes.c_void_p), ("scores_kind", ctypes.c_int), ("plan", ctypes.c_void_p),
+                ("grad_plan", ctypes.c_void_p), ("grad_cost", ctypes.c_void_p),
+                ("B", ctypes.c_int), ("M", ctypes.c_int), ("N", ctypes.c_int), ("tau", ctypes.c_float),
+                ("iters", ctypes.c_int), ("u_hist", ctypes.c_void_p), ("v_hist", ctypes.c_void_p),
+                ("grad_scores", ctypes.c_void_p), ("grad_tau", ctypes.c_void_p),
+                ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t),
+                ("status", ctypes.c_void_p), ("exchange", ctypes.c_void_p), ("exchange_epoch", ctypes.c_uint32)]
+
+
+@pytest.mark.parametrize("B,M,N,tau,T,tol", [(16, 512, 512, 0.1, 200, 1e-6), (6, 200, 136, 0.25, 30, 0.0),
+                                            (8, 64, 64, 1.0, 40, 1e-6)])
+def test_capi_exchange_words_match_the_workspace_path(B, M, N, tau, T, tol):
+    """Through the C ABI: the register-resident forward and adjoint with
+    caller-owned exchange words (epoch-tagged, never cleared by the library)
+    give the bits of the workspace path (slots cleared per call), call after
+    call; an epoch of 0 or above DOT_SINKHORN_MAX_EPOCH is rejected."""
+    print(f"[sk_gpu] C ABI exchange words B={B} M={M} N={N} tol={tol}", flush=True)
+    lib = ctypes.CDLL(os.path.join(ROOT, "dot_amd", "libdot_amd.so"))
+    for f in ("dot_sinkhorn_exchange_bytes", "dot_sinkhorn_forward_workspace_bytes",
+              "dot_sinkhorn_backward_implicit_workspace_bytes"):
+        getattr(lib, f).restype = ctypes.c_size_t
+    lib.dot_sinkhorn_forward.argtypes = [ctypes.POINTER(SkFwdArgs), ctypes.c_void_p]
+    lib.dot_sinkhorn_backward_implicit.argtypes = [ctypes.POINTER(SkBwdArgs), ctypes.c_void_p]
+    rng = np.random.default_rng(B + M + N)
+    C = _t(rng.random((B, M, N)).astype(np.float32))
+    G = _t(rng.standard_normal((B, M, N)).astype(np.float32))
+    gc = _t(rng.random(B).astype(np.float32))
+    ws = torch.empty(max(lib.dot_sinkhorn_forward_workspace_bytes(B, M, N, T, 0),
+                         lib.dot_sinkhorn_backward_implicit_workspace_bytes(B, M, N)), dtype=torch.uint8, device=DEV)
+    xw = torch.zeros(lib.dot_sinkhorn_exchange_bytes(), dtype=torch.uint8, device=DEV)
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def run(exchange, epoch):
+        P = torch.empty_like(C)
+        cost = torch.empty(B, device=DEV)
+        counts = torch.zeros(2, dtype=torch.int32, device=DEV)
+        f = SkFwdArgs(C.data_ptr(), None, None, B, M, N, -1, tau, T, tol, 0, P.data_ptr(), cost.data_ptr(),
+                      None, None, None, None, counts.data_ptr(), counts.data_ptr() + 4, ws.data_ptr(), ws.numel(),
+                      exchange, epoch)
+        assert lib.dot_sinkhorn_forward(ctypes.byref(f), stream) == 0
+        grad = torch.empty_like(C)
+        gtau = torch.empty(B, device=DEV)
+        status = torch.full((1,), 7, dtype=torch.int32, device=DEV)
+        b = SkBwdArgs(C.data_ptr(), -1, P.data_ptr(), G.data_ptr(), gc.data_ptr(), B, M, N, tau, T, None, None,
+                      grad.data_ptr(), gtau.data_ptr(), ws.data_ptr(), ws.numel(), status.data_ptr(), exchange,
+                      epoch + 1 if exchange else 0)
+        assert lib.dot_sinkhorn_backward_implicit(ctypes.byref(b), stream) == 0
+        torch.cuda.synchronize()
+        return P, cost, counts, grad, gtau, status
+
+    ref = run(None, 0)
+    assert int(ref[5]) == 0
+    for epoch in (1, 3, 5):
+        out = run(xw.data_ptr(), epoch)
+        for a, e in zip(out, ref):
+            assert torch.equal(a, e), epoch
+    P = torch.empty_like(C)
+    counts = torch.zeros(2, dtype=torch.int32, device=DEV)
+    for bad in (0, 65535):
+        f = SkFwdArgs(C.data_ptr(), None, None, B, M, N, -1, tau, T, tol, 0, P.data_ptr(), None, None, None, None,
+                      None, counts.data_ptr(), counts.data_ptr() + 4, ws.data_ptr(), ws.numel(), xw.data_ptr(), bad)
+        assert lib.dot_sinkhorn_forward(ctypes.byref(f), stream) == 1
 
 
 def test_resident_launches_on_two_streams():
