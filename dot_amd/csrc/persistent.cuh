@@ -266,6 +266,7 @@ struct FwdArgs {
     unsigned long long* dxchg;  // [kDeltaSlots, G] tagged per-workgroup deltas
     int* status;
     int B, M, N, W, R, spin_limit;
+    float* ebuf;                // [B,M,N] scaled kernel (scaling domain), or null
 };
 
 // Dual Sinkhorn forward (torch_cuda.cpp:147-264), streaming each workgroup's
@@ -275,6 +276,22 @@ struct FwdArgs {
 // max-shifted LSE of column j over all M rows when colsum underflows,
 // kernels.cu:629-671), all-gather of v.  The batch-global stop test of
 // iteration t-1 is read during iteration t, as in res::forward.
+//
+// Scaling domain (ebuf set, one K scale for every iteration): the workgroup
+// first writes E_ij = 2^(x_ij kscale log2(e) - mx_i) for its rows (mx_i: the
+// row's maximum) and then streams E instead of the scores: with V_j =
+// 2^(v_j log2(e) - mv) (mv: the maximum over columns), s_i = sum_j E_ij V_j,
+// u_i = log a_i - ln2 (mx_i + mv + log2 s_i), and the column sums are
+// V_j sum_i E_ij a_i / s_i -- the sums of exp(K + u + v) the log-domain update
+// forms, at two FMAs per element instead of an exponential and a maximum.  The
+// largest term of a row is at least 2^-(max_j v - min_j v) log2(e), so while
+// that range is within kScalingRange every kept term is exact to float
+// precision; past it the workgroup streams the scores in the log domain for
+// the remaining iterations.  The exact column LSE and the plan read the scores.
+// Rows of 64 floats per lane (N > 2048), which are processed one at a time,
+// gain (C5: 42.5 -> 40.6 us per iteration).
+constexpr float kScalingRange = 64.0f;  // log2 units
+
 template <int VEC, int CH, bool SCHED = false>
 __global__ __launch_bounds__(kThreads) void forward(FwdArgs a) {
     using R = Row<VEC, CH>;
@@ -289,7 +306,8 @@ __global__ __launch_bounds__(kThreads) void forward(FwdArgs a) {
     float* red = lds_lb + a.N;
     float* lds_u = red + ((a.N + a.W + 3) & ~3);
     float* lds_la = lds_u + 2 * a.R;
-    float* scratch = lds_la + a.R;  // [0] global delta, [1..kWaves] wave deltas, [16..] reductions
+    float* lds_mx = lds_la + a.R;  // scaling domain: row maxima of x kscale log2(e)
+    float* scratch = lds_mx + a.R;  // [0] global delta, [1..kWaves] wave deltas, [16..] reductions
     const int lane = threadIdx.x % kWave;
     const int wave = threadIdx.x / kWave;
     const int G = gridDim.x;
@@ -314,10 +332,34 @@ __global__ __launch_bounds__(kThreads) void forward(FwdArgs a) {
         lds_u[l] = 0.0f;
         lds_u[a.R + l] = 0.0f;
     }
+    // (rows of 64 floats per lane only: the pipelined rows of up to 32 floats
+    // hide their arithmetic under the stream already -- C4 lost 1 us per
+    // iteration to the scaling domain's per-iteration range reduction)
+    bool scal = !SCHED && PL > 32 && a.ebuf != nullptr;
+    float mv = 0.0f;  // scaling domain: lds_v2 holds V = 2^(v log2(e) - mv)
     for (int j = threadIdx.x; j < a.N; j += kThreads) {
         lds_lb[j] = a.log_b ? a.log_b[bN + j] : a.log_b_default;
         lds_v[j] = 0.0f;
-        lds_v2[j] = 0.0f;
+        lds_v2[j] = scal ? 1.0f : 0.0f;
+    }
+    if (scal) {
+        // E rows of this workgroup, each written and later read by the same wave
+        for (int l = wave; l < rend - row0; l += kWaves) {
+            const int ln = opaque_lane();
+            float x[PL];
+            R::load(a.X + (bM + row0 + l) * a.N, ln, a.N, x, 0.0f);
+            float ml = -FLT_MAX;
+#pragma unroll
+            for (int e = 0; e < PL; ++e) {
+                x[e] = R::valid(ln, e, a.N) ? x[e] * kscale2 : -INFINITY;
+                ml = fmaxf(ml, x[e]);
+            }
+            const float m = wave_max(ml);
+#pragma unroll
+            for (int e = 0; e < PL; ++e) x[e] = __builtin_amdgcn_exp2f(x[e] - m);  // 0 for -inf
+            R::store(a.ebuf + (bM + row0 + l) * a.N, ln, a.N, x);
+            if (ln == 0) lds_mx[l] = m;
+        }
     }
     __syncthreads();
     bool dead = false;
@@ -392,7 +434,59 @@ __global__ __launch_bounds__(kThreads) void forward(FwdArgs a) {
                 if (a.u_hist) a.u_hist[(size_t(t - 1) * a.B + b) * a.M + i] = u;
             }
         };
-        if constexpr (PL <= 32) {
+        // scaling domain: the E row, s = sum E V, and the column partials sum E a / s
+        auto load_row_e = [&](int l, RowBuf<R>& buf) {
+            R::load_clamped(a.ebuf + (bM + row0 + l) * a.N, opaque_lane(), a.N, buf.v, 0.0f);
+        };
+        auto row_e = [&](int l, RowBuf<R>& buf) {
+            const int i = row0 + l;
+            const int ln = opaque_lane();
+            float(&ev)[PL] = buf.v;
+            float sl = 0.0f;
+#pragma unroll
+            for (int k = 0; k < CH; ++k) {
+                float vv[VEC];
+                v2.chunk(ln, k, a.N, vv);  // V, 0 past N
+#pragma unroll
+                for (int q = 0; q < VEC; ++q) sl = fmaf(ev[k * VEC + q], vv[q], sl);
+            }
+            const float s_sum = wave_sum(sl);
+            const float s = s_sum > 0.0f ? s_sum : sk::kSumFloor;  // 0: a row with no finite K
+            const float lga = lds_la[l];
+            const float lg2 = __builtin_amdgcn_logf(s);
+            const float u = lga - kLn2 * ((lds_mx[l] + mv) + lg2);
+            const float wgt = __builtin_amdgcn_exp2f(fmaf(lga, kLog2E, -lg2));
+#pragma unroll
+            for (int e = 0; e < PL; ++e) acc[e] = fmaf(ev[e], wgt, acc[e]);
+#pragma unroll
+            for (int e = 0; e < PL; ++e) asm volatile("" : "+v"(acc[e]));  // keep the update here
+            dmax = fmaxf(dmax, fabsf(u - lds_u[prev * a.R + l]));
+            if (lane == 0) {
+                lds_u[cur * a.R + l] = u;
+                publish(a.uslot + size_t(cur) * a.B * a.M + bM + i, u, unsigned(t), local);
+                if (a.u_hist) a.u_hist[(size_t(t - 1) * a.B + b) * a.M + i] = u;
+            }
+        };
+        if (scal) {
+            if constexpr (PL <= 32) {
+                pipelined_rows<RowBuf<R>>(wave, rend - row0, kWaves, load_row_e, row_e);
+            } else {
+                for (int l = wave; l < rend - row0; l += kWaves) {
+                    RowBuf<R> buf;
+                    load_row_e(l, buf);
+                    row_e(l, buf);
+                }
+            }
+            // times V: the partials of exp(K + u + v) that the log-domain rows form
+            const int ln = opaque_lane();
+#pragma unroll
+            for (int k = 0; k < CH; ++k) {
+                float vv[VEC];
+                v2.chunk(ln, k, a.N, vv);
+#pragma unroll
+                for (int q = 0; q < VEC; ++q) acc[k * VEC + q] *= vv[q];
+            }
+        } else if constexpr (PL <= 32) {
             pipelined_rows<RowBuf<R>>(wave, rend - row0, kWaves, load_row, row);
         } else {  // 64-float rows: a second buffer would spill
             for (int l = wave; l < rend - row0; l += kWaves) {
@@ -439,7 +533,20 @@ __global__ __launch_bounds__(kThreads) void forward(FwdArgs a) {
                      });
         __syncthreads();  // the owners have read lds_v (v_{t-1}); it now receives v_t
         gather(res_row, a.N, unsigned(t), lds_v, a.spin_limit, a.status, dead);
-        for (int j = threadIdx.x; j < a.N; j += kThreads) lds_v2[j] = lds_v[j] * kLog2E;  // own writes
+        if (scal) {  // stays in the scaling domain while max v - min v (log2) is within range
+            float hi = -FLT_MAX, nlo = -FLT_MAX;
+            for (int j = threadIdx.x; j < a.N; j += kThreads) {  // own writes
+                const float q = lds_v[j] * kLog2E;
+                hi = fmaxf(hi, q);
+                nlo = fmaxf(nlo, -q);
+            }
+            hi = block_reduce<kWaves>(wave_max(hi), scratch + 16, OpMax{});
+            nlo = block_reduce<kWaves>(wave_max(nlo), scratch + 16, OpMax{});
+            scal = hi + nlo <= kScalingRange;  // false for NaN
+            mv = hi;
+        }
+        for (int j = threadIdx.x; j < a.N; j += kThreads)  // own writes
+            lds_v2[j] = scal ? __builtin_amdgcn_exp2f(fmaf(lds_v[j], kLog2E, -mv)) : lds_v[j] * kLog2E;
         if (test && wave == 0) {
             float gmax = 0.0f;
 #pragma unroll

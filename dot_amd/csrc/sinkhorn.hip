@@ -343,12 +343,24 @@ StreamCfg stream_config(int B, int M, int N) {
     return c;
 }
 
-// One cooperative launch `kernel(args)` of G workgroups with `lds` bytes, if
-// the device can hold them all at once.
+// Bytes of the persistent forward's scaled kernel E (pst::forward, scaling
+// domain) for shapes that take that tier; the workspace query includes them,
+// and a smaller workspace that still holds fwd_layout runs without E.
+size_t scaled_kernel_bytes(int B, int M, int N) {
+    // rows of 64 floats per lane only (pst::forward)
+    if (N <= 2048 || resident_config<true>(B, M, N, N % 4 == 0).ok || !stream_config(B, M, N).ok) return 0;
+    return (size_t(B) * M * N * sizeof(float) + 255) & ~size_t(255);
+}
+
+float* scaled_kernel(const dot_sinkhorn_fwd_args* a, const FwdLayout& L) {
+    const size_t ek = scaled_kernel_bytes(a->B, a->M, a->N);
+    if (ek == 0 || !a->workspace || a->workspace_bytes < L.bytes + ek) return nullptr;
+    return reinterpret_cast<float*>(static_cast<char*>(a->workspace) + L.bytes);
+}
 
 bool launch_stream_forward(const dot_sinkhorn_fwd_args* a, const FwdLayout& L, const StreamCfg& sc,
                            float kscale, const float* ks_dev, float log_a_default, float log_b_default,
-                           bool keep, bool ret_log, bool vec4, hipStream_t stream) {
+                           bool keep, bool ret_log, bool vec4, float* ebuf, hipStream_t stream) {
     const int B = a->B, M = a->M, N = a->N, G = B * sc.W;
     if (!L.pst || size_t(G) > L.pst_groups) return false;
     pst::FwdArgs r{};
@@ -382,14 +394,15 @@ bool launch_stream_forward(const dot_sinkhorn_fwd_args* a, const FwdLayout& L, c
     r.W = sc.W;
     r.R = sc.R;
     r.spin_limit = spin_limit();
+    r.ebuf = ks_dev ? nullptr : ebuf;
     const size_t words = size_t(reinterpret_cast<unsigned long long*>(r.status) - L.pst) + 1;
     bool ok = false;
     dispatch_row(N, vec4, [&](auto vc, auto cc) {
         constexpr int V = decltype(vc)::value;
         constexpr int C = decltype(cc)::value;
-        // fold rows | v, v log2(e), log b | red (padded to 4) | u 2R, log a R | scratch
+        // fold rows | v, v log2(e), log b | red (padded to 4) | u 2R, log a R, row maxima R | scratch
         const size_t lds = (size_t(pst::kFoldRows<V, C> + 3) * N + ((size_t(N) + sc.W + 3) & ~size_t(3)) +
-                            3 * size_t(sc.R) + res::kFwdScratch) *
+                            4 * size_t(sc.R) + res::kFwdScratch) *
                            sizeof(float);
         launch_fill_zero(L.pst, 2 * words, stream);
         ProfScope prof("sk_fwd_persistent", stream);
@@ -586,7 +599,7 @@ using namespace dot_amd;
 extern "C" size_t dot_sinkhorn_forward_workspace_bytes(int B, int M, int N, int max_iter, int flags) {
     (void)flags;
     if (B < 0 || M < 0 || N < 0 || max_iter < 0) return 0;
-    return fwd_layout(nullptr, B, M, N, max_iter).bytes;
+    return fwd_layout(nullptr, B, M, N, max_iter).bytes + scaled_kernel_bytes(B, M, N);
 }
 
 extern "C" size_t dot_sinkhorn_exchange_bytes(void) {
@@ -651,7 +664,7 @@ int dot_amd::sinkhorn_forward_scheduled(const dot_sinkhorn_fwd_args* a, const fl
     (void)hipGetLastError();  // a refused cooperative launch falls back to the next tier
     const StreamCfg sc = stream_config(B, M, N);
     if (sc.ok && launch_stream_forward(a, L, sc, kscale, ks_dev, log_a_default, log_b_default, keep, ret_log,
-                                       vec4, stream))
+                                       vec4, scaled_kernel(a, L), stream))
         return check_launch("dot_sinkhorn_forward");
     (void)hipGetLastError();
 
@@ -1262,8 +1275,11 @@ int scratch_on_device(hipStream_t stream, void** out) {
 extern "C" int dot_sinkhorn_forward_noalloc(const dot_sinkhorn_fwd_args* args, dot_stream_t stream_) {
     if (!args) return fail(DOT_ERR_INVALID_ARG, "args is NULL");
     hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
-    const size_t need =
-        dot_sinkhorn_forward_workspace_bytes(args->B, args->M, args->N, args->max_iter, args->flags);
+    // the workspace without the persistent tier's optional scaled kernel (which
+    // the static scratch does not hold: that tier then runs without it)
+    const size_t need = (args->B < 0 || args->M < 0 || args->N < 0 || args->max_iter < 0)
+                            ? 0
+                            : fwd_layout(nullptr, args->B, args->M, args->N, args->max_iter).bytes;
     if (need > size_t(DOT_STATIC_SCRATCH_BYTES))
         return fail(DOT_ERR_UNSUPPORTED, "dot_sinkhorn_forward_noalloc: this shape needs " +
                                              std::to_string(need) + " bytes of scratch; the static scratch holds " +

@@ -91,6 +91,11 @@ typedef struct {
  * sinkhorn_log ops (torch_cuda.cpp:599-715), and
  * sinkhorn_dual_forward_with_intermediates_cuda (kernels.cuh:164) when
  * DOT_SK_KEEP_HISTORY is set.  Ops: src/sinkhorn/registry.cpp:31-45. */
+/* For shapes that take the persistent streaming tier the workspace includes
+ * room for a scaled copy of the kernel ([B,M,N] floats) that lets that tier
+ * iterate without an exponential per element; a workspace of at least the
+ * size without it (as the static scratch of dot_sinkhorn_forward_noalloc)
+ * runs without it, to the same tolerance. */
 size_t dot_sinkhorn_forward_workspace_bytes(int B, int M, int N, int max_iter, int flags);
 int dot_sinkhorn_forward(const dot_sinkhorn_fwd_args* args, dot_stream_t stream);
 
@@ -101,8 +106,11 @@ int dot_sinkhorn_forward(const dot_sinkhorn_fwd_args* args, dot_stream_t stream)
  * allocation: args->workspace and args->workspace_bytes are ignored and the
  * scratch is a file-scope device array of DOT_STATIC_SCRATCH_BYTES per GPU,
  * held from the first call on that GPU until the process ends.  Shapes whose
- * dot_sinkhorn_forward_workspace_bytes() exceeds DOT_STATIC_SCRATCH_BYTES
- * return DOT_ERR_UNSUPPORTED.  Results are those of dot_sinkhorn_forward.
+ * workspace exceeds DOT_STATIC_SCRATCH_BYTES return DOT_ERR_UNSUPPORTED (the
+ * workspace without the optional scaled kernel that
+ * dot_sinkhorn_forward_workspace_bytes() adds for the persistent tier's
+ * shapes; without it that tier iterates in the log domain throughout).
+ * Results are those of dot_sinkhorn_forward.
  * All calls on one GPU share its array (each call clears what must start at
  * zero), so calls that overlap on one GPU — on different streams, or from
  * different threads — race and must be serialised by the caller.

@@ -759,6 +759,55 @@ def test_capi_exchange_words_match_the_workspace_path(B, M, N, tau, T, tol):
         assert lib.dot_sinkhorn_forward(ctypes.byref(f), stream) == 1
 
 
+@pytest.mark.parametrize("B,M,N,tau,T,tol,b_range", [
+    (2, 300, 4096, 0.1, 40, 0.0, None),
+    (4, 512, 3072, 0.05, 60, 1e-6, None),
+    (1, 1000, 4096, 0.02, 30, 0.0, None),
+    (3, 256, 2560, 0.05, 40, 0.0, 60.0),   # v spreads past the range after iteration 1: log domain from there
+])
+def test_persistent_forward_scaled_kernel_matches_log_domain(B, M, N, tau, T, tol, b_range):
+    """The persistent forward with rows of 64 floats per lane (N > 2048)
+    streams a scaled copy of the kernel when the workspace holds it
+    (dot_sinkhorn_forward_workspace_bytes) and the scores in the log domain
+    when it does not: both against the oracle and each other."""
+    print(f"[sk_gpu] persistent scaled kernel B={B} M={M} N={N} tau={tau} b_range={b_range}", flush=True)
+    lib = ctypes.CDLL(os.path.join(ROOT, "dot_amd", "libdot_amd.so"))
+    lib.dot_sinkhorn_forward_workspace_bytes.restype = ctypes.c_size_t
+    lib.dot_sinkhorn_forward.argtypes = [ctypes.POINTER(SkFwdArgs), ctypes.c_void_p]
+    rng = np.random.default_rng(B * M + N)
+    C = rng.random((B, M, N)).astype(np.float32)
+    lgb = None
+    if b_range is not None:
+        lb = -b_range * rng.random((B, N))
+        lgb = (lb - np.log(np.exp(lb).sum(1, keepdims=True))).astype(np.float32)
+    Cd = _t(C)
+    lgbd = None if lgb is None else _t(lgb)
+    full = lib.dot_sinkhorn_forward_workspace_bytes(B, M, N, T, 0)
+    ek = (B * M * N * 4 + 255) // 256 * 256
+    assert full > ek  # this shape takes the persistent tier on this device
+    ws = torch.empty(full, dtype=torch.uint8, device=DEV)
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    out = {}
+    for name, nbytes in (("scaled", full), ("log", full - ek)):
+        P = torch.empty_like(Cd)
+        cost = torch.empty(B, device=DEV)
+        counts = torch.zeros(2, dtype=torch.int32, device=DEV)
+        f = SkFwdArgs(Cd.data_ptr(), None, None if lgbd is None else lgbd.data_ptr(), B, M, N, -1, tau, T, tol, 0,
+                      P.data_ptr(), cost.data_ptr(), None, None, None, None, counts.data_ptr(), counts.data_ptr() + 4,
+                      ws.data_ptr(), nbytes, None, 0)
+        assert lib.dot_sinkhorn_forward(ctypes.byref(f), stream) == 0
+        torch.cuda.synchronize()
+        out[name] = (P, cost, [int(x) for x in counts.tolist()])
+    for name, (P, cost, (used, _)) in out.items():
+        o = osk.dual_forward(-C, tau, used, log_b=lgb)
+        assert rel_err(P, o.P) < FWD_TOL, name
+        assert rel_err(cost, osk.transport_cost(o.P, C)) < FWD_TOL, name
+    if out["scaled"][2] == out["log"][2]:
+        assert rel_err(out["scaled"][0], out["log"][0].cpu().numpy()) < 2e-6
+    else:  # fp32 rounding at the stop threshold: one iteration apart at most
+        assert abs(out["scaled"][2][0] - out["log"][2][0]) <= 1
+
+
 def test_resident_launches_on_two_streams():
     """Resident forwards and adjoints enqueued on two streams with no host wait
     in between, each batch filling the device: the library orders its exchange
