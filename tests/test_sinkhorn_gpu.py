@@ -747,7 +747,12 @@ def test_capi_exchange_words_match_the_workspace_path(B, M, N, tau, T, tol):
 
     ref = run(None, 0)
     assert int(ref[5]) == 0
-    for epoch in (1, 3, 5):
+    # growing epochs; the last pair of the sequence (DOT_SINKHORN_MAX_EPOCH = 65534);
+    # then the words cleared again and the sequence restarted at 1
+    for epoch in (1, 3, 5, 65533, "clear", 1):
+        if epoch == "clear":
+            xw.zero_()
+            continue
         out = run(xw.data_ptr(), epoch)
         for a, e in zip(out, ref):
             assert torch.equal(a, e), epoch
