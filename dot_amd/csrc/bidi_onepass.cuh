@@ -112,7 +112,7 @@ __device__ __forceinline__ bool poll2(unsigned long long* p0, unsigned long long
             return true;
         }
         if (now_ticks() > deadline) return false;
-        __builtin_amdgcn_s_sleep(1);
+        // rounds back to back: each is a memory round trip already
     }
 }
 
