@@ -304,6 +304,21 @@ def _run_fused(scores, reg, scores_kind, n_iters, backward_iters, log_a, log_b, 
 
 
 _METHOD_CODES = {"vanilla": 0, "momentum": 1, "anderson": 2, "adam": 3}
+# Longest Anderson ring the device kernels hold (DOT_SK_MAX_ANDERSON in
+# include/dot_amd.h); the ring keeps min(anderson_k, n_iters) pairs.
+MAX_ANDERSON_RING = 64
+
+
+def _check_anderson_ring(anderson_k: int, n_iters: int) -> None:
+    """Rejects, before any kernel, an Anderson ring the device path cannot hold.
+
+    The reference's CUDA dual path (torch_cuda.cpp:290, 369-424) takes any
+    anderson_k; this build's kernels keep at most MAX_ANDERSON_RING pairs."""
+    if min(int(anderson_k), int(n_iters)) > MAX_ANDERSON_RING:
+        raise ValueError(
+            f"method='anderson' on a GPU tensor keeps min(anderson_k, n_iters) = "
+            f"{min(int(anderson_k), int(n_iters))} pairs, above the {MAX_ANDERSON_RING} this build's kernels "
+            f"hold; use anderson_k <= {MAX_ANDERSON_RING}")
 _SCHEDULE_CODES = {None: 0, "linear": 1, "exponential": 2, "cosine": 3}
 
 
@@ -626,6 +641,8 @@ def sinkhorn(
 
     mode = _MODE_UNROLLED if backward_mode == "unrolled" else _MODE_IMPLICIT
     if cuda_dual and not plain:
+        if effective == "anderson":
+            _check_anderson_ring(anderson_k, n_iters)
         params = (_METHOD_CODES[effective], float(omega) if omega is not None else 1.4, int(anderson_k),
                   float(mixing_beta), float(lr), float(beta1), float(beta2), float(eps_adam),
                   bool(bias_correction), -1.0 if eff_reg_start is None else float(eff_reg_start),

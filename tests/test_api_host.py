@@ -134,3 +134,13 @@ def test_sinkhorn_result_deferred_counts():
     assert vars(r5)["n_iters_used"] == 9 and vars(r5)["converged"] is False
     r6 = dot.SinkhornResult._deferred(P, None, lambda: (4, True))
     assert copy.copy(r6).n_iters_used == 4 and r6 == dot.SinkhornResult(P, None, True, 4)
+
+
+def test_anderson_ring_limit_message():
+    from dot_amd.sinkhorn import MAX_ANDERSON_RING, _check_anderson_ring
+    _check_anderson_ring(MAX_ANDERSON_RING, 1000)  # at the limit: accepted
+    _check_anderson_ring(1000, MAX_ANDERSON_RING)  # the ring holds min(k, n_iters)
+    with pytest.raises(ValueError, match="anderson_k <= 64"):
+        _check_anderson_ring(MAX_ANDERSON_RING + 1, MAX_ANDERSON_RING + 1)
+    assert f"#define DOT_SK_MAX_ANDERSON {MAX_ANDERSON_RING}" in open(
+        __import__("os").path.join(__import__("os").path.dirname(__file__), "..", "include", "dot_amd.h")).read()

@@ -317,6 +317,8 @@ def test_dual_false_is_the_fixed_count_path():
 
 def test_api_errors():
     C = torch.rand(2, 6, 6, device=DEV)
+    with pytest.raises(ValueError, match="anderson_k <= 64"):  # a ring longer than the kernels hold
+        dot_amd.sinkhorn(C, method="anderson", anderson_k=100, n_iters=200, reg=0.02)
     with pytest.raises(ValueError, match="strictly positive"):
         dot_amd.sinkhorn(C, a=torch.zeros(6, device=DEV))
     with pytest.raises(ValueError, match="sum to 1"):
