@@ -40,6 +40,7 @@ ONEPASS_SHAPES = [
     (12, 1024, 516, 2.0, "ragged"),
     (16, 777, 1024, 0.8, "ragged"),
     (8, 513, 772, 1.0, None),
+    (8, 1024, 768, 1.3, "ragged"),  # 768 columns: constant column bounds with lengths
 ]
 
 
@@ -105,11 +106,12 @@ def test_fallback_is_bitwise_the_exchange(monkeypatch, ticks, tile):
     assert torch.equal(g1, g2)
 
 
-def test_full_tile_matches_oracle():
-    """No lengths and 1024 x 1024 elements: the kernels whose extents are
-    constants, against the oracle."""
+@pytest.mark.parametrize("L2", [1024, 768])
+def test_full_tile_matches_oracle(L2):
+    """No lengths and 1024 x 1024 (or 1024 x 768) elements: the kernels whose
+    extents are constants, against the oracle."""
     rng = np.random.default_rng(21)
-    B, L1, L2, tau = 8, 1024, 1024, 0.6
+    B, L1, tau = 8, 1024, 0.6
     s = (2.0 * rng.standard_normal((B, L1, L2))).astype(np.float32)
     g = rng.standard_normal((B, L1, L2)).astype(np.float32)
     ln = np.array([[L1, L2]] * B, np.int32)
