@@ -1,5 +1,6 @@
-// Host-side helpers shared by the cooperative (one launch, exchange through
-// tagged words) kernels of both operators.
+// Host-side helpers shared by the one-launch kernels of both operators whose
+// workgroups exchange values through tagged words (resident and persistent
+// tiers, one-pass bidirectional softmax).
 #pragma once
 
 #include <hip/hip_ext.h>
@@ -111,18 +112,19 @@ inline hipError_t launch_grid(const void* kernel, int G, int threads, void** par
 }
 
 // Launch of a persistent-tier kernel (workgroups that wait on one another,
-// milliseconds long, so the ~18 us of a cooperative launch do not count):
-// only if all G workgroups can be resident at once (false, with nothing
-// launched, otherwise); cooperative, and ordered with the resident launches.
+// milliseconds long): only if all G workgroups can be resident at once
+// (false, with nothing launched, otherwise).  Launched as the resident tier's
+// kernels are: plainly, in resident_order, cooperative only when
+// DOT_AMD_COOPERATIVE=1.
 template <class K, class A>
-bool launch_cooperative(K kernel, A& args, int G, int threads, size_t lds, hipStream_t stream) {
+bool launch_persistent(K kernel, A& args, int G, int threads, size_t lds, hipStream_t stream) {
     int per_cu = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, lds) != hipSuccess ||
         per_cu < 1 || int64_t(per_cu) * device_cus() < G)
         return false;
     void* params[] = {&args};
     return resident_order().launch(reinterpret_cast<const void*>(kernel), G, threads, params, lds, stream,
-                                   true) == hipSuccess;
+                                   cooperative_requested()) == hipSuccess;
 }
 
 }  // namespace dot_amd

@@ -296,7 +296,6 @@ template <int VEC, int CH, bool SCHED = false>
 __global__ __launch_bounds__(kThreads) void forward(FwdArgs a) {
     using R = Row<VEC, CH>;
     constexpr int PL = R::PL;
-    constexpr float kLn2 = 0.69314718055994531f;
     // LDS: fold (kFoldRows) N | v N | v log2(e) N | log b N | red N + W (padded to 4) | u 2R | log a R | scratch 32
     extern __shared__ float lds[];
     float* tree = lds;

@@ -683,7 +683,6 @@ __global__ __launch_bounds__(kThreads) void forward(FwdResArgs a) {
     constexpr int PL = R::PL;
     constexpr int ROWS = kWaves * RPW;
     constexpr int GR = RPW < 4 ? RPW : 4;  // rows per reduction group
-    constexpr float kLn2 = 0.69314718055994531f;
     // LDS: wave rows 8N | v 2N | log b N | column max N | u 2*ROWS | log a ROWS | scratch 32
     extern __shared__ float lds[];
     float* part = lds;

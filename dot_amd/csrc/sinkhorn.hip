@@ -406,8 +406,8 @@ bool launch_stream_forward(const dot_sinkhorn_fwd_args* a, const FwdLayout& L, c
                            sizeof(float);
         launch_fill_zero(L.pst, 2 * words, stream);
         ProfScope prof("sk_fwd_persistent", stream);
-        ok = ks_dev ? launch_cooperative(pst::forward<V, C, true>, r, G, res::kThreads, lds, stream)
-                    : launch_cooperative(pst::forward<V, C>, r, G, res::kThreads, lds, stream);
+        ok = ks_dev ? launch_persistent(pst::forward<V, C, true>, r, G, res::kThreads, lds, stream)
+                    : launch_persistent(pst::forward<V, C>, r, G, res::kThreads, lds, stream);
     });
     if (!ok) return false;
     if (a->cost) {
@@ -897,7 +897,7 @@ bool launch_stream_adjoint(const dot_sinkhorn_bwd_args* a, const ImpLayout& L, c
             (size_t(pst::kFoldRows<V, C> + 2) * N + sc.W + 3 * size_t(sc.R) + 2 * S + 16) * sizeof(float);
         launch_fill_zero(L.pst, 2 * words, stream);
         ProfScope prof("sk_imp_persistent", stream);
-        ok = launch_cooperative(pst::implicit_adjoint<V, C>, r, G, res::kThreads, lds, stream);
+        ok = launch_persistent(pst::implicit_adjoint<V, C>, r, G, res::kThreads, lds, stream);
     });
     if (!ok) return false;
     ProfScope prof("sk_batch_sum", stream);
@@ -1001,7 +1001,7 @@ bool launch_stream_unrolled(const dot_sinkhorn_bwd_args* a, const UnrLayout& L, 
             const size_t lds = (size_t(pst::kFoldRows<V, C> + 4) * N + sc.W + 16) * sizeof(float);
             launch_fill_zero(L.pst, 2 * words, stream);
             ProfScope prof("sk_unr_persistent", stream);
-            ok = launch_cooperative(pst::unrolled<V, C>, r, G, res::kThreads, lds, stream);
+            ok = launch_persistent(pst::unrolled<V, C>, r, G, res::kThreads, lds, stream);
         }
     });
     if (!ok) return false;

@@ -100,6 +100,10 @@ struct FwdSweepArgs {
 //   colsum_j += e_ij * exp(log a_i - log s_i) = exp(K_ij + u_i + v_j),
 // so the column update needs no second pass over K:
 //   v_j' = log b_j - LSE_i(K_ij + u_i) = log b_j + v_j - log colsum_j.
+// The row is reduced in base 2 (y = K log2 e + v log2 e, m = max y,
+// s = sum 2^(y - m), u = log a - ln2 (m + log2 s)), the same arithmetic as
+// the register-resident and persistent forwards, so that every tier rounds
+// u alike and the stop test fires at the same iteration on every tier.
 template <int VEC, int CH>
 __global__ __launch_bounds__(kBlock) void fwd_sweep(FwdSweepArgs a) {
     if (stopped_before(a.delta_bits, a.t, a.tol)) return;
@@ -114,11 +118,15 @@ __global__ __launch_bounds__(kBlock) void fwd_sweep(FwdSweepArgs a) {
     const int r1 = min(r0 + a.rows, a.M);
     const size_t bM = size_t(b) * a.M;
 
-    float v[R::PL];
-    R::load(a.v_old + size_t(b) * a.N, lane, a.N, v, 0.0f);
+    float v2[R::PL];
+    R::load(a.v_old + size_t(b) * a.N, lane, a.N, v2, 0.0f);
+    const float kscale2 = a.kscale * kLog2E;
     float acc[R::PL];
 #pragma unroll
-    for (int e = 0; e < R::PL; ++e) acc[e] = 0.0f;
+    for (int e = 0; e < R::PL; ++e) {
+        v2[e] *= kLog2E;
+        acc[e] = 0.0f;
+    }
     float dmax = 0.0f;
 
     for (int i = r0 + wave; i < r1; i += kWavesPerBlock) {
@@ -127,21 +135,21 @@ __global__ __launch_bounds__(kBlock) void fwd_sweep(FwdSweepArgs a) {
         float mloc = -FLT_MAX;
 #pragma unroll
         for (int e = 0; e < R::PL; ++e) {
-            x[e] = R::valid(lane, e, a.N) ? fmaf(x[e], a.kscale, v[e]) : -INFINITY;
+            x[e] = R::valid(lane, e, a.N) ? fmaf(x[e], kscale2, v2[e]) : -INFINITY;
             mloc = fmaxf(mloc, x[e]);
         }
         const float m = wave_max(mloc);
         float sloc = 0.0f;
 #pragma unroll
         for (int e = 0; e < R::PL; ++e) {
-            x[e] = fast_exp(x[e] - m);
+            x[e] = __builtin_amdgcn_exp2f(x[e] - m);
             sloc += x[e];
         }
         const float ssum = wave_sum(sloc);
         const float lga = a.log_a ? a.log_a[bM + i] : a.log_a_default;
-        const float ls = logf(fmaxf(ssum, kSumFloor));
-        const float u = lga - (m + ls);
-        const float w = fast_exp(lga - ls);
+        const float lg2 = __builtin_amdgcn_logf(fmaxf(ssum, kSumFloor));  // log2
+        const float u = lga - kLn2 * (m + lg2);
+        const float w = __builtin_amdgcn_exp2f(fmaf(lga, kLog2E, -lg2));  // a / s
 #pragma unroll
         for (int e = 0; e < R::PL; ++e) acc[e] = fmaf(x[e], w, acc[e]);
         if (lane == 0) {
@@ -345,6 +353,48 @@ __device__ __forceinline__ void load_upstream(const GradSource& g, int b, size_t
 // -------------------------------------------------------------------------
 // Implicit adjoint
 // -------------------------------------------------------------------------
+
+// Early end of the one-launch adjoints (register-resident and persistent
+// tiers).  A sweep's lambda_i is a P-weighted average of the previous sweep's
+// mu, and its mu_k a P-weighted average of its lambda (plus constants), so
+// with d_t = max_k |mu_t - mu_{t-1}| every change of lambda after sweep t is
+// at most d_t, each sweep's change is at most the previous one's, and all
+// later changes of lambda_i + mu_k together are at most
+// sum_{j>t} (d_{j-1} + d_j) = d_t (1 + rho) / (1 - rho) when the changes
+// shrink by at least rho per sweep.  The adjoint ends after sweep t when
+//  * d_t = 0: mu is a fixed point and every later sweep would repeat this
+//    one bit for bit, so the result is exactly the full count's; or
+//  * the last three ratios d_j / d_{j-1} are at most kAdjRhoMax and, with rho
+//    their maximum, d_t (1 + rho) / (1 - rho) <= kAdjEps * max_k |mu_t,k|:
+//    what the remaining sweeps could still change is a few units in the last
+//    place of the largest mu, the size of the fp32 rounding of G - lambda - mu
+//    that the gradient carries in any case (past that point the fp32 sweeps
+//    only move within that rounding).
+// Slowly contracting problems (ratios above kAdjRhoMax) run every sweep.
+// d_t and max|mu_t| are the same bits in every workgroup of a batch element
+// (they all hold the same mu), so the element's workgroups stop together.
+constexpr float kAdjRhoMax = 0.5f;
+constexpr float kAdjEps = 4.76837158e-7f;  // 2^-21
+
+struct AdjointStop {
+    float d1 = 0.0f, d2 = 0.0f, d3 = 0.0f;  // changes of the three previous sweeps
+
+    // Sweep t (1-based) changed mu by at most d and ends with max|mu| = s;
+    // true when the adjoint ends here.  A NaN (an exchange that timed out)
+    // ends it too.
+    __device__ __forceinline__ bool done(int t, float d, float s) {
+        bool stop = !(d > 0.0f);
+        if (!stop && t >= 4) {
+            const float rho = fmaxf(fmaxf(d / d1, d1 / d2), d2 / d3);
+            stop = rho <= kAdjRhoMax && d * (1.0f + rho) <= kAdjEps * s * (1.0f - rho);
+        }
+        d3 = d2;
+        d2 = d1;
+        d1 = d;
+        return stop;
+    }
+};
+
 struct ImpArgs {
     GradSource g;
     const float* P;

@@ -59,6 +59,20 @@ __device__ __forceinline__ void fold_lse(const float2* p, size_t stride, int nch
     s = wave_sum(ls * fast_exp(lm - m));
 }
 
+// fold_lse for partials in base 2: s = sum_c s_c 2^(m_c - m).
+__device__ __forceinline__ void fold_lse2(const float2* p, size_t stride, int nchunks, float& m, float& s) {
+    const int lane = threadIdx.x % kWave;
+    float lm = -FLT_MAX, ls = 0.0f;
+    for (int c = lane; c < nchunks; c += kWave) {
+        const float2 q = p[size_t(c) * stride];
+        const float nm = fmaxf(lm, q.x);
+        ls = ls * __builtin_amdgcn_exp2f(lm - nm) + q.y * __builtin_amdgcn_exp2f(q.x - nm);
+        lm = nm;
+    }
+    m = wave_max(lm);
+    s = wave_sum(ls * __builtin_amdgcn_exp2f(lm - m));
+}
+
 // Plain sum of row i's chunk partials (same layout as fold_lse).
 __device__ __forceinline__ float fold_sum(const float* p, size_t stride, int nchunks) {
     const int lane = threadIdx.x % kWave;

@@ -76,6 +76,7 @@ __device__ __forceinline__ float block_reduce(float wave_value, float* scratch, 
 // Exponentials.  The reference's safe_exp (src/sinkhorn/kernels.cu:21-25):
 // 0 below -88, exp(88) above 88.  fast_exp2 is the hardware v_exp_f32 (2^x).
 constexpr float kLog2E = 1.4426950408889634f;
+constexpr float kLn2 = 0.69314718055994531f;
 
 __device__ __forceinline__ float fast_exp(float x) { return __builtin_amdgcn_exp2f(x * kLog2E); }
 

@@ -45,7 +45,7 @@ struct FwdArgs {
     const float* u_old;    // [B,M]
     float* u_new;          // [B,M]
     float* u_hist;         // [B,M] slice of the history, or null
-    float2* rpart;         // [B,nchunks,M] (max, sum) of K + v over each chunk
+    float2* rpart;         // [B,nchunks,M] (max, sum) of (K + v) log2 e over each chunk, base 2
     float* partial;        // [B,nstrips,N]
     unsigned* delta_bits;  // [max_iter+1]
     int B, M, N, rows, nstrips, nchunks, t;
@@ -53,7 +53,8 @@ struct FwdArgs {
 };
 
 // Rows pass of iteration t: per row and chunk, m = max_j(K_ij + v_j) and
-// s = sum_j exp(K_ij + v_j - m) over the chunk's columns (kernels.cu:547-581).
+// s = sum_j exp(K_ij + v_j - m) over the chunk's columns (kernels.cu:547-581),
+// in base 2 as the streaming sweep (y = (K + v) log2 e, s = sum 2^(y - m)).
 template <int VEC, int CH>
 __global__ __launch_bounds__(kBlock) void fwd_rows(FwdArgs a) {
     if (sk::stopped_before(a.delta_bits, a.t, a.tol)) return;
@@ -66,8 +67,11 @@ __global__ __launch_bounds__(kBlock) void fwd_rows(FwdArgs a) {
     const int r0 = tl.s * a.rows;
     const int r1 = min(r0 + a.rows, a.M);
     const size_t bM = size_t(b) * a.M;
-    float v[R::PL];
-    R::load(a.v_old + size_t(b) * a.N + tl.c0, lane, tl.nc, v, 0.0f);
+    float v2[R::PL];
+    R::load(a.v_old + size_t(b) * a.N + tl.c0, lane, tl.nc, v2, 0.0f);
+#pragma unroll
+    for (int e = 0; e < R::PL; ++e) v2[e] *= kLog2E;
+    const float kscale2 = a.kscale * kLog2E;
     float2* part = a.rpart + (size_t(b) * a.nchunks + tl.c) * a.M;
     for (int i = r0 + wave; i < r1; i += kWavesPerBlock) {
         float x[R::PL];
@@ -75,20 +79,20 @@ __global__ __launch_bounds__(kBlock) void fwd_rows(FwdArgs a) {
         float mloc = -FLT_MAX;
 #pragma unroll
         for (int e = 0; e < R::PL; ++e) {
-            x[e] = R::valid(lane, e, tl.nc) ? fmaf(x[e], a.kscale, v[e]) : -INFINITY;
+            x[e] = R::valid(lane, e, tl.nc) ? fmaf(x[e], kscale2, v2[e]) : -INFINITY;
             mloc = fmaxf(mloc, x[e]);
         }
         const float m = wave_max(mloc);
         float sloc = 0.0f;
 #pragma unroll
-        for (int e = 0; e < R::PL; ++e) sloc += fast_exp(x[e] - m);
+        for (int e = 0; e < R::PL; ++e) sloc += __builtin_amdgcn_exp2f(x[e] - m);
         const float s = wave_sum(sloc);
         if (lane == 0) part[i] = make_float2(m, s);
     }
 }
 
 // Columns pass of iteration t: u_i = log a_i - (m_i + log max(s_i, 1e-12))
-// from the folded chunk partials (kernels.cu:583-627), and the column sums
+// from the folded chunk partials (kernels.cu:583-627; base 2 as fwd_rows), and the column sums
 // sum_i exp(K_ij + u_i + v_j) = sum_i exp(K_ij + v_j - m_i) exp(log a_i - log s_i)
 // of the chunk's columns, one partial row per strip (read by sk::fwd_combine).
 // Chunk 0's tiles write u and the stop test's |u_t - u_{t-1}|.
@@ -105,26 +109,30 @@ __global__ __launch_bounds__(kBlock) void fwd_cols(FwdArgs a) {
     const int r0 = tl.s * a.rows;
     const int r1 = min(r0 + a.rows, a.M);
     const size_t bM = size_t(b) * a.M;
-    float v[R::PL];
-    R::load(a.v_old + size_t(b) * a.N + tl.c0, lane, tl.nc, v, 0.0f);
+    float v2[R::PL];
+    R::load(a.v_old + size_t(b) * a.N + tl.c0, lane, tl.nc, v2, 0.0f);
+    const float kscale2 = a.kscale * kLog2E;
     const float2* part = a.rpart + size_t(b) * a.nchunks * a.M;
     float acc[R::PL];
 #pragma unroll
-    for (int e = 0; e < R::PL; ++e) acc[e] = 0.0f;
+    for (int e = 0; e < R::PL; ++e) {
+        v2[e] *= kLog2E;
+        acc[e] = 0.0f;
+    }
     float dmax = 0.0f;
     for (int i = r0 + wave; i < r1; i += kWavesPerBlock) {
         float x[R::PL];
         R::load(a.X + (bM + i) * a.N + tl.c0, lane, tl.nc, x, 0.0f);
         float m, ssum;
-        fold_lse(part + i, a.M, a.nchunks, m, ssum);
+        fold_lse2(part + i, a.M, a.nchunks, m, ssum);
         const float lga = a.log_a ? a.log_a[bM + i] : a.log_a_default;
-        const float ls = logf(fmaxf(ssum, kSumFloor));
-        const float u = lga - (m + ls);
-        const float w = fast_exp(lga - ls);
+        const float lg2 = __builtin_amdgcn_logf(fmaxf(ssum, kSumFloor));  // log2
+        const float u = lga - kLn2 * (m + lg2);
+        const float w = __builtin_amdgcn_exp2f(fmaf(lga, kLog2E, -lg2));  // a / s
 #pragma unroll
         for (int e = 0; e < R::PL; ++e) {
-            const float y = R::valid(lane, e, tl.nc) ? fmaf(x[e], a.kscale, v[e]) : -INFINITY;
-            acc[e] = fmaf(fast_exp(y - m), w, acc[e]);
+            const float y = R::valid(lane, e, tl.nc) ? fmaf(x[e], kscale2, v2[e]) : -INFINITY;
+            acc[e] = fmaf(__builtin_amdgcn_exp2f(y - m), w, acc[e]);
         }
         if (tl.c == 0 && lane == 0) {
             a.u_new[bM + i] = u;

@@ -585,7 +585,7 @@ def _both_paths(monkeypatch, fn):
 
 @pytest.mark.parametrize("B,M,N,tau,T,tol,nonuni", [
     (8, 64, 64, 1.0, 50, 0.0, False),
-    (16, 512, 512, 0.1, 200, 1e-4, False),
+    (16, 512, 512, 0.1, 200, 1e-6, False),
     (4, 96, 128, 0.05, 300, 1e-6, True),
     (3, 130, 70, 0.5, 40, 0.0, True),
     (2, 1000, 1024, 0.2, 20, 0.0, False),
@@ -613,6 +613,44 @@ def test_resident_and_streaming_forwards_agree_with_oracle(B, M, N, tau, T, tol,
         assert rel_err(P, Po) < FWD_TOL, mode
     if counts["1"] == counts["0"]:
         assert rel_err(res["1"][0], res["0"][0].cpu().numpy()) < 1e-5
+
+
+_TIERS = (("resident", {}), ("persistent", {"DOT_AMD_RESIDENT": "0"}),
+          ("sweeps", {"DOT_AMD_RESIDENT": "0", "DOT_AMD_PERSISTENT": "0"}))
+
+
+def test_c3_stop_count_is_the_same_on_every_tier(monkeypatch):
+    """n_iters_used is a function of the input, not of the tier the batch size
+    selects: C3's input (seed 3, its first 16 elements, reg 0.1, tol 1e-6) on
+    the register-resident tier, the persistent tier and the per-iteration
+    sweeps stops within one iteration of both the float64 and the float32
+    oracle (torch_cuda.cpp:199-238), and so does a batch of 300 (above the
+    CUs, so the sweeps by shape) made of those 16 elements repeated, whose
+    batch-global stop test sees the same maxima."""
+    C = _c3_cost()[:16].contiguous()
+    Cn = C.cpu().numpy()
+    o64 = osk.dual_forward(-Cn, 0.1, 200, tol=1e-6).n_iters_used
+    o32 = osk.dual_forward(-Cn, 0.1, 200, tol=1e-6, dtype=np.float32).n_iters_used
+    print(f"[c3 stop] oracle float64 {o64} float32 {o32}", flush=True)
+    counts = {}
+    for name, env in _TIERS:
+        for k, v in env.items():
+            monkeypatch.setenv(k, v)
+        res = dot_amd.sinkhorn(C, reg=0.1, n_iters=200, tol=1e-6)
+        counts[name] = res.n_iters_used
+        assert res.converged, name
+        Po = osk.dual_forward(-Cn[:2], 0.1, res.n_iters_used).P
+        assert rel_err(res.transport_plan[:2], Po) < FWD_TOL, name
+        for k in env:
+            monkeypatch.delenv(k)
+    reps = C.repeat(19, 1, 1)[:300].contiguous()
+    res = dot_amd.sinkhorn(reps, reg=0.1, n_iters=200, tol=1e-6)
+    counts["B=300"] = res.n_iters_used
+    Po = osk.dual_forward(-Cn[:2], 0.1, res.n_iters_used).P
+    assert rel_err(res.transport_plan[16:18], Po) < FWD_TOL
+    print(f"[c3 stop] counts {counts}", flush=True)
+    for name, used in counts.items():
+        assert abs(used - o64) <= 1 and abs(used - o32) <= 1, (name, counts, o64, o32)
 
 
 def test_resident_forward_outputs_cost_log_and_history(monkeypatch):
