@@ -15,22 +15,23 @@ in HBM before the timed region starts.
 
 Printed: one JSON line.  ``value`` is Sinkhorn element-iterations per second,
 E * (T_f + T_b) per step with E = B*M*N, T_f = forward iterations executed
-and T_b = adjoint sweeps executed.  The same line carries
+and T_b = adjoint sweeps executed (averaged over the batch: the one-launch
+tiers end each element's sweeps once converged, ``result.adjoint_sweeps``), so
+it falls as the step gets shorter; ``ms_per_step`` is the step's wall time.
+The same line carries
 
-* ``roofline`` — the dominant kernel against the roof that bounds it, with its
-  average launch duration measured with HIP events on the launch stream over a
-  second pass of the same K steps run right after the timed ones (the events
-  would otherwise add their own cost to ``value``):
-  - streaming tiers (the matrix is re-read from HBM / the Infinity Cache every
-    sweep): ``bound`` "hbm", 4 bytes per element-sweep over the duration
-    against 8 TB/s;
-  - the register-resident tier (the matrix stays in VGPRs for all sweeps):
-    ``bound`` "valu", the kernel's arithmetic — 4 flops per element-sweep in
-    the adjoint (two FMAs: the row dot and the column sum), 8 per
-    element-iteration in the forward (FMA, max, subtract, exp2, add, FMA) —
-    against the 157.3 TFLOP/s fp32 vector peak, beside the HBM traffic the
-    counters measured and the HBM-equivalent bytes the same sweeps would
-    stream;
+* ``roofline`` — the dominant kernel (the most time per step) against the
+  roof it comes closer to, with its average launch duration measured with HIP
+  events on the launch stream over a second pass of the same K steps run right
+  after the timed ones (the events would otherwise add their own cost to
+  ``value``).  Its algorithmic work per launch (KERNEL_WORK) is the
+  irreducible traffic of its tier — inputs read and output written once (8
+  bytes per element in the forward, 12 in the adjoint), plus 4 bytes per
+  element-sweep for tiers that re-read the matrix every sweep (the
+  register-resident tier keeps it in VGPRs) — and its arithmetic, 8 flops per
+  element-iteration in the forward and 4 per element-sweep in the adjoint, over
+  the sweeps it executed.  ``hbm`` and ``valu`` give both fractions (8 TB/s,
+  157.3 TFLOP/s); ``bound`` names the larger;
 * ``cpu_baseline`` — the reference's own CPU kernels (oracle/_ref, compiled
   from the reference sources) timed on a bounded sample of the same input,
   pinned to one host core with one torch thread, or the numpy oracle when
@@ -62,8 +63,6 @@ import time
 HBM_PEAK_GBPS = 8000.0  # MI355X HBM3E, 8 TB/s
 FP32_PEAK_TFLOPS = 157.3  # MI355X fp32 vector peak (packed dual-issue)
 FP32_NONPACKED_TFLOPS = 78.6  # the same without packed fp32 instructions (this build disables them)
-# Algorithmic flops per element-sweep of the register-resident kernels.
-RESIDENT_FLOPS = {"sk_imp_resident": 4.0, "sk_fwd_resident": 8.0}
 ROOT = os.path.dirname(os.path.abspath(__file__))
 
 WORKLOADS = {
@@ -279,39 +278,57 @@ def profiled_pass(profiler, names, step, steps, torch):
     return kernel_stats(profiler, names)
 
 
+# Algorithmic work of each Sinkhorn kernel per matrix element: (HBM bytes once
+# per launch, HBM bytes per sweep, flops per sweep, which count the sweeps are).
+# Bytes are the irreducible traffic of the kernel's tier: the register-resident
+# kernels read their inputs and write their output once (the matrix then stays
+# in VGPRs: no bytes per sweep); the persistent and streaming kernels also
+# re-read the matrix every sweep.  Forward: read C, write P (8); adjoint: read
+# P and C, write the gradient (12).  Flops per sweep: the forward's row update
+# and shared-exponential column sum (FMA, max, subtract, exp2, add, FMA, plus
+# the column FMA: 8), the adjoint's row dot and column sum (two FMAs: 4).
+KERNEL_WORK = {
+    "sk_fwd_resident": (8.0, 0.0, 8.0, "T_f"),
+    "sk_imp_resident": (12.0, 0.0, 4.0, "T_b"),
+    "sk_fwd_persistent": (8.0, 4.0, 8.0, "T_f"),
+    "sk_imp_persistent": (12.0, 4.0, 4.0, "T_b"),
+    "sk_fwd_sweep": (0.0, 4.0, 8.0, "one"),
+    "sk_imp_sweep": (0.0, 4.0, 4.0, "one"),
+    "sk_unr_step": (0.0, 12.0, 0.0, "one"),
+    "sk_unr_persistent": (12.0, 12.0, 0.0, "T_b"),
+}
+
+
 def sinkhorn_roofline(dominant, stats, E, T_f, T_b, workload):
-    """Roofline object of the dominant Sinkhorn kernel (see the module docstring)."""
-    sweeps = {"sk_imp_resident": T_b, "sk_fwd_resident": T_f, "sk_imp_persistent": T_b,
-              "sk_fwd_persistent": T_f, "sk_unr_persistent": T_b}.get(dominant, 1)
+    """Roofline object of the dominant Sinkhorn kernel (see the module docstring):
+    its algorithmic bytes and flops per launch over its event-timed average
+    duration, against the HBM and fp32 vector peaks; ``bound`` is the roof the
+    kernel comes closer to."""
+    once, per_sweep, flops_sweep, count = KERNEL_WORK.get(dominant, (0.0, 4.0, 0.0, "one"))
+    sweeps = {"T_f": T_f, "T_b": T_b, "one": 1}[count]
     avg_s = stats[dominant]["avg_us"] * 1e-6
-    hbm_equiv = 4.0 * E * sweeps  # one fp32 read of the [B,M,N] matrix per sweep
-    if dominant in ("sk_unr_step", "sk_unr_persistent"):
-        # a reverse step of the unrolled backward reads Gamma and C and writes Gamma
-        hbm_equiv = 12.0 * E * sweeps
+    bytes_launch = (once + per_sweep * sweeps) * E
+    flops_launch = flops_sweep * sweeps * E
+    hbm = bytes_launch / avg_s / 1e9
+    valu = flops_launch / avg_s / 1e12
     traffic = _pmc_traffic(dominant, workload)
     measured = None if traffic is None else {
         "GBps": round(traffic / avg_s / 1e9, 1), "frac": round(traffic / avg_s / 1e9 / HBM_PEAK_GBPS, 4)}
-    if dominant in RESIDENT_FLOPS:
-        flops = RESIDENT_FLOPS[dominant] * E * sweeps
-        achieved = flops / avg_s / 1e12
-        return {"bound": "valu", "kernel": dominant, "achieved": round(achieved, 2),
-                "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / FP32_PEAK_TFLOPS, 4),
-                "frac_of_nonpacked_peak": round(achieved / FP32_NONPACKED_TFLOPS, 4),
-                "flops_per_launch": flops, "flops_per_elem_sweep": RESIDENT_FLOPS[dominant],
-                "sweeps_per_launch": sweeps, "traffic": traffic, "hbm_measured": measured,
-                "hbm_equivalent": {"bytes_per_launch": hbm_equiv,
-                                   "GBps": round(hbm_equiv / avg_s / 1e9, 1),
-                                   "note": "bytes the same sweeps would stream; the matrix stays in VGPRs"},
-                "tier": "register-resident (one launch, the matrix held in VGPRs; bound by VALU issue "
-                        "and the per-sweep cross-workgroup column exchange)"}
-    achieved = hbm_equiv / avg_s / 1e9
-    return {"bound": "hbm", "kernel": dominant, "achieved": round(achieved, 1),
-            "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
-            "traffic": traffic, "hbm_measured": measured, "bytes_per_launch": hbm_equiv,
-            "sweeps_per_launch": sweeps,
-            "tier": "persistent streaming (one launch; the matrix is re-read every sweep)"
-            if "persistent" in dominant else "streaming sweeps (one launch per sweep)",
-            "bytes_per_elem_sweep": 12.0 if "unr" in dominant else 4.0}
+    tier = ("register-resident (one launch, the matrix held in VGPRs for every sweep)" if "resident" in dominant
+            else "persistent streaming (one launch; the matrix is re-read every sweep)" if "persistent" in dominant
+            else "streaming sweeps (one launch per sweep)")
+    common = {"kernel": dominant, "tier": tier, "sweeps_per_launch": sweeps, "avg_us": round(avg_s * 1e6, 2),
+              "bytes_per_launch": bytes_launch, "bytes_per_elem": {"once": once, "per_sweep": per_sweep},
+              "flops_per_launch": flops_launch, "flops_per_elem_sweep": flops_sweep,
+              "hbm": {"achieved_GBps": round(hbm, 1), "frac": round(hbm / HBM_PEAK_GBPS, 4)},
+              "valu": {"achieved_TFLOPs": round(valu, 2), "frac": round(valu / FP32_PEAK_TFLOPS, 4),
+                       "frac_of_nonpacked_peak": round(valu / FP32_NONPACKED_TFLOPS, 4)},
+              "traffic": traffic, "traffic_source": TRAFFIC_SOURCE, "hbm_measured": measured}
+    if valu / FP32_PEAK_TFLOPS > hbm / HBM_PEAK_GBPS:
+        return {"bound": "valu", "achieved": round(valu, 2), "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(valu / FP32_PEAK_TFLOPS, 4), **common}
+    return {"bound": "hbm", "achieved": round(hbm, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+            "frac": round(hbm / HBM_PEAK_GBPS, 4), **common}
 
 
 SINKHORN_KERNELS = ["sk_fwd_sweep", "sk_imp_sweep", "sk_fwd_resident", "sk_imp_resident",
@@ -329,10 +346,13 @@ def bench_sinkhorn(args, workload, steps, warmup, torch, dot_amd, profiler, solv
     reg, n_iters, tol = cfg["reg"], cfg["n_iters"], cfg["tol"]
     solver = solver or {}
 
+    last = {}
+
     def step():
         leaf = C.detach().requires_grad_(True)
         res = dot_amd.sinkhorn(leaf, reg=reg, n_iters=n_iters, tol=tol, a=a, b=b, **solver)
         res.cost.sum().backward()
+        last["res"] = res
         return res.n_iters_used
 
     from dot_amd.sinkhorn import _effective_method
@@ -353,9 +373,15 @@ def bench_sinkhorn(args, workload, steps, warmup, torch, dot_amd, profiler, solv
     stats = profiled_pass(profiler, SINKHORN_KERNELS, step, steps, torch)
 
     T_f = sum(used) / len(used)
-    # implicit: backward_iters defaults to n_iters and the adjoint runs exactly that many
-    # sweeps; unrolled: one reverse step per recorded forward iteration
-    T_b = T_f if solver.get("backward_mode") == "unrolled" else n_iters
+    # implicit: the sweeps each element's adjoint executed (at most backward_iters =
+    # n_iters; the one-launch tiers end an element's sweeps once converged), averaged
+    # over the batch (same input every step, same counts); unrolled: one reverse step
+    # per recorded forward iteration
+    sweeps = last["res"].adjoint_sweeps
+    if solver.get("backward_mode") == "unrolled":
+        T_b = T_f
+    else:
+        T_b = sum(sweeps) / len(sweeps) if sweeps else n_iters
     sec_per_step = (t1 - t0) / steps
     value = E * (T_f + T_b) / sec_per_step
 
@@ -375,7 +401,8 @@ def bench_sinkhorn(args, workload, steps, warmup, torch, dot_amd, profiler, solv
                                   f" method={effective} schedule={eff_schedule}"),
                    "method": effective, "schedule": eff_schedule,
                    "B": B, "M": M, "N": N, "reg": reg, "n_iters": n_iters, "tol": tol,
-                   "n_iters_used": used[-1], "backward_iters": T_b,
+                   "n_iters_used": used[-1], "backward_iters": n_iters,
+                   "adjoint_sweeps_executed": T_b,
                    "backward_mode": solver.get("backward_mode", "implicit")},
         "algorithmic_GBps": algo_bytes / sec_per_step / 1e9,
         "frac_of_hbm_peak": algo_bytes / sec_per_step / 1e9 / HBM_PEAK_GBPS,
@@ -436,6 +463,7 @@ def bench_bidi(args, torch, dot_amd, profiler):
                 "achieved": round(algo, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                 "frac": round(algo / HBM_PEAK_GBPS, 4),
                 "traffic": sum(traffic) if traffic and None not in traffic else None,
+                "traffic_source": TRAFFIC_SOURCE,
                 "bytes_per_step": 20.0 * E,
                 "note": "20 B/elem algorithmic over ms_per_step; kernels_own_traffic gives each "
                         "sweep's own bytes over its event-timed duration"}
@@ -451,6 +479,10 @@ def bench_bidi(args, torch, dot_amd, profiler):
         "roofline": roofline,
         "_cpu": (sim, G, lengths.cpu().numpy()),
     }
+
+
+TRAFFIC_SOURCE = ("profiles/pmc_traffic.json: HBM bytes per dispatch from committed rocprofv3 --pmc "
+                  "FETCH_SIZE and WRITE_SIZE runs, calibrated on a device copy; not measured in this run")
 
 
 def _pmc_traffic(kernel, workload):

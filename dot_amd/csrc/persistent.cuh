@@ -238,6 +238,32 @@ __device__ __forceinline__ void gather(const unsigned long long* res_row, int N,
         if (r < mine) out[tid + r * kThreads] = got[r];
 }
 
+// gather() of a row that carries W more words after its N results (one per
+// slice owner), which are not stored: returns this thread's largest
+// |new - old| over the N results (old: what `out` held before) and its
+// largest extra word.
+__device__ __forceinline__ void gather_track(const unsigned long long* res_row, int N, int W, unsigned t,
+                                             float* out, int spin_limit, int* status, bool& dead, float& dmax,
+                                             float& xmax) {
+    int tid = threadIdx.x;  // opaque, as in reduce_slice
+    asm volatile("" : "+v"(tid));
+    const int n = N + W;
+    const int mine = n > tid ? (n - 1 - tid) / kThreads + 1 : 0;
+    float got[kLoadsPerThread];
+    poll_many(res_row, mine, [&](int r) { return unsigned(tid + r * kThreads); }, t, spin_limit, status, dead,
+              got);
+#pragma unroll
+    for (int r = 0; r < kLoadsPerThread; ++r) {
+        const int j = tid + r * kThreads;
+        if (r < mine && j < N) {
+            dmax = fmaxf(dmax, fabsf(got[r] - out[j]));
+            out[j] = got[r];
+        } else if (r < mine) {
+            xmax = fmaxf(xmax, got[r]);
+        }
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Forward
 // ---------------------------------------------------------------------------
@@ -640,13 +666,15 @@ struct ImpArgs {
     const float* gC;      // [B] or null
     const float* P;       // [B,M,N]
     unsigned long long* part;  // [2, G, N] tagged workgroup column sums
-    unsigned long long* res;   // [2, B, N] tagged mu
+    unsigned long long* res;   // [2, B, N + kMaxGroups] tagged mu, then each slice owner's stop-test scale
     unsigned long long* pro;   // [2, G, N] tagged prologue sums (P G, P)
     float* grad;
     float* tau_partial;   // [G] by logical workgroup
     int* status;
     float inv_tau;
     int B, M, N, W, R, iters, spin_limit;
+    int32_t* sweeps;      // [B] sweeps executed per batch element, or null
+    int early;            // nonzero: end each element's sweeps once converged (sk::AdjointStop)
 };
 
 template <int VEC, int CH>
@@ -672,11 +700,15 @@ __device__ __forceinline__ void upstream(const ImpArgs& a, size_t off, int lane,
 // form mu_k = (c_k - sum) / max(cs_k, 1e-12), all-gather of mu; final phase
 // grad = P (G - lambda - mu) / tau (log-alpha kind: that - grad_cost P; cost
 // kind: grad_cost P - that) and the workgroup's share of sum(grad * log_alpha).
+// With `early`, an element's sweeps end once sk::AdjointStop finds them
+// converged: the slice owners publish their slice's largest
+// (|c_k| + |sum_i P lambda_i|) / cs_k after their mu, and every workgroup
+// gathers those W words with mu, so all of them decide on the same values.
 template <int VEC, int CH>
 __global__ __launch_bounds__(kThreads) void implicit_adjoint(ImpArgs a) {
     using R = Row<VEC, CH>;
     constexpr int PL = R::PL;
-    // LDS: fold (kFoldRows) N | mu N | red N + W | r R | 1/rs R | lambda R | c S | cs S | scratch 16
+    // LDS: fold (kFoldRows) N | mu N | red N + W | r R | 1/rs R | lambda R | c S | cs S | scratch 32
     extern __shared__ float lds[];
     const int lane = threadIdx.x % kWave;
     const int wave = threadIdx.x / kWave;
@@ -742,6 +774,8 @@ __global__ __launch_bounds__(kThreads) void implicit_adjoint(ImpArgs a) {
     __syncthreads();
 
     // Sweeps.
+    sk::AdjointStop stop;
+    int done_t = a.iters;
     for (int t = 1; t <= a.iters; ++t) {
         const int cur = t & 1;
         ColVec<VEC, CH> mu;
@@ -767,14 +801,46 @@ __global__ __launch_bounds__(kThreads) void implicit_adjoint(ImpArgs a) {
             if (lane == 0) lds_lam[l] = lam;
         }
         publish_row<VEC, CH>(acc, tree, a.N, a.part + (size_t(cur) * G + gid) * a.N, unsigned(t), local);
-        unsigned long long* res_row = a.res + (size_t(cur) * a.B + b) * a.N;
+        unsigned long long* res_row = a.res + (size_t(cur) * a.B + b) * (size_t(a.N) + kMaxGroups);
+        float sl = 0.0f;  // this thread's largest (|c_k| + |sum_i P lambda_i|) / cs_k of the slice
         reduce_slice(a.part + size_t(cur) * G * a.N + size_t(b) * a.W * a.N, a.N, a.W, c0, c1, unsigned(t),
                      red, a.spin_limit, a.status, dead, [&](int j, float tot) {
-                         publish(res_row + j, (lds_c[j - c0] - tot) / lds_cs[j - c0], unsigned(t), local);
+                         const float cj = lds_c[j - c0], csj = lds_cs[j - c0];
+                         sl = fmaxf(sl, (fabsf(cj) + fabsf(tot)) / csj);
+                         publish(res_row + j, (cj - tot) / csj, unsigned(t), local);
                      });
-        gather(res_row, a.N, unsigned(t), lds_mu, a.spin_limit, a.status, dead);
+        if (a.early) {
+            // stop-test values live at scratch + 16: block_reduce uses the first 8
+            sl = block_reduce<kWaves>(wave_max(sl), scratch, OpMax{});
+            if (threadIdx.x == 0) publish(res_row + a.N + w, sl, unsigned(t), local);
+            float dmu = 0.0f, smu = 0.0f;
+            gather_track(res_row, a.N, a.W, unsigned(t), lds_mu, a.spin_limit, a.status, dead, dmu, smu);
+            dmu = wave_max(dmu);
+            smu = wave_max(smu);
+            // the last readers of these words are behind the barriers of the
+            // next sweep's publish_row
+            if (lane == 0) {
+                scratch[16 + wave] = dmu;
+                scratch[16 + kWaves + wave] = smu;
+            }
+        } else {
+            gather(res_row, a.N, unsigned(t), lds_mu, a.spin_limit, a.status, dead);
+        }
         __syncthreads();
+        if (a.early && t < a.iters) {
+            float d = scratch[16], sm = scratch[16 + kWaves];
+#pragma unroll
+            for (int q = 1; q < kWaves; ++q) {
+                d = fmaxf(d, scratch[16 + q]);
+                sm = fmaxf(sm, scratch[16 + kWaves + q]);
+            }
+            if (stop.done(t, d, sm)) {
+                done_t = t;
+                break;
+            }
+        }
     }
+    if (a.sweeps && w == 0 && threadIdx.x == 0) a.sweeps[b] = done_t;
 
     // Final phase: stream P and G again and write this workgroup's gradient rows.
     const bool failed = __hip_atomic_load(a.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;

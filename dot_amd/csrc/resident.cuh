@@ -422,6 +422,8 @@ struct ImpResArgs {
     unsigned tag_base;         // exchange tags are tag_base | t (0: slots cleared for the call)
     unsigned xcc_tag;          // tag of the XCD-id words
     int mark;                  // failure mark in *status (forced_timeout)
+    int32_t* sweeps;           // [B] sweeps executed per batch element, or null
+    int early;                 // nonzero: end each element's sweeps once converged (sk::AdjointStop)
 };
 
 // Upstream gradient of one row: G = grad_plan + grad_cost[b] * C, C = csign * scores.
@@ -450,16 +452,18 @@ __device__ __forceinline__ void upstream_row(const ImpResArgs& a, size_t off, in
 //   mu_k = (c_k - sum_i P lambda_i) / max(cs_k, 1e-12)   (one exchange)
 // Final phase: grad = P (G - lambda - mu) / tau (cost kind: grad_cost P - that;
 // log-alpha kind: that - grad_cost P) and this workgroup's share of
-// sum(grad * log_alpha) for grad_tau.  MG >= W (exchange_columns).
+// sum(grad * log_alpha) for grad_tau.  MG >= W (exchange_columns).  With
+// `early`, an element's sweeps end once sk::AdjointStop finds them converged.
 template <int VEC, int CH, int RPW, int MG = kMaxGroup>
 __global__ __launch_bounds__(kThreads) void implicit_adjoint(ImpResArgs a) {
     using R = Row<VEC, CH>;
     constexpr int PL = R::PL;
-    // LDS: one row of N per wave | mu N | scratch kWaves
+    // LDS: one row of N per wave | mu N | scratch kWaves | per-wave values of the stop test 2 kWaves
     extern __shared__ float lds[];
     float* part = lds;
     float* lds_mu = lds + kWaves * a.N;
     float* scratch = lds_mu + a.N;
+    float* stopbuf = scratch + kWaves;
     const int lane = threadIdx.x % kWave;
     const int wave = threadIdx.x / kWave;
     const int G = gridDim.x;
@@ -533,11 +537,15 @@ __global__ __launch_bounds__(kThreads) void implicit_adjoint(ImpResArgs a) {
                                          put(cs_own, (j - threadIdx.x) / kThreads, fmaxf(tot, sk::kSumFloor));
                                      });
 
-    // Sweeps.
+    // Sweeps, from mu = 0.  Thread j % kThreads writes (and reads back) column j of
+    // lds_mu in exchange_columns' callback, so its own zeroing needs no barrier.
     float mu[PL];
 #pragma unroll
     for (int e = 0; e < PL; ++e) mu[e] = 0.0f;
+    for (int j = threadIdx.x; j < a.N; j += kThreads) lds_mu[j] = 0.0f;
     float lam_l = 0.0f;
+    sk::AdjointStop stop;
+    int done_t = a.iters;
     for (int t = 1; t <= a.iters; ++t) {
         float d[RPW];  // one dependent chain per row; the rows give the parallelism
 #pragma unroll
@@ -561,15 +569,43 @@ __global__ __launch_bounds__(kThreads) void implicit_adjoint(ImpResArgs a) {
         // the previous sweep.
         R::store(part + wave * a.N, lane, a.N, acc);
         __syncthreads();
+        // this thread's largest |mu_t - mu_{t-1}| and (|c_k| + |sum_i P lambda_i|) / cs_k
+        float dmu = 0.0f, smu = 0.0f;
         exchange_columns<kColRounds<PL>, MG>(part, a.xchg + size_t(t & 1) * G * a.N, a.N, b, a.W, w,
                                              a.tag_base | unsigned(t), local, a.spin_limit, a.status, dead,
                                              a.mark, [&](int j, float tot) {
                                              const int q = (j - threadIdx.x) / kThreads;
-                                             lds_mu[j] = (pick(c_own, q) - tot) / pick(cs_own, q);
+                                             const float cj = pick(c_own, q), csj = pick(cs_own, q);
+                                             const float m = (cj - tot) / csj;
+                                             dmu = fmaxf(dmu, fabsf(m - lds_mu[j]));
+                                             smu = fmaxf(smu, (fabsf(cj) + fabsf(tot)) / csj);
+                                             lds_mu[j] = m;
                                          });
+        if (a.early) {
+            dmu = wave_max(dmu);
+            smu = wave_max(smu);
+            if (lane == 0) {
+                stopbuf[wave] = dmu;
+                stopbuf[kWaves + wave] = smu;
+            }
+        }
         __syncthreads();
         R::load(lds_mu, lane, a.N, mu, 0.0f);
+        if (a.early && t < a.iters) {
+            // The last readers of stopbuf are behind the barrier before the next exchange.
+            float d = stopbuf[0], sm = stopbuf[kWaves];
+#pragma unroll
+            for (int q = 1; q < kWaves; ++q) {
+                d = fmaxf(d, stopbuf[q]);
+                sm = fmaxf(sm, stopbuf[kWaves + q]);
+            }
+            if (stop.done(t, d, sm)) {
+                done_t = t;
+                break;
+            }
+        }
     }
+    if (a.sweeps && w == 0 && threadIdx.x == 0) a.sweeps[b] = done_t;
 
     // Final phase: stream G again and write this workgroup's gradient rows.
     const bool failed = __hip_atomic_load(a.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= a.mark;

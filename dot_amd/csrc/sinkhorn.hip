@@ -139,9 +139,10 @@ ImpLayout imp_layout(void* ws, int B, int M, int N) {
     L.xchg = c.take<unsigned long long>(4 * groups * size_t(N) + 1);
     L.status = reinterpret_cast<int*>(L.xchg ? L.xchg + 4 * groups * size_t(N) : nullptr);
     L.xchg_words = (4 * groups * size_t(N) + 1) * 2;
-    // [2, G, N] sweep rows | [2, B, N] mu | [2, G, N] prologue rows | status
+    // [2, G, N] sweep rows | [2, B, N + kMaxGroups] mu and stop-test scales | [2, G, N] prologue rows | status
     L.pst_groups = pst_groups_max(B, M, N);
-    L.pst = c.take<unsigned long long>(L.pst_groups ? 4 * L.pst_groups * size_t(N) + 2 * size_t(B) * N + 1 : 0);
+    L.pst = c.take<unsigned long long>(
+        L.pst_groups ? 4 * L.pst_groups * size_t(N) + 2 * size_t(B) * (size_t(N) + pst::kMaxGroups) + 1 : 0);
     L.bytes = c.used();
     return L;
 }
@@ -779,7 +780,19 @@ int check_bwd(const dot_sinkhorn_bwd_args* a) {
     if (elems > 0 && (!a->scores || !a->plan || !a->grad_scores))
         return fail(DOT_ERR_INVALID_ARG, "scores, plan and grad_scores must be non-NULL");
     if (a->B > 0 && !a->grad_tau) return fail(DOT_ERR_INVALID_ARG, "grad_tau must be non-NULL");
+    if (a->flags & ~DOT_SK_EXACT_SWEEPS) return fail(DOT_ERR_INVALID_ARG, "unknown flag bits");
     return check_exchange(a->exchange, a->exchange_epoch);
+}
+
+__global__ void fill_int(int32_t* p, int n, int value) {
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = value;
+}
+
+// sweeps_used of a call whose adjoint runs every sweep.
+void report_all_sweeps(const dot_sinkhorn_bwd_args* a, hipStream_t stream) {
+    if (a->sweeps_used && a->B > 0)
+        hipLaunchKernelGGL(fill_int, dim3(unsigned(std::min((a->B + kBlock - 1) / kBlock, 1024))), dim3(kBlock),
+                           0, stream, a->sweeps_used, a->B, a->iters);
 }
 
 bool bwd_vec4(const dot_sinkhorn_bwd_args* a) {
@@ -836,12 +849,15 @@ bool launch_resident_adjoint(const dot_sinkhorn_bwd_args* a, const ImpLayout& L,
     r.R = rc.R;
     r.iters = a->iters;
     r.spin_limit = spin_limit();
+    r.sweeps = a->sweeps_used;
+    r.early = (a->flags & DOT_SK_EXACT_SWEEPS) ? 0 : 1;
     bool ok = false;
     dispatch_resident<false>(rc, [&](auto vc, auto cc, auto rr) {
         constexpr int V = decltype(vc)::value;
         constexpr int C = decltype(cc)::value;
         constexpr int RPW = decltype(rr)::value;
-        const size_t lds = (size_t(res::kWaves + 1) * a->N + res::kWaves) * sizeof(float);
+        // wave rows 8N | mu N | scratch 8 | the stop test's per-wave values 16
+        const size_t lds = (size_t(res::kWaves + 1) * a->N + 3 * res::kWaves) * sizeof(float);
         // elements of at most 4 workgroups poll their exchange from fewer registers
         auto kernel = rc.W <= 4 ? res::implicit_adjoint<V, C, RPW, 4> : res::implicit_adjoint<V, C, RPW>;
         int per_cu = 0;
@@ -874,7 +890,7 @@ bool launch_stream_adjoint(const dot_sinkhorn_bwd_args* a, const ImpLayout& L, c
     r.P = a->plan;
     r.part = L.pst;
     r.res = r.part + 2 * size_t(G) * N;
-    r.pro = r.res + 2 * size_t(B) * N;
+    r.pro = r.res + 2 * size_t(B) * (size_t(N) + pst::kMaxGroups);
     r.status = reinterpret_cast<int*>(r.pro + 2 * size_t(G) * N);
     r.grad = a->grad_scores;
     r.tau_partial = L.tau_partial;
@@ -886,6 +902,8 @@ bool launch_stream_adjoint(const dot_sinkhorn_bwd_args* a, const ImpLayout& L, c
     r.R = sc.R;
     r.iters = a->iters;
     r.spin_limit = spin_limit();
+    r.sweeps = a->sweeps_used;
+    r.early = (a->flags & DOT_SK_EXACT_SWEEPS) ? 0 : 1;
     const size_t words = size_t(reinterpret_cast<unsigned long long*>(r.status) - L.pst) + 1;
     const size_t S = (size_t(N) + sc.W - 1) / sc.W;
     bool ok = false;
@@ -894,7 +912,7 @@ bool launch_stream_adjoint(const dot_sinkhorn_bwd_args* a, const ImpLayout& L, c
         constexpr int C = decltype(cc)::value;
         // fold rows | mu | red N + W | r, 1/rs, lambda R each | c, cs S each | scratch
         const size_t lds =
-            (size_t(pst::kFoldRows<V, C> + 2) * N + sc.W + 3 * size_t(sc.R) + 2 * S + 16) * sizeof(float);
+            (size_t(pst::kFoldRows<V, C> + 2) * N + sc.W + 3 * size_t(sc.R) + 2 * S + 32) * sizeof(float);
         launch_fill_zero(L.pst, 2 * words, stream);
         ProfScope prof("sk_imp_persistent", stream);
         ok = launch_persistent(pst::implicit_adjoint<V, C>, r, G, res::kThreads, lds, stream);
@@ -1070,7 +1088,10 @@ extern "C" int dot_sinkhorn_backward_implicit(const dot_sinkhorn_bwd_args* a, do
     hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
     if (int rc = check_bwd(a)) return rc;
     const int B = a->B, M = a->M, N = a->N;
-    if (size_t(B) * M * N == 0) return bwd_degenerate(a, stream, "dot_sinkhorn_backward_implicit");
+    if (size_t(B) * M * N == 0) {
+        report_all_sweeps(a, stream);
+        return bwd_degenerate(a, stream, "dot_sinkhorn_backward_implicit");
+    }
     const ImpLayout L = imp_layout(a->workspace, B, M, N);
     if (!a->workspace || a->workspace_bytes < L.bytes)
         return fail(DOT_ERR_WORKSPACE,
@@ -1105,6 +1126,7 @@ extern "C" int dot_sinkhorn_backward_implicit(const dot_sinkhorn_bwd_args* a, do
     if (sc.ok && launch_stream_adjoint(a, L, sc, inv_tau, bwd_vec4(a), stream))
         return check_launch("dot_sinkhorn_backward_implicit");
     (void)hipGetLastError();
+    report_all_sweeps(a, stream);  // the per-sweep launches run every sweep
     if (L.nchunks > 1) {
         launch_wide_implicit(a, L, x, inv_tau, stream);
         return check_launch("dot_sinkhorn_backward_implicit");

@@ -358,33 +358,42 @@ __device__ __forceinline__ void load_upstream(const GradSource& g, int b, size_t
 // tiers).  A sweep's lambda_i is a P-weighted average of the previous sweep's
 // mu, and its mu_k a P-weighted average of its lambda (plus constants), so
 // with d_t = max_k |mu_t - mu_{t-1}| every change of lambda after sweep t is
-// at most d_t, each sweep's change is at most the previous one's, and all
-// later changes of lambda_i + mu_k together are at most
-// sum_{j>t} (d_{j-1} + d_j) = d_t (1 + rho) / (1 - rho) when the changes
-// shrink by at least rho per sweep.  The adjoint ends after sweep t when
-//  * d_t = 0: mu is a fixed point and every later sweep would repeat this
-//    one bit for bit, so the result is exactly the full count's; or
-//  * the last three ratios d_j / d_{j-1} are at most kAdjRhoMax and, with rho
-//    their maximum, d_t (1 + rho) / (1 - rho) <= kAdjEps * max_k |mu_t,k|:
-//    what the remaining sweeps could still change is a few units in the last
-//    place of the largest mu, the size of the fp32 rounding of G - lambda - mu
-//    that the gradient carries in any case (past that point the fp32 sweeps
-//    only move within that rounding).
-// Slowly contracting problems (ratios above kAdjRhoMax) run every sweep.
-// d_t and max|mu_t| are the same bits in every workgroup of a batch element
-// (they all hold the same mu), so the element's workgroups stop together.
+// at most d_t and, in exact arithmetic, d_{t+1} <= d_t: all later changes of
+// lambda_i + mu_k together are at most sum_{j>t} (d_{j-1} + d_j)
+// = d_t (1 + rho) / (1 - rho) when the changes shrink by at least rho per
+// sweep.  With s_t = max_k (|c_k| + |sum_i P_ik lambda_i|) / cs_k, the size of
+// the operands of sweep t's mu update (its fp32 rounding is a few units in
+// the last place of s_t), the adjoint ends after sweep t when
+//  (a) d_t = 0: mu is a fixed point and every later sweep would repeat this
+//      one bit for bit, so the result is exactly the full count's;
+//  (b) the last three ratios d_j / d_{j-1} are at most kAdjRhoMax and, with
+//      rho their maximum, d_t (1 + rho) / (1 - rho) <= kAdjEps s_t: what the
+//      remaining sweeps could still change is below the rounding of the
+//      operands; or
+//  (c) d_t >= d_{t-1} and d_t <= kAdjFloor s_t: the change did not shrink,
+//      which exact arithmetic excludes for a nonzero change (the iteration
+//      operator's eigenvalues below 1 are non-negative, and the modes of
+//      eigenvalue 1 are constant offsets that never change), so rounding now
+//      dominates it: the fp32 sweeps have reached their floor (a rounding
+//      cycle) and later sweeps only move within it.
+// Slowly contracting problems (ratios above kAdjRhoMax that never reach the
+// rounding floor) run every sweep.  d_t and s_t are the same bits in every
+// workgroup of a batch element (they all hold the same column sums and mu),
+// so the element's workgroups stop together.
 constexpr float kAdjRhoMax = 0.5f;
-constexpr float kAdjEps = 4.76837158e-7f;  // 2^-21
+constexpr float kAdjEps = 2.38418579e-7f;    // 2^-22
+constexpr float kAdjFloor = 3.81469727e-6f;  // 2^-18
 
 struct AdjointStop {
     float d1 = 0.0f, d2 = 0.0f, d3 = 0.0f;  // changes of the three previous sweeps
 
-    // Sweep t (1-based) changed mu by at most d and ends with max|mu| = s;
+    // Sweep t (1-based) changed mu by at most d, with operands of size s;
     // true when the adjoint ends here.  A NaN (an exchange that timed out)
     // ends it too.
     __device__ __forceinline__ bool done(int t, float d, float s) {
-        bool stop = !(d > 0.0f);
-        if (!stop && t >= 4) {
+        bool stop = !(d > 0.0f);                             // (a)
+        if (!stop && t >= 2) stop = d >= d1 && d <= kAdjFloor * s;  // (c)
+        if (!stop && t >= 4) {                               // (b)
             const float rho = fmaxf(fmaxf(d / d1, d1 / d2), d2 / d3);
             stop = rho <= kAdjRhoMax && d * (1.0f + rho) <= kAdjEps * s * (1.0f - rho);
         }

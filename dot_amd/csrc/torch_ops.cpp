@@ -14,9 +14,11 @@
 #include <ATen/ATen.h>
 #include <c10/core/DeviceGuard.h>
 #include <c10/hip/HIPStream.h>
+#include <hip/hip_runtime_api.h>
 #include <torch/library.h>
 
 #include <cmath>
+#include <cstdlib>
 #include <map>
 #include <mutex>
 #include <string>
@@ -56,19 +58,44 @@ Tensor workspace(size_t bytes, const Tensor& like) {
 // reading words an earlier call left.  Cleared once (and again when the epoch
 // would pass its limit); held until the process ends (the map is never
 // destroyed, so no device memory is freed during interpreter teardown).
+//
+// Two cases get no set ({nullptr, 0}: the library then takes the words from
+// the call's workspace and clears them with a kernel of the call):
+//  * a stream under graph capture: the epoch is fixed when the call is
+//    recorded, so every replay would poll for tags that the previous replay
+//    already wrote; a clearing kernel recorded with the call runs on every
+//    replay instead;
+//  * a stream beyond the first kMaxSetsPerDevice of its device, so that
+//    programs that cycle through many streams do not hold a set for each.
+constexpr size_t kMaxSetsPerDevice = 16;
+
 struct ExchangeSet {
     Tensor words;
     uint32_t epoch = 0;
 };
 
+bool stream_capturing(void* stream) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    return hipStreamIsCapturing(static_cast<hipStream_t>(stream), &cs) != hipSuccess ||
+           cs != hipStreamCaptureStatusNone;
+}
+
 template <size_t (*Bytes)(), uint32_t MaxEpoch>
 std::pair<void*, uint32_t> stream_exchange(const Tensor& like) {
     static std::mutex mu;
     static auto* sets = new std::map<std::pair<int, void*>, ExchangeSet>();
+    static auto* per_device = new std::map<int, size_t>();
     const int dev = like.device().index();
     void* stream = c10::hip::getCurrentHIPStream(dev).stream();
+    if (stream_capturing(stream)) return {nullptr, 0};
     std::lock_guard<std::mutex> lock(mu);
-    ExchangeSet& x = (*sets)[{dev, stream}];
+    auto it = sets->find({dev, stream});
+    if (it == sets->end()) {
+        if ((*per_device)[dev] >= kMaxSetsPerDevice) return {nullptr, 0};
+        ++(*per_device)[dev];
+        it = sets->emplace(std::make_pair(dev, stream), ExchangeSet{}).first;
+    }
+    ExchangeSet& x = it->second;
     if (!x.words.defined() || x.epoch >= MaxEpoch) {
         if (!x.words.defined())
             x.words = at::empty({static_cast<int64_t>(Bytes())}, like.options().dtype(at::kByte));
@@ -315,8 +342,17 @@ Tensor sinkhorn_spectral_preflight_op(Tensor log_alpha, double tau, int64_t n_po
     return tau_est;
 }
 
+// DOT_AMD_EXACT_SWEEPS=1: the implicit adjoint runs exactly backward_iters
+// sweeps (DOT_SK_EXACT_SWEEPS) instead of ending each element once converged.
+int backward_flags() {
+    const char* e = std::getenv("DOT_AMD_EXACT_SWEEPS");
+    return (e && e[0] == '1') ? DOT_SK_EXACT_SWEEPS : 0;
+}
+
 // status_on_host: the status word is pinned host memory that the backward's
-// last kernel writes through, so reading it needs no device-to-host copy.
+// last kernel writes through, so reading it needs no device-to-host copy; it
+// is followed there by the adjoint sweeps executed per batch element
+// (implicit), which the adjoint kernel writes the same way.
 std::vector<Tensor> run_backward(bool implicit, const Tensor& scores_f, int kind, const Tensor& plan,
                                  const optional<Tensor>& grad_plan, const optional<Tensor>& grad_cost,
                                  double tau, int64_t iters, const Tensor& u_hist, const Tensor& v_hist,
@@ -325,7 +361,8 @@ std::vector<Tensor> run_backward(bool implicit, const Tensor& scores_f, int kind
     auto opts = scores_f.options().dtype(at::kFloat);
     Tensor grad = at::empty({B, M, N}, opts);
     Tensor grad_tau = at::empty({B}, opts);
-    Tensor status = status_on_host ? at::empty({1}, at::TensorOptions().dtype(at::kInt).pinned_memory(true))
+    const int64_t words = (status_on_host && implicit) ? 1 + B : 1;
+    Tensor status = status_on_host ? at::empty({words}, at::TensorOptions().dtype(at::kInt).pinned_memory(true))
                                    : at::empty({1}, scores_f.options().dtype(at::kInt));
     const size_t ws_bytes = implicit ? dot_sinkhorn_backward_implicit_workspace_bytes(int(B), int(M), int(N))
                                      : dot_sinkhorn_backward_unrolled_workspace_bytes(int(B), int(M), int(N));
@@ -349,6 +386,8 @@ std::vector<Tensor> run_backward(bool implicit, const Tensor& scores_f, int kind
     a.workspace = ws.data_ptr();
     a.workspace_bytes = ws_bytes;
     a.status = status.data_ptr<int32_t>();
+    a.sweeps_used = words > 1 ? status.data_ptr<int32_t>() + 1 : nullptr;
+    a.flags = implicit ? backward_flags() : 0;
     std::tie(a.exchange, a.exchange_epoch) = sinkhorn_exchange(scores_f);
     const dot_stream_t s = current_stream(scores_f);
     if (implicit) check_rc(dot_sinkhorn_backward_implicit(&a, s), "dot_sinkhorn_backward_implicit");
@@ -390,7 +429,8 @@ std::vector<Tensor> sinkhorn_with_grads_unrolled_op(Tensor log_alpha, Tensor gra
 }
 
 // sinkhorn_with_grads_implicit (torch_cuda.cpp:803-871): forward with tol = 0,
-// then exactly backward_iters adjoint sweeps -> [P, grad_log_alpha, grad_tau].
+// then at most backward_iters adjoint sweeps (exactly that many with
+// DOT_AMD_EXACT_SWEEPS=1) -> [P, grad_log_alpha, grad_tau].
 std::vector<Tensor> sinkhorn_with_grads_implicit_op(Tensor log_alpha, Tensor grad_P, double tau,
                                                     int64_t n_iters, int64_t backward_iters,
                                                     optional<Tensor> log_a, optional<Tensor> log_b) {
@@ -537,10 +577,11 @@ std::vector<Tensor> fused_forward_method_op(Tensor scores, int64_t scores_kind, 
     return {o.plan, cost, o.counts};
 }
 
-// -> [grad_scores, grad_tau (B,), status (int32 [1] in pinned host memory,
-// written by the backward's last kernel: 1 when a cross-workgroup exchange
-// timed out; read it after the stream has passed the call)]; mode 0 implicit
-// (iters = adjoint sweeps), 1 unrolled (iters = T).
+// -> [grad_scores, grad_tau (B,), status (int32 in pinned host memory, written
+// by the backward's kernels: [0] is 1 when a cross-workgroup exchange timed
+// out; implicit mode: [1 + b] the adjoint sweeps batch element b ran; read it
+// after the stream has passed the call)]; mode 0 implicit (iters = adjoint
+// sweeps at most), 1 unrolled (iters = T).
 std::vector<Tensor> fused_backward_op(Tensor scores, int64_t scores_kind, Tensor plan,
                                       optional<Tensor> grad_plan, optional<Tensor> grad_cost,
                                       double tau, int64_t mode, int64_t iters,

@@ -39,7 +39,7 @@ import atexit
 import collections
 import math
 from dataclasses import dataclass
-from typing import Literal, Optional
+from typing import List, Literal, Optional
 
 import torch
 import torch.nn as nn
@@ -97,19 +97,37 @@ class SinkhornResult:
         getattr(self, "n_iters_used")
         state = dict(self.__dict__)
         state.pop("_resolve", None)
+        state.pop("_adjoint", None)
         return state
 
+    @property
+    def adjoint_sweeps(self) -> Optional[List[int]]:
+        """Adjoint sweeps each batch element ran in this result's implicit
+        backward on HIP tensors (waits for that backward; raises if one of its
+        exchanges timed out), or None before a backward ran or on other paths.
+
+        An extension of this build: the register-resident and persistent
+        adjoints end an element's sweeps once they have converged (at most
+        ``backward_iters``; exactly that many with DOT_AMD_EXACT_SWEEPS=1)."""
+        report = self.__dict__.get("_adjoint")
+        if report is None or report.status is None:
+            return None
+        return report.status.sweeps()
+
     @classmethod
-    def _deferred(cls, transport_plan, cost, resolve):
+    def _deferred(cls, transport_plan, cost, resolve, report=None):
         """A result whose (n_iters_used, converged) come from ``resolve()`` on first read.
 
         Until then the two fields are absent from the instance ``__dict__`` (so
         ``vars(result)`` never shows placeholder values); every attribute read,
-        ``dataclasses.asdict``, ``repr``, ``==`` and pickling resolve them first."""
+        ``dataclasses.asdict``, ``repr``, ``==`` and pickling resolve them first.
+        ``report`` (an _AdjointReport) receives the backward's status words."""
         r = cls(transport_plan=transport_plan, cost=cost)
         d = r.__dict__
         del d["n_iters_used"], d["converged"]
         d["_resolve"] = resolve
+        if report is not None:
+            d["_adjoint"] = report
         return r
 
 
@@ -158,7 +176,8 @@ class _DeviceCounts:
 
 class _DeviceStatus(_DeviceCounts):
     """A device backward's int32 status word (1 when a cross-workgroup exchange
-    of the adjoint timed out); ``get()`` raises for it."""
+    of the adjoint timed out), followed for the implicit adjoint by the sweeps
+    each batch element ran; ``get()`` raises for a timeout."""
 
     __slots__ = ()
 
@@ -166,6 +185,20 @@ class _DeviceStatus(_DeviceCounts):
         if words[0] != 0:
             raise RuntimeError(_BWD_TIMEOUT_MESSAGE)
         return True
+
+    def sweeps(self) -> Optional[List[int]]:
+        self.get()
+        words = [int(x) for x in self._host.tolist()]
+        return words[1:] if len(words) > 1 else None
+
+
+class _AdjointReport:
+    """Where a result's backward leaves its _DeviceStatus."""
+
+    __slots__ = ("status",)
+
+    def __init__(self):
+        self.status = None
 
 
 # Device calls whose status nobody has read yet: each new device forward or
@@ -210,9 +243,12 @@ def _track(counts: torch.Tensor) -> _DeviceCounts:
     return dc
 
 
-def _track_status(status: torch.Tensor, device: torch.device) -> None:
+def _track_status(status: torch.Tensor, device: torch.device, report=None) -> None:
     _check_finished_forwards()
-    _unchecked.append(_DeviceStatus(status, device))
+    ds = _DeviceStatus(status, device)
+    _unchecked.append(ds)
+    if report is not None:
+        report.status = ds
 
 
 def _tau_value(tau) -> float:
@@ -237,9 +273,10 @@ class _SinkhornFusedFunction(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, scores, tau, scores_kind, n_iters, backward_iters, log_a, log_b, tol, mode,
-                want_cost):
+                want_cost, report):
         _check_tau_tensor(tau)
         tau_value = _tau_value(tau)
+        ctx.report = report
         needs_grad = ctx.needs_input_grad[0] or (torch.is_tensor(tau) and ctx.needs_input_grad[1])
         keep_history = bool(needs_grad and mode == _MODE_UNROLLED)
         P, cost, counts, u_hist, v_hist = _ops.fused.sinkhorn_forward(
@@ -266,7 +303,7 @@ class _SinkhornFusedFunction(torch.autograd.Function):
         if grad_cost is not None and grad_cost.numel() == 0:
             grad_cost = None
         if grad_P is None and grad_cost is None:
-            return (torch.zeros_like(scores), None, None, None, None, None, None, None, None, None)
+            return (torch.zeros_like(scores),) + (None,) * 10
         if ctx.mode == _MODE_UNROLLED:
             iters = int(counts[0].item())
             uh, vh = u_hist, v_hist
@@ -285,20 +322,21 @@ class _SinkhornFusedFunction(torch.autograd.Function):
             uh,
             vh,
         )
-        _track_status(status, scores.device)
+        _track_status(status, scores.device, ctx.report)
         tau_grad = None
         if ctx.tau_is_tensor and ctx.needs_input_grad[1]:
             tau_grad = grad_tau.sum()
-        return grad_scores.to(ctx.scores_dtype), tau_grad, None, None, None, None, None, None, None, None
+        return (grad_scores.to(ctx.scores_dtype), tau_grad) + (None,) * 9
 
 
-def _run_fused(scores, reg, scores_kind, n_iters, backward_iters, log_a, log_b, tol, mode, want_cost):
+def _run_fused(scores, reg, scores_kind, n_iters, backward_iters, log_a, log_b, tol, mode, want_cost,
+               report=None):
     tau_arg = reg
     if torch.is_tensor(reg):
         tau_arg = reg.reshape(()).to(device=scores.device)
     P, cost, counts = _SinkhornFusedFunction.apply(
         scores, tau_arg, scores_kind, int(n_iters), int(backward_iters), log_a, log_b, float(tol),
-        mode, want_cost
+        mode, want_cost, report
     )
     return P, cost, _track(counts)
 
@@ -337,9 +375,10 @@ class _SinkhornMethodFunction(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, scores, tau, scores_kind, n_iters, backward_iters, log_a, log_b, tol, params,
-                want_cost):
+                want_cost, report):
         _check_tau_tensor(tau)
         tau_value = _tau_value(tau)
+        ctx.report = report
         P, cost, counts = _ops.fused.sinkhorn_forward_method(
             scores, scores_kind, tau_value, n_iters, tol, log_a, log_b, *params, want_cost)
         ctx.mark_non_differentiable(counts)
@@ -362,7 +401,7 @@ class _SinkhornMethodFunction(torch.autograd.Function):
         scores, P, counts, log_a, log_b = ctx.saved_tensors
         log_a = log_a if ctx.has_log_a else None
         log_b = log_b if ctx.has_log_b else None
-        none = (None,) * 9
+        none = (None,) * 10
         if grad_cost is not None and grad_cost.numel() == 0:
             grad_cost = None
         if grad_P is None and grad_cost is None:
@@ -375,7 +414,7 @@ class _SinkhornMethodFunction(torch.autograd.Function):
             grad_P.contiguous() if grad_P is not None else None,
             grad_cost.contiguous() if grad_cost is not None else None,
             ctx.tau, _MODE_IMPLICIT, ctx.backward_iters, None, None)
-        _track_status(status, scores.device)
+        _track_status(status, scores.device, ctx.report)
         if grad_cost is not None:
             # the fused backward's direct cost term used P_vanilla; the cost was
             # computed from this forward's plan (d sum(P C)/dC = P, C = -log_alpha)
@@ -387,13 +426,14 @@ class _SinkhornMethodFunction(torch.autograd.Function):
         return (grad_scores.to(ctx.scores_dtype), tau_grad) + none[1:]
 
 
-def _run_method(scores, reg, scores_kind, n_iters, backward_iters, log_a, log_b, tol, params, want_cost):
+def _run_method(scores, reg, scores_kind, n_iters, backward_iters, log_a, log_b, tol, params, want_cost,
+                report=None):
     tau_arg = reg
     if torch.is_tensor(reg):
         tau_arg = reg.reshape(()).to(device=scores.device)
     P, cost, counts = _SinkhornMethodFunction.apply(
         scores, tau_arg, scores_kind, int(n_iters), int(backward_iters), log_a, log_b, float(tol), params,
-        want_cost)
+        want_cost, report)
     return P, cost, _track(counts)
 
 
@@ -640,6 +680,7 @@ def sinkhorn(
         return SinkhornResult(transport_plan=P, cost=cost, converged=converged, n_iters_used=used)
 
     mode = _MODE_UNROLLED if backward_mode == "unrolled" else _MODE_IMPLICIT
+    report = _AdjointReport() if on_gpu else None
     if cuda_dual and not plain:
         if effective == "anderson":
             _check_anderson_ring(anderson_k, n_iters)
@@ -648,14 +689,14 @@ def sinkhorn(
                   bool(bias_correction), -1.0 if eff_reg_start is None else float(eff_reg_start),
                   _SCHEDULE_CODES[eff_schedule])
         P, cost, counts = _run_method(cost_matrix, reg, SCORES_COST, n_iters, backward_iters, log_a, log_b,
-                                      tol, params, True)
+                                      tol, params, True, report)
         rule = _dual_converged(tol)
     elif on_gpu:
         # dual=False is the reference's full-matrix path: it ignores tol and
         # always runs n_iters (sinkhorn.py:1693 with torch_cuda.cpp:599-656).
         run_tol = tol if dual else 0.0
         P, cost, counts = _run_fused(cost_matrix, reg, SCORES_COST, n_iters, backward_iters,
-                                     log_a, log_b, run_tol, mode, True)
+                                     log_a, log_b, run_tol, mode, True, report)
         rule = _dual_converged(tol) if dual else _count_converged(tol, n_iters)
     else:
         log_alpha = -cost_matrix
@@ -676,7 +717,7 @@ def sinkhorn(
         def resolve():
             used, conv = counts.get()
             return used, rule(used, conv)
-        return SinkhornResult._deferred(P, cost, resolve)
+        return SinkhornResult._deferred(P, cost, resolve, report)
     return SinkhornResult(transport_plan=P, cost=cost, converged=converged, n_iters_used=used)
 
 

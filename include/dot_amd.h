@@ -198,12 +198,31 @@ typedef struct {
                                  timed out (the gradients are then NaN) */
     void* exchange;           /* optional exchange words, as in dot_sinkhorn_fwd_args */
     uint32_t exchange_epoch;
+    int32_t* sweeps_used;     /* implicit only: [B] int32 out (device memory, or pinned host memory the
+                                 device can reach), or NULL: adjoint sweeps executed per batch element */
+    int flags;                /* DOT_SK_EXACT_SWEEPS or 0 */
 } dot_sinkhorn_bwd_args;
 
-/* Implicit-function adjoint: exactly `iters` Gauss-Seidel sweeps
+/* Flag of dot_sinkhorn_bwd_args.flags: run exactly `iters` adjoint sweeps. */
+#define DOT_SK_EXACT_SWEEPS 0x4
+
+/* Implicit-function adjoint: up to `iters` Gauss-Seidel sweeps
  * lambda_i = (sum_k P G - sum_k P mu_k) / max(sum_k P, 1e-12),
  * mu_k = (sum_i P G - sum_i P lambda_i) / max(sum_i P, 1e-12),
  * grad = P (G - lambda_i - mu_k) / tau, grad_tau = -sum(grad * log_alpha) / tau.
+ * Without DOT_SK_EXACT_SWEEPS, shapes that run in one launch (the register-
+ * resident and persistent tiers) end a batch element's sweeps early once
+ * they have converged, with d = max|mu_t - mu_{t-1}| and s the size of the
+ * mu update's operands, max_k (|sum_i P G| + |sum_i P lambda|) / sum_i P:
+ * when a sweep leaves mu unchanged (a fixed point: the result is the full
+ * count's bit for bit); when three successive changes each shrank by at least
+ * half and the geometric bound on everything the remaining sweeps could change
+ * is at most 2^-22 s; or when d did not shrink, which exact arithmetic
+ * excludes for a nonzero change (the sweeps have reached their fp32 rounding
+ * floor), while at most 2^-18 s.  The
+ * reference's GPU op runs every sweep (kernels.cu:1715-1718); its CPU op also
+ * stops early, at a change below 1e-6 (kernels_cpu.cpp:276-312).  Other shapes
+ * run every sweep.  sweeps_used reports what ran.
  * Replaces sinkhorn_backward_implicit_cuda (src/sinkhorn/kernels.cuh:325;
  * kernels.cu:1682-1726) behind sinkhorn_with_grads_implicit
  * (torch_cuda.cpp:803-871; registry.cpp:56). */

@@ -183,8 +183,9 @@ def implicit_backward(log_alpha, P, grad_P, tau: float, iters: int,
     for _ in range(iters):
         if not active.any():
             break
-        lam_new = (r - np.einsum("bik,bk->bi", P, mu)) / rs
-        mu_new = (c - np.einsum("bik,bi->bk", P, lam_new)) / cs
+        # P mu and P^T lambda as batched matrix-vector products (BLAS)
+        lam_new = (r - np.matmul(P, mu[:, :, None])[:, :, 0]) / rs
+        mu_new = (c - np.matmul(lam_new[:, None, :], P)[:, 0, :]) / cs
         change = np.maximum(np.abs(lam_new - lam).max(axis=1, initial=0.0),
                             np.abs(mu_new - mu).max(axis=1, initial=0.0))
         lam = np.where(active[:, None], lam_new, lam)

@@ -741,7 +741,8 @@ class SkBwdArgs(ctypes.Structure):
                 ("iters", ctypes.c_int), ("u_hist", ctypes.c_void_p), ("v_hist", ctypes.c_void_p),
                 ("grad_scores", ctypes.c_void_p), ("grad_tau", ctypes.c_void_p),
                 ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t),
-                ("status", ctypes.c_void_p), ("exchange", ctypes.c_void_p), ("exchange_epoch", ctypes.c_uint32)]
+                ("status", ctypes.c_void_p), ("exchange", ctypes.c_void_p), ("exchange_epoch", ctypes.c_uint32),
+                ("sweeps_used", ctypes.c_void_p), ("flags", ctypes.c_int)]
 
 
 @pytest.mark.parametrize("B,M,N,tau,T,tol", [(16, 512, 512, 0.1, 200, 1e-6), (6, 200, 136, 0.25, 30, 0.0),
