@@ -593,7 +593,8 @@ def main():
         "data": "synthetic (seeded inputs per BASELINE.md section 3)",
         "config": sk["config"],
         "n_iters_used": sk["T_f"],
-        "backward_iters": sk["T_b"],
+        "backward_iters": sk["config"]["backward_iters"],
+        "adjoint_sweeps_executed": sk["T_b"],
         "algorithmic_GBps": sk["algorithmic_GBps"],
         "frac_of_hbm_peak": sk["frac_of_hbm_peak"],
         "frac_of_hbm_peak_note": sk["frac_of_hbm_peak_note"],
