@@ -73,7 +73,14 @@ WORKLOADS = {
     # not a BASELINE configuration: rows of 16384 columns, the strips x chunks
     # tiles of the streaming sweeps (``--workload wide``; never in other_configs)
     "wide": dict(B=4, M=1024, N=16384, reg=0.05, n_iters=100, tol=0.0, seed=6),
+    # not BASELINE configurations: C3's shape, inputs and solver at larger
+    # batches (``batch_scaling`` in the default line): B = 128 and 256 take the
+    # persistent tier, B = 512 the per-iteration sweeps
+    "c3b128": dict(B=128, M=512, N=512, reg=0.1, n_iters=200, tol=1e-6, seed=3),
+    "c3b256": dict(B=256, M=512, N=512, reg=0.1, n_iters=200, tol=1e-6, seed=3),
+    "c3b512": dict(B=512, M=512, N=512, reg=0.1, n_iters=200, tol=1e-6, seed=3),
 }
+BATCH_SCALING = ("c3b128", "c3b256", "c3b512")
 
 
 def _cpu_model() -> str:
@@ -95,7 +102,7 @@ def make_inputs(name: str, torch, device):
     a = b = None
     if name in ("c1", "wide"):
         C = torch.rand(B, M, N, generator=g)
-    elif name == "c3":
+    elif name.startswith("c3"):
         x = torch.randn(B, M, 64, generator=g)
         y = torch.randn(B, N, 64, generator=g)
         C = torch.cdist(x.to(device), y.to(device)).square()
@@ -565,6 +572,15 @@ def main():
             if w != args.workload:
                 others[w] = bench_sinkhorn(args, w, args.steps, min(args.warmup, 2), torch, dot_amd, profiler)
 
+    batch = {}
+    if (not args.headline_only and args.workload == "c3" and args.method == "vanilla" and args.schedule is None
+            and args.backward_mode == "implicit"):
+        for w in BATCH_SCALING:
+            r = bench_sinkhorn(args, w, args.steps, min(args.warmup, 2), torch, dot_amd, profiler)
+            batch[w] = {"ms_per_step": r["ms_per_step"], "ratio_to_c3": r["ms_per_step"] / sk["ms_per_step"],
+                        "T_f": r["T_f"], "T_b": r["T_b"], "value": r["value"], "unit": r["unit"],
+                        "kernels": r["kernels"], "config": r["config"]}
+
     cpu = None
     if not args.no_cpu_baseline:
         cpu = sinkhorn_cpu_baseline(sk["C_cpu"], sk["reg"], sk["a"], sk["b"], args.cpu_seconds)
@@ -608,6 +624,9 @@ def main():
         line["bidirectional_softmax"] = bidi
     if others:
         line["other_configs"] = {w: _public(o) for w, o in others.items()}
+    if batch:
+        line["batch_scaling"] = {"note": "not BASELINE configurations: C3's shape, inputs and solver at B = 128, "
+                                         "256, 512; ratio_to_c3 = ms_per_step over the headline's", **batch}
     print(json.dumps(line), flush=True)
 
 

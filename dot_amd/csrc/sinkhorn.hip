@@ -4,6 +4,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdlib>
+#include <cstring>
 #include <mutex>
 #include <string>
 
@@ -491,14 +492,48 @@ bool launch_resident_forward(const dot_sinkhorn_fwd_args* a, const FwdLayout& L,
     return true;
 }
 
+// The per-iteration forward sweeps with tol > 0 read the device's stop test
+// back after iterations 4, 8, 16, ... (one wait on the stream each) and stop
+// launching once it has fired: delta[t] < tol, where an iteration that did not
+// run left 0.  The launches of a stopped run return at once, but each still
+// costs ~2.5 us of the queue, which at C3's shape (stop at 5 of 200) was most
+// of the step.  Not on a stream under capture: a replay could not re-decide.
+struct StopCheck {
+    const uint32_t* delta;
+    float tol;
+    bool on = false;
+    int rc = DOT_OK;
+
+    StopCheck(const uint32_t* d, float t, int max_iter, hipStream_t stream) : delta(d), tol(t) {
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        on = tol > 0.0f && max_iter > 4 && hipStreamIsCapturing(stream, &cs) == hipSuccess &&
+             cs == hipStreamCaptureStatusNone;
+    }
+
+    // true when iteration t (1-based, just launched) ends the launches
+    bool stopped(int t, int max_iter, hipStream_t stream) {
+        if (!on || t < 4 || (t & (t - 1)) != 0 || t >= max_iter) return false;
+        uint32_t w = 0;
+        if (hipMemcpyAsync(&w, delta + t, sizeof(w), hipMemcpyDeviceToHost, stream) != hipSuccess ||
+            hipStreamSynchronize(stream) != hipSuccess) {
+            rc = fail(DOT_ERR_HIP, "dot_sinkhorn_forward: stop-flag read failed");
+            return true;
+        }
+        float d;
+        std::memcpy(&d, &w, sizeof(d));
+        return d < tol;
+    }
+};
+
 // Rows longer than kMaxRowLen: per iteration a rows pass (chunk partials of
 // the row log-sum-exp), a columns pass (u and the column sums) and the column
 // combine; then the plan in chunk tiles.  The workspace's delta and potential
 // buffers are already cleared.
-void launch_wide_forward(const dot_sinkhorn_fwd_args* a, const FwdLayout& L, const float* ks_host,
-                         float kscale, float log_a_default, float log_b_default, bool keep, bool ret_log,
-                         bool vec4, hipStream_t stream) {
+int launch_wide_forward(const dot_sinkhorn_fwd_args* a, const FwdLayout& L, const float* ks_host,
+                        float kscale, float log_a_default, float log_b_default, bool keep, bool ret_log,
+                        bool vec4, hipStream_t stream) {
     const int B = a->B, M = a->M, N = a->N, T = a->max_iter;
+    StopCheck stop(L.delta, a->tol, T, stream);
     const dim3 tiles = batch_grid(unsigned(L.nstrips) * unsigned(L.nchunks), B);
     const size_t lds = (size_t(2) * wide::kChunk + 8) * sizeof(float);
     wide::dispatch_chunk(vec4, [&](auto vc, auto cc) {
@@ -556,6 +591,7 @@ void launch_wide_forward(const dot_sinkhorn_fwd_args* a, const FwdLayout& L, con
                 ProfScope prof("sk_fwd_combine", stream);
                 hipLaunchKernelGGL(sk::fwd_combine, sk::fold_grid(N, B), dim3(kBlock), 0, stream, cb);
             }
+            if (stop.stopped(t, T, stream)) break;
         }
         {
             ProfScope prof("sk_fwd_finalize", stream);
@@ -590,6 +626,7 @@ void launch_wide_forward(const dot_sinkhorn_fwd_args* a, const FwdLayout& L, con
             }
         }
     });
+    return stop.rc;
 }
 
 }  // namespace
@@ -671,10 +708,13 @@ int dot_amd::sinkhorn_forward_scheduled(const dot_sinkhorn_fwd_args* a, const fl
 
     launch_fill_zero(a->workspace, L.zero_words, stream);
     if (L.nchunks > 1) {
-        launch_wide_forward(a, L, ks_host, kscale, log_a_default, log_b_default, keep, ret_log, vec4, stream);
+        if (int rc = launch_wide_forward(a, L, ks_host, kscale, log_a_default, log_b_default, keep, ret_log, vec4,
+                                         stream))
+            return rc;
         return check_launch("dot_sinkhorn_forward");
     }
 
+    StopCheck stop(L.delta, a->tol, T, stream);
     bool launched = dispatch_row(N, vec4, [&](auto vc, auto cc) {
         constexpr int V = decltype(vc)::value;
         constexpr int C = decltype(cc)::value;
@@ -725,6 +765,7 @@ int dot_amd::sinkhorn_forward_scheduled(const dot_sinkhorn_fwd_args* a, const fl
                 ProfScope prof("sk_fwd_combine", stream);
                 hipLaunchKernelGGL(sk::fwd_combine, sk::fold_grid(N, B), dim3(kBlock), 0, stream, cb);
             }
+            if (stop.stopped(t, T, stream)) break;
         }
         {
             ProfScope prof("sk_fwd_finalize", stream);
@@ -761,6 +802,7 @@ int dot_amd::sinkhorn_forward_scheduled(const dot_sinkhorn_fwd_args* a, const fl
         }
     });
     if (!launched) return fail(DOT_ERR_UNSUPPORTED, "row length outside the supported range");
+    if (stop.rc) return stop.rc;
     return check_launch("dot_sinkhorn_forward");
 }
 
@@ -822,9 +864,11 @@ int bwd_degenerate(const dot_sinkhorn_bwd_args* a, hipStream_t stream, const cha
 namespace {
 
 // Launch of the register-resident adjoint; false when this shape or
-// device cannot host it (the caller then runs the streaming sweeps).
+// device cannot host it (the caller then runs the next tier).  keep_status:
+// a later slab of the call (launch_resident_slabs), which must not clear the
+// failure mark an earlier slab left in a->status.
 bool launch_resident_adjoint(const dot_sinkhorn_bwd_args* a, const ImpLayout& L, const ResidentCfg& rc,
-                             float inv_tau, hipStream_t stream) {
+                             float inv_tau, hipStream_t stream, bool keep_status = false) {
     const int groups = a->B * rc.W;
     if (!L.xchg || size_t(groups) > L.groups) return false;
     res::ImpResArgs r{};
@@ -874,7 +918,44 @@ bool launch_resident_adjoint(const dot_sinkhorn_bwd_args* a, const ImpLayout& L,
     if (!ok) return false;
     ProfScope prof("sk_batch_sum", stream);
     hipLaunchKernelGGL(sk::batch_sum, dim3(a->B), dim3(kWave), 0, stream, L.tau_partial, rc.W,
-                       -inv_tau, a->grad_tau, tg.status, a->status, tg.mark);
+                       -inv_tau, a->grad_tau, tg.status, a->status, tg.mark, keep_status ? 1 : 0);
+    return true;
+}
+
+// Elements per launch of the register-resident adjoint at this shape (the
+// most that fit the chip's registers at once), or 0 when one does not fit.
+int resident_slab(int B, int M, int N, bool vec4) {
+    const ResidentCfg one = resident_config<false>(1, M, N, vec4);
+    if (!one.ok) return 0;
+    return std::min(B, std::max(1, std::min(device_cus(), 1024) / one.W));
+}
+
+// A batch larger than the register-resident adjoint holds at once, in slabs
+// of `slab` elements, one launch each on the stream.  The adjoint couples no
+// batch elements, so every slab computes exactly its elements' share of the
+// call; each launch clears its own workspace exchange words (caller-owned
+// words would repeat one epoch across the slabs).  False when a slab cannot
+// be hosted (every slab has the first one's shape, or a smaller batch of it);
+// the caller then runs the whole batch on the next tier, which overwrites
+// every output.
+bool launch_resident_slabs(const dot_sinkhorn_bwd_args* a, const ImpLayout& L, int slab, float inv_tau,
+                           hipStream_t stream) {
+    const size_t MN = size_t(a->M) * a->N;
+    for (int b0 = 0; b0 < a->B; b0 += slab) {
+        dot_sinkhorn_bwd_args s = *a;
+        s.B = std::min(slab, a->B - b0);
+        s.scores = a->scores + b0 * MN;
+        s.plan = a->plan + b0 * MN;
+        s.grad_plan = a->grad_plan ? a->grad_plan + b0 * MN : nullptr;
+        s.grad_cost = a->grad_cost ? a->grad_cost + b0 : nullptr;
+        s.grad_scores = a->grad_scores + b0 * MN;
+        s.grad_tau = a->grad_tau + b0;
+        s.sweeps_used = a->sweeps_used ? a->sweeps_used + b0 : nullptr;
+        s.exchange = nullptr;
+        s.exchange_epoch = 0;
+        const ResidentCfg rc = resident_config<false>(s.B, s.M, s.N, bwd_vec4(&s));
+        if (!rc.ok || !launch_resident_adjoint(&s, L, rc, inv_tau, stream, b0 > 0)) return false;
+    }
     return true;
 }
 
@@ -1121,7 +1202,16 @@ extern "C" int dot_sinkhorn_backward_implicit(const dot_sinkhorn_bwd_args* a, do
     const ResidentCfg rc = resident_config<false>(B, M, N, bwd_vec4(a));
     if (rc.ok && launch_resident_adjoint(a, L, rc, inv_tau, stream))
         return check_launch("dot_sinkhorn_backward_implicit");
-    (void)hipGetLastError();  // a refused cooperative launch falls back to the next tier
+    (void)hipGetLastError();  // a refused launch falls back to the next tier
+    if (!rc.ok) {
+        const int slab = resident_slab(B, M, N, bwd_vec4(a));
+        if (slab > 0 && slab < B) {
+            if (launch_resident_slabs(a, L, slab, inv_tau, stream))
+                return check_launch("dot_sinkhorn_backward_implicit");
+            if (int e = check_launch("dot_sinkhorn_backward_implicit")) return e;
+            (void)hipGetLastError();
+        }
+    }
     const StreamCfg sc = stream_config(B, M, N);
     if (sc.ok && launch_stream_adjoint(a, L, sc, inv_tau, bwd_vec4(a), stream))
         return check_launch("dot_sinkhorn_backward_implicit");

@@ -296,14 +296,22 @@ __global__ __launch_bounds__(kBlock) void materialize(MaterializeArgs a) {
 // kernel on the stream, so the word is final.
 // status_out (block 0): 1 when *status_in has reached `mark` (the call's
 // failure mark, 1 for a status word cleared for the call), else 0.
+// Per-element sums of nblk partials; block 0 also turns the exchange status
+// into the caller's status word (1 when a wait gave up), or with `keep` raises
+// it only, so that a failure of an earlier launch of the call stays visible.
 static __global__ void batch_sum(const float* partial, int nblk, float scale, float* out,
-                                 const int* status_in = nullptr, int32_t* status_out = nullptr, int mark = 1) {
+                                 const int* status_in = nullptr, int32_t* status_out = nullptr, int mark = 1,
+                                 int keep = 0) {
     const int b = blockIdx.x;
     float s = 0.0f;
     for (int k = threadIdx.x; k < nblk; k += kWave) s += partial[size_t(b) * nblk + k];
     s = wave_sum(s);
     if (threadIdx.x == 0) out[b] = s * scale;
-    if (status_out && b == 0 && threadIdx.x == 0) *status_out = status_in ? (*status_in >= mark) : 0;
+    if (status_out && b == 0 && threadIdx.x == 0) {
+        const int failed = status_in ? (*status_in >= mark) : 0;
+        if (!keep) *status_out = failed;
+        else if (failed) *status_out = 1;
+    }
 }
 
 static __global__ void fill_zero(uint32_t* p, size_t n) {

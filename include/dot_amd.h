@@ -90,7 +90,12 @@ typedef struct {
  * primal sinkhorn_forward_cuda (kernels.cuh:61) behind the sinkhorn /
  * sinkhorn_log ops (torch_cuda.cpp:599-715), and
  * sinkhorn_dual_forward_with_intermediates_cuda (kernels.cuh:164) when
- * DOT_SK_KEEP_HISTORY is set.  Ops: src/sinkhorn/registry.cpp:31-45. */
+ * DOT_SK_KEEP_HISTORY is set.  Ops: src/sinkhorn/registry.cpp:31-45.
+ * Shapes beyond the one-launch tiers (batches larger than the chip holds,
+ * rows longer than 4096 columns) run one launch pair per iteration; with
+ * tol > 0 those calls read the device's stop test back after iterations 4, 8,
+ * 16, ... (a wait on `stream` each, not while the stream is captured) and
+ * stop launching once it has fired. */
 /* For shapes that take the persistent streaming tier the workspace includes
  * room for a scaled copy of the kernel ([B,M,N] floats) that lets that tier
  * iterate without an exponential per element; a workspace of at least the

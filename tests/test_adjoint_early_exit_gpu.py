@@ -174,3 +174,28 @@ def test_config_c5_one_element_full_count():
     assert rel_err(res.transport_plan, Po) < FWD_TOL
     assert rel_err(gr, go) < GRAD_TOL
     assert res.adjoint_sweeps[0] < 1000
+
+
+@pytest.mark.parametrize("B", [128, 300])
+def test_c3_shape_at_larger_batches(B):
+    """C3's shape, inputs and solver at B = 128 (persistent forward) and B =
+    300 (per-iteration forward sweeps); both adjoints run as slabs of the
+    register-resident adjoint (64 elements each at 512 x 512), which end
+    early: the forward's stop count, and the first and last element of the
+    first and last slab against the float64 oracle (plan at the run's count,
+    cost gradient after the full 200 sweeps)."""
+    g = torch.Generator().manual_seed(3)
+    x, y = torch.randn(B, 512, 64, generator=g), torch.randn(B, 512, 64, generator=g)
+    C = torch.cdist(x.to(DEV), y.to(DEV)).square()
+    C = (C / C.amax(dim=(-2, -1), keepdim=True)).contiguous()
+    res, gr = _run(C, 0.1, 200, 200, tol=1e-6)
+    T = res.n_iters_used
+    sweeps = res.adjoint_sweeps
+    print(f"[early-end] C3 shape B={B}: T_f={T} sweeps min {min(sweeps)} max {max(sweeps)}", flush=True)
+    assert res.converged and abs(T - 5) <= 1
+    Cn = C.cpu().numpy()
+    for b in (0, 63, 64, B - 1):
+        Po, go = _oracle_grad(Cn[b:b + 1], 0.1, T, 200)
+        assert rel_err(res.transport_plan[b:b + 1], Po) < FWD_TOL, b
+        assert rel_err(gr[b:b + 1], go) < GRAD_TOL, b
+    assert max(sweeps) < 200

@@ -854,6 +854,47 @@ def test_persistent_forward_scaled_kernel_matches_log_domain(B, M, N, tau, T, to
         assert abs(out["scaled"][2][0] - out["log"][2][0]) <= 1
 
 
+def test_config_c5_forward_scaled_matches_log_domain_full_count():
+    """C5 at its full count (4 x 4096^2, reg 0.02, 1000 iterations, tol 1e-6):
+    the default persistent forward streams the scaled kernel (scaling domain
+    while the range of v allows); the same call with a workspace that has no
+    room for it runs the log domain, which the oracle pins at short counts
+    (test_persistent_forward_scaled_kernel_matches_log_domain,
+    test_config_c5_full_size).  The two 1000-iteration plans and costs agree
+    within 1e-5."""
+    lib = ctypes.CDLL(os.path.join(ROOT, "dot_amd", "libdot_amd.so"))
+    lib.dot_sinkhorn_forward_workspace_bytes.restype = ctypes.c_size_t
+    lib.dot_sinkhorn_forward.argtypes = [ctypes.POINTER(SkFwdArgs), ctypes.c_void_p]
+    g = torch.Generator().manual_seed(5)
+    x, y = torch.randn(4, 4096, 128, generator=g), torch.randn(4, 4096, 128, generator=g)
+    C = torch.cdist(x.to(DEV), y.to(DEV))
+    C = (C / C.amax(dim=(-2, -1), keepdim=True)).contiguous()
+    B, M, N, T = 4, 4096, 4096, 1000
+    full = lib.dot_sinkhorn_forward_workspace_bytes(B, M, N, T, 0)
+    ek = (B * M * N * 4 + 255) // 256 * 256
+    assert full > ek
+    ws = torch.empty(full, dtype=torch.uint8, device=DEV)
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    out = {}
+    for name, nbytes in (("scaled", full), ("log", full - ek)):
+        P = torch.empty_like(C)
+        cost = torch.empty(B, device=DEV)
+        counts = torch.zeros(2, dtype=torch.int32, device=DEV)
+        f = SkFwdArgs(C.data_ptr(), None, None, B, M, N, -1, 0.02, T, 1e-6, 0, P.data_ptr(), cost.data_ptr(),
+                      None, None, None, None, counts.data_ptr(), counts.data_ptr() + 4, ws.data_ptr(), nbytes,
+                      None, 0)
+        assert lib.dot_sinkhorn_forward(ctypes.byref(f), stream) == 0
+        torch.cuda.synchronize()
+        out[name] = (P, cost, [int(v) for v in counts.tolist()])
+    print(f"[sk_gpu] C5 full count: counts {out['scaled'][2]} {out['log'][2]}", flush=True)
+    assert out["scaled"][2] == out["log"][2] == [T, 0]
+    (Ps, cs, _), (Pl, cl, _) = out["scaled"], out["log"]
+    assert rel_err(Ps, Pl.cpu().numpy()) < FWD_TOL
+    assert rel_err(cs, cl.cpu().numpy()) < FWD_TOL
+    for P in (Ps, Pl):
+        assert torch.allclose(P.sum(-2), torch.full_like(P.sum(-2), 1 / 4096), rtol=1e-4, atol=0)
+
+
 def test_resident_launches_on_two_streams():
     """Resident forwards and adjoints enqueued on two streams with no host wait
     in between, each batch filling the device: the library orders its exchange
