@@ -664,6 +664,7 @@ struct ImpArgs {
     int scores_kind;
     const float* gP;      // [B,M,N] or null
     const float* gC;      // [B] or null
+    int gc_step;          // 1, or 0: gC holds one value for every batch element
     const float* P;       // [B,M,N]
     unsigned long long* part;  // [2, G, N] tagged workgroup column sums
     unsigned long long* res;   // [2, B, N + kMaxGroups] tagged mu, then each slice owner's stop-test scale
@@ -731,7 +732,7 @@ __global__ __launch_bounds__(kThreads) void implicit_adjoint(ImpArgs a) {
     float* scratch = lds_cs + S;
     const size_t bM = size_t(b) * a.M;
     const bool cost_kind = a.scores_kind < 0;
-    const float gc = a.gC ? a.gC[b] : 0.0f;
+    const float gc = a.gC ? a.gC[b * a.gc_step] : 0.0f;
     const float csign = cost_kind ? 1.0f : -1.0f;  // C = csign * scores
     bool dead = false;
     res::announce_xcc(a.part, a.N, b, a.W, w);
@@ -882,6 +883,7 @@ struct UnrArgs {
     float kscale;          // K = X * kscale
     const float* gP;       // [B,M,N] or null
     const float* gC;       // [B] or null
+    int gc_step;           // 1, or 0: gC holds one value for every batch element
     const float* P;        // [B,M,N]
     const float* u_hist;   // [T,B,M]
     const float* v_hist;   // [T,B,N]
@@ -924,7 +926,7 @@ __global__ __launch_bounds__(kThreads) void unrolled(UnrArgs a) {
     float* scratch = red + a.N + a.W;
     const size_t bM = size_t(b) * a.M;
     const bool cost_kind = a.scores_kind < 0;
-    const float gc = a.gC ? a.gC[b] : 0.0f;
+    const float gc = a.gC ? a.gC[b * a.gc_step] : 0.0f;
     const float csign = cost_kind ? 1.0f : -1.0f;  // C = csign * scores
     bool dead = false;
     float tacc = 0.0f;

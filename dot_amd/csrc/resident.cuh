@@ -411,6 +411,7 @@ struct ImpResArgs {
     int scores_kind;
     const float* gP;           // [B,M,N] or null
     const float* gC;           // [B] or null
+    int gc_step;               // 1, or 0: gC holds one value for every batch element
     const float* P;            // [B,M,N]
     unsigned long long* xchg;  // [2, G, N] tagged sweep column sums
     unsigned long long* pro;   // [2, G, N] tagged prologue column sums (P G, then P)
@@ -474,7 +475,7 @@ __global__ __launch_bounds__(kThreads) void implicit_adjoint(ImpResArgs a) {
     const int rend = min(row0 + a.R, a.M);
     const size_t bM = size_t(b) * a.M;
     const bool cost_kind = a.scores_kind < 0;
-    const float gc = a.gC ? a.gC[b] : 0.0f;
+    const float gc = a.gC ? a.gC[b * a.gc_step] : 0.0f;
     const float csign = cost_kind ? 1.0f : -1.0f;  // C = csign * scores
     bool dead = false;
     announce_xcc(a.xchg, a.N, b, a.W, w, a.xcc_tag);

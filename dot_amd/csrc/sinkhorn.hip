@@ -822,7 +822,8 @@ int check_bwd(const dot_sinkhorn_bwd_args* a) {
     if (elems > 0 && (!a->scores || !a->plan || !a->grad_scores))
         return fail(DOT_ERR_INVALID_ARG, "scores, plan and grad_scores must be non-NULL");
     if (a->B > 0 && !a->grad_tau) return fail(DOT_ERR_INVALID_ARG, "grad_tau must be non-NULL");
-    if (a->flags & ~DOT_SK_EXACT_SWEEPS) return fail(DOT_ERR_INVALID_ARG, "unknown flag bits");
+    if (a->flags & ~(DOT_SK_EXACT_SWEEPS | DOT_SK_GRAD_COST_SCALAR))
+        return fail(DOT_ERR_INVALID_ARG, "unknown flag bits");
     return check_exchange(a->exchange, a->exchange_epoch);
 }
 
@@ -848,6 +849,7 @@ sk::GradSource grad_source(const dot_sinkhorn_bwd_args* a) {
     g.scores_kind = a->scores_kind;
     g.gP = a->grad_plan;
     g.gC = a->grad_cost;
+    g.gc_step = (a->flags & DOT_SK_GRAD_COST_SCALAR) ? 0 : 1;
     return g;
 }
 
@@ -876,6 +878,7 @@ bool launch_resident_adjoint(const dot_sinkhorn_bwd_args* a, const ImpLayout& L,
     r.scores_kind = a->scores_kind;
     r.gP = a->grad_plan;
     r.gC = a->grad_cost;
+    r.gc_step = (a->flags & DOT_SK_GRAD_COST_SCALAR) ? 0 : 1;
     r.P = a->plan;
     const Tagging tg = tagging(a->exchange, a->exchange_epoch, a->iters, L.xchg, L.status);
     r.xchg = tg.slots;
@@ -947,7 +950,7 @@ bool launch_resident_slabs(const dot_sinkhorn_bwd_args* a, const ImpLayout& L, i
         s.scores = a->scores + b0 * MN;
         s.plan = a->plan + b0 * MN;
         s.grad_plan = a->grad_plan ? a->grad_plan + b0 * MN : nullptr;
-        s.grad_cost = a->grad_cost ? a->grad_cost + b0 : nullptr;
+        s.grad_cost = a->grad_cost ? a->grad_cost + ((a->flags & DOT_SK_GRAD_COST_SCALAR) ? 0 : b0) : nullptr;
         s.grad_scores = a->grad_scores + b0 * MN;
         s.grad_tau = a->grad_tau + b0;
         s.sweeps_used = a->sweeps_used ? a->sweeps_used + b0 : nullptr;
@@ -968,6 +971,7 @@ bool launch_stream_adjoint(const dot_sinkhorn_bwd_args* a, const ImpLayout& L, c
     r.scores_kind = a->scores_kind;
     r.gP = a->grad_plan;
     r.gC = a->grad_cost;
+    r.gc_step = (a->flags & DOT_SK_GRAD_COST_SCALAR) ? 0 : 1;
     r.P = a->plan;
     r.part = L.pst;
     r.res = r.part + 2 * size_t(G) * N;
@@ -1073,6 +1077,7 @@ bool launch_stream_unrolled(const dot_sinkhorn_bwd_args* a, const UnrLayout& L, 
     r.kscale = float(a->scores_kind) * inv_tau;
     r.gP = a->grad_plan;
     r.gC = a->grad_cost;
+    r.gc_step = (a->flags & DOT_SK_GRAD_COST_SCALAR) ? 0 : 1;
     r.P = a->plan;
     r.u_hist = a->u_hist;
     r.v_hist = a->v_hist;

@@ -337,6 +337,7 @@ struct GradSource {
     int scores_kind;
     const float* gP;   // [B,M,N] or null
     const float* gC;   // [B] or null
+    int gc_step;       // 1, or 0: gC holds one value for every batch element
 };
 
 template <int VEC, int CH>
@@ -351,7 +352,7 @@ __device__ __forceinline__ void load_upstream(const GradSource& g, int b, size_t
         for (int e = 0; e < R::PL; ++e) G[e] = 0.0f;
     }
     if (g.gC) {
-        const float gc = g.gC[b];
+        const float gc = g.gC[b * g.gc_step];
         const float csign = g.scores_kind < 0 ? 1.0f : -1.0f;
 #pragma unroll
         for (int e = 0; e < R::PL; ++e) G[e] += gc * (csign * x[e]);
@@ -552,7 +553,7 @@ __global__ __launch_bounds__(kBlock) void imp_final(ImpArgs a) {
     const int r1 = min(r0 + a.rows, a.M);
     const size_t bM = size_t(b) * a.M;
     const bool cost_kind = a.g.scores_kind < 0;
-    const float gc = a.g.gC ? a.g.gC[b] : 0.0f;
+    const float gc = a.g.gC ? a.g.gC[b * a.g.gc_step] : 0.0f;
     float mu[R::PL];
     R::load(a.mu + size_t(b) * a.N, lane, a.N, mu, 0.0f);
     float tacc = 0.0f;
@@ -603,7 +604,7 @@ __device__ __forceinline__ void unr_epilogue(const UnrArgs& a, int b, size_t off
                                              const float (&x)[VEC * CH], float& tacc) {
     using R = Row<VEC, CH>;
     const bool cost_kind = a.g.scores_kind < 0;
-    const float gc = a.g.gC ? a.g.gC[b] : 0.0f;
+    const float gc = a.g.gC ? a.g.gC[b * a.g.gc_step] : 0.0f;
     float o[R::PL];
 #pragma unroll
     for (int e = 0; e < R::PL; ++e) {

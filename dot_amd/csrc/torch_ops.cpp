@@ -137,16 +137,21 @@ struct ForwardOut {
 };
 
 // One call of dot_sinkhorn_forward; counts = int32 [2] on the device: (iters_used, converged).
+// counts_on_host: [iters_used, converged] go to pinned host memory, written
+// there by the forward's last kernel (no device-to-host copy); valid once the
+// stream has passed the call.
 ForwardOut run_forward(const Tensor& scores_f, int kind, double tau, int64_t n_iters, double tol,
                        const optional<Tensor>& log_a_f, const optional<Tensor>& log_b_f,
-                       bool return_log, bool want_plan, bool want_cost, bool keep_history) {
+                       bool return_log, bool want_plan, bool want_cost, bool keep_history,
+                       bool counts_on_host = false) {
     const int64_t B = scores_f.size(0), M = scores_f.size(1), N = scores_f.size(2);
     TORCH_CHECK(n_iters <= INT32_MAX, "n_iters too large");
     auto opts = scores_f.options().dtype(at::kFloat);
     ForwardOut o;
     if (want_plan) o.plan = at::empty({B, M, N}, opts);
     if (want_cost) o.cost = at::empty({B}, opts);
-    o.counts = at::empty({2}, scores_f.options().dtype(at::kInt));
+    o.counts = counts_on_host ? at::empty({2}, at::TensorOptions().dtype(at::kInt).pinned_memory(true))
+                              : at::empty({2}, scores_f.options().dtype(at::kInt));
     const int flags = (return_log ? DOT_SK_RETURN_LOG : 0) | (keep_history ? DOT_SK_KEEP_HISTORY : 0);
     if (keep_history) {
         o.u_hist = at::empty({n_iters, B, M}, opts);
@@ -353,10 +358,11 @@ int backward_flags() {
 // last kernel writes through, so reading it needs no device-to-host copy; it
 // is followed there by the adjoint sweeps executed per batch element
 // (implicit), which the adjoint kernel writes the same way.
+// grad_cost_scalar: grad_cost holds one value that is every batch element's.
 std::vector<Tensor> run_backward(bool implicit, const Tensor& scores_f, int kind, const Tensor& plan,
                                  const optional<Tensor>& grad_plan, const optional<Tensor>& grad_cost,
                                  double tau, int64_t iters, const Tensor& u_hist, const Tensor& v_hist,
-                                 bool status_on_host = false) {
+                                 bool status_on_host = false, bool grad_cost_scalar = false) {
     const int64_t B = scores_f.size(0), M = scores_f.size(1), N = scores_f.size(2);
     auto opts = scores_f.options().dtype(at::kFloat);
     Tensor grad = at::empty({B, M, N}, opts);
@@ -387,7 +393,7 @@ std::vector<Tensor> run_backward(bool implicit, const Tensor& scores_f, int kind
     a.workspace_bytes = ws_bytes;
     a.status = status.data_ptr<int32_t>();
     a.sweeps_used = words > 1 ? status.data_ptr<int32_t>() + 1 : nullptr;
-    a.flags = implicit ? backward_flags() : 0;
+    a.flags = (implicit ? backward_flags() : 0) | (grad_cost_scalar ? DOT_SK_GRAD_COST_SCALAR : 0);
     std::tie(a.exchange, a.exchange_epoch) = sinkhorn_exchange(scores_f);
     const dot_stream_t s = current_stream(scores_f);
     if (implicit) check_rc(dot_sinkhorn_backward_implicit(&a, s), "dot_sinkhorn_backward_implicit");
@@ -541,7 +547,8 @@ std::vector<Tensor> bidirectional_softmax_backward_op(Tensor sim, Tensor output,
 // torch.ops.dot_amd.* fused operators (HIP only)
 // ---------------------------------------------------------------------------
 
-// -> [P, cost (B,) or undefined, counts int32[2] on device, u_hist, v_hist]
+// -> [P, cost (B,) or undefined, counts int32[2] in pinned host memory (written by the
+// forward's last kernel; read them once the stream has passed the call), u_hist, v_hist]
 std::vector<Tensor> fused_forward_op(Tensor scores, int64_t scores_kind, double tau, int64_t n_iters,
                                      double tol, optional<Tensor> log_a, optional<Tensor> log_b,
                                      bool want_cost, bool keep_history) {
@@ -551,7 +558,7 @@ std::vector<Tensor> fused_forward_op(Tensor scores, int64_t scores_kind, double 
     check_marginals(log_a, log_b, scores.size(0), scores.size(1), scores.size(2));
     c10::OptionalDeviceGuard guard(scores.device());
     ForwardOut o = run_forward(f32c(scores), int(scores_kind), tau, n_iters, tol, f32c_opt(log_a),
-                               f32c_opt(log_b), false, true, want_cost, keep_history);
+                               f32c_opt(log_b), false, true, want_cost, keep_history, /*counts_on_host=*/true);
     auto or_empty = [&](const Tensor& t) { return t.defined() ? t : at::empty({0}, scores.options().dtype(at::kFloat)); };
     return {o.plan, or_empty(o.cost), o.counts, or_empty(o.u_hist), or_empty(o.v_hist)};
 }
@@ -585,7 +592,7 @@ std::vector<Tensor> fused_forward_method_op(Tensor scores, int64_t scores_kind, 
 std::vector<Tensor> fused_backward_op(Tensor scores, int64_t scores_kind, Tensor plan,
                                       optional<Tensor> grad_plan, optional<Tensor> grad_cost,
                                       double tau, int64_t mode, int64_t iters,
-                                      optional<Tensor> u_hist, optional<Tensor> v_hist) {
+                                      optional<Tensor> u_hist, optional<Tensor> v_hist, bool grad_cost_scalar) {
     check_hip_input(scores, "scores");
     check_hip_input(plan, "plan");
     TORCH_CHECK(scores.dim() == 3 && plan.sizes() == scores.sizes(), "plan must match scores");
@@ -593,7 +600,8 @@ std::vector<Tensor> fused_backward_op(Tensor scores, int64_t scores_kind, Tensor
     TORCH_CHECK(iters >= 0, "iters must be >= 0");
     if (grad_plan.has_value()) TORCH_CHECK(grad_plan->sizes() == scores.sizes(), "grad_plan shape");
     if (grad_cost.has_value())
-        TORCH_CHECK(grad_cost->dim() == 1 && grad_cost->size(0) == scores.size(0), "grad_cost shape");
+        TORCH_CHECK(grad_cost->dim() == 1 && grad_cost->size(0) == (grad_cost_scalar ? 1 : scores.size(0)),
+                    "grad_cost shape");
     c10::OptionalDeviceGuard guard(scores.device());
     Tensor uh = u_hist.has_value() ? f32c(*u_hist) : Tensor();
     Tensor vh = v_hist.has_value() ? f32c(*v_hist) : Tensor();
@@ -601,7 +609,7 @@ std::vector<Tensor> fused_backward_op(Tensor scores, int64_t scores_kind, Tensor
         TORCH_CHECK(uh.defined() && vh.defined() && uh.size(0) >= iters && vh.size(0) >= iters,
                     "unrolled backward needs the u/v history of every iteration");
     return run_backward(mode == 0, f32c(scores), int(scores_kind), f32c(plan), f32c_opt(grad_plan),
-                        f32c_opt(grad_cost), tau, iters, uh, vh, /*status_on_host=*/true);
+                        f32c_opt(grad_cost), tau, iters, uh, vh, /*status_on_host=*/true, grad_cost_scalar);
 }
 
 // -> [out, row_stats (B,2,L1), col_stats (B,2,L2)]; no lengths: every element full
@@ -683,7 +691,7 @@ TORCH_LIBRARY_IMPL(dot, CUDA, m) {
 TORCH_LIBRARY(dot_amd, m) {
     m.def("sinkhorn_forward(Tensor scores, int scores_kind, float tau, int n_iters, float tol, Tensor? log_a, Tensor? log_b, bool want_cost, bool keep_history) -> Tensor[]");
     m.def("sinkhorn_forward_method(Tensor scores, int scores_kind, float tau, int n_iters, float tol, Tensor? log_a, Tensor? log_b, int method, float omega, int anderson_k, float mixing_beta, float lr, float beta1, float beta2, float eps_adam, bool bias_correction, float reg_start, int schedule, bool want_cost) -> Tensor[]");
-    m.def("sinkhorn_backward(Tensor scores, int scores_kind, Tensor plan, Tensor? grad_plan, Tensor? grad_cost, float tau, int mode, int iters, Tensor? u_hist, Tensor? v_hist) -> Tensor[]");
+    m.def("sinkhorn_backward(Tensor scores, int scores_kind, Tensor plan, Tensor? grad_plan, Tensor? grad_cost, float tau, int mode, int iters, Tensor? u_hist, Tensor? v_hist, bool grad_cost_scalar=False) -> Tensor[]");
     m.def("bidirectional_softmax_forward(Tensor sim, float tau, Tensor? lengths) -> Tensor[]");
     m.def("bidirectional_softmax_backward(Tensor sim, Tensor grad_output, Tensor row_stats, Tensor col_stats, float tau, Tensor? lengths) -> Tensor[]");
 }

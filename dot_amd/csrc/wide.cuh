@@ -336,7 +336,7 @@ __global__ __launch_bounds__(kBlock) void imp_final(ImpArgs w) {
     const int r1 = min(r0 + a.rows, a.M);
     const size_t bM = size_t(b) * a.M;
     const bool cost_kind = a.g.scores_kind < 0;
-    const float gc = a.g.gC ? a.g.gC[b] : 0.0f;
+    const float gc = a.g.gC ? a.g.gC[b * a.g.gc_step] : 0.0f;
     float mu[R::PL];
     R::load(a.mu + size_t(b) * a.N + tl.c0, lane, tl.nc, mu, 0.0f);
     float tacc = 0.0f;
@@ -375,7 +375,7 @@ __device__ __forceinline__ void unr_epilogue(const sk::UnrArgs& a, int b, size_t
                                              const float (&x)[VEC * CH], float& tacc) {
     using R = Row<VEC, CH>;
     const bool cost_kind = a.g.scores_kind < 0;
-    const float gc = a.g.gC ? a.g.gC[b] : 0.0f;
+    const float gc = a.g.gC ? a.g.gC[b * a.g.gc_step] : 0.0f;
     float o[R::PL];
 #pragma unroll
     for (int e = 0; e < R::PL; ++e) {

@@ -121,7 +121,7 @@ class SinkhornResult:
         Until then the two fields are absent from the instance ``__dict__`` (so
         ``vars(result)`` never shows placeholder values); every attribute read,
         ``dataclasses.asdict``, ``repr``, ``==`` and pickling resolve them first.
-        ``report`` (an _AdjointReport) receives the backward's status words."""
+        ``report`` (a _CallRecord) receives the backward's status words."""
         r = cls(transport_plan=transport_plan, cost=cost)
         d = r.__dict__
         del d["n_iters_used"], d["converged"]
@@ -192,12 +192,14 @@ class _DeviceStatus(_DeviceCounts):
         return words[1:] if len(words) > 1 else None
 
 
-class _AdjointReport:
-    """Where a result's backward leaves its _DeviceStatus."""
+class _CallRecord:
+    """A device call's trackers: the forward's _DeviceCounts and, once the
+    result's backward has run, its _DeviceStatus."""
 
-    __slots__ = ("status",)
+    __slots__ = ("counts", "status")
 
     def __init__(self):
+        self.counts = None
         self.status = None
 
 
@@ -236,9 +238,9 @@ def check_device_errors() -> None:
         _unchecked.popleft().get()
 
 
-def _track(counts: torch.Tensor) -> _DeviceCounts:
+def _track(counts: torch.Tensor, device: Optional[torch.device] = None) -> _DeviceCounts:
     _check_finished_forwards()
-    dc = _DeviceCounts(counts)
+    dc = _DeviceCounts(counts, device)
     _unchecked.append(dc)
     return dc
 
@@ -266,63 +268,73 @@ def _check_tau_tensor(tau):
 class _SinkhornFusedFunction(torch.autograd.Function):
     """Fused forward (plan + cost + device-side stop) and fused backward on HIP tensors.
 
-    Outputs ``(P, cost, counts)``; ``counts`` is int32 ``[iters_used, converged]``
-    on the device.  ``scores_kind`` says whether ``scores`` is a cost matrix C
-    (log_alpha = -C) or log_alpha itself.
+    Outputs ``(P, cost)``.  ``record`` (a _CallRecord) receives the tracker of
+    the int32 ``[iters_used, converged]`` that the forward's last kernel writes
+    to pinned host memory, and the backward's status tracker.  ``scores_kind``
+    says whether ``scores`` is a cost matrix C (log_alpha = -C) or log_alpha
+    itself.
     """
 
     @staticmethod
     def forward(ctx, scores, tau, scores_kind, n_iters, backward_iters, log_a, log_b, tol, mode,
-                want_cost, report):
+                want_cost, record):
         _check_tau_tensor(tau)
         tau_value = _tau_value(tau)
-        ctx.report = report
+        ctx.record = record
         needs_grad = ctx.needs_input_grad[0] or (torch.is_tensor(tau) and ctx.needs_input_grad[1])
         keep_history = bool(needs_grad and mode == _MODE_UNROLLED)
         P, cost, counts, u_hist, v_hist = _ops.fused.sinkhorn_forward(
             scores, scores_kind, tau_value, n_iters, tol, log_a, log_b, want_cost, keep_history
         )
-        ctx.mark_non_differentiable(counts)
+        record.counts = _track(counts, scores.device)
         if not want_cost:
             ctx.mark_non_differentiable(cost)
         # An unused plan or cost reaches backward as None, not as a zero-filled
         # [B, M, N] tensor the adjoint would have to read.
         ctx.set_materialize_grads(False)
-        ctx.save_for_backward(scores, P, counts, u_hist, v_hist)
+        ctx.save_for_backward(scores, P, u_hist, v_hist)
         ctx.tau = tau_value
         ctx.tau_is_tensor = torch.is_tensor(tau)
         ctx.scores_kind = scores_kind
         ctx.backward_iters = backward_iters
         ctx.mode = mode
         ctx.scores_dtype = scores.dtype
-        return P, cost, counts
+        return P, cost
 
     @staticmethod
-    def backward(ctx, grad_P, grad_cost, _grad_counts):
-        scores, P, counts, u_hist, v_hist = ctx.saved_tensors
+    def backward(ctx, grad_P, grad_cost):
+        scores, P, u_hist, v_hist = ctx.saved_tensors
         if grad_cost is not None and grad_cost.numel() == 0:
             grad_cost = None
         if grad_P is None and grad_cost is None:
             return (torch.zeros_like(scores),) + (None,) * 10
         if ctx.mode == _MODE_UNROLLED:
-            iters = int(counts[0].item())
+            iters = ctx.record.counts.get()[0]  # waits for the forward only
             uh, vh = u_hist, v_hist
         else:
             iters = ctx.backward_iters
             uh = vh = None
+        gc_scalar = False
+        if grad_cost is not None:
+            if grad_cost.dim() == 1 and grad_cost.numel() > 1 and grad_cost.stride(0) == 0:
+                # an expanded scalar (the gradient of cost.sum()): its one value
+                grad_cost, gc_scalar = grad_cost[:1], True
+            else:
+                grad_cost = grad_cost.contiguous()
         grad_scores, grad_tau, status = _ops.fused.sinkhorn_backward(
             scores,
             ctx.scores_kind,
             P,
             grad_P.contiguous() if grad_P is not None else None,
-            grad_cost.contiguous() if grad_cost is not None else None,
+            grad_cost,
             ctx.tau,
             ctx.mode,
             iters,
             uh,
             vh,
+            gc_scalar,
         )
-        _track_status(status, scores.device, ctx.report)
+        _track_status(status, scores.device, ctx.record)
         tau_grad = None
         if ctx.tau_is_tensor and ctx.needs_input_grad[1]:
             tau_grad = grad_tau.sum()
@@ -330,15 +342,17 @@ class _SinkhornFusedFunction(torch.autograd.Function):
 
 
 def _run_fused(scores, reg, scores_kind, n_iters, backward_iters, log_a, log_b, tol, mode, want_cost,
-               report=None):
+               record=None):
     tau_arg = reg
     if torch.is_tensor(reg):
         tau_arg = reg.reshape(()).to(device=scores.device)
-    P, cost, counts = _SinkhornFusedFunction.apply(
+    if record is None:
+        record = _CallRecord()
+    P, cost = _SinkhornFusedFunction.apply(
         scores, tau_arg, scores_kind, int(n_iters), int(backward_iters), log_a, log_b, float(tol),
-        mode, want_cost, report
+        mode, want_cost, record
     )
-    return P, cost, _track(counts)
+    return P, cost, record.counts
 
 
 _METHOD_CODES = {"vanilla": 0, "momentum": 1, "anderson": 2, "adam": 3}
@@ -680,7 +694,7 @@ def sinkhorn(
         return SinkhornResult(transport_plan=P, cost=cost, converged=converged, n_iters_used=used)
 
     mode = _MODE_UNROLLED if backward_mode == "unrolled" else _MODE_IMPLICIT
-    report = _AdjointReport() if on_gpu else None
+    report = _CallRecord() if on_gpu else None
     if cuda_dual and not plain:
         if effective == "anderson":
             _check_anderson_ring(anderson_k, n_iters)
@@ -708,7 +722,7 @@ def sinkhorn(
         converged = True if tol == 0 else used < n_iters
         cost = (P * cost_matrix).sum(dim=(-2, -1))
 
-    if on_gpu:
+    if on_gpu and cost.dtype != cost_matrix.dtype:
         cost = cost.to(torch.result_type(P, cost_matrix))
     if unbatched:
         P = P.squeeze(0)

@@ -187,7 +187,7 @@ typedef struct {
     int scores_kind;
     const float* plan;        /* [B,M,N] P of the forward */
     const float* grad_plan;   /* [B,M,N] or NULL */
-    const float* grad_cost;   /* [B] or NULL */
+    const float* grad_cost;   /* [B] or NULL (with DOT_SK_GRAD_COST_SCALAR: one value for every element) */
     int B, M, N;
     float tau;
     int iters;                /* implicit: adjoint sweeps; unrolled: T (history length used) */
@@ -205,11 +205,15 @@ typedef struct {
     uint32_t exchange_epoch;
     int32_t* sweeps_used;     /* implicit only: [B] int32 out (device memory, or pinned host memory the
                                  device can reach), or NULL: adjoint sweeps executed per batch element */
-    int flags;                /* DOT_SK_EXACT_SWEEPS or 0 */
+    int flags;                /* DOT_SK_EXACT_SWEEPS, DOT_SK_GRAD_COST_SCALAR */
 } dot_sinkhorn_bwd_args;
 
-/* Flag of dot_sinkhorn_bwd_args.flags: run exactly `iters` adjoint sweeps. */
+/* Flags of dot_sinkhorn_bwd_args.flags.  DOT_SK_EXACT_SWEEPS: run exactly
+ * `iters` adjoint sweeps.  DOT_SK_GRAD_COST_SCALAR: grad_cost points to one
+ * value that is every batch element's (the upstream gradient of cost.sum()),
+ * so callers need not expand it to [B]. */
 #define DOT_SK_EXACT_SWEEPS 0x4
+#define DOT_SK_GRAD_COST_SCALAR 0x8
 
 /* Implicit-function adjoint: up to `iters` Gauss-Seidel sweeps
  * lambda_i = (sum_k P G - sum_k P mu_k) / max(sum_k P, 1e-12),
