@@ -480,36 +480,7 @@ __global__ __launch_bounds__(kThreads) void implicit_adjoint(ImpResArgs a) {
     bool dead = false;
     announce_xcc(a.xchg, a.N, b, a.W, w, a.xcc_tag);
 
-    // Prologue, streamed (one row at a time, nothing kept): row sums r and rs
-    // of this lane's row slot and the workgroup's column partials of P G and P.
-    float cg[PL], cp[PL];
-    float r_l = 0.0f, rs_l = 0.0f;
-#pragma unroll
-    for (int e = 0; e < PL; ++e) cg[e] = cp[e] = 0.0f;
-#pragma unroll 1
-    for (int k = 0; k < RPW; ++k) {
-        const int i = row0 + wave + kWaves * k;
-        if (i >= rend) break;
-        const size_t off = (bM + i) * a.N;
-        float pr[PL], x[PL], Gr[PL];
-        R::load(a.P + off, lane, a.N, pr, 0.0f);
-        upstream_row<VEC, CH>(a, off, lane, gc, csign, x, Gr);
-        float sg = 0.0f, sp = 0.0f;
-#pragma unroll
-        for (int e = 0; e < PL; ++e) {
-            sg = fmaf(pr[e], Gr[e], sg);
-            sp += pr[e];
-            cg[e] = fmaf(pr[e], Gr[e], cg[e]);
-            cp[e] += pr[e];
-        }
-        sg = wave_sum(sg);
-        sp = wave_sum(sp);
-        if (slot_of_lane<RPW>(lane) == k) {
-            r_l = sg;
-            rs_l = sp;
-        }
-    }
-    // The strip of P, held in registers from here on (a second read of the rows).
+    // The strip of P, loaded once into the registers it stays in for every sweep.
     float p[RPW][PL];
 #pragma unroll
     for (int k = 0; k < RPW; ++k) {
@@ -521,6 +492,31 @@ __global__ __launch_bounds__(kThreads) void implicit_adjoint(ImpResArgs a) {
             for (int e = 0; e < PL; ++e) p[k][e] = 0.0f;
         }
     }
+    // Prologue, from the registers with G streamed row by row: row sums
+    // r = sum_k P G and rs = sum_k P of this wave's rows (reduced across the
+    // wave together, each lane keeping one row's, as the sweeps' row dots) and
+    // the workgroup's column partials of P G and P.
+    float cg[PL], cp[PL], sg[RPW], sp[RPW];
+#pragma unroll
+    for (int e = 0; e < PL; ++e) cg[e] = cp[e] = 0.0f;
+#pragma unroll
+    for (int k = 0; k < RPW; ++k) {
+        sg[k] = sp[k] = 0.0f;
+        const int i = row0 + wave + kWaves * k;
+        if (i < rend) {
+            float x[PL], Gr[PL];
+            upstream_row<VEC, CH>(a, (bM + i) * a.N, lane, gc, csign, x, Gr);
+#pragma unroll
+            for (int e = 0; e < PL; ++e) {
+                sg[k] = fmaf(p[k][e], Gr[e], sg[k]);
+                sp[k] += p[k][e];
+                cg[e] = fmaf(p[k][e], Gr[e], cg[e]);
+                cp[e] += p[k][e];
+            }
+        }
+    }
+    const float r_l = transposed_sum<RPW>(sg);
+    const float rs_l = transposed_sum<RPW>(sp);
     const float inv_rs = 1.0f / fmaxf(rs_l, sk::kSumFloor);
     float c_own[kColRounds<PL>], cs_own[kColRounds<PL>];
     const bool local =
