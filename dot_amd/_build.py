@@ -30,7 +30,7 @@ ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 HIPCC = os.path.join(ROCM, "bin", "hipcc")
 ARCH = os.environ.get("DOT_AMD_ARCH", "gfx950")
 
-HIP_SOURCES = ["sinkhorn.hip", "bidi.hip", "preflight.hip", "methods.hip", "capi.hip"]
+HIP_SOURCES = ["sinkhorn.hip", "bidi.hip", "preflight.hip", "methods.hip", "capi.hip", "noalloc.hip"]
 HIP_FLAGS = [
     "-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-mcode-object-version=5",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",

@@ -87,6 +87,11 @@ inline int sweep_strip_rows(int B, int M) {
 int sinkhorn_forward_scheduled(const dot_sinkhorn_fwd_args* a, const float* ks_host, const float* ks_dev,
                                hipStream_t stream);
 
+// Bytes of the forward's workspace without the persistent tier's optional
+// scaled kernel (what dot_sinkhorn_forward needs at the least); 0 for a
+// negative size.  Defined in sinkhorn.hip.
+size_t forward_workspace_base_bytes(int B, int M, int N, int max_iter);
+
 // sweep_strip_rows, or the value of DOT_AMD_ROWS when set (tuning only).
 inline int tuned_strip_rows(int B, int M) {
     static const int forced = [] {

@@ -110,7 +110,10 @@ int dot_sinkhorn_forward(const dot_sinkhorn_fwd_args* args, dot_stream_t stream)
 /* dot_sinkhorn_forward without a workspace argument and without any
  * allocation: args->workspace and args->workspace_bytes are ignored and the
  * scratch is a file-scope device array of DOT_STATIC_SCRATCH_BYTES per GPU,
- * held from the first call on that GPU until the process ends.  Shapes whose
+ * held from the first call on that GPU until the process ends (the array is
+ * a code object of its own, without kernels, which the HIP runtime's deferred
+ * loading places on a GPU only when this call first looks it up there; using
+ * the other entry points does not reserve it).  Shapes whose
  * workspace exceeds DOT_STATIC_SCRATCH_BYTES return DOT_ERR_UNSUPPORTED (the
  * workspace without the optional scaled kernel that
  * dot_sinkhorn_forward_workspace_bytes() adds for the persistent tier's

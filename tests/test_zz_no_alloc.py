@@ -63,6 +63,36 @@ def _run(lib, entry, C, log_a, log_b, tau, T, tol, workspace):
     return out
 
 
+def test_scratch_is_reserved_by_the_first_noalloc_call(lib):
+    """The static scratch is a code object of its own (noalloc.hip, no
+    kernels): the Sinkhorn kernels' use does not place it on the GPU, the first
+    dot_sinkhorn_forward_noalloc call on the GPU does.  Runs before every other
+    call of the entry point in the process (this file's first test; no other
+    test file calls it)."""
+    B, M, N, T = 4, 64, 64, 20
+    C = torch.rand(B, M, N, device=DEV)
+    out = {k: torch.empty(n, device=DEV) for k, n in (("plan", B * M * N), ("cost", B))}
+    counts = torch.zeros(2, dtype=torch.int32, device=DEV)
+    ws = torch.empty(lib.dot_sinkhorn_forward_workspace_bytes(B, M, N, T, 0), dtype=torch.uint8, device=DEV)
+    a = FwdArgs(scores=C.data_ptr(), B=B, M=M, N=N, scores_kind=-1, tau=0.5, max_iter=T, tol=0.0,
+                plan=out["plan"].data_ptr(), cost=out["cost"].data_ptr(), iters_used=counts.data_ptr(),
+                converged=counts.data_ptr() + 4, workspace=ws.data_ptr(), workspace_bytes=ws.numel())
+    stream = ctypes.c_void_p(torch.cuda.current_stream(DEV).cuda_stream)
+    assert lib.dot_sinkhorn_forward(ctypes.byref(a), stream) == 0
+    torch.cuda.synchronize(DEV)
+    free0 = torch.cuda.mem_get_info(DEV)[0]
+    assert lib.dot_sinkhorn_forward_noalloc(ctypes.byref(a), stream) == 0
+    torch.cuda.synchronize(DEV)
+    free1 = torch.cuda.mem_get_info(DEV)[0]
+    assert lib.dot_sinkhorn_forward_noalloc(ctypes.byref(a), stream) == 0
+    torch.cuda.synchronize(DEV)
+    free2 = torch.cuda.mem_get_info(DEV)[0]
+    print(f"[no_alloc] device free bytes: {free0} before the first call, {free1} after, {free2} after the second",
+          flush=True)
+    assert free0 - free1 >= STATIC_SCRATCH_BYTES
+    assert free1 == free2
+
+
 # (B, M, N, tau, T, tol, Dirichlet marginals): the register-resident tier with a
 # batch-global stop test first, then a smaller streaming-tier shape with fixed
 # iterations and marginals, so the second call starts on the first one's scratch.
