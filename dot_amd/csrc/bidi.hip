@@ -91,6 +91,7 @@ bool onepass_exchange(void* caller, uint32_t epoch, unsigned long long* ws_words
     }
     x.groups = onepass_groups();
     x.wait_ticks = onepass_wait_ticks();
+    x.local_ok = local_exchange_allowed();
     return true;
 }
 

@@ -84,6 +84,7 @@ struct Exchange {
     int groups;
     unsigned epoch;             // 1 .. kMaxEpoch
     int wait_ticks;             // deadline of a wait in s_memrealtime ticks (10 ns); < 0: never wait
+    int local_ok;               // XCD-local exchange stores allowed (local_exchange_allowed)
 };
 
 __device__ __forceinline__ unsigned long long* part_row(const Exchange& x, int g, int p, int m) {
@@ -525,7 +526,8 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(FwdArgs1 a) {
         }
         if (!rs_ok || block_any(!ok, votes[1]))
             fwd_fallback<CH, FW>(a, e, l1, l2, g, m, p, tag, local, !rs_ok, lm, ls, clse);
-        if (k == 0) local = group_on_one_xcd(a.x, g, tag0, now_ticks() + a.x.wait_ticks, never, &flag);
+        if (k == 0)
+            local = group_on_one_xcd(a.x, g, tag0, now_ticks() + a.x.wait_ticks, never, &flag) && a.x.local_ok;
         // ---- write; each row is refilled with the element after next
         const int kn = k + 2;
         const bool real = kn < n;
@@ -835,7 +837,8 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_kernel(BwdArgs1 a) {
         }
         if (!rs_ok || block_any(!ok, votes[1])) bwd_fallback<CH, FW>(a, e, l1, l2, g, m, p, tag, local, !rs_ok, lacc,
                                                             lcl, ldc);
-        if (k == 0) local = group_on_one_xcd(a.x, g, tag0, now_ticks() + a.x.wait_ticks, never, &flag);
+        if (k == 0)
+            local = group_on_one_xcd(a.x, g, tag0, now_ticks() + a.x.wait_ticks, never, &flag) && a.x.local_ok;
         // ---- phase B; each row is refilled with the next element's
         const bool real = k + 1 < n;
         const int en = g + G * (real ? k + 1 : k);

@@ -9,6 +9,7 @@
 #include <atomic>
 #include <cstdint>
 #include <cstdlib>
+#include <cstring>
 
 namespace dot_amd {
 
@@ -30,6 +31,27 @@ inline int device_cus() {
     if (hipGetDevice(&dev) != hipSuccess) return 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
     return cus;
+}
+
+// 1 when exchange stores may stop in the writer's XCD L2 for readers on the
+// same XCD (workgroup-scope stores read by agent-scope loads, a behaviour of
+// the L2 measured on gfx950 and checked per launch by the XCC ids the
+// workgroups announce), 0 to keep every exchange store at agent scope: on
+// devices other than gfx950, and with DOT_AMD_AGENT_SCOPE=1.
+inline int local_exchange_allowed() {
+    const char* e = std::getenv("DOT_AMD_AGENT_SCOPE");
+    if (e && e[0] == '1') return 0;
+    static std::atomic<int> known[64];  // per device: 0 unknown, 1 gfx950, 2 other
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+    int k = known[dev].load(std::memory_order_relaxed);
+    if (k == 0) {
+        hipDeviceProp_t prop;
+        k = (hipGetDeviceProperties(&prop, dev) == hipSuccess && std::strncmp(prop.gcnArchName, "gfx950", 6) == 0)
+                ? 1 : 2;
+        known[dev].store(k, std::memory_order_relaxed);
+    }
+    return k == 1 ? 1 : 0;
 }
 
 inline int pow2_ceil(int x) {

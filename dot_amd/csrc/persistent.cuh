@@ -292,6 +292,7 @@ struct FwdArgs {
     unsigned long long* dxchg;  // [kDeltaSlots, G] tagged per-workgroup deltas
     int* status;
     int B, M, N, W, R, spin_limit;
+    int local_ok;         // XCD-local exchange stores allowed (local_exchange_allowed)
     float* ebuf;                // [B,M,N] scaled kernel (scaling domain), or null
 };
 
@@ -388,7 +389,8 @@ __global__ __launch_bounds__(kThreads) void forward(FwdArgs a) {
     }
     __syncthreads();
     bool dead = false;
-    const bool local = res::element_on_one_xcd(a.part, a.N, b, a.W, w, a.spin_limit, a.status, dead, scratch);
+    const bool local =
+        res::element_on_one_xcd(a.part, a.N, b, a.W, w, a.spin_limit, a.status, dead, scratch) && a.local_ok;
     int used = a.max_iter;
     int conv = 0;
 
@@ -674,6 +676,7 @@ struct ImpArgs {
     int* status;
     float inv_tau;
     int B, M, N, W, R, iters, spin_limit;
+    int local_ok;         // XCD-local exchange stores allowed (local_exchange_allowed)
     int32_t* sweeps;      // [B] sweeps executed per batch element, or null
     int early;            // nonzero: end each element's sweeps once converged (sk::AdjointStop)
 };
@@ -763,7 +766,8 @@ __global__ __launch_bounds__(kThreads) void implicit_adjoint(ImpArgs a) {
             lds_lam[l] = 0.0f;
         }
     }
-    const bool local = res::element_on_one_xcd(a.part, a.N, b, a.W, w, a.spin_limit, a.status, dead, scratch);
+    const bool local =
+        res::element_on_one_xcd(a.part, a.N, b, a.W, w, a.spin_limit, a.status, dead, scratch) && a.local_ok;
     publish_row<VEC, CH>(cg, tree, a.N, a.pro + size_t(gid) * a.N, 1u, local);
     publish_row<VEC, CH>(cp, tree, a.N, a.pro + (size_t(G) + gid) * a.N, 1u, local);
     reduce_slice(a.pro + size_t(b) * a.W * a.N, a.N, a.W, c0, c1, 1u, red, a.spin_limit, a.status, dead,
@@ -895,6 +899,7 @@ struct UnrArgs {
     int* status;
     float inv_tau;
     int B, M, N, W, R, T, spin_limit;
+    int local_ok;          // XCD-local exchange stores allowed (local_exchange_allowed)
 };
 
 // The unrolled backward (kernels.cu:1622-1680) streaming Gamma and the scores
@@ -981,7 +986,7 @@ __global__ __launch_bounds__(kThreads) void unrolled(UnrArgs a) {
         if (a.T == 0) epilogue(off, ln, gam, x);
         else R::store(a.gamma + off, ln, a.N, gam);
     }
-    local = res::element_on_one_xcd(a.part, a.N, b, a.W, w, a.spin_limit, a.status, dead, scratch);
+    local = res::element_on_one_xcd(a.part, a.N, b, a.W, w, a.spin_limit, a.status, dead, scratch) && a.local_ok;
     unsigned tag = 1;
     if (a.T > 0) exchange(acc, tag);
 

@@ -425,6 +425,7 @@ struct ImpResArgs {
     int mark;                  // failure mark in *status (forced_timeout)
     int32_t* sweeps;           // [B] sweeps executed per batch element, or null
     int early;                 // nonzero: end each element's sweeps once converged (sk::AdjointStop)
+    int local_ok;              // XCD-local exchange stores allowed (local_exchange_allowed)
 };
 
 // Upstream gradient of one row: G = grad_plan + grad_cost[b] * C, C = csign * scores.
@@ -520,7 +521,8 @@ __global__ __launch_bounds__(kThreads) void implicit_adjoint(ImpResArgs a) {
     const float inv_rs = 1.0f / fmaxf(rs_l, sk::kSumFloor);
     float c_own[kColRounds<PL>], cs_own[kColRounds<PL>];
     const bool local =
-        element_on_one_xcd(a.xchg, a.N, b, a.W, w, a.spin_limit, a.status, dead, scratch, a.xcc_tag, a.mark);
+        element_on_one_xcd(a.xchg, a.N, b, a.W, w, a.spin_limit, a.status, dead, scratch, a.xcc_tag, a.mark) &&
+        a.local_ok;
     R::store(part + wave * a.N, lane, a.N, cg);
     __syncthreads();
     exchange_columns<kColRounds<PL>, MG>(part, a.pro, a.N, b, a.W, w, a.tag_base | 1u, local, a.spin_limit,
@@ -670,6 +672,7 @@ struct FwdResArgs {
     unsigned tag_base;          // exchange tags are tag_base | t (0: slots cleared for the call)
     unsigned xcc_tag;           // tag of the XCD-id words
     int mark;                   // failure mark in *status (forced_timeout)
+    int local_ok;               // XCD-local exchange stores allowed (local_exchange_allowed)
 };
 
 // Waits for G tagged per-workgroup deltas of iteration t and returns their
@@ -779,7 +782,8 @@ __global__ __launch_bounds__(kThreads) void forward(FwdResArgs a) {
     float ks_next = (SCHED && a.max_iter > 0) ? a.kscale_t[0] : a.kscale;
     bool dead = false;
     const bool local =
-        element_on_one_xcd(a.xchg, a.N, b, a.W, w, a.spin_limit, a.status, dead, scratch, a.xcc_tag, a.mark);
+        element_on_one_xcd(a.xchg, a.N, b, a.W, w, a.spin_limit, a.status, dead, scratch, a.xcc_tag, a.mark) &&
+        a.local_ok;
     int used = a.max_iter;
     int conv = 0;
 

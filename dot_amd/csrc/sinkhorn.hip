@@ -396,6 +396,7 @@ bool launch_stream_forward(const dot_sinkhorn_fwd_args* a, const FwdLayout& L, c
     r.W = sc.W;
     r.R = sc.R;
     r.spin_limit = spin_limit();
+    r.local_ok = local_exchange_allowed();
     r.ebuf = ks_dev ? nullptr : ebuf;
     const size_t words = size_t(reinterpret_cast<unsigned long long*>(r.status) - L.pst) + 1;
     bool ok = false;
@@ -462,6 +463,7 @@ bool launch_resident_forward(const dot_sinkhorn_fwd_args* a, const FwdLayout& L,
     r.W = rc.W;
     r.R = rc.R;
     r.spin_limit = spin_limit();
+    r.local_ok = local_exchange_allowed();
     bool ok = false;
     dispatch_resident<true>(rc, [&](auto vc, auto cc, auto rr) {
         constexpr int V = decltype(vc)::value;
@@ -896,6 +898,7 @@ bool launch_resident_adjoint(const dot_sinkhorn_bwd_args* a, const ImpLayout& L,
     r.R = rc.R;
     r.iters = a->iters;
     r.spin_limit = spin_limit();
+    r.local_ok = local_exchange_allowed();
     r.sweeps = a->sweeps_used;
     r.early = (a->flags & DOT_SK_EXACT_SWEEPS) ? 0 : 1;
     bool ok = false;
@@ -987,6 +990,7 @@ bool launch_stream_adjoint(const dot_sinkhorn_bwd_args* a, const ImpLayout& L, c
     r.R = sc.R;
     r.iters = a->iters;
     r.spin_limit = spin_limit();
+    r.local_ok = local_exchange_allowed();
     r.sweeps = a->sweeps_used;
     r.early = (a->flags & DOT_SK_EXACT_SWEEPS) ? 0 : 1;
     const size_t words = size_t(reinterpret_cast<unsigned long long*>(r.status) - L.pst) + 1;
@@ -1095,6 +1099,7 @@ bool launch_stream_unrolled(const dot_sinkhorn_bwd_args* a, const UnrLayout& L, 
     r.R = sc.R;
     r.T = a->iters;
     r.spin_limit = spin_limit();
+    r.local_ok = local_exchange_allowed();
     const size_t words = size_t(reinterpret_cast<unsigned long long*>(r.status) - L.pst) + 1;
     bool ok = false;
     dispatch_row(N, vec4, [&](auto vc, auto cc) {
