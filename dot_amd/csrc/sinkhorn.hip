@@ -936,37 +936,51 @@ int resident_slab(int B, int M, int N, bool vec4) {
     return std::min(B, std::max(1, std::min(device_cus(), 1024) / one.W));
 }
 
-// A batch larger than the register-resident adjoint holds at once, in slabs
-// of `slab` elements, one launch each on the stream.  The adjoint couples no
-// batch elements, so every slab computes exactly its elements' share of the
-// call; each launch clears its own workspace exchange words (caller-owned
-// words would repeat one epoch across the slabs).  False when a slab cannot
-// be hosted (every slab has the first one's shape, or a smaller batch of it);
-// the caller then runs the whole batch on the next tier, which overwrites
-// every output.
-bool launch_resident_slabs(const dot_sinkhorn_bwd_args* a, const ImpLayout& L, int slab, float inv_tau,
-                           hipStream_t stream) {
+// The arguments of batch elements [b0, b0 + n) of a backward call, with the
+// exchange words left to the launch's own workspace (caller-owned words would
+// repeat one epoch across the slabs).
+dot_sinkhorn_bwd_args slab_args(const dot_sinkhorn_bwd_args* a, int b0, int n) {
     const size_t MN = size_t(a->M) * a->N;
+    dot_sinkhorn_bwd_args s = *a;
+    s.B = n;
+    s.scores = a->scores + b0 * MN;
+    s.plan = a->plan + b0 * MN;
+    s.grad_plan = a->grad_plan ? a->grad_plan + b0 * MN : nullptr;
+    s.grad_cost = a->grad_cost ? a->grad_cost + ((a->flags & DOT_SK_GRAD_COST_SCALAR) ? 0 : b0) : nullptr;
+    s.grad_scores = a->grad_scores + b0 * MN;
+    s.grad_tau = a->grad_tau + b0;
+    s.sweeps_used = a->sweeps_used ? a->sweeps_used + b0 : nullptr;
+    s.exchange = nullptr;
+    s.exchange_epoch = 0;
+    return s;
+}
+
+// A batch larger than a one-launch adjoint holds at once, in slabs of `slab`
+// elements, one launch each on the stream: launch(slab arguments, whether an
+// earlier slab ran).  The adjoint couples no batch elements, so every slab
+// computes exactly its elements' share of the call, and each launch clears
+// its own workspace exchange words.  False when a slab cannot be hosted; the
+// caller then runs the whole batch on the next tier, which overwrites every
+// output.
+template <class Launch>
+bool launch_slabs(const dot_sinkhorn_bwd_args* a, int slab, Launch&& launch) {
     for (int b0 = 0; b0 < a->B; b0 += slab) {
-        dot_sinkhorn_bwd_args s = *a;
-        s.B = std::min(slab, a->B - b0);
-        s.scores = a->scores + b0 * MN;
-        s.plan = a->plan + b0 * MN;
-        s.grad_plan = a->grad_plan ? a->grad_plan + b0 * MN : nullptr;
-        s.grad_cost = a->grad_cost ? a->grad_cost + ((a->flags & DOT_SK_GRAD_COST_SCALAR) ? 0 : b0) : nullptr;
-        s.grad_scores = a->grad_scores + b0 * MN;
-        s.grad_tau = a->grad_tau + b0;
-        s.sweeps_used = a->sweeps_used ? a->sweeps_used + b0 : nullptr;
-        s.exchange = nullptr;
-        s.exchange_epoch = 0;
-        const ResidentCfg rc = resident_config<false>(s.B, s.M, s.N, bwd_vec4(&s));
-        if (!rc.ok || !launch_resident_adjoint(&s, L, rc, inv_tau, stream, b0 > 0)) return false;
+        const dot_sinkhorn_bwd_args s = slab_args(a, b0, std::min(slab, a->B - b0));
+        if (!launch(s, b0 > 0)) return false;
     }
     return true;
 }
 
+bool launch_resident_slabs(const dot_sinkhorn_bwd_args* a, const ImpLayout& L, int slab, float inv_tau,
+                           hipStream_t stream) {
+    return launch_slabs(a, slab, [&](const dot_sinkhorn_bwd_args& s, bool keep) {
+        const ResidentCfg rc = resident_config<false>(s.B, s.M, s.N, bwd_vec4(&s));
+        return rc.ok && launch_resident_adjoint(&s, L, rc, inv_tau, stream, keep);
+    });
+}
+
 bool launch_stream_adjoint(const dot_sinkhorn_bwd_args* a, const ImpLayout& L, const StreamCfg& sc,
-                           float inv_tau, bool vec4, hipStream_t stream) {
+                           float inv_tau, bool vec4, hipStream_t stream, bool keep_status = false) {
     const int B = a->B, N = a->N, G = B * sc.W;
     if (!L.pst || size_t(G) > L.pst_groups) return false;
     pst::ImpArgs r{};
@@ -1009,7 +1023,7 @@ bool launch_stream_adjoint(const dot_sinkhorn_bwd_args* a, const ImpLayout& L, c
     if (!ok) return false;
     ProfScope prof("sk_batch_sum", stream);
     hipLaunchKernelGGL(sk::batch_sum, dim3(B), dim3(kWave), 0, stream, L.tau_partial, sc.W, -inv_tau,
-                       a->grad_tau, static_cast<const int*>(r.status), a->status);
+                       a->grad_tau, static_cast<const int*>(r.status), a->status, 1, keep_status ? 1 : 0);
     return true;
 }
 
@@ -1226,6 +1240,17 @@ extern "C" int dot_sinkhorn_backward_implicit(const dot_sinkhorn_bwd_args* a, do
     if (sc.ok && launch_stream_adjoint(a, L, sc, inv_tau, bwd_vec4(a), stream))
         return check_launch("dot_sinkhorn_backward_implicit");
     (void)hipGetLastError();
+    // More elements than CUs: slabs of one element per CU on the persistent tier.
+    const int cus = device_cus();
+    if (!sc.ok && cus > 0 && B > cus && stream_config(cus, M, N).ok) {
+        const bool done = launch_slabs(a, cus, [&](const dot_sinkhorn_bwd_args& s, bool keep) {
+            const StreamCfg ss = stream_config(s.B, M, N);
+            return ss.ok && launch_stream_adjoint(&s, L, ss, inv_tau, bwd_vec4(&s), stream, keep);
+        });
+        if (done) return check_launch("dot_sinkhorn_backward_implicit");
+        if (int e = check_launch("dot_sinkhorn_backward_implicit")) return e;
+        (void)hipGetLastError();
+    }
     report_all_sweeps(a, stream);  // the per-sweep launches run every sweep
     if (L.nchunks > 1) {
         launch_wide_implicit(a, L, x, inv_tau, stream);

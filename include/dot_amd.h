@@ -222,8 +222,9 @@ typedef struct {
  * lambda_i = (sum_k P G - sum_k P mu_k) / max(sum_k P, 1e-12),
  * mu_k = (sum_i P G - sum_i P lambda_i) / max(sum_i P, 1e-12),
  * grad = P (G - lambda_i - mu_k) / tau, grad_tau = -sum(grad * log_alpha) / tau.
- * Without DOT_SK_EXACT_SWEEPS, shapes that run in one launch (the register-
- * resident and persistent tiers) end a batch element's sweeps early once
+ * Without DOT_SK_EXACT_SWEEPS, rows of at most 4096 columns (the register-
+ * resident and persistent tiers, batches beyond the chip in slabs of them)
+ * end a batch element's sweeps early once
  * they have converged, with d = max|mu_t - mu_{t-1}| and s the size of the
  * mu update's operands, max_k (|sum_i P G| + |sum_i P lambda|) / sum_i P:
  * when a sweep leaves mu unchanged (a fixed point: the result is the full

@@ -199,3 +199,30 @@ def test_c3_shape_at_larger_batches(B):
         assert rel_err(res.transport_plan[b:b + 1], Po) < FWD_TOL, b
         assert rel_err(gr[b:b + 1], go) < GRAD_TOL, b
     assert max(sweeps) < 200
+
+
+def test_persistent_slabs_beyond_the_cus(monkeypatch):
+    """More batch elements than CUs at rows of 1025-4096 columns: the
+    adjoint runs as slabs of the persistent adjoint (one element per CU),
+    each ending its elements' sweeps early.  Elements at the slabs' edges
+    against the float64 oracle at the full sweep count; the exact run reports
+    every sweep."""
+    cus = torch.cuda.get_device_properties(DEV).multi_processor_count
+    B, M, N, tau, T, BT = cus + 44, 64, 1100, 0.3, 60, 150
+    print(f"[early-end] persistent slabs B={B} M={M} N={N}", flush=True)
+    rng = np.random.default_rng(77)
+    Cn = rng.random((B, M, N)).astype(np.float32)
+    a, b = _dirichlet(rng, B, M), _dirichlet(rng, B, N)
+    C = _t(Cn)
+    res, g = _run(C, tau, T, BT, _t(a), _t(b))
+    sweeps = res.adjoint_sweeps
+    print(f"[early-end] slab sweeps min {min(sweeps)} max {max(sweeps)}", flush=True)
+    assert len(sweeps) == B and all(1 <= s < BT for s in sweeps)
+    for e in (0, cus - 1, cus, B - 1):
+        Po, go = _oracle_grad(Cn[e:e + 1], tau, T, BT, a[e:e + 1], b[e:e + 1])
+        assert rel_err(res.transport_plan[e:e + 1], Po) < FWD_TOL, e
+        assert rel_err(g[e:e + 1], go) < GRAD_TOL, e
+    monkeypatch.setenv("DOT_AMD_EXACT_SWEEPS", "1")
+    res_x, g_x = _run(C, tau, T, BT, _t(a), _t(b))
+    assert res_x.adjoint_sweeps == [BT] * B
+    assert rel_err(g, g_x.cpu().numpy()) < 1e-5
