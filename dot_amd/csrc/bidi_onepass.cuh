@@ -70,6 +70,12 @@ constexpr int kMaxGroups = 8;
 constexpr int kStageBits = 12;
 constexpr int kMaxStages = (1 << kStageBits) - 1;         // elements per group per call
 constexpr unsigned kMaxEpoch = (1u << (32 - kStageBits)) - 1;
+// Backward: waves [0, kPollWaves) wait on the exchange while the others
+// prefetch rows 1 .. kRowsPerWave - 1 of every wave's next grad_out rows into
+// LDS (their loads then do not queue ahead of the polls: a wave's vector loads
+// complete in issue order).
+constexpr int kPollWaves = kWaves / 2;
+constexpr int kPreRows = kRowsPerWave - 1;
 
 // Exchange words: partials [groups][2][kMembers][kMaxCols], results
 // [groups][2][kMaxCols], XCC announces [groups][kMembers]; the middle 2 is the
@@ -117,13 +123,48 @@ __device__ __forceinline__ bool poll2(unsigned long long* p0, unsigned long long
     }
 }
 
+// Waits until all four words carry `tag` (see poll2).
+__device__ __forceinline__ bool poll4(unsigned long long* const (&w)[4], unsigned tag, long long deadline, bool never,
+                                      float (&v)[4]) {
+    if (never) return false;
+    for (;;) {
+        unsigned long long x[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) x[i] = __hip_atomic_load(w[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        bool all = true;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) all = all && unsigned(x[i] >> 32) == tag;
+        if (all) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v[i] = __uint_as_float(unsigned(x[i]));
+            return true;
+        }
+        if (now_ticks() > deadline) return false;
+    }
+}
+
+// Workgroup barrier for data passed through LDS only: this wave's LDS
+// accesses complete (lgkmcnt 0), then s_barrier, with compiler barriers on
+// both sides.  Unlike __syncthreads() (a workgroup release fence) it does not
+// wait for the wave's outstanding vector-memory loads into LDS, so a wave may
+// pass it while its prefetch is still in flight; the prefetched words are read
+// only after a later vmcnt wait and barrier.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0); vmcnt and expcnt at their maxima (no wait)
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
 // True in every thread when `pred` holds in any thread of the workgroup: a
 // wave ballot per wave into `votes` (kWaves ints), one barrier, every thread
 // reads all.  Two calls with no barrier between them need separate `votes`.
-__device__ __forceinline__ bool block_any(bool pred, int* votes) {
+// Every lane of wave `wave` (wave-uniform) writes the same vote: no lane test,
+// so no per-lane value is held (or spilled) for it.
+__device__ __forceinline__ bool block_any(bool pred, int* votes, int wave) {
     const bool any = __ballot(pred) != 0;
-    if (threadIdx.x % kWave == 0) votes[threadIdx.x / kWave] = any;
-    __syncthreads();
+    votes[wave] = any;
+    lds_barrier();
     const int4 v0 = reinterpret_cast<const int4*>(votes)[0];
     const int4 v1 = reinterpret_cast<const int4*>(votes)[1];
     return (v0.x | v0.y | v0.z | v0.w | v1.x | v1.y | v1.z | v1.w) != 0;
@@ -205,6 +246,17 @@ __device__ __forceinline__ int fresh(int x) {
     return x;
 }
 
+// The lane's index in its wave, computed (two VALU instructions) at each use:
+// inside the element loops thread indices are formed from it and the
+// wave-uniform wave index, so that no per-lane index is held across the loop
+// (a held one is spilled, and its reload is a memory load that completes only
+// after every row load the wave has in flight).
+__device__ __forceinline__ int lane_now() {
+    int l;
+    asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+    return l;
+}
+
 template <int CH>
 __device__ __forceinline__ void load_row(__amdgpu_buffer_rsrc_t r, int row, int L2, int lane, float (&x)[4 * CH]) {
     const unsigned off = fresh(unsigned(row) * unsigned(L2) * 4u + unsigned(lane) * 16u);
@@ -215,6 +267,44 @@ __device__ __forceinline__ void load_row(__amdgpu_buffer_rsrc_t r, int row, int 
         x[4 * kk + 1] = __uint_as_float(t.y);
         x[4 * kk + 2] = __uint_as_float(t.z);
         x[4 * kk + 3] = __uint_as_float(t.w);
+    }
+}
+
+// The words of element_rsrc's descriptor (base, stride 0, byte size, the
+// same flags), wave-uniform, for the LDS loads below.
+__device__ __forceinline__ v4u element_words(const float* base, size_t elem, int e) {
+    const uintptr_t p = reinterpret_cast<uintptr_t>(base + size_t(e) * elem);
+    v4u w;
+    w.x = __builtin_amdgcn_readfirstlane(unsigned(p));
+    w.y = __builtin_amdgcn_readfirstlane(unsigned(p >> 32)) & 0xffffu;
+    w.z = __builtin_amdgcn_readfirstlane(unsigned(elem * 4));
+    w.w = 0x00020000u;
+    return w;
+}
+
+// load_row into LDS instead of registers: 16-byte buffer loads that write LDS
+// directly (M0 = the wave-uniform LDS byte address; lane l's 16 bytes land at
+// M0 + 16 l, so columns kk*256 + 4l .. +3 sit at float offset kk*256 + 4l of
+// `dst`, the layout load_row gives the registers; no instruction offset, which
+// would move the LDS address too).  Issued from inline
+// assembly so that the compiler adds no wait for them: the data is there once
+// this wave has waited for vmcnt(0), and other waves may read it after a
+// barrier that follows that wait.  M0 is restored after each load.
+template <int CH>
+__device__ __forceinline__ void load_row_lds(v4u r, int row, int L2, int lane, unsigned dst) {
+    const unsigned off = fresh(unsigned(row) * unsigned(L2) * 4u + unsigned(lane) * 16u);
+#pragma unroll
+    for (int kk = 0; kk < CH; ++kk) {
+        unsigned saved;
+        asm volatile(
+            "s_mov_b32 %0, m0\n\t"
+            "s_mov_b32 m0, %1\n\t"
+            "s_nop 0\n\t"
+            "buffer_load_dwordx4 %2, %3, 0 offen lds\n\t"
+            "s_mov_b32 m0, %0"
+            : "=&s"(saved)
+            : "s"(dst + kk * 1024u), "v"(off + kk * 1024u), "s"(r)
+            : "memory");
     }
 }
 
@@ -310,15 +400,14 @@ __device__ __forceinline__ void scale_mask(float (&v)[R::PL], float sc, bool row
 // column statistics).  Contains barriers.
 template <int CH, bool FW>
 __device__ void fwd_fallback(const FwdArgs1& a, int e, int l1, int l2, int g, int m, int p, unsigned tag, bool local,
-                             bool own, float* lm, float* ls, float* clse) {
+                             bool own, float* lm, float* ls, float* clse, int wave) {
     using R = Row<4, CH>;
     // FW (full tile): no lengths, 1024 rows of 256 * CH columns; the extents
     // are then constants and every row and column check folds away
     const int L2 = FW ? 4 * kWave * CH : a.L2;
     const int L1 = FW ? kMaxRows : a.L1;
-    const int lane = threadIdx.x % kWave;
-    const int wave = threadIdx.x / kWave;
-    const int t = threadIdx.x;
+    const int lane = lane_now();
+    const int t = wave * kWave + lane;
     const auto rs = element_rsrc(a.sim, size_t(L1) * L2, e);
     float M0 = -FLT_MAX, S0 = 0.0f, M1 = -FLT_MAX, S1 = 0.0f;
     for (int mm = 0; mm < kMembers; ++mm) {
@@ -375,21 +464,22 @@ __device__ void fwd_fallback(const FwdArgs1& a, int e, int l1, int l2, int g, in
 // announced XCC ids); a wait past the deadline reads as "no".  Contains
 // barriers.
 __device__ __forceinline__ bool group_on_one_xcd(const Exchange& x, int g, unsigned tag0, long long deadline,
-                                                 bool never, int* flag) {
+                                                 bool never, int* flag, int wave) {
     const int me = res::xcc_id();
-    if (threadIdx.x < kWave) {
+    if (wave == 0) {
+        const int lane = lane_now();
         int same = 1;
-        if (threadIdx.x < kMembers) {
+        if (lane < kMembers) {
             float v0, v1;
-            unsigned long long* w = xcc_word(x, g, threadIdx.x);
+            unsigned long long* w = xcc_word(x, g, lane);
             same = poll2(w, w, tag0, deadline, never, v0, v1) && __float_as_int(v0) == me;
         }
         const int all = __all(same);
-        if (threadIdx.x == 0) *flag = all;
+        *flag = all;  // every lane of wave 0: the same value
     }
-    __syncthreads();
+    lds_barrier();
     const bool local = *flag != 0;
-    __syncthreads();
+    lds_barrier();
     return local;
 }
 
@@ -439,8 +529,8 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(FwdArgs1 a) {
     auto stage = [&](int k, float(&buf)[kRowsPerWave][PL]) {
         // thread indices re-formed per element: addresses derived from them are
         // computed here, not hoisted out of the element loop and spilled
-        const int t = fresh(int(threadIdx.x));
-        const int lane = t % kWave;
+        const int lane = lane_now();
+        const int t = wave * kWave + lane;
         const int e = g + G * k;
         const unsigned tag = tag0 | unsigned(k + 1);
         const int p = k & 1;
@@ -504,7 +594,7 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(FwdArgs1 a) {
             rsv[2 * h][c] = v0;
             rsv[2 * h + 1][c] = v1;
         }
-        const bool rs_ok = !block_any(!ok, votes[0]);
+        const bool rs_ok = !block_any(!ok, votes[0], wave);
         if (rs_ok) {
             if (t < kOwn) {
                 float M = -FLT_MAX, S = 0.0f;
@@ -524,10 +614,10 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(FwdArgs1 a) {
             clse[2 * t] = v0;
             clse[2 * t + 1] = v1;
         }
-        if (!rs_ok || block_any(!ok, votes[1]))
-            fwd_fallback<CH, FW>(a, e, l1, l2, g, m, p, tag, local, !rs_ok, lm, ls, clse);
+        if (!rs_ok || block_any(!ok, votes[1], wave))
+            fwd_fallback<CH, FW>(a, e, l1, l2, g, m, p, tag, local, !rs_ok, lm, ls, clse, wave);
         if (k == 0)
-            local = group_on_one_xcd(a.x, g, tag0, now_ticks() + a.x.wait_ticks, never, &flag) && a.x.local_ok;
+            local = group_on_one_xcd(a.x, g, tag0, now_ticks() + a.x.wait_ticks, never, &flag, wave) && a.x.local_ok;
         // ---- write; each row is refilled with the element after next
         const int kn = k + 2;
         const bool real = kn < n;
@@ -667,13 +757,12 @@ __device__ __forceinline__ void acc_row(float* dst, int lane, int L2, const floa
 // barriers.
 template <int CH, bool FW>
 __device__ void bwd_fallback(const BwdArgs1& a, int e, int l1, int l2, int g, int m, int p, unsigned tag,
-                             bool local, bool own, float* lacc, const float* lcl, float* ldc) {
+                             bool local, bool own, float* lacc, const float* lcl, float* ldc, int wave) {
     using R = Row<4, CH>;
     const int L2 = FW ? 4 * kWave * CH : a.L2;  // full-width rows: a constant
     constexpr int PL = R::PL;
-    const int lane = threadIdx.x % kWave;
-    const int wave = threadIdx.x / kWave;
-    const int t = threadIdx.x;
+    const int lane = lane_now();
+    const int t = wave * kWave + lane;
     const float* rst = a.row_stats + size_t(e) * 2 * a.L1;
     const auto ry = element_rsrc(a.sim, size_t(a.L1) * L2, e);
     const auto rg = element_rsrc(a.grad_out, size_t(a.L1) * L2, e);
@@ -725,6 +814,7 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_kernel(BwdArgs1 a) {
     __shared__ float rsv[kMembers][kOwn + 1];
     __shared__ __align__(16) float lcl[kMaxCols];  // column log-normalisers
     __shared__ __align__(16) float ldc[kMaxCols];
+    __shared__ __align__(16) float pre[kWaves * kPreRows * kMaxCols];  // next grad_out rows 1..3 of each wave
     __shared__ int flag;
     __shared__ __align__(16) int votes[2][kWaves];
     const int lane = threadIdx.x % kWave;
@@ -741,14 +831,25 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_kernel(BwdArgs1 a) {
     const int row0 = m * kRowsPerMember + wave * kRowsPerWave;
     float Yv[kRowsPerWave][PL], Gv[kRowsPerWave][PL];
     const size_t elem = size_t(a.L1) * L2;
+    const unsigned pre0 = unsigned(uintptr_t((__attribute__((address_space(3))) float*)(pre)));
     {
+        // grad_out rows 1..3 into LDS (as every later element's), then the
+        // register rows; the LDS rows have landed once at most the 5 CH
+        // register-row loads issued after them are outstanding
+        const v4u rgw = element_words(a.grad_out, elem, g);
+#pragma unroll
+        for (int j = 1; j < kRowsPerWave; ++j)
+            load_row_lds<CH>(rgw, min(row0 + j, a.L1 - 1), L2, lane,
+                             pre0 + unsigned(wave * kPreRows + j - 1) * kMaxCols * 4u);
         const auto ry = element_rsrc(a.sim, elem, g);
         const auto rg = element_rsrc(a.grad_out, elem, g);
 #pragma unroll
-        for (int j = 0; j < kRowsPerWave; ++j) {
-            load_row<CH>(ry, min(row0 + j, a.L1 - 1), L2, lane, Yv[j]);
-            load_row<CH>(rg, min(row0 + j, a.L1 - 1), L2, lane, Gv[j]);
-        }
+        for (int j = 0; j < kRowsPerWave; ++j) load_row<CH>(ry, min(row0 + j, a.L1 - 1), L2, lane, Yv[j]);
+        load_row<CH>(rg, min(row0, a.L1 - 1), L2, lane, Gv[0]);
+        asm volatile("" ::: "memory");  // every load above is issued before the wait
+        constexpr unsigned vm = 5 * CH;
+        static_assert(vm < 64, "vmcnt field");
+        __builtin_amdgcn_s_waitcnt((vm & 15u) | ((vm >> 4) << 14) | 0x0f70u);
     }
     // column log-normalisers of an element, two columns per thread
     auto col_norm_of = [&](int e, int t) {
@@ -765,9 +866,9 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_kernel(BwdArgs1 a) {
     // that no wait for it delays the first element.
     bool local = false;
     for (int k = 0; k < n; ++k) {
-        // thread indices re-formed per element (see fwd_kernel)
-        const int t = fresh(int(threadIdx.x));
-        const int lane = t % kWave;
+        // thread indices re-formed per element (see lane_now)
+        const int lane = lane_now();
+        const int t = wave * kWave + lane;
         const int e = g + G * k;
         const unsigned tag = tag0 | unsigned(k + 1);
         const int p = k & 1;
@@ -783,6 +884,17 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_kernel(BwdArgs1 a) {
             const bool row_ok = i < l1;
             const float rl = row_ok ? log_norm(scalar_load(rst + i), scalar_load(rst + a.L1 + i)) : INFINITY;
             __builtin_amdgcn_sched_barrier(0);  // one row at a time: bounded live ranges
+            if (j > 0) {  // in LDS (prefetched during the previous element's exchange)
+                const float* src = pre + (wave * kPreRows + j - 1) * kMaxCols + 4 * lane;
+#pragma unroll
+                for (int kk = 0; kk < CH; ++kk) {
+                    const float4 v = *reinterpret_cast<const float4*>(src + kk * 256);
+                    Gv[j][4 * kk + 0] = v.x;
+                    Gv[j][4 * kk + 1] = v.y;
+                    Gv[j][4 * kk + 2] = v.z;
+                    Gv[j][4 * kk + 3] = v.w;
+                }
+            }
             float r[PL];
             row_q<CH>(Yv[j], Gv[j], r, rl, row_ok, lane, l2, L2, a.sc, lcl, row_ok && l2 == 4 * kWave * CH);
             acc_row<CH>(lacc + wave * kMaxCols, lane, L2, Gv[j], j == 0);
@@ -790,8 +902,14 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_kernel(BwdArgs1 a) {
 #pragma unroll
             for (int qq = 0; qq < PL; ++qq) dl += Gv[j][qq];
             const float dr = wave_sum(dl);
+            // t formed here: without the asm the compiler sinks this update
+            // past the exchange into phase B, keeping r and q both live there
+            // (the register file then overflows and spills)
 #pragma unroll
-            for (int qq = 0; qq < PL; ++qq) Gv[j][qq] = fmaf(-dr, r[qq], 2.0f * Gv[j][qq]);
+            for (int qq = 0; qq < PL; ++qq) {
+                Gv[j][qq] = fmaf(-dr, r[qq], 2.0f * Gv[j][qq]);
+                asm volatile("" : "+v"(Gv[j][qq]));
+            }
         }
         // ---- fold the waves, publish this member's column partials
         __syncthreads();
@@ -812,17 +930,38 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_kernel(BwdArgs1 a) {
             res::publish(dst + 1, s.y, tag, local);
         }
         const long long deadline = now_ticks() + a.x.wait_ticks;
-        bool ok;
-        {
+        const bool real = k + 1 < n;
+        // ---- the prefetching waves: the next element's grad_out rows 1..3 of
+        // every wave into LDS (phase A above has read this element's)
+        if (wave >= kPollWaves && real) {
+            const v4u rg = element_words(a.grad_out, elem, g + G * (k + 1));
+            constexpr int per = kWaves / (kWaves - kPollWaves);
+#pragma unroll
+            for (int q = 0; q < per; ++q) {
+                const int tw = (wave - kPollWaves) * per + q;
+#pragma unroll
+                for (int j = 1; j < kRowsPerWave; ++j) {
+                    const int i = m * kRowsPerMember + tw * kRowsPerWave + j;
+                    load_row_lds<CH>(rg, min(i, a.L1 - 1), L2, lane,
+                                     pre0 + unsigned(tw * kPreRows + j - 1) * kMaxCols * 4u);
+                }
+            }
+        }
+        // ---- the polling waves: reduce-scatter, thread t < 256 reads members
+        // 4h .. 4h + 3 (h = t / 32) of column 32m + t % 32
+        bool ok = true;
+        if (wave < kPollWaves) {
             const int c = t & (kOwn - 1);
             const int h = t >> 5;
-            float v0 = 0.0f, v1 = 0.0f;
-            ok = poll2(part_row(a.x, g, p, 2 * h) + kOwn * m + c, part_row(a.x, g, p, 2 * h + 1) + kOwn * m + c,
-                       tag, deadline, never, v0, v1);
-            rsv[2 * h][c] = v0;
-            rsv[2 * h + 1][c] = v1;
+            unsigned long long* const w[4] = {
+                part_row(a.x, g, p, 4 * h) + kOwn * m + c, part_row(a.x, g, p, 4 * h + 1) + kOwn * m + c,
+                part_row(a.x, g, p, 4 * h + 2) + kOwn * m + c, part_row(a.x, g, p, 4 * h + 3) + kOwn * m + c};
+            float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            ok = poll4(w, tag, deadline, never, v);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) rsv[4 * h + i][c] = v[i];
         }
-        const bool rs_ok = !block_any(!ok, votes[0]);
+        const bool rs_ok = !block_any(!ok, votes[0], wave);
         if (rs_ok) {
             if (t < kOwn) {
                 float s = 0.0f;
@@ -830,24 +969,34 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_kernel(BwdArgs1 a) {
                 for (int w = 0; w < kMembers; ++w) s += rsv[w][t];
                 res::publish(res_row(a.x, g, p) + kOwn * m + t, s, tag, local);
             }
-            float v0 = 0.0f, v1 = 0.0f;
-            ok = poll2(res_row(a.x, g, p) + 2 * t, res_row(a.x, g, p) + 2 * t + 1, tag, deadline, never, v0, v1);
-            ldc[2 * t] = v0;
-            ldc[2 * t + 1] = v1;
+            // all-gather: thread t < 256 reads columns 4t .. 4t + 3
+            if (wave < kPollWaves) {
+                unsigned long long* r = res_row(a.x, g, p) + 4 * t;
+                unsigned long long* const w[4] = {r, r + 1, r + 2, r + 3};
+                float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+                ok = poll4(w, tag, deadline, never, v);
+                *reinterpret_cast<float4*>(ldc + 4 * t) = make_float4(v[0], v[1], v[2], v[3]);
+            }
         }
-        if (!rs_ok || block_any(!ok, votes[1])) bwd_fallback<CH, FW>(a, e, l1, l2, g, m, p, tag, local, !rs_ok, lacc,
-                                                            lcl, ldc);
+        if (!rs_ok || block_any(!ok, votes[1], wave))
+            bwd_fallback<CH, FW>(a, e, l1, l2, g, m, p, tag, local, !rs_ok, lacc, lcl, ldc, wave);
         if (k == 0)
-            local = group_on_one_xcd(a.x, g, tag0, now_ticks() + a.x.wait_ticks, never, &flag) && a.x.local_ok;
-        // ---- phase B; each row is refilled with the next element's
-        const bool real = k + 1 < n;
+            local = group_on_one_xcd(a.x, g, tag0, now_ticks() + a.x.wait_ticks, never, &flag, wave) && a.x.local_ok;
+        // ---- phase B; each row is refilled with the next element's (grad_out
+        // rows 1..3: already on their way to LDS)
+        if (wave >= kPollWaves) __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): the prefetch has landed
         const int en = g + G * (real ? k + 1 : k);
         ncl = col_norm_of(en, t);
         const auto ro = element_rsrc(a.grad_sim, elem, e);
         const auto ry = element_rsrc(a.sim, elem, en);
         const auto rg = element_rsrc(a.grad_out, elem, en);
+        // One row at a time, its loads after its stores (scheduling barriers):
+        // loads hoisted ahead into fresh registers would raise the register
+        // count past the file and spill, and a spill reload waits for every
+        // store and load the wave has in flight.
 #pragma unroll
         for (int j = 0; j < kRowsPerWave; ++j) {
+            __builtin_amdgcn_sched_barrier(0);
             const int i = row0 + j;
             float o[PL];
             const int z = fresh(0);  // column values read per row (see row_q)
@@ -862,10 +1011,12 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_kernel(BwdArgs1 a) {
                 }
             }
             if (i < a.L1) store_row<CH>(ro, i, L2, lane, o);
+            __builtin_amdgcn_sched_barrier(0);
             const int ir = real ? min(i, a.L1 - 1) : 0;
             load_row<CH>(ry, ir, L2, lane, Yv[j]);
-            load_row<CH>(rg, ir, L2, lane, Gv[j]);
+            if (j == 0) load_row<CH>(rg, ir, L2, lane, Gv[j]);
         }
+        __builtin_amdgcn_sched_barrier(0);
     }
 }
 
