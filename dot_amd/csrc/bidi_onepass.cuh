@@ -76,6 +76,9 @@ constexpr unsigned kMaxEpoch = (1u << (32 - kStageBits)) - 1;
 // complete in issue order).
 constexpr int kPollWaves = kWaves / 2;
 constexpr int kPreRows = kRowsPerWave - 1;
+// Forward: rows of each wave's element after next loaded into LDS while the
+// exchange runs.
+constexpr int kFwdPreRows = 2;
 
 // Exchange words: partials [groups][2][kMembers][kMaxCols], results
 // [groups][2][kMaxCols], XCC announces [groups][kMembers]; the middle 2 is the
@@ -460,27 +463,29 @@ __device__ void fwd_fallback(const FwdArgs1& a, int e, int l1, int l2, int g, in
     __syncthreads();
 }
 
-// True when every member of group g runs on this workgroup's XCD (their
-// announced XCC ids); a wait past the deadline reads as "no".  Contains
-// barriers.
-__device__ __forceinline__ bool group_on_one_xcd(const Exchange& x, int g, unsigned tag0, long long deadline,
-                                                 bool never, int* flag, int wave) {
+// Deadline of the XCD check (s_memrealtime ticks of 10 ns): the members of a
+// launch start within a few microseconds of each other.
+constexpr int kXcdCheckTicks = 500;
+
+// Run by one wave at the start of a launch, before it issues any row load
+// (its poll then queues behind nothing): *flag = 1 when every member of group
+// g runs on this workgroup's XCD (their announced XCC ids), else 0; a member
+// not yet announced by the deadline reads as "no" and leaves the call's
+// exchange at agent scope.  The other waves read the flag after a barrier.
+// Each member decides alone: one that sees all 32 ids on its own XCD knows
+// that every reader of its words is there, and a member that does not uses
+// agent-scope stores, which every reader sees.
+__device__ __forceinline__ void check_group_xcd(const Exchange& x, int g, unsigned tag0, bool never, int* flag) {
     const int me = res::xcc_id();
-    if (wave == 0) {
-        const int lane = lane_now();
-        int same = 1;
-        if (lane < kMembers) {
-            float v0, v1;
-            unsigned long long* w = xcc_word(x, g, lane);
-            same = poll2(w, w, tag0, deadline, never, v0, v1) && __float_as_int(v0) == me;
-        }
-        const int all = __all(same);
-        *flag = all;  // every lane of wave 0: the same value
+    const long long deadline = now_ticks() + kXcdCheckTicks;
+    const int lane = lane_now();
+    int same = 1;
+    if (lane < kMembers) {
+        float v0, v1;
+        unsigned long long* w = xcc_word(x, g, lane);
+        same = poll2(w, w, tag0, deadline, never, v0, v1) && __float_as_int(v0) == me;
     }
-    lds_barrier();
-    const bool local = *flag != 0;
-    lds_barrier();
-    return local;
+    *flag = __all(same);  // every lane: the same value
 }
 
 template <int CH, bool FW>
@@ -493,6 +498,9 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(FwdArgs1 a) {
     constexpr int PL = R::PL;
     __shared__ __align__(16) float lm[kWaves * kMaxCols];
     __shared__ __align__(16) float ls[kWaves * kMaxCols];
+    // rows 0 .. kFwdPreRows - 1 of each wave's element after next, loaded
+    // during the exchange
+    __shared__ __align__(16) float pre[kWaves * kFwdPreRows * kMaxCols];
     __shared__ float rsv[kMembers][kOwn + 1];
     __shared__ __align__(16) float clse[kMaxCols];
     __shared__ int flag;
@@ -504,6 +512,7 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(FwdArgs1 a) {
     const int g = blockIdx.x % G;
     const int m = blockIdx.x / G;
     const int n = (a.B - g + G - 1) / G;  // this group's elements
+    const unsigned pre0 = unsigned(uintptr_t((__attribute__((address_space(3))) float*)(pre)));
     if (n <= 0) return;
     const bool never = a.x.wait_ticks < 0;
     const unsigned tag0 = a.x.epoch << kStageBits;
@@ -519,12 +528,10 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(FwdArgs1 a) {
 #pragma unroll
         for (int j = 0; j < kRowsPerWave; ++j) load_row<CH>(rs, real ? min(row0 + j, L1 - 1) : 0, L2, lane, buf[j]);
     };
+    if (wave == kWaves - 1) check_group_xcd(a.x, g, tag0, never, &flag);
     load(0, 0, X);
     load(1, 0, Y);
-    // Element 0 is exchanged with agent-scope stores (visible on every XCD);
-    // the XCD check runs after it, when every member has long announced, so
-    // that no wait for it delays the first element.
-    bool local = false;
+    bool local = false;  // set at element 0's first barrier from the check's flag
 
     auto stage = [&](int k, float(&buf)[kRowsPerWave][PL]) {
         // thread indices re-formed per element: addresses derived from them are
@@ -575,6 +582,7 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(FwdArgs1 a) {
         R::store(lm + wave * kMaxCols, lane, L2, cm);
         R::store(ls + wave * kMaxCols, lane, L2, cs);
         __syncthreads();
+        if (k == 0) local = flag != 0 && a.x.local_ok;
         {
             float l0, l1v;
             fold_lse(lm, ls, t, L2, l0, l1v);
@@ -583,16 +591,36 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(FwdArgs1 a) {
             res::publish(dst + 1, l1v, tag, local);
         }
         const long long deadline = now_ticks() + a.x.wait_ticks;
-        // ---- reduce-scatter: member m owns columns [32m, 32m + 32)
-        bool ok;
-        {
+        // ---- the first rows of every wave's element after next, into LDS
+        // by the non-polling waves: HBM traffic while the exchange runs, not
+        // queued ahead of any poll
+        const int kn = k + 2;
+        const bool real = kn < n;
+        if (wave >= kPollWaves && real) {
+            const v4u rw = element_words(a.sim, elem, g + G * kn);
+            constexpr int per = kWaves / (kWaves - kPollWaves);
+#pragma unroll
+            for (int q = 0; q < per; ++q) {
+                const int tw = (wave - kPollWaves) * per + q;
+#pragma unroll
+                for (int j = 0; j < kFwdPreRows; ++j)
+                    load_row_lds<CH>(rw, min(m * kRowsPerMember + tw * kRowsPerWave + j, L1 - 1), L2, lane,
+                                     pre0 + unsigned(tw * kFwdPreRows + j) * kMaxCols * 4u);
+            }
+        }
+        // ---- reduce-scatter (waves < kPollWaves): member m owns columns
+        // [32m, 32m + 32); thread t < 256 reads members 4h .. 4h + 3 (h = t / 32)
+        bool ok = true;
+        if (wave < kPollWaves) {
             const int c = t & (kOwn - 1);
-            const int h = t >> 5;  // members 2h, 2h + 1
-            float v0 = 0.0f, v1 = 0.0f;
-            ok = poll2(part_row(a.x, g, p, 2 * h) + kOwn * m + c, part_row(a.x, g, p, 2 * h + 1) + kOwn * m + c,
-                       tag, deadline, never, v0, v1);
-            rsv[2 * h][c] = v0;
-            rsv[2 * h + 1][c] = v1;
+            const int h = t >> 5;
+            unsigned long long* const w[4] = {
+                part_row(a.x, g, p, 4 * h) + kOwn * m + c, part_row(a.x, g, p, 4 * h + 1) + kOwn * m + c,
+                part_row(a.x, g, p, 4 * h + 2) + kOwn * m + c, part_row(a.x, g, p, 4 * h + 3) + kOwn * m + c};
+            float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            ok = poll4(w, tag, deadline, never, v);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) rsv[4 * h + i][c] = v[i];
         }
         const bool rs_ok = !block_any(!ok, votes[0], wave);
         if (rs_ok) {
@@ -608,19 +636,22 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(FwdArgs1 a) {
                     cst[L2 + col] = S;
                 }
             }
-            // ---- all-gather
-            float v0 = 0.0f, v1 = 0.0f;
-            ok = poll2(res_row(a.x, g, p) + 2 * t, res_row(a.x, g, p) + 2 * t + 1, tag, deadline, never, v0, v1);
-            clse[2 * t] = v0;
-            clse[2 * t + 1] = v1;
+            // ---- all-gather (waves < kPollWaves): thread t < 256 reads columns 4t .. 4t + 3
+            if (wave < kPollWaves) {
+                unsigned long long* r = res_row(a.x, g, p) + 4 * t;
+                unsigned long long* const w[4] = {r, r + 1, r + 2, r + 3};
+                float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+                ok = poll4(w, tag, deadline, never, v);
+                *reinterpret_cast<float4*>(clse + 4 * t) = make_float4(v[0], v[1], v[2], v[3]);
+            }
         }
         if (!rs_ok || block_any(!ok, votes[1], wave))
             fwd_fallback<CH, FW>(a, e, l1, l2, g, m, p, tag, local, !rs_ok, lm, ls, clse, wave);
-        if (k == 0)
-            local = group_on_one_xcd(a.x, g, tag0, now_ticks() + a.x.wait_ticks, never, &flag, wave) && a.x.local_ok;
-        // ---- write; each row is refilled with the element after next
-        const int kn = k + 2;
-        const bool real = kn < n;
+        // ---- write; each row is refilled with the element after next (its
+        // first rows from LDS, once the loading waves have waited for them and
+        // passed a barrier)
+        if (wave >= kPollWaves && real) __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+        lds_barrier();
         const auto rs = element_rsrc(a.sim, elem, g + G * (real ? kn : k));
         const auto ro = element_rsrc(a.out, elem, e);
 #pragma unroll
@@ -646,7 +677,19 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(FwdArgs1 a) {
                 for (int ee = 0; ee < PL; ++ee) o[ee] = (i < l1 && R::valid(lane, ee, l2)) ? o[ee] : 0.0f;
             }
             if (i < L1) store_row<CH>(ro, i, L2, lane, o);
-            load_row<CH>(rs, real ? min(i, L1 - 1) : 0, L2, lane, buf[j]);
+            if (j < kFwdPreRows && real) {
+                const float* src = pre + (wave * kFwdPreRows + j) * kMaxCols + 4 * lane;
+#pragma unroll
+                for (int kk = 0; kk < CH; ++kk) {
+                    const float4 v = *reinterpret_cast<const float4*>(src + kk * 256);
+                    buf[j][4 * kk + 0] = v.x;
+                    buf[j][4 * kk + 1] = v.y;
+                    buf[j][4 * kk + 2] = v.z;
+                    buf[j][4 * kk + 3] = v.w;
+                }
+            } else {
+                load_row<CH>(rs, real ? min(i, L1 - 1) : 0, L2, lane, buf[j]);
+            }
         }
     };
     for (int k = 0; k < n; k += 2) {
@@ -828,6 +871,7 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_kernel(BwdArgs1 a) {
     const bool never = a.x.wait_ticks < 0;
     const unsigned tag0 = a.x.epoch << kStageBits;
     if (t == 0) res::publish(xcc_word(a.x, g, m), __int_as_float(res::xcc_id()), tag0);
+    if (wave == kWaves - 1) check_group_xcd(a.x, g, tag0, never, &flag);
     const int row0 = m * kRowsPerMember + wave * kRowsPerWave;
     float Yv[kRowsPerWave][PL], Gv[kRowsPerWave][PL];
     const size_t elem = size_t(a.L1) * L2;
@@ -861,10 +905,7 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_kernel(BwdArgs1 a) {
         return v;
     };
     float2 ncl = col_norm_of(g, t);
-    // Element 0 is exchanged with agent-scope stores (visible on every XCD);
-    // the XCD check runs after it, when every member has long announced, so
-    // that no wait for it delays the first element.
-    bool local = false;
+    bool local = false;  // set at element 0's first barrier from the check's flag
     for (int k = 0; k < n; ++k) {
         // thread indices re-formed per element (see lane_now)
         const int lane = lane_now();
@@ -913,6 +954,7 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_kernel(BwdArgs1 a) {
         }
         // ---- fold the waves, publish this member's column partials
         __syncthreads();
+        if (k == 0) local = flag != 0 && a.x.local_ok;
         {
             float2 s = make_float2(0.0f, 0.0f);
             if (2 * t < L2) {
@@ -980,8 +1022,6 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_kernel(BwdArgs1 a) {
         }
         if (!rs_ok || block_any(!ok, votes[1], wave))
             bwd_fallback<CH, FW>(a, e, l1, l2, g, m, p, tag, local, !rs_ok, lacc, lcl, ldc, wave);
-        if (k == 0)
-            local = group_on_one_xcd(a.x, g, tag0, now_ticks() + a.x.wait_ticks, never, &flag, wave) && a.x.local_ok;
         // ---- phase B; each row is refilled with the next element's (grad_out
         // rows 1..3: already on their way to LDS)
         if (wave >= kPollWaves) __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): the prefetch has landed
