@@ -1042,5 +1042,227 @@ __global__ __launch_bounds__(kThreads) void unrolled(UnrArgs a) {
     if (threadIdx.x == 0) a.tau_partial[gid] = dead ? __builtin_nanf("") : tsum;
 }
 
+// Half rows (32 floats a lane: chunks k = 0 .. HCH - 1 of 256 columns) of a
+// [B, M, N] matrix through a buffer resource: one 32-bit offset per row and
+// the chunk offsets as constants, so that a row costs one address register
+// instead of a 64-bit address per chunk.  `base` is the matrix (at most 2 GiB,
+// checked by the launcher).
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t matrix_rsrc(const float* base, size_t floats) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), 0, unsigned(floats * 4), 0x00020000);
+}
+
+// x = the half row at byte offset `off` (the lane's first column); columns
+// past `nh` (the half's valid width) read as 0 unless FULL.
+template <int HCH, bool FULL>
+__device__ __forceinline__ void hload(__amdgpu_buffer_rsrc_t r, unsigned off, int lane, int nh, float (&x)[4 * HCH]) {
+#pragma unroll
+    for (int k = 0; k < HCH; ++k) {
+        const u32x4 t = __builtin_amdgcn_raw_buffer_load_b128(r, off, k * 1024, 0);
+        const bool in = FULL || k * 256 + 4 * lane < nh;
+        x[4 * k + 0] = in ? __uint_as_float(t.x) : 0.0f;
+        x[4 * k + 1] = in ? __uint_as_float(t.y) : 0.0f;
+        x[4 * k + 2] = in ? __uint_as_float(t.z) : 0.0f;
+        x[4 * k + 3] = in ? __uint_as_float(t.w) : 0.0f;
+    }
+}
+
+// Stores the half row's valid columns (aux 2: non-temporal).
+template <int HCH, bool FULL, int AUX>
+__device__ __forceinline__ void hstore(__amdgpu_buffer_rsrc_t r, unsigned off, int lane, int nh,
+                                       const float (&x)[4 * HCH]) {
+#pragma unroll
+    for (int k = 0; k < HCH; ++k) {
+        const u32x4 t = {__float_as_uint(x[4 * k + 0]), __float_as_uint(x[4 * k + 1]), __float_as_uint(x[4 * k + 2]),
+                         __float_as_uint(x[4 * k + 3])};
+        if (FULL || k * 256 + 4 * lane < nh) __builtin_amdgcn_raw_buffer_store_b128(t, r, off, k * 1024, AUX);
+    }
+}
+
+// unrolled() for rows of 2049 .. 4096 floats (64 per lane), where Gamma,
+// the scores and the column sums of a row would not all fit a lane's
+// registers: each row is streamed in two halves of HCH chunks (32 floats per
+// lane).  Gamma_Y of both halves and the column sums stay in registers; the
+// scores of the half processed first are read again (from the caches) for the
+// second update, those of the other half are still in registers.  The
+// arithmetic per element, and its order, are unrolled()'s.  FULL: N = 2 HN
+// (no partial chunks).
+template <int HCH, bool FULL>
+__global__ __launch_bounds__(kThreads) void unrolled_halves(UnrArgs a) {
+    constexpr int VEC = 4;
+    constexpr int CH = 2 * HCH;
+    constexpr int HL = VEC * HCH;         // floats per lane per half
+    constexpr int HN = HCH * kWave * VEC;  // columns per half
+    extern __shared__ float lds[];
+    const int wave = threadIdx.x / kWave;
+    const int gid = res::logical_group(a.W);
+    const int b = gid / a.W;
+    const int w = gid % a.W;
+    const int row0 = w * a.R;
+    const int rend = min(row0 + a.R, a.M);
+    const int c0 = slice_begin(w, a.W, a.N), c1 = slice_begin(w + 1, a.W, a.N);
+    const int G = gridDim.x;
+    float* tree = lds;
+    float* lds_cs = tree + kFoldRows<VEC, CH> * a.N;
+    float* lds_v = lds_cs + a.N;
+    float* lds_vm = lds_v + a.N;
+    float* red = lds_vm + a.N;
+    float* scratch = red + a.N + a.W;
+    const size_t bM = size_t(b) * a.M;
+    const size_t total = size_t(a.B) * a.M * a.N;
+    const auto rX = matrix_rsrc(a.X, total);
+    const auto rG = matrix_rsrc(a.gamma, total);
+    const auto rP = matrix_rsrc(a.P, total);
+    const auto rGrad = matrix_rsrc(a.grad, total);
+    const bool cost_kind = a.scores_kind < 0;
+    const float gc = a.gC ? a.gC[b * a.gc_step] : 0.0f;
+    const float csign = cost_kind ? 1.0f : -1.0f;  // C = csign * scores
+    bool dead = false;
+    float tacc = 0.0f;
+    res::announce_xcc(a.part, a.N, b, a.W, w);
+    bool local = false;  // set by the XCD check before the first exchange
+    // byte offset of a lane's first column of half h of row i
+    auto offset = [&](int i, int h, int ln) {
+        return unsigned((bM + i) * a.N + h * HN) * 4u + unsigned(ln) * 16u;
+    };
+
+    // Half h of a row's gradient from its final Gamma (kernels.cu:926-963).
+    auto epilogue = [&](unsigned off, int ln, int nh, float (&gam)[HL], const float (&x)[HL]) {
+        float p[HL];
+        hload<HCH, FULL>(rP, off, ln, nh, p);
+#pragma unroll
+        for (int e = 0; e < HL; ++e) {
+            const float gl = gam[e] * a.inv_tau;
+            const float la = cost_kind ? -x[e] : x[e];
+            if (FULL || (e / VEC) * 256 + VEC * ln < nh) tacc = fmaf(gam[e], la, tacc);
+            gam[e] = cost_kind ? gc * p[e] - gl : gl - gc * p[e];
+        }
+        hstore<HCH, FULL, 2>(rGrad, off, ln, nh, gam);
+    };
+    auto exchange = [&](float (&acc)[2 * HL], unsigned tag) {
+        const int cur = tag & 1;
+        publish_row<VEC, CH>(acc, tree, a.N, a.part + (size_t(cur) * G + gid) * a.N, tag, local);
+        unsigned long long* res_row = a.res + (size_t(cur) * a.B + b) * a.N;
+        reduce_slice(a.part + size_t(cur) * G * a.N + size_t(b) * a.W * a.N, a.N, a.W, c0, c1, tag, red,
+                     a.spin_limit, a.status, dead, [&](int j, float tot) { publish(res_row + j, tot, tag, local); });
+        gather(res_row, a.N, tag, lds_cs, a.spin_limit, a.status, dead);
+        __syncthreads();
+    };
+
+    // Gamma = G * P (kernels.cu:844-854), half by half.
+    float acc[2 * HL];
+#pragma unroll
+    for (int e = 0; e < 2 * HL; ++e) acc[e] = 0.0f;
+#pragma unroll 1
+    for (int l = wave; row0 + l < rend; l += kWaves) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int ln = opaque_lane();
+            const int nh = a.N - h * HN;
+            const unsigned off = offset(row0 + l, h, ln);
+            float gam[HL], x[HL];
+            hload<HCH, FULL>(rP, off, ln, nh, gam);
+            hload<HCH, FULL>(rX, off, ln, nh, x);
+            if (a.gP) {
+                float g[HL];
+                hload<HCH, FULL>(matrix_rsrc(a.gP, total), off, ln, nh, g);
+#pragma unroll
+                for (int e = 0; e < HL; ++e) gam[e] *= g[e] + (a.gC ? gc * (csign * x[e]) : 0.0f);
+            } else {
+#pragma unroll
+                for (int e = 0; e < HL; ++e) gam[e] *= a.gC ? gc * (csign * x[e]) : 0.0f;
+            }
+#pragma unroll
+            for (int e = 0; e < HL; ++e) acc[h * HL + e] += gam[e];
+            if (a.T == 0) epilogue(off, ln, nh, gam, x);
+            else hstore<HCH, FULL, 0>(rG, off, ln, nh, gam);
+        }
+    }
+    local = res::element_on_one_xcd(a.part, a.N, b, a.W, w, a.spin_limit, a.status, dead, scratch) && a.local_ok;
+    unsigned tag = 1;
+    if (a.T > 0) exchange(acc, tag);
+
+    for (int t = a.T - 1; t >= 0; --t) {
+        const float* vt = a.v_hist + (size_t(t) * a.B + b) * a.N;
+        const float* vm = t > 0 ? a.v_hist + (size_t(t - 1) * a.B + b) * a.N : nullptr;
+        for (int j = threadIdx.x; j < a.N; j += kThreads) {
+            lds_v[j] = vt[j];
+            lds_vm[j] = vm ? vm[j] : 0.0f;
+        }
+        __syncthreads();
+        const float* ut = a.u_hist + size_t(t) * a.B * a.M + bM;
+#pragma unroll
+        for (int e = 0; e < 2 * HL; ++e) acc[e] = 0.0f;
+#pragma unroll 1
+        for (int l = wave; row0 + l < rend; l += kWaves) {
+            // u_t of the row: wave-uniform, read through the scalar unit (this
+            // kernel does not write u_hist)
+            const float ui = *(const __attribute__((address_space(4))) float*)(reinterpret_cast<uintptr_t>(ut + row0 + l));
+            float gy[2 * HL];  // Gamma_Y of the row
+            float x[HL];       // the scores of the half processed last
+            float tl = 0.0f;
+            // Gamma_Y = Gamma - safe_exp(K + u_t + v_t) colsum(Gamma), and its row sum
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int ln = opaque_lane();
+                const int nh = a.N - h * HN;
+                const unsigned off = offset(row0 + l, h, ln);
+                float gam[HL];
+                hload<HCH, FULL>(rG, off, ln, nh, gam);
+                hload<HCH, FULL>(rX, off, ln, nh, x);
+#pragma unroll
+                for (int k = 0; k < HCH; ++k) {
+                    float cs[VEC], vv[VEC];
+                    const int c = h * HN + k * 256 + VEC * ln;
+                    const float4 cs4 = *reinterpret_cast<const float4*>(lds_cs + min(c, a.N - VEC));
+                    const float4 vv4 = *reinterpret_cast<const float4*>(lds_v + min(c, a.N - VEC));
+                    cs[0] = cs4.x; cs[1] = cs4.y; cs[2] = cs4.z; cs[3] = cs4.w;
+                    vv[0] = vv4.x; vv[1] = vv4.y; vv[2] = vv4.z; vv[3] = vv4.w;
+                    const bool in = FULL || k * 256 + VEC * ln < nh;
+#pragma unroll
+                    for (int q = 0; q < VEC; ++q) {
+                        const int e = k * VEC + q;
+                        const float y = gam[e] - safe_fast_exp((x[e] * a.kscale + ui) + vv[q]) * (in ? cs[q] : 0.0f);
+                        gy[h * HL + e] = y;
+                        if (in) tl += y;
+                    }
+                }
+            }
+            const float ti = wave_sum(tl);
+            // Gamma = Gamma_Y - safe_exp(K + u_t + v_{t-1}) rowsum(Gamma_Y): the
+            // second half first (its scores are in registers), then the first
+            // half with its scores read again
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                const int h = 1 - hh;
+                const int ln = opaque_lane();
+                const int nh = a.N - h * HN;
+                const unsigned off = offset(row0 + l, h, ln);
+                if (h == 0) hload<HCH, FULL>(rX, off, ln, nh, x);
+                float gam[HL];
+#pragma unroll
+                for (int k = 0; k < HCH; ++k) {
+                    float vv[VEC];
+                    const int c = h * HN + k * 256 + VEC * ln;
+                    const float4 vv4 = *reinterpret_cast<const float4*>(lds_vm + min(c, a.N - VEC));
+                    vv[0] = vv4.x; vv[1] = vv4.y; vv[2] = vv4.z; vv[3] = vv4.w;
+#pragma unroll
+                    for (int q = 0; q < VEC; ++q) {
+                        const int e = k * VEC + q;
+                        gam[e] = gy[h * HL + e] - safe_fast_exp((x[e] * a.kscale + ui) + vv[q]) * ti;
+                        acc[h * HL + e] += gam[e];
+                    }
+                }
+                if (t == 0) epilogue(off, ln, nh, gam, x);
+                else hstore<HCH, FULL, 0>(rG, off, ln, nh, gam);
+            }
+        }
+        if (t > 0) exchange(acc, ++tag);
+    }
+    const float tsum = block_reduce<kWaves>(wave_sum(tacc), scratch, OpSum{});
+    if (threadIdx.x == 0) a.tau_partial[gid] = dead ? __builtin_nanf("") : tsum;
+}
+
 }  // namespace pst
 }  // namespace dot_amd

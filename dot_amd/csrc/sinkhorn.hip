@@ -1119,12 +1119,21 @@ bool launch_stream_unrolled(const dot_sinkhorn_bwd_args* a, const UnrLayout& L, 
     dispatch_row(N, vec4, [&](auto vc, auto cc) {
         constexpr int V = decltype(vc)::value;
         constexpr int C = decltype(cc)::value;
-        if constexpr (V * C <= 32) {  // longer rows would spill: Gamma, the scores and the sums per lane
-            // fold rows | colsum | v_t | v_{t-1} N each | red N + W | scratch
-            const size_t lds = (size_t(pst::kFoldRows<V, C> + 4) * N + sc.W + 16) * sizeof(float);
+        // fold rows | colsum | v_t | v_{t-1} N each | red N + W | scratch
+        const size_t lds = (size_t(pst::kFoldRows<V, C> + 4) * N + sc.W + 16) * sizeof(float);
+        if constexpr (V * C <= 32) {
             launch_fill_zero(L.pst, 2 * words, stream);
             ProfScope prof("sk_unr_persistent", stream);
             ok = launch_persistent(pst::unrolled<V, C>, r, G, res::kThreads, lds, stream);
+        } else if constexpr (V == 4 && C == 16) {
+            // rows of exactly 4096 floats, streamed in halves through 32-bit
+            // buffer offsets (the matrix below 4 GiB); other lengths of 64 floats a
+            // lane take the per-step sweeps
+            if (N == 4 * C * kWave && size_t(B) * a->M * N * sizeof(float) <= 0xffffffffull) {
+                launch_fill_zero(L.pst, 2 * words, stream);
+                ProfScope prof("sk_unr_persistent", stream);
+                ok = launch_persistent(pst::unrolled_halves<C / 2, true>, r, G, res::kThreads, lds, stream);
+            }
         }
     });
     if (!ok) return false;

@@ -147,6 +147,30 @@ def test_unrolled_matches_oracle(B, M, N, tau, T, nonuni):
     assert sum_err(gtu, gto, go * -C / tau) < GRAD_TOL
 
 
+@pytest.mark.parametrize("B,M,N,tau,T,nonuni", [(2, 300, 4096, 0.3, 12, True), (3, 64, 4096, 0.1, 25, False)])
+def test_unrolled_rows_of_4096_persistent(B, M, N, tau, T, nonuni, monkeypatch):
+    """Rows of 4096 floats: the persistent unrolled kernel streams each row in
+    two halves (C5's shape).  Against the float64 oracle, and against the
+    per-step sweeps (DOT_AMD_PERSISTENT=0) of the same arithmetic."""
+    print(f"[sk_gpu] unrolled halves B={B} M={M} N={N} T={T}", flush=True)
+    rng = np.random.default_rng(B * 31 + M)
+    C = rng.random((B, M, N)).astype(np.float32)
+    G = rng.standard_normal((B, M, N)).astype(np.float32)
+    lga = lgb = None
+    if nonuni:
+        lga, lgb = np.log(_dirichlet(rng, B, M)), np.log(_dirichlet(rng, B, N))
+    t = lambda x: None if x is None else _t(x)
+    P, gu, gtu = _ops.sinkhorn_with_grads_unrolled(_t(-C), _t(G), tau, T, t(lga), t(lgb))
+    Po, go, gto = osk.with_grads_unrolled(-C, G, tau, T, lga, lgb)
+    assert rel_err(P, Po) < FWD_TOL
+    assert rel_err(gu, go) < GRAD_TOL
+    assert sum_err(gtu, gto, go * -C / tau) < GRAD_TOL
+    monkeypatch.setenv("DOT_AMD_PERSISTENT", "0")
+    P2, gu2, gtu2 = _ops.sinkhorn_with_grads_unrolled(_t(-C), _t(G), tau, T, t(lga), t(lgb))
+    assert rel_err(gu, gu2.cpu().numpy()) < 1e-5
+    assert torch.allclose(gtu, gtu2, rtol=1e-4, atol=1e-6)
+
+
 @pytest.mark.parametrize("seed,shape,tau", [(0, (1, 256, 256), 0.1), (1, (4, 96, 128), 0.05),
                                             (2, (3, 40, 60), 0.5), (3, (2, 512, 300), 0.02)])
 def test_early_stop_matches_oracle(seed, shape, tau):
