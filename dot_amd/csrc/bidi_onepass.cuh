@@ -70,12 +70,11 @@ constexpr int kMaxGroups = 8;
 constexpr int kStageBits = 12;
 constexpr int kMaxStages = (1 << kStageBits) - 1;         // elements per group per call
 constexpr unsigned kMaxEpoch = (1u << (32 - kStageBits)) - 1;
-// Backward: waves [0, kPollWaves) wait on the exchange while the others
-// prefetch rows 1 .. kRowsPerWave - 1 of every wave's next grad_out rows into
-// LDS (their loads then do not queue ahead of the polls: a wave's vector loads
-// complete in issue order).
+// Backward: waves [0, kPollWaves) wait on the exchange while the others load
+// every wave's rows of the next grad_out into LDS (their loads then do not
+// queue ahead of the polls: a wave's vector loads complete in issue order).
 constexpr int kPollWaves = kWaves / 2;
-constexpr int kPreRows = kRowsPerWave - 1;
+constexpr int kPreRows = kRowsPerWave;
 // Forward: rows of each wave's element after next loaded into LDS while the
 // exchange runs.
 constexpr int kFwdPreRows = 2;
@@ -171,6 +170,16 @@ __device__ __forceinline__ bool block_any(bool pred, int* votes, int wave) {
     const int4 v0 = reinterpret_cast<const int4*>(votes)[0];
     const int4 v1 = reinterpret_cast<const int4*>(votes)[1];
     return (v0.x | v0.y | v0.z | v0.w | v1.x | v1.y | v1.z | v1.w) != 0;
+}
+
+// The OR over the workgroup's waves of a wave-uniform `bits` (every lane of
+// wave `wave` writes the same vote), in every thread; one barrier.
+__device__ __forceinline__ int block_or(int bits, int* votes, int wave) {
+    votes[wave] = bits;
+    lds_barrier();
+    const int4 v0 = reinterpret_cast<const int4*>(votes)[0];
+    const int4 v1 = reinterpret_cast<const int4*>(votes)[1];
+    return v0.x | v0.y | v0.z | v0.w | v1.x | v1.y | v1.z | v1.w;
 }
 
 // Wave-uniform reads of inputs that no kernel of this file writes (lengths,
@@ -853,13 +862,17 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_kernel(BwdArgs1 a) {
     using R = Row<4, CH>;
     const int L2 = FW ? 4 * kWave * CH : a.L2;  // full-width rows: a constant
     constexpr int PL = R::PL;
-    __shared__ __align__(16) float lacc[kWaves * kMaxCols];
     __shared__ float rsv[kMembers][kOwn + 1];
     __shared__ __align__(16) float lcl[kMaxCols];  // column log-normalisers
     __shared__ __align__(16) float ldc[kMaxCols];
-    __shared__ __align__(16) float pre[kWaves * kPreRows * kMaxCols];  // next grad_out rows 1..3 of each wave
+    // every wave's grad_out rows of the element (loaded during the previous
+    // element's exchange); once phase A has read them, the first kWaves rows'
+    // worth holds the waves' column partials for the fold
+    __shared__ __align__(16) float pre[kWaves * kPreRows * kMaxCols];
+    float* const lacc = pre;
     __shared__ int flag;
     __shared__ __align__(16) int votes[2][kWaves];
+    __shared__ int rsflag[kPollWaves];  // (element + 1) << 1 | failed, per polling wave
     const int lane = threadIdx.x % kWave;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const int t = threadIdx.x;
@@ -872,29 +885,46 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_kernel(BwdArgs1 a) {
     const unsigned tag0 = a.x.epoch << kStageBits;
     if (t == 0) res::publish(xcc_word(a.x, g, m), __int_as_float(res::xcc_id()), tag0);
     if (wave == kWaves - 1) check_group_xcd(a.x, g, tag0, never, &flag);
+    if (t < kPollWaves) rsflag[t] = 0;  // read after the first element's barriers
     const int row0 = m * kRowsPerMember + wave * kRowsPerWave;
     float Yv[kRowsPerWave][PL], Gv[kRowsPerWave][PL];
     const size_t elem = size_t(a.L1) * L2;
     const unsigned pre0 = unsigned(uintptr_t((__attribute__((address_space(3))) float*)(pre)));
     {
-        // grad_out rows 1..3 into LDS (as every later element's), then the
-        // register rows; the LDS rows have landed once at most the 5 CH
-        // register-row loads issued after them are outstanding
+        // this wave's grad_out rows into LDS (as every later element's), then
+        // the sim rows into registers; the LDS rows have landed once at most
+        // the 4 CH register-row loads issued after them are outstanding
         const v4u rgw = element_words(a.grad_out, elem, g);
 #pragma unroll
-        for (int j = 1; j < kRowsPerWave; ++j)
+        for (int j = 0; j < kRowsPerWave; ++j)
             load_row_lds<CH>(rgw, min(row0 + j, a.L1 - 1), L2, lane,
-                             pre0 + unsigned(wave * kPreRows + j - 1) * kMaxCols * 4u);
+                             pre0 + unsigned(wave * kPreRows + j) * kMaxCols * 4u);
         const auto ry = element_rsrc(a.sim, elem, g);
-        const auto rg = element_rsrc(a.grad_out, elem, g);
 #pragma unroll
         for (int j = 0; j < kRowsPerWave; ++j) load_row<CH>(ry, min(row0 + j, a.L1 - 1), L2, lane, Yv[j]);
-        load_row<CH>(rg, min(row0, a.L1 - 1), L2, lane, Gv[0]);
         asm volatile("" ::: "memory");  // every load above is issued before the wait
-        constexpr unsigned vm = 5 * CH;
+        constexpr unsigned vm = 4 * CH;
         static_assert(vm < 64, "vmcnt field");
         __builtin_amdgcn_s_waitcnt((vm & 15u) | ((vm >> 4) << 14) | 0x0f70u);
     }
+    // The next element's grad_out rows of every wave into LDS, by the
+    // non-polling waves (each loads two waves' rows)
+    auto prefetch = [&](int kn) {
+        if (wave >= kPollWaves) {
+            const v4u rg = element_words(a.grad_out, elem, g + G * kn);
+            const int ln = lane_now();
+            constexpr int per = kWaves / (kWaves - kPollWaves);
+#pragma unroll
+            for (int q = 0; q < per; ++q) {
+                const int tw = (wave - kPollWaves) * per + q;
+#pragma unroll
+                for (int j = 0; j < kRowsPerWave; ++j) {
+                    const int i = m * kRowsPerMember + tw * kRowsPerWave + j;
+                    load_row_lds<CH>(rg, min(i, a.L1 - 1), L2, ln, pre0 + unsigned(tw * kPreRows + j) * kMaxCols * 4u);
+                }
+            }
+        }
+    };
     // column log-normalisers of an element, two columns per thread
     auto col_norm_of = [&](int e, int t) {
         float2 v = make_float2(INFINITY, INFINITY);
@@ -917,16 +947,18 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_kernel(BwdArgs1 a) {
         scalar_extent(a.lengths, e, a.L1, L2, l1, l2);
         reinterpret_cast<float2*>(lcl)[t] = ncl;
         __syncthreads();
-        // ---- phase A: (y, g) -> (c, t) and the column-dot partials
+        // ---- phase A: (y, g) -> (c, t) and the column-dot partials (in
+        // registers: 0 + q of row 0 + ... + q of row 3, acc_row's order)
         const float* rst = a.row_stats + size_t(e) * 2 * a.L1;
+        float part[PL];
 #pragma unroll
         for (int j = 0; j < kRowsPerWave; ++j) {
             const int i = row0 + j;
             const bool row_ok = i < l1;
             const float rl = row_ok ? log_norm(scalar_load(rst + i), scalar_load(rst + a.L1 + i)) : INFINITY;
             __builtin_amdgcn_sched_barrier(0);  // one row at a time: bounded live ranges
-            if (j > 0) {  // in LDS (prefetched during the previous element's exchange)
-                const float* src = pre + (wave * kPreRows + j - 1) * kMaxCols + 4 * lane;
+            {  // grad_out from LDS (loaded during the previous element's exchange)
+                const float* src = pre + (wave * kPreRows + j) * kMaxCols + 4 * lane;
 #pragma unroll
                 for (int kk = 0; kk < CH; ++kk) {
                     const float4 v = *reinterpret_cast<const float4*>(src + kk * 256);
@@ -938,7 +970,8 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_kernel(BwdArgs1 a) {
             }
             float r[PL];
             row_q<CH>(Yv[j], Gv[j], r, rl, row_ok, lane, l2, L2, a.sc, lcl, row_ok && l2 == 4 * kWave * CH);
-            acc_row<CH>(lacc + wave * kMaxCols, lane, L2, Gv[j], j == 0);
+#pragma unroll
+            for (int qq = 0; qq < PL; ++qq) part[qq] = (j == 0 ? 0.0f : part[qq]) + Gv[j][qq];
             float dl = 0.0f;
 #pragma unroll
             for (int qq = 0; qq < PL; ++qq) dl += Gv[j][qq];
@@ -952,7 +985,10 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_kernel(BwdArgs1 a) {
                 asm volatile("" : "+v"(Gv[j][qq]));
             }
         }
-        // ---- fold the waves, publish this member's column partials
+        // ---- fold the waves, publish this member's column partials (the
+        // partials go where the rows were, once every wave has read its rows)
+        lds_barrier();
+        R::store(lacc + wave * kMaxCols, lane, L2, part);
         __syncthreads();
         if (k == 0) local = flag != 0 && a.x.local_ok;
         {
@@ -973,25 +1009,16 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_kernel(BwdArgs1 a) {
         }
         const long long deadline = now_ticks() + a.x.wait_ticks;
         const bool real = k + 1 < n;
-        // ---- the prefetching waves: the next element's grad_out rows 1..3 of
-        // every wave into LDS (phase A above has read this element's)
-        if (wave >= kPollWaves && real) {
-            const v4u rg = element_words(a.grad_out, elem, g + G * (k + 1));
-            constexpr int per = kWaves / (kWaves - kPollWaves);
-#pragma unroll
-            for (int q = 0; q < per; ++q) {
-                const int tw = (wave - kPollWaves) * per + q;
-#pragma unroll
-                for (int j = 1; j < kRowsPerWave; ++j) {
-                    const int i = m * kRowsPerMember + tw * kRowsPerWave + j;
-                    load_row_lds<CH>(rg, min(i, a.L1 - 1), L2, lane,
-                                     pre0 + unsigned(tw * kPreRows + j - 1) * kMaxCols * 4u);
-                }
-            }
-        }
+        // ---- the non-polling waves: the next element's grad_out rows into
+        // LDS, once every wave has read the partials there
+        lds_barrier();
+        if (real) prefetch(k + 1);
         // ---- the polling waves: reduce-scatter, thread t < 256 reads members
-        // 4h .. 4h + 3 (h = t / 32) of column 32m + t % 32
-        bool ok = true;
+        // 4h .. 4h + 3 (h = t / 32) of column 32m + t % 32; then the owner's
+        // sums and the all-gather.  The polling waves meet through LDS flags,
+        // not a workgroup barrier: the other waves are still issuing their
+        // loads, which takes microseconds while HBM is busy.
+        int fails = 0;  // bit 1: a reduce-scatter wait expired; bit 0: an all-gather wait
         if (wave < kPollWaves) {
             const int c = t & (kOwn - 1);
             const int h = t >> 5;
@@ -999,37 +1026,52 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_kernel(BwdArgs1 a) {
                 part_row(a.x, g, p, 4 * h) + kOwn * m + c, part_row(a.x, g, p, 4 * h + 1) + kOwn * m + c,
                 part_row(a.x, g, p, 4 * h + 2) + kOwn * m + c, part_row(a.x, g, p, 4 * h + 3) + kOwn * m + c};
             float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-            ok = poll4(w, tag, deadline, never, v);
+            const bool ok = poll4(w, tag, deadline, never, v);
 #pragma unroll
             for (int i = 0; i < 4; ++i) rsv[4 * h + i][c] = v[i];
-        }
-        const bool rs_ok = !block_any(!ok, votes[0], wave);
-        if (rs_ok) {
-            if (t < kOwn) {
-                float s = 0.0f;
+            const int mine = ((k + 1) << 1) | (__ballot(!ok) != 0 ? 1 : 0);
+            __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's rsv values are written
+            __hip_atomic_store(&rsflag[wave], mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+#pragma unroll 1
+            for (int q = 0; q < kPollWaves; ++q) {
+                int f;
+                do {
+                    f = __hip_atomic_load(&rsflag[q], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                } while ((f >> 1) != k + 1);
+                fails |= (f & 1) << 1;
+            }
+            asm volatile("" ::: "memory");  // rsv is read after the flags
+            if (!fails) {
+                if (t < kOwn) {
+                    float s = 0.0f;
 #pragma unroll 8
-                for (int w = 0; w < kMembers; ++w) s += rsv[w][t];
-                res::publish(res_row(a.x, g, p) + kOwn * m + t, s, tag, local);
-            }
-            // all-gather: thread t < 256 reads columns 4t .. 4t + 3
-            if (wave < kPollWaves) {
+                    for (int q = 0; q < kMembers; ++q) s += rsv[q][t];
+                    res::publish(res_row(a.x, g, p) + kOwn * m + t, s, tag, local);
+                }
+                // all-gather: thread t < 256 reads columns 4t .. 4t + 3
                 unsigned long long* r = res_row(a.x, g, p) + 4 * t;
-                unsigned long long* const w[4] = {r, r + 1, r + 2, r + 3};
-                float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-                ok = poll4(w, tag, deadline, never, v);
-                *reinterpret_cast<float4*>(ldc + 4 * t) = make_float4(v[0], v[1], v[2], v[3]);
+                unsigned long long* const wr[4] = {r, r + 1, r + 2, r + 3};
+                float u[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+                const bool ok2 = poll4(wr, tag, deadline, never, u);
+                *reinterpret_cast<float4*>(ldc + 4 * t) = make_float4(u[0], u[1], u[2], u[3]);
+                fails |= __ballot(!ok2) != 0 ? 1 : 0;
             }
         }
-        if (!rs_ok || block_any(!ok, votes[1], wave))
-            bwd_fallback<CH, FW>(a, e, l1, l2, g, m, p, tag, local, !rs_ok, lacc, lcl, ldc, wave);
-        // ---- phase B; each row is refilled with the next element's (grad_out
-        // rows 1..3: already on their way to LDS)
+        fails = block_or(fails, votes[1], wave);
+        if (fails) {
+            // the fallback folds through the rows' LDS: the loads into it
+            // land first, and are issued again after it
+            if (wave >= kPollWaves) __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+            bwd_fallback<CH, FW>(a, e, l1, l2, g, m, p, tag, local, (fails & 2) != 0, lacc, lcl, ldc, wave);
+            if (real) prefetch(k + 1);
+        }
+        // ---- phase B; each row's sim is refilled with the next element's
+        // (its grad_out rows are already on their way to LDS)
         if (wave >= kPollWaves) __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): the prefetch has landed
         const int en = g + G * (real ? k + 1 : k);
         ncl = col_norm_of(en, t);
         const auto ro = element_rsrc(a.grad_sim, elem, e);
         const auto ry = element_rsrc(a.sim, elem, en);
-        const auto rg = element_rsrc(a.grad_out, elem, en);
         // One row at a time, its loads after its stores (scheduling barriers):
         // loads hoisted ahead into fresh registers would raise the register
         // count past the file and spill, and a spill reload waits for every
@@ -1054,7 +1096,6 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_kernel(BwdArgs1 a) {
             __builtin_amdgcn_sched_barrier(0);
             const int ir = real ? min(i, a.L1 - 1) : 0;
             load_row<CH>(ry, ir, L2, lane, Yv[j]);
-            if (j == 0) load_row<CH>(rg, ir, L2, lane, Gv[j]);
         }
         __builtin_amdgcn_sched_barrier(0);
     }
