@@ -158,20 +158,6 @@ __device__ __forceinline__ void lds_barrier() {
     asm volatile("" ::: "memory");
 }
 
-// True in every thread when `pred` holds in any thread of the workgroup: a
-// wave ballot per wave into `votes` (kWaves ints), one barrier, every thread
-// reads all.  Two calls with no barrier between them need separate `votes`.
-// Every lane of wave `wave` (wave-uniform) writes the same vote: no lane test,
-// so no per-lane value is held (or spilled) for it.
-__device__ __forceinline__ bool block_any(bool pred, int* votes, int wave) {
-    const bool any = __ballot(pred) != 0;
-    votes[wave] = any;
-    lds_barrier();
-    const int4 v0 = reinterpret_cast<const int4*>(votes)[0];
-    const int4 v1 = reinterpret_cast<const int4*>(votes)[1];
-    return (v0.x | v0.y | v0.z | v0.w | v1.x | v1.y | v1.z | v1.w) != 0;
-}
-
 // The OR over the workgroup's waves of a wave-uniform `bits` (every lane of
 // wave `wave` writes the same vote), in every thread; one barrier.
 __device__ __forceinline__ int block_or(int bits, int* votes, int wave) {
@@ -513,7 +499,8 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(FwdArgs1 a) {
     __shared__ float rsv[kMembers][kOwn + 1];
     __shared__ __align__(16) float clse[kMaxCols];
     __shared__ int flag;
-    __shared__ __align__(16) int votes[2][kWaves];
+    __shared__ __align__(16) int votes[kWaves];
+    __shared__ int rsflag[kPollWaves];  // (element + 1) << 1 | failed, per polling wave
     const int lane = threadIdx.x % kWave;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const int t = threadIdx.x;
@@ -538,6 +525,7 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(FwdArgs1 a) {
         for (int j = 0; j < kRowsPerWave; ++j) load_row<CH>(rs, real ? min(row0 + j, L1 - 1) : 0, L2, lane, buf[j]);
     };
     if (wave == kWaves - 1) check_group_xcd(a.x, g, tag0, never, &flag);
+    if (t < kPollWaves) rsflag[t] = 0;  // read after the first element's barriers
     load(0, 0, X);
     load(1, 0, Y);
     bool local = false;  // set at element 0's first barrier from the check's flag
@@ -618,8 +606,11 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(FwdArgs1 a) {
             }
         }
         // ---- reduce-scatter (waves < kPollWaves): member m owns columns
-        // [32m, 32m + 32); thread t < 256 reads members 4h .. 4h + 3 (h = t / 32)
-        bool ok = true;
+        // [32m, 32m + 32); thread t < 256 reads members 4h .. 4h + 3 (h = t / 32);
+        // then the owner's merge and the all-gather.  The polling waves meet
+        // through LDS flags, not a workgroup barrier: the other waves are
+        // still issuing their loads.
+        int fails = 0;  // bit 1: a reduce-scatter wait expired; bit 0: an all-gather wait
         if (wave < kPollWaves) {
             const int c = t & (kOwn - 1);
             const int h = t >> 5;
@@ -627,35 +618,45 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(FwdArgs1 a) {
                 part_row(a.x, g, p, 4 * h) + kOwn * m + c, part_row(a.x, g, p, 4 * h + 1) + kOwn * m + c,
                 part_row(a.x, g, p, 4 * h + 2) + kOwn * m + c, part_row(a.x, g, p, 4 * h + 3) + kOwn * m + c};
             float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-            ok = poll4(w, tag, deadline, never, v);
+            const bool ok = poll4(w, tag, deadline, never, v);
 #pragma unroll
             for (int i = 0; i < 4; ++i) rsv[4 * h + i][c] = v[i];
-        }
-        const bool rs_ok = !block_any(!ok, votes[0], wave);
-        if (rs_ok) {
-            if (t < kOwn) {
-                float M = -FLT_MAX, S = 0.0f;
+            const int mine = ((k + 1) << 1) | (__ballot(!ok) != 0 ? 1 : 0);
+            __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's rsv values are written
+            __hip_atomic_store(&rsflag[wave], mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+#pragma unroll 1
+            for (int q = 0; q < kPollWaves; ++q) {
+                int f;
+                do {
+                    f = __hip_atomic_load(&rsflag[q], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                } while ((f >> 1) != k + 1);
+                fails |= (f & 1) << 1;
+            }
+            asm volatile("" ::: "memory");  // rsv is read after the flags
+            if (!fails) {
+                if (t < kOwn) {
+                    float M = -FLT_MAX, S = 0.0f;
 #pragma unroll 8
-                for (int w = 0; w < kMembers; ++w) online_add(M, S, rsv[w][t]);
-                const int col = kOwn * m + t;
-                res::publish(res_row(a.x, g, p) + col, state_lse(M, S), tag, local);
-                if (col < L2) {
-                    float* cst = a.col_stats + size_t(e) * 2 * L2;
-                    cst[col] = M;
-                    cst[L2 + col] = S;
+                    for (int q = 0; q < kMembers; ++q) online_add(M, S, rsv[q][t]);
+                    const int col = kOwn * m + t;
+                    res::publish(res_row(a.x, g, p) + col, state_lse(M, S), tag, local);
+                    if (col < L2) {
+                        float* cst = a.col_stats + size_t(e) * 2 * L2;
+                        cst[col] = M;
+                        cst[L2 + col] = S;
+                    }
                 }
-            }
-            // ---- all-gather (waves < kPollWaves): thread t < 256 reads columns 4t .. 4t + 3
-            if (wave < kPollWaves) {
+                // ---- all-gather: thread t < 256 reads columns 4t .. 4t + 3
                 unsigned long long* r = res_row(a.x, g, p) + 4 * t;
-                unsigned long long* const w[4] = {r, r + 1, r + 2, r + 3};
-                float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-                ok = poll4(w, tag, deadline, never, v);
-                *reinterpret_cast<float4*>(clse + 4 * t) = make_float4(v[0], v[1], v[2], v[3]);
+                unsigned long long* const wr[4] = {r, r + 1, r + 2, r + 3};
+                float u[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+                const bool ok2 = poll4(wr, tag, deadline, never, u);
+                *reinterpret_cast<float4*>(clse + 4 * t) = make_float4(u[0], u[1], u[2], u[3]);
+                fails |= __ballot(!ok2) != 0 ? 1 : 0;
             }
         }
-        if (!rs_ok || block_any(!ok, votes[1], wave))
-            fwd_fallback<CH, FW>(a, e, l1, l2, g, m, p, tag, local, !rs_ok, lm, ls, clse, wave);
+        fails = block_or(fails, votes, wave);
+        if (fails) fwd_fallback<CH, FW>(a, e, l1, l2, g, m, p, tag, local, (fails & 2) != 0, lm, ls, clse, wave);
         // ---- write; each row is refilled with the element after next (its
         // first rows from LDS, once the loading waves have waited for them and
         // passed a barrier)
@@ -871,7 +872,7 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_kernel(BwdArgs1 a) {
     __shared__ __align__(16) float pre[kWaves * kPreRows * kMaxCols];
     float* const lacc = pre;
     __shared__ int flag;
-    __shared__ __align__(16) int votes[2][kWaves];
+    __shared__ __align__(16) int votes[kWaves];
     __shared__ int rsflag[kPollWaves];  // (element + 1) << 1 | failed, per polling wave
     const int lane = threadIdx.x % kWave;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -1057,7 +1058,7 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_kernel(BwdArgs1 a) {
                 fails |= __ballot(!ok2) != 0 ? 1 : 0;
             }
         }
-        fails = block_or(fails, votes[1], wave);
+        fails = block_or(fails, votes, wave);
         if (fails) {
             // the fallback folds through the rows' LDS: the loads into it
             // land first, and are issued again after it
