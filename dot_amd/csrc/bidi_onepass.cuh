@@ -1093,10 +1093,12 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_kernel(BwdArgs1 a) {
                     o[ee] = fmaf(-dc[q], Yv[j][ee], Gv[j][ee]) * a.inv_T;
                 }
             }
-            if (i < a.L1) store_row<CH>(ro, i, L2, lane, o);
-            __builtin_amdgcn_sched_barrier(0);
+            // the next element's row first: its load waits on HBM, the store
+            // can drain behind it
             const int ir = real ? min(i, a.L1 - 1) : 0;
             load_row<CH>(ry, ir, L2, lane, Yv[j]);
+            if (i < a.L1) store_row<CH>(ro, i, L2, lane, o);
+            __builtin_amdgcn_sched_barrier(0);
         }
         __builtin_amdgcn_sched_barrier(0);
     }
