@@ -37,8 +37,10 @@ The same line carries
   pinned to one host core with one torch thread, or the numpy oracle when
   oracle/_ref is absent;
 * ``bidirectional_softmax`` — config C2 (B=32, 1024x1024, fwd+bwd) in GB/s of
-  algorithmic traffic (20 bytes per element over the whole step), with the four
-  sweeps' own traffic beside it;
+  algorithmic traffic (20 bytes per element over the whole step), with the
+  one-pass kernels' own traffic beside it, and ``two_sweep_shape``: the same
+  element count at 128 x 512 x 512 (not a BASELINE configuration), where rows
+  of at most 512 take the two-sweep kernels;
 * ``other_configs`` — C1, C4 and C5 measured the same way (``--headline-only``
   skips them).
 
@@ -484,8 +486,43 @@ def bench_bidi(args, torch, dot_amd, profiler):
         "kernels": stats,
         "kernels_own_traffic": own,
         "roofline": roofline,
+        "two_sweep_shape": bench_bidi_two_sweep(args, torch, dot_amd, profiler),
         "_cpu": (sim, G, lengths.cpu().numpy()),
     }
+
+
+def bench_bidi_two_sweep(args, torch, dot_amd, profiler):
+    """C2's element count at 128 x 512 x 512 (not a BASELINE configuration):
+    rows of at most 512 take the two-sweep kernels, which read sim twice in
+    the forward and sim and grad_out twice in the backward (32 B/elem against
+    the 20 of one pass; the metric counts 20)."""
+    dev = torch.device("cuda", 0)
+    B, L1, L2 = 128, 512, 512
+    gen = torch.Generator(device=dev).manual_seed(7)
+    sim = torch.randn(B, L1, L2, generator=gen, device=dev)
+    G = torch.randn(B, L1, L2, generator=gen, device=dev)
+
+    def step():
+        leaf = sim.detach().requires_grad_(True)
+        P = dot_amd.bidirectional_softmax(leaf, 1.0)
+        P.backward(G)
+
+    for _ in range(max(args.warmup, 2)):
+        step()
+    torch.cuda.synchronize()
+    steps = max(args.steps, 10)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    sec = (time.perf_counter() - t0) / steps
+    stats = profiled_pass(profiler, sorted(BIDI_KERNEL_BYTES), step, steps, torch)
+    E = B * L1 * L2
+    own = {k: round(BIDI_KERNEL_BYTES[k] * E / (st["avg_us"] * 1e-6) / 1e9, 1) for k, st in stats.items()}
+    return {"config": {"workload": f"bidirectional_softmax fwd+bwd B={B} L1=L2={L2} tau=1.0 (not a BASELINE config)"},
+            "ms_per_step": 1000.0 * sec, "algorithmic_GBps": 20.0 * E / sec / 1e9,
+            "frac_of_hbm_peak": 20.0 * E / sec / 1e9 / HBM_PEAK_GBPS,
+            "kernels": stats, "kernels_own_GBps": own}
 
 
 TRAFFIC_SOURCE = ("profiles/pmc_traffic.json: HBM bytes per dispatch from committed rocprofv3 --pmc "
