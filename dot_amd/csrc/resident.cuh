@@ -112,6 +112,42 @@ __device__ __forceinline__ float collect(unsigned long long* p, unsigned t, int 
 // the XCD ids (callers pass `tag`).
 constexpr unsigned kXccTag = 0xfffffffeu;
 
+// Tag of the per-workgroup result words (partial sums and failure flags
+// published once, at the end of a launch) in slots cleared for the call; an
+// iteration tag reaches it only past 2^32 - 4 iterations.  Slots that persist
+// across calls use (epoch << 16) | 0xfffe, above every tagged iteration.
+constexpr unsigned kResultTag = 0xfffffffdu;
+
+// The sum over batch element b's W workgroups of one value each, added in the
+// order w = 0, 1, ... by workgroup 0 of the element, which waits for the
+// other W - 1 in `words` (one per logical workgroup gid = b * W + w) and
+// returns the sum; the others publish theirs and return 0.  Thread 0 only.
+__device__ __forceinline__ float element_sum(unsigned long long* words, int gid, int w, int W, float mine,
+                                             unsigned tag, int spin_limit, int* status, bool& dead, int mark) {
+    if (w != 0) {
+        publish(words + gid, mine, tag);
+        return 0.0f;
+    }
+    float s = mine;
+    for (int q = 1; q < W; ++q) s += collect(words + gid + q, tag, spin_limit, status, dead, mark);
+    return s;
+}
+
+// Whether any workgroup of the grid failed (a wait that gave up, or the
+// status word at the call's failure mark): every workgroup publishes its
+// flag `bad` to words[gid] and logical workgroup 0 waits for all G flags (a
+// wait for one that gives up counts as a failure).  Returns the verdict in
+// every thread of workgroup 0, and false elsewhere.  Every thread must call it.
+__device__ __forceinline__ bool grid_failed(unsigned long long* words, int gid, int G, bool bad, unsigned tag,
+                                            int spin_limit, int* status, bool& dead, int mark) {
+    if (threadIdx.x == 0) publish(words + gid, bad ? 1.0f : 0.0f, tag);
+    if (gid != 0) return false;
+    int any = 0;
+    for (int g = threadIdx.x; g < G; g += blockDim.x)
+        any |= collect(words + g, tag, spin_limit, status, dead, mark) != 0.0f;  // NaN: gave up
+    return __syncthreads_or(any) != 0;
+}
+
 // XCD check of a batch element, in two steps so that the round trip hides
 // under other work.  announce_xcc: each workgroup publishes its XCC id (agent
 // scope) into word 0 of its row `rows + (b * W + w) * stride`.  The row must
@@ -416,7 +452,12 @@ struct ImpResArgs {
     unsigned long long* xchg;  // [2, G, N] tagged sweep column sums
     unsigned long long* pro;   // [2, G, N] tagged prologue column sums (P G, then P)
     float* grad;               // [B,M,N]
-    float* tau_partial;        // [G] by logical workgroup b * W + w
+    float* grad_tau;           // [B] out: tau_scale * sum(grad * log_alpha)
+    float tau_scale;
+    unsigned long long* rwords;  // [2, G] tagged result words: grad_tau partials, failure flags
+    unsigned result_tag;
+    int32_t* status_out;       // the caller's status word (1: a wait gave up), or null
+    int keep_status;           // nonzero: raise status_out only (a later slab of one call)
     int* status;
     float inv_tau;
     int M, N, W, R, iters, spin_limit;
@@ -454,8 +495,11 @@ __device__ __forceinline__ void upstream_row(const ImpResArgs& a, size_t off, in
 //   mu_k = (c_k - sum_i P lambda_i) / max(cs_k, 1e-12)   (one exchange)
 // Final phase: grad = P (G - lambda - mu) / tau (cost kind: grad_cost P - that;
 // log-alpha kind: that - grad_cost P) and this workgroup's share of
-// sum(grad * log_alpha) for grad_tau.  MG >= W (exchange_columns).  With
-// `early`, an element's sweeps end once sk::AdjointStop finds them converged.
+// sum(grad * log_alpha), which workgroup 0 of the element adds up into
+// grad_tau; with status_out, logical workgroup 0 also writes the call's
+// status word once every workgroup has reported.  MG >= W (exchange_columns).
+// With `early`, an element's sweeps end once sk::AdjointStop finds them
+// converged.
 template <int VEC, int CH, int RPW, int MG = kMaxGroup>
 __global__ __launch_bounds__(kThreads) void implicit_adjoint(ImpResArgs a) {
     using R = Row<VEC, CH>;
@@ -627,7 +671,20 @@ __global__ __launch_bounds__(kThreads) void implicit_adjoint(ImpResArgs a) {
         R::store_stream(a.grad + off, lane, a.N, o);
     }
     const float tsum = block_reduce<kWaves>(wave_sum(tacc), scratch, OpSum{});
-    if (threadIdx.x == 0) a.tau_partial[gid] = failed ? __builtin_nanf("") : tsum;
+    if (threadIdx.x == 0) {
+        const float s = element_sum(a.rwords, gid, w, a.W, failed ? __builtin_nanf("") : tsum, a.result_tag,
+                                    a.spin_limit, a.status, dead, a.mark);
+        if (w == 0) a.grad_tau[b] = s * a.tau_scale;
+    }
+    if (a.status_out) {
+        const bool bad = __syncthreads_or(dead) != 0 || failed;
+        const bool any = grid_failed(a.rwords + G, gid, G, bad, a.result_tag, a.spin_limit, a.status, dead,
+                                     a.mark);
+        if (gid == 0 && threadIdx.x == 0) {
+            if (any) *a.status_out = 1;
+            else if (!a.keep_status) *a.status_out = 0;
+        }
+    }
 }
 
 }  // namespace res
@@ -657,7 +714,9 @@ struct FwdResArgs {
     int max_iter;
     int return_log;
     float* plan;          // [B,M,N] or null
-    float* cost_partial;  // [B*W] by logical workgroup, or null
+    float* cost;          // [B] out: sum(P C), or null
+    unsigned long long* cwords;  // [G] tagged cost partials of the workgroups
+    unsigned result_tag;
     float* u_out;         // [B,M] or null
     float* v_out;         // [B,N] or null
     float* u_hist;        // [T,B,M] or null
@@ -1010,7 +1069,8 @@ __global__ __launch_bounds__(kThreads) void forward(FwdResArgs a) {
         if (global_delta(a, a.max_iter, scratch, dead) < a.tol) conv = 1;  // the last iteration
     }
 
-    // P = safe_exp(K + u + v) (kernels.cu:755-775) and this workgroup's share of sum(P C).
+    // P = safe_exp(K + u + v) (kernels.cu:755-775) and this workgroup's share of
+    // sum(P C), which workgroup 0 of the element adds up into the cost.
     const int par = used & 1;
     __syncthreads();
     const bool failed = __hip_atomic_load(a.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= a.mark;
@@ -1031,14 +1091,18 @@ __global__ __launch_bounds__(kThreads) void forward(FwdResArgs a) {
         for (int e = 0; e < PL; ++e) {
             const float lp = (x[k][e] * a.kscale + ui) + vf[e];
             pv[e] = a.return_log ? lp : safe_exp(lp);
-            if (a.cost_partial && R::valid(lane, e, a.N)) cacc = fmaf(pv[e], csign * x[k][e], cacc);
+            if (a.cost && R::valid(lane, e, a.N)) cacc = fmaf(pv[e], csign * x[k][e], cacc);
             if (failed) pv[e] = __builtin_nanf("");
         }
         if (a.plan) R::store(a.plan + (bM + i) * a.N, lane, a.N, pv);
     }
-    if (a.cost_partial) {
+    if (a.cost) {
         const float cs = block_reduce<kWaves>(wave_sum(cacc), scratch + 16, OpSum{});
-        if (threadIdx.x == 0) a.cost_partial[gid] = failed ? __builtin_nanf("") : cs;
+        if (threadIdx.x == 0) {
+            const float s = element_sum(a.cwords, gid, w, a.W, failed ? __builtin_nanf("") : cs, a.result_tag,
+                                        a.spin_limit, a.status, dead, a.mark);
+            if (w == 0) a.cost[b] = s;
+        }
     }
     if (blockIdx.x == 0 && threadIdx.x == 0) {
         *a.iters_used = failed ? -1 : used;  // -1: an exchange timed out, the outputs are NaN

@@ -51,7 +51,7 @@ struct FwdLayout {
     // resident path: tagged exchange slots, cleared before each resident launch
     unsigned long long* xchg;   // [2, G, N]
     unsigned long long* fxchg;  // [2, 2, G, N]
-    unsigned long long* dxchg;  // [kDeltaSlots, G]
+    unsigned long long* dxchg;  // [kDeltaSlots, G], then [G] cost partials
     int* status;
     size_t groups;
     size_t res_words;           // 32-bit words from xchg through status
@@ -86,12 +86,12 @@ FwdLayout fwd_layout(void* ws, int B, int M, int N, int max_iter) {
         std::max(size_t(B) * std::max(size_t(L.nstrips) * L.nchunks, size_t(res::kMaxGroup)), L.pst_groups));
     L.groups = resident_groups_max(B, M, N);
     const size_t gn = L.groups * size_t(N);
-    const size_t words = 6 * gn + res::kDeltaSlots * L.groups + 1;
+    const size_t words = 6 * gn + (res::kDeltaSlots + 1) * L.groups + 1;
     L.xchg = c.take<unsigned long long>(words);
     if (L.xchg) {
         L.fxchg = L.xchg + 2 * gn;
         L.dxchg = L.fxchg + 4 * gn;
-        L.status = reinterpret_cast<int*>(L.dxchg + res::kDeltaSlots * L.groups);
+        L.status = reinterpret_cast<int*>(L.dxchg + (res::kDeltaSlots + 1) * L.groups);
     }
     L.res_words = 2 * words;
     // [2, G, N] partial rows | [2, B, N] v | [2, B, M] u | deltas [kDeltaSlots, G] | status
@@ -135,11 +135,12 @@ ImpLayout imp_layout(void* ws, int B, int M, int N) {
     L.dpart = c.take<float>(L.nchunks > 1 ? size_t(B) * L.nchunks * M : 0);
     // The resident path runs at most one workgroup per CU and only for N <= 1024.
     const size_t groups = resident_groups_max(B, M, N);
-    // [2, G, N] sweep slots, [2, G, N] prologue slots, then the status word
+    // [2, G, N] sweep slots, [2, G, N] prologue slots, [2, G] result words, then the status word
     L.groups = groups;
-    L.xchg = c.take<unsigned long long>(4 * groups * size_t(N) + 1);
-    L.status = reinterpret_cast<int*>(L.xchg ? L.xchg + 4 * groups * size_t(N) : nullptr);
-    L.xchg_words = (4 * groups * size_t(N) + 1) * 2;
+    const size_t words = 4 * groups * size_t(N) + 2 * groups + 1;
+    L.xchg = c.take<unsigned long long>(words);
+    L.status = reinterpret_cast<int*>(L.xchg ? L.xchg + words - 1 : nullptr);
+    L.xchg_words = words * 2;
     // [2, G, N] sweep rows | [2, B, N + kMaxGroups] mu and stop-test scales | [2, G, N] prologue rows | status
     L.pst_groups = pst_groups_max(B, M, N);
     L.pst = c.take<unsigned long long>(
@@ -209,8 +210,10 @@ void launch_fill_zero(void* p, size_t words, hipStream_t stream) {
 // `exchange` fields): word 0 is the status, whose failure mark is the call's
 // epoch; the tagged slots follow at kExchangeHead, tagged (epoch << 16) | t.
 // The slots of the forward ([2, G, N] column sums, [2, 2, G, N] exact-LSE
-// rows, [kDeltaSlots, G] deltas) are the larger set; the adjoint's ([2, G, N]
-// sweep sums, [2, G, N] prologue sums) fit in them.
+// rows, [kDeltaSlots, G] deltas, [G] cost partials) are the larger set; the
+// adjoint's ([2, G, N] sweep sums, [2, G, N] prologue sums, [2, G] result
+// words) fit in them.  The result words of either launch are tagged
+// (epoch << 16) | 0xfffe.
 constexpr size_t kExchangeHead = 32;  // 256 bytes
 
 size_t exchange_groups_max() { return size_t(std::max(0, std::min(device_cus(), 1024))); }
@@ -218,7 +221,7 @@ size_t exchange_groups_max() { return size_t(std::max(0, std::min(device_cus(), 
 struct Tagging {
     unsigned long long* slots;
     int* status;
-    unsigned tag_base, xcc_tag;
+    unsigned tag_base, xcc_tag, result_tag;
     int mark;
     bool cleared_per_call;  // slots from the workspace: clear them before the launch
 };
@@ -227,9 +230,9 @@ Tagging tagging(void* exchange, uint32_t epoch, int iters, unsigned long long* w
     if (exchange && iters <= DOT_SINKHORN_MAX_TAGGED_ITERS) {
         const unsigned base = epoch << 16;
         return {static_cast<unsigned long long*>(exchange) + kExchangeHead, static_cast<int*>(exchange), base,
-                base | 0xffffu, int(epoch), false};
+                base | 0xffffu, base | 0xfffeu, int(epoch), false};
     }
-    return {ws_slots, ws_status, 0u, res::kXccTag, 1, true};
+    return {ws_slots, ws_status, 0u, res::kXccTag, res::kResultTag, 1, true};
 }
 
 int check_exchange(const void* exchange, uint32_t epoch) {
@@ -441,7 +444,7 @@ bool launch_resident_forward(const dot_sinkhorn_fwd_args* a, const FwdLayout& L,
     r.max_iter = a->max_iter;
     r.return_log = ret_log ? 1 : 0;
     r.plan = a->plan;
-    r.cost_partial = a->cost ? L.cost_partial : nullptr;
+    r.cost = a->cost;
     r.u_out = a->u_out;
     r.v_out = a->v_out;
     r.u_hist = keep ? a->u_hist : nullptr;
@@ -453,6 +456,8 @@ bool launch_resident_forward(const dot_sinkhorn_fwd_args* a, const FwdLayout& L,
     r.xchg = tg.slots;
     r.fxchg = tg.slots + 2 * size_t(groups) * a->N;
     r.dxchg = r.fxchg + 4 * size_t(groups) * a->N;
+    r.cwords = r.dxchg + res::kDeltaSlots * size_t(groups);
+    r.result_tag = tg.result_tag;
     r.status = tg.status;
     r.tag_base = tg.tag_base;
     r.xcc_tag = tg.xcc_tag;
@@ -485,13 +490,7 @@ bool launch_resident_forward(const dot_sinkhorn_fwd_args* a, const FwdLayout& L,
         ok = launch_grid(reinterpret_cast<const void*>(kernel), groups, res::kThreads, params, lds, stream,
                          independent) == hipSuccess;
     });
-    if (!ok) return false;
-    if (a->cost) {
-        ProfScope prof("sk_batch_sum", stream);
-        hipLaunchKernelGGL(sk::batch_sum, dim3(a->B), dim3(kWave), 0, stream, L.cost_partial, rc.W,
-                           1.0f, a->cost);
-    }
-    return true;
+    return ok;
 }
 
 // The per-iteration forward sweeps with tol > 0 read the device's stop test
@@ -644,7 +643,7 @@ extern "C" size_t dot_sinkhorn_forward_workspace_bytes(int B, int M, int N, int 
 
 extern "C" size_t dot_sinkhorn_exchange_bytes(void) {
     const size_t G = exchange_groups_max();
-    return (kExchangeHead + 6 * G * 1024 + res::kDeltaSlots * G) * sizeof(unsigned long long);
+    return (kExchangeHead + 6 * G * 1024 + (res::kDeltaSlots + 1) * G) * sizeof(unsigned long long);
 }
 
 extern "C" int dot_sinkhorn_forward(const dot_sinkhorn_fwd_args* a, dot_stream_t stream_) {
@@ -886,7 +885,12 @@ bool launch_resident_adjoint(const dot_sinkhorn_bwd_args* a, const ImpLayout& L,
     r.xchg = tg.slots;
     r.pro = tg.slots + 2 * size_t(groups) * a->N;
     r.grad = a->grad_scores;
-    r.tau_partial = L.tau_partial;
+    r.grad_tau = a->grad_tau;
+    r.tau_scale = -inv_tau;
+    r.rwords = r.pro + 2 * size_t(groups) * a->N;
+    r.result_tag = tg.result_tag;
+    r.status_out = a->status;
+    r.keep_status = keep_status ? 1 : 0;
     r.status = tg.status;
     r.tag_base = tg.tag_base;
     r.xcc_tag = tg.xcc_tag;
@@ -917,15 +921,12 @@ bool launch_resident_adjoint(const dot_sinkhorn_bwd_args* a, const ImpLayout& L,
         if (tg.cleared_per_call) launch_fill_zero(L.xchg, L.xchg_words, stream);
         void* params[] = {&r};
         ProfScope prof("sk_imp_resident", stream);
-        // the adjoint's exchanges stay within a batch element's W workgroups
+        // the adjoint's exchanges stay within a batch element's W workgroups,
+        // but the status word waits for the whole grid
         ok = launch_grid(reinterpret_cast<const void*>(kernel), groups, res::kThreads, params, lds, stream,
-                         rc.W == 1) == hipSuccess;
+                         rc.W == 1 && !a->status) == hipSuccess;
     });
-    if (!ok) return false;
-    ProfScope prof("sk_batch_sum", stream);
-    hipLaunchKernelGGL(sk::batch_sum, dim3(a->B), dim3(kWave), 0, stream, L.tau_partial, rc.W,
-                       -inv_tau, a->grad_tau, tg.status, a->status, tg.mark, keep_status ? 1 : 0);
-    return true;
+    return ok;
 }
 
 // Elements per launch of the register-resident adjoint at this shape (the
