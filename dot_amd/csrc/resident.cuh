@@ -732,6 +732,7 @@ struct FwdResArgs {
     unsigned xcc_tag;           // tag of the XCD-id words
     int mark;                   // failure mark in *status (forced_timeout)
     int local_ok;               // XCD-local exchange stores allowed (local_exchange_allowed)
+    int lagged_shift;           // shift the row exponentials by the last iteration's LSE
 };
 
 // Waits for G tagged per-workgroup deltas of iteration t and returns their
@@ -835,6 +836,9 @@ __global__ __launch_bounds__(kThreads) void forward(FwdResArgs a) {
     float lga_slot[RPW / GR];
 #pragma unroll
     for (int g = 0; g < RPW / GR; ++g) lga_slot[g] = lds_la[wave + kWaves * (g * GR + slot_of_lane<GR>(lane))];
+    float lse_slot[RPW / GR];  // the same row's log2-sum-exp of the last iteration (the next shift)
+#pragma unroll
+    for (int g = 0; g < RPW / GR; ++g) lse_slot[g] = 0.0f;
     float kscale2 = a.kscale * kLog2E;
     // scheduled runs: this iteration's scale, and the next one's already in flight
     float ks_it = a.kscale;
@@ -879,32 +883,60 @@ __global__ __launch_bounds__(kThreads) void forward(FwdResArgs a) {
         float uk[RPW];  // this wave's new u values; stored after the loop, which keeps it branch-free
 #pragma unroll
         for (int g0 = 0; g0 < RPW; g0 += GR) {
-            float y[GR][PL], lm[GR];
+            float y[GR][PL];
+            // The shift m of a row's exponentials: its log2-sum-exp of the
+            // previous iteration, which spares the row maximum and keeps the sum
+            // near 1 once v settles; the row maximum itself in the first
+            // iteration and whenever the shifted sum leaves [2^-30, 2^30] (a
+            // large change of v or of the scale, a row without a finite score).
+            // Within it the largest term is at least 2^-42, so every term that
+            // matters is a normal float, and the sum is above the floor
+            // (1e-12) that applies only to a maximum-shifted sum.
+            auto row_max = [&](const float (&v2)[PL]) {
+                float lm[GR];
 #pragma unroll
-            for (int r = 0; r < GR; ++r) {
-                lm[r] = -FLT_MAX;
+                for (int r = 0; r < GR; ++r) {
+                    lm[r] = -FLT_MAX;
+#pragma unroll
+                    for (int e = 0; e < PL; ++e) lm[r] = fmaxf(lm[r], fmaf(x[g0 + r][e], kscale2, v2[e]));
+                }
+                return transposed_reduce<GR>(lm, OpMax{});
+            };
+            auto shifted_exps = [&](float m, const float (&v2)[PL]) {
+                float ls[GR];
+#pragma unroll
+                for (int r = 0; r < GR; ++r) {
+                    const float mr = read_lane(m, lane_of_slot<GR>(r));
+                    ls[r] = 0.0f;
+#pragma unroll
+                    for (int e = 0; e < PL; ++e) {
+                        y[r][e] = __builtin_amdgcn_exp2f(fmaf(x[g0 + r][e], kscale2, v2[e]) - mr);
+                        ls[r] += y[r][e];
+                    }
+                }
+                return transposed_sum<GR>(ls);
+            };
+            const bool exact = t == 1 || !a.lagged_shift;
+            float m_l = exact ? row_max(v2) : lse_slot[g0 / GR];
+            float s_sum = shifted_exps(m_l, v2);
+            if (!exact && !__all(s_sum >= 0x1p-30f && s_sum <= 0x1p30f)) {
+                // v2 again, opaque to the compiler: kept from sharing the first
+                // pass's products, whose registers the exponentials then reuse
+                float v2r[PL];
 #pragma unroll
                 for (int e = 0; e < PL; ++e) {
-                    y[r][e] = fmaf(x[g0 + r][e], kscale2, v2[e]);
-                    lm[r] = fmaxf(lm[r], y[r][e]);
+                    v2r[e] = v2[e];
+                    asm volatile("" : "+v"(v2r[e]));
                 }
+                m_l = row_max(v2r);
+                s_sum = shifted_exps(m_l, v2r);
             }
-            const float m_l = transposed_reduce<GR>(lm, OpMax{});
-            float ls[GR], mr[GR];
-#pragma unroll
-            for (int r = 0; r < GR; ++r) {
-                mr[r] = read_lane(m_l, lane_of_slot<GR>(r));
-                ls[r] = 0.0f;
-#pragma unroll
-                for (int e = 0; e < PL; ++e) {
-                    y[r][e] = __builtin_amdgcn_exp2f(y[r][e] - mr[r]);
-                    ls[r] += y[r][e];
-                }
-            }
-            const float s_l = fmaxf(transposed_sum<GR>(ls), sk::kSumFloor);
+            const float s_l = fmaxf(s_sum, sk::kSumFloor);
             const float lga_l = lga_slot[g0 / GR];
             const float lg2 = __builtin_amdgcn_logf(s_l);  // log2
-            const float u_l = lga_l - kLn2 * (m_l + lg2);
+            const float lse = m_l + lg2;
+            lse_slot[g0 / GR] = lse;
+            const float u_l = lga_l - kLn2 * lse;
             const float w_l = __builtin_amdgcn_exp2f(fmaf(lga_l, kLog2E, -lg2));  // a / s
 #pragma unroll
             for (int r = 0; r < GR; ++r) {

@@ -469,6 +469,9 @@ bool launch_resident_forward(const dot_sinkhorn_fwd_args* a, const FwdLayout& L,
     r.R = rc.R;
     r.spin_limit = spin_limit();
     r.local_ok = local_exchange_allowed();
+    // DOT_AMD_EXACT_ROWMAX=1: every row update shifts by the row maximum
+    const char* exact_max = std::getenv("DOT_AMD_EXACT_ROWMAX");
+    r.lagged_shift = (exact_max && exact_max[0] == '1') ? 0 : 1;
     bool ok = false;
     dispatch_resident<true>(rc, [&](auto vc, auto cc, auto rr) {
         constexpr int V = decltype(vc)::value;

@@ -691,6 +691,12 @@ def test_resident_forward_outputs_cost_log_and_history(monkeypatch):
         a, b = res["1"][i], res["0"][i]
         if name == "counts":
             assert a.tolist() == b.tolist() == [T, 0]
+        elif name.endswith("_hist"):
+            # log-domain: the potentials of two fp32 paths that round differently
+            # (the resident row update shifts by the last iteration's LSE, the
+            # sweeps by the row maximum) agree to an absolute 1e-5, as each does
+            # with the float64 oracle below
+            assert (a - b).abs().max().item() < FWD_TOL, name
         else:
             assert rel_err(a, b.cpu().numpy()) < 1e-5, name
     o = osk.dual_forward(-C.cpu().numpy(), tau, T, log_a=lga.cpu().numpy(), keep_history=True)
