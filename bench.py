@@ -18,6 +18,8 @@ E * (T_f + T_b) per step with E = B*M*N, T_f = forward iterations executed
 and T_b = adjoint sweeps executed (averaged over the batch: the one-launch
 tiers end each element's sweeps once converged, ``result.adjoint_sweeps``), so
 it falls as the step gets shorter; ``ms_per_step`` is the step's wall time.
+The steps do not read ``n_iters_used`` (a wait for the forward): every step
+runs the same input, and the count is read once after the timed steps.
 The same line carries
 
 * ``roofline`` — the dominant kernel (the most time per step) against the
@@ -362,7 +364,6 @@ def bench_sinkhorn(args, workload, steps, warmup, torch, dot_amd, profiler, solv
         res = dot_amd.sinkhorn(leaf, reg=reg, n_iters=n_iters, tol=tol, a=a, b=b, **solver)
         res.cost.sum().backward()
         last["res"] = res
-        return res.n_iters_used
 
     from dot_amd.sinkhorn import _effective_method
     _, effective, eff_schedule, _ = _effective_method(
@@ -374,14 +375,17 @@ def bench_sinkhorn(args, workload, steps, warmup, torch, dot_amd, profiler, solv
         step()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    used = []
     for _ in range(steps):
-        used.append(step())
+        step()
     torch.cuda.synchronize()
     t1 = time.perf_counter()
+    # Every step runs the same input, so every step executes the same
+    # iterations: the count is read once, after the timed steps.  Reading it
+    # inside a step (a device-to-host wait for that step's forward) would
+    # time a loop that stalls the launch queue once per step.
+    T_f = float(last["res"].n_iters_used)
     stats = profiled_pass(profiler, SINKHORN_KERNELS, step, steps, torch)
 
-    T_f = sum(used) / len(used)
     # implicit: the sweeps each element's adjoint executed (at most backward_iters =
     # n_iters; the one-launch tiers end an element's sweeps once converged), averaged
     # over the batch (same input every step, same counts); unrolled: one reverse step
@@ -410,7 +414,7 @@ def bench_sinkhorn(args, workload, steps, warmup, torch, dot_amd, profiler, solv
                                   f" method={effective} schedule={eff_schedule}"),
                    "method": effective, "schedule": eff_schedule,
                    "B": B, "M": M, "N": N, "reg": reg, "n_iters": n_iters, "tol": tol,
-                   "n_iters_used": used[-1], "backward_iters": n_iters,
+                   "n_iters_used": int(T_f), "backward_iters": n_iters,
                    "adjoint_sweeps_executed": T_b,
                    "backward_mode": solver.get("backward_mode", "implicit")},
         "algorithmic_GBps": algo_bytes / sec_per_step / 1e9,

